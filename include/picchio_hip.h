@@ -1,0 +1,192 @@
+/* picchio_hip.h — C ABI of the MI355X (gfx950) quantized-MoE expert path.
+ *
+ * Drop-in boundary for picchio's expert path. Each entry point replaces one
+ * reference function (cited file:line into picchio) at its existing call
+ * site; all arguments are plain pointers, sizes and opaque handles.
+ *
+ * Conventions
+ *  - Every function returns PK_OK (0) or a negative PK_ERR_* code and never
+ *    exits the process; pk_last_error() gives a message for the calling thread.
+ *    (The reference exits on OOM / unknown format, quant.h:60-72, :334-336, and
+ *    silently skips a missing expert, picchio.c:730-733 / :1394; here both are
+ *    error codes, and a missing expert is fatal for the call.)
+ *  - Pointers named *_dev are device (HBM) pointers; *_host are host pointers.
+ *    Device work is queued on the engine's stream; functions that return host
+ *    results synchronise that stream before returning.
+ *  - Weight tensors are handed over in picchio's host layout (pk_qt_host ==
+ *    QT, quant.h:32-40) and re-laid out in HBM by the library.
+ */
+#ifndef PICCHIO_HIP_H
+#define PICCHIO_HIP_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PK_OK               0
+#define PK_ERR_ARG         -1   /* bad argument: null pointer, shape, id      */
+#define PK_ERR_HIP         -2   /* HIP runtime error                           */
+#define PK_ERR_OOM         -3   /* device allocation / store budget exceeded   */
+#define PK_ERR_UNSUPPORTED -4   /* format or shape the path does not implement */
+#define PK_ERR_MISSING     -5   /* expert / layer / tensor never uploaded      */
+#define PK_ERR_CONTEXT_FULL -6  /* pos >= context capacity                     */
+
+/* Tensor formats: QT.fmt values (quant.h:33). */
+#define PK_FMT_F32  0
+#define PK_FMT_INT8 1
+#define PK_FMT_INT4 2
+
+/* Model configuration. Field-for-field the parameter set of picchio's Cfg
+ * (picchio.c:53-83, defaults picchio.c:363-392), plus the two settings that
+ * picchio reads from the checkpoint instead of config.json (group_size,
+ * inferred at picchio.c:781-784; lm_head_fmt, picchio.c:2534-2650). */
+typedef struct pk_cfg {
+    int32_t hidden;            /* D (2880)                                  */
+    int32_t n_layers;          /* 24 (20B) / 36 (120B)                      */
+    int32_t n_heads;           /* 64                                        */
+    int32_t n_kv_heads;        /* 8                                         */
+    int32_t head_dim;          /* 64                                        */
+    int32_t n_experts;         /* 32 (20B) / 128 (120B)                     */
+    int32_t topk;              /* 4                                         */
+    int32_t moe_inter;         /* gate_up rows = 2 * intermediate (5760)    */
+    int32_t vocab;             /* 201088                                    */
+    int32_t ctx_len;           /* KV capacity in positions (kv_init max_pos)*/
+    int32_t sliding_window;    /* 128                                       */
+    float   eps;               /* RMSNorm epsilon (1e-5)                    */
+    float   theta;             /* RoPE base (150000)                        */
+    float   rope_factor;       /* YaRN factor (32)                          */
+    float   rope_beta_fast;    /* 32                                        */
+    float   rope_beta_slow;    /* 1                                         */
+    int32_t rope_original_ctx; /* 4096                                      */
+    int32_t rope_truncate;     /* 0/1                                       */
+    float   rope_attn_factor;  /* 0.1*ln(factor)+1 when factor > 1          */
+    float   swiglu_limit;      /* 7.0                                       */
+    float   swiglu_alpha;      /* 1.702                                     */
+    float   routed_scale;      /* 1.0                                       */
+    int32_t group_size;        /* expert INT4 scale group (64)              */
+    int32_t lm_head_fmt;       /* PK_FMT_F32 or PK_FMT_INT8                 */
+    int8_t  layer_type[128];   /* 0 = sliding window, 1 = full causal       */
+} pk_cfg;
+
+/* Host tensor in picchio's QT layout (quant.h:32-40):
+ *  F32 : data = float[O][I]
+ *  INT8: data = int8[O][I],  s = float[O]                 (per row)
+ *  INT4: data = uint8[O][ceil(I/2)], low nibble = even column, value = nib-8;
+ *        block_size == 0 -> s = float[O] (per row, quant.h:191-253)
+ *        block_size  > 0 -> s = float[O][ceil(I/block_size)] (quant.h:259-319) */
+typedef struct pk_qt_host {
+    int32_t fmt;
+    const void *data;
+    const float *s;
+    int32_t O, I;
+    int32_t block_size;
+} pk_qt_host;
+
+typedef struct pk_engine pk_engine;   /* one GPU, one stream, one HBM store  */
+typedef struct pk_qt pk_qt;           /* a weight tensor resident in HBM     */
+
+const char *pk_last_error(void);
+const char *pk_version(void);
+
+/* ── engine ────────────────────────────────────────────────────────────── */
+
+/* Creates an engine on `device` for `cfg`: allocates the HBM expert store
+ * (n_layers x n_experts slots, replacing the LRU pool of picchio.c:117-136 and
+ * its sizing at picchio.c:2938-3000), the dense-weight slots and the KV cache
+ * (kv_init, picchio.c:479-490). */
+int pk_engine_create(const pk_cfg *cfg, int device, pk_engine **out);
+int pk_engine_destroy(pk_engine *e);
+/* hipStream_t the engine queues its work on. */
+void *pk_engine_stream(pk_engine *e);
+int pk_engine_sync(pk_engine *e);
+/* Bytes of HBM held by the engine (store + dense + KV + scratch). */
+int64_t pk_engine_device_bytes(pk_engine *e);
+
+/* ── loading (replaces expert_load / load_dense_weights; picchio.c:698-888,
+ *    :2534-2650). Host tensors are copied; the caller keeps ownership. ── */
+
+/* One expert of one layer: gate_up [moe_inter][hidden], down [hidden][moe_inter/2],
+ * both INT4 group-scaled (block_size == cfg.group_size); biases fp32. */
+int pk_store_expert(pk_engine *e, int layer, int eid,
+                    const pk_qt_host *gate_up, const pk_qt_host *down,
+                    const float *gu_bias_host, const float *d_bias_host);
+
+/* Dense tensors of one layer (Layer, picchio.c:89-116). wq/wk/wv/wo must be F32. */
+typedef struct pk_layer_host {
+    const float *in_ln, *post_ln;              /* [hidden]                     */
+    pk_qt_host wq, wk, wv, wo;                 /* F32                          */
+    const float *bq, *bk, *bv, *bo;            /* biases                       */
+    const float *sinks;                        /* [n_heads]                    */
+    const float *router;                       /* [n_experts][hidden]          */
+    const float *router_bias;                  /* [n_experts]                  */
+} pk_layer_host;
+int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l);
+
+/* Embedding (F32), lm_head (F32 or INT8 per row) and the final norm. */
+int pk_store_globals(pk_engine *e, const pk_qt_host *embed,
+                     const pk_qt_host *lm_head, const float *final_norm_host);
+
+/* Builds every tensor of the engine's cfg from `seed` with the generator of
+ * pk_synth.h (N(0,0.02) weights, norms 1.0), quantizing the experts on the GPU
+ * with pk_quantize_int4_gs. `what`: bit 0 experts+routers, bit 1 attention,
+ * bit 2 embedding/lm_head/final norm. */
+int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, int n_threads);
+
+/* ── quantization (convert.py:45-93, the gs64 converter) ── */
+
+/* Device fp32 w[O][I] -> packed uint8[O][ceil(I/2)] + float[O][ceil(I/gs)],
+ * byte-identical to convert.quantize_int4(w, group_size=gs). */
+int pk_quantize_int4_gs(pk_engine *e, const float *w_dev, int O, int I, int gs,
+                        uint8_t *packed_dev, float *scales_dev);
+
+/* ── tensors and matmul_qt (quant.h:323-337) ── */
+
+int pk_qt_upload(pk_engine *e, const pk_qt_host *h, pk_qt **out);
+int pk_qt_free(pk_engine *e, pk_qt *t);
+/* y_dev[S][O] = x_dev[S][I] · Wᵀ (matmul_qt, quant.h:323). INT4 group-scaled
+ * results are bit-identical to quant.h's AVX2 matmul_i4_gs. */
+int pk_matmul_qt(pk_engine *e, float *y_dev, const float *x_dev, const pk_qt *w, int S);
+
+/* ── expert path ── */
+
+/* expert_apply (picchio.c:1768-1791): dst_dev[hidden] += w · expert(x_dev). */
+int pk_expert_apply(pk_engine *e, int layer, int eid, const float *x_dev,
+                    float *dst_dev, float w);
+
+/* moe_forward (picchio.c:1309-1466): out_dev = Σ_k (w_k·routed_scale)·expert_k(x).
+ * Optional host outputs: sel_host[topk], w_host[topk] (softmaxed weights) —
+ * passing either forces a stream sync. */
+int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
+                   int32_t *sel_host, float *w_host);
+
+/* Batched form for T tokens at once (the expert-grouped prefill of
+ * forward_prefill, picchio.c:1829-1916): x_dev[T][hidden] -> out_dev[T][hidden];
+ * sel_dev[T][topk] / w_dev[T][topk] optional device outputs. */
+int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
+                         float *out_dev, int32_t *sel_dev, float *w_dev);
+
+/* gqa_attention (picchio.c:504-623) for one token at `pos`; writes K/V. */
+int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
+                     float *out_dev);
+
+/* forward_token (picchio.c:1655-1756), greedy (TEMPERATURE=0, REP=1):
+ * returns the next token id in *next_host; logits_dev optional [vocab]. */
+int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host,
+                     float *logits_dev);
+
+/* prefill_tokens (picchio.c:1936-1975): runs ids[0..n) at pos_base.. and
+ * returns the token sampled after the last one. */
+int pk_prefill_tokens(pk_engine *e, const int32_t *ids_host, int n, int pos_base,
+                      int32_t *next_host);
+
+/* Greedy decode of n_steps after a prompt: out_host[n_steps] token ids. */
+int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
+                int n_steps, int32_t *out_host);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* PICCHIO_HIP_H */

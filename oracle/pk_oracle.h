@@ -1,0 +1,102 @@
+/* pk_oracle.h — CPU restatement of picchio's quantized-MoE expert path.
+ *
+ * TEST INFRASTRUCTURE ONLY. This library is the parity checker for the HIP
+ * path and the host-CPU baseline timed beside it. Only tests/, the smoke
+ * check and bench.py's cpu_baseline leg load it; the product library never
+ * links or calls it.
+ *
+ * Every function follows one reference function, cited file:line into
+ * picchio (quant.h, picchio.c, convert.py). Arithmetic order follows the
+ * reference as built by its Makefile (gcc -O3 with AVX2/FMA enabled, default
+ * -ffp-contract=fast): matmuls keep quant.h's 8-lane accumulators and hsum256
+ * tree, and every `a += b * c` the compiler contracts is an explicit fmaf here.
+ *
+ * Parity status per function (what pins it):
+ *   po_quantize_int4_gs    closed forms + exhaustive small cases (tests/)
+ *   po_quantize_int8_rows  closed forms (tests/)
+ *   po_quantize_rows_i4    golden vectors from quant.h (tests/golden)
+ *   po_matmul_*            golden vectors from quant.h (bit-exact)
+ *   po_rmsnorm/po_softmax  golden vectors + KATs from picchio.c self-test
+ *   po_swiglu_clamped      golden vectors from picchio.c (moe_forward)
+ *   po_moe_forward/po_expert_apply   golden vectors from picchio.c
+ *   po_gqa_attention/rope  golden vectors from picchio.c
+ *   po_forward_token/po_forward_prefill  golden token streams from picchio.c
+ */
+#ifndef PK_ORACLE_H
+#define PK_ORACLE_H
+
+#include <stdint.h>
+#include "../include/picchio_hip.h"   /* pk_cfg: the shared configuration type */
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ── quantizers ── */
+void po_quantize_int4_gs(const float *w, int O, int I, int gs,
+                         uint8_t *packed, float *scales);
+void po_quantize_int8_rows(const float *w, int O, int I, int8_t *q, float *scales);
+void po_quantize_rows_i4(const float *w, int O, int I, uint8_t *q4, float *scales);
+
+/* ── matmuls: y[S,O] = x[S,I] · Wᵀ ── */
+void po_matmul_f32(float *y, const float *x, const float *W, int S, int I, int O);
+void po_matmul_q8(float *y, const float *x, const int8_t *q, const float *scale,
+                  int S, int I, int O);
+void po_matmul_i4(float *y, const float *x, const uint8_t *q4, const float *scale,
+                  int S, int I, int O);
+void po_matmul_i4_gs(float *y, const float *x, const uint8_t *q4, const float *scale,
+                     int S, int I, int O, int gs);
+
+/* ── elementwise ── */
+void po_rmsnorm(float *out, const float *x, const float *w, int D, float eps);
+void po_softmax(float *x, int n);
+void po_swiglu_clamped(float *gu, int inter, float limit, float alpha);
+
+/* ── synthetic model (weights drawn with pk_synth.h) ── */
+typedef struct po_model po_model;
+
+/* Builds every tensor of `cfg` from `seed`. Experts are drawn fp32 and
+ * quantized with po_quantize_int4_gs(group_size); norms are 1.0. */
+po_model *po_model_build(const pk_cfg *cfg, uint64_t seed, int n_threads);
+void po_model_free(po_model *m);
+void po_model_reset_kv(po_model *m);
+
+/* Raw views of one expert (reference layout) for tests. */
+int po_model_expert(po_model *m, int layer, int eid,
+                    const uint8_t **gu_q4, const float **gu_s,
+                    const uint8_t **d_q4, const float **d_s,
+                    const float **gu_b, const float **d_b);
+const float *po_model_router(po_model *m, int layer, const float **bias);
+/* Dense fp32 tensor of the model by pk_synth kind (PK_T_ROUTER.. PK_T_LM_HEAD;
+ * kind 0 = final norm, kind -1/-2 = in_ln/post_ln of `layer`); for INT8
+ * lm_head, PK_T_LM_HEAD returns the int8 rows and *scales the row scales. */
+const void *po_model_tensor(po_model *m, int kind, int layer, const float **scales);
+/* Counter-based N(0,1)*std samples of pk_synth.h stream (seed, kind, layer, idx). */
+void po_fill_normal(uint64_t seed, int kind, int layer, int idx, int64_t first,
+                    int64_t n, float std, float *out);
+
+/* expert_apply (picchio.c:1768-1791): dst += w · expert(x). */
+void po_expert_apply(po_model *m, int layer, int eid, const float *x, float *dst, float w);
+/* moe_forward (picchio.c:1309-1466): out = Σ_k w_k·expert_k(x). */
+void po_moe_forward(po_model *m, int layer, const float *x, float *out,
+                    int *sel, float *wsel, float *logits);
+/* gqa_attention (picchio.c:504-623): writes K/V at pos, returns out[D]. */
+void po_gqa_attention(po_model *m, int layer, const float *x, int pos, float *out);
+/* rope_apply (picchio.c:455-473) on q[n_heads*hd], k[n_kv_heads*hd]. */
+void po_rope_apply(const pk_cfg *c, float *q, float *k, int pos);
+float po_yarn_inv_freq(const pk_cfg *c, int j);
+/* embed_token (picchio.c:1472-1503), fp32 table. */
+void po_embed(po_model *m, int tok, float *x);
+/* forward_token (picchio.c:1655-1756) with greedy sampling; logits optional. */
+int po_forward_token(po_model *m, int tok, int pos, float *logits);
+/* forward_prefill (picchio.c:1795-1932) for n tokens at pos_base. */
+int po_forward_prefill(po_model *m, const int *ids, int n, int pos_base);
+/* prefill_tokens (picchio.c:1936-1975): chunks of `batch` through forward_prefill. */
+int po_prefill_tokens(po_model *m, const int *ids, int n, int pos_base, int batch);
+/* greedy branch of sample_logits (picchio.c:1555-1560). */
+int po_argmax(const float *logits, int n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif
