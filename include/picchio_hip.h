@@ -186,6 +186,31 @@ int pk_prefill_tokens(pk_engine *e, const int32_t *ids_host, int n, int pos_base
 int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
                 int n_steps, int32_t *out_host);
 
+/* ── measurement (no reference counterpart: benchmark plumbing) ──
+ * With profiling on, the engine brackets each launch of the listed kernels
+ * with a pair of HIP events on its stream; pk_engine_profile_read syncs and
+ * returns the summed kernel time and launch count since the last reset. */
+#define PK_PROF_EXPERT_GATE_UP 0   /* INT4 gate_up GEMV + SwiGLU (all top-k experts) */
+#define PK_PROF_EXPERT_DOWN    1   /* INT4 down GEMV                                 */
+#define PK_PROF_ROUTER         2   /* router GEMV + top-k                            */
+#define PK_PROF_COMBINE        3   /* weighted combine                               */
+#define PK_PROF_N              8
+int pk_engine_profile(pk_engine *e, int enable);
+int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);
+/* Queues a bounded idle kernel (about `usec` microseconds, at most 1 s) so
+ * that the host can queue work ahead of the GPU before a profiled pass. */
+int pk_engine_stall(pk_engine *e, int usec);
+
+/* ── HIP graphs (no reference counterpart: launch amortisation) ──
+ * Everything the engine queues between pk_capture_begin and pk_capture_end
+ * (calls that return host results are refused while capturing) becomes one
+ * executable graph; pk_graph_launch replays it on the engine stream. */
+typedef struct pk_graph pk_graph;
+int pk_capture_begin(pk_engine *e);
+int pk_capture_end(pk_engine *e, pk_graph **out);
+int pk_graph_launch(pk_engine *e, pk_graph *g);
+int pk_graph_destroy(pk_graph *g);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,270 @@
+"""picchio_amd — MI355X (gfx950) quantized-MoE expert path of picchio.
+
+The product is the C-ABI library libpicchio_hip.so (include/picchio_hip.h).
+This module binds it with ctypes for tests and benchmarks; there is no
+Python or CPU fallback: loading fails loudly when the library is missing.
+"""
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(HERE)
+LIB_PATH = os.path.join(HERE, "libpicchio_hip.so")
+HEADER = os.path.join(ROOT, "include", "picchio_hip.h")
+
+PK_OK = 0
+ERRORS = {-1: "PK_ERR_ARG", -2: "PK_ERR_HIP", -3: "PK_ERR_OOM", -4: "PK_ERR_UNSUPPORTED",
+          -5: "PK_ERR_MISSING", -6: "PK_ERR_CONTEXT_FULL"}
+FMT_F32, FMT_INT8, FMT_INT4 = 0, 1, 2
+PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE = 0, 1, 2, 3
+
+
+class PkError(RuntimeError):
+    def __init__(self, code, msg):
+        super().__init__(f"{ERRORS.get(code, code)}: {msg}")
+        self.code = code
+
+
+class PkCfg(C.Structure):
+    """pk_cfg (include/picchio_hip.h)."""
+    _fields_ = [
+        ("hidden", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
+        ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("n_experts", C.c_int32),
+        ("topk", C.c_int32), ("moe_inter", C.c_int32), ("vocab", C.c_int32),
+        ("ctx_len", C.c_int32), ("sliding_window", C.c_int32),
+        ("eps", C.c_float), ("theta", C.c_float), ("rope_factor", C.c_float),
+        ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float),
+        ("rope_original_ctx", C.c_int32), ("rope_truncate", C.c_int32),
+        ("rope_attn_factor", C.c_float), ("swiglu_limit", C.c_float),
+        ("swiglu_alpha", C.c_float), ("routed_scale", C.c_float),
+        ("group_size", C.c_int32), ("lm_head_fmt", C.c_int32),
+        ("layer_type", C.c_int8 * 128),
+    ]
+
+
+class PkQtHost(C.Structure):
+    """pk_qt_host == picchio's QT (quant.h:32-40), host pointers."""
+    _fields_ = [("fmt", C.c_int32), ("data", C.c_void_p), ("s", C.c_void_p),
+                ("O", C.c_int32), ("I", C.c_int32), ("block_size", C.c_int32)]
+
+
+class PkLayerHost(C.Structure):
+    _fields_ = [("in_ln", C.c_void_p), ("post_ln", C.c_void_p),
+                ("wq", PkQtHost), ("wk", PkQtHost), ("wv", PkQtHost), ("wo", PkQtHost),
+                ("bq", C.c_void_p), ("bk", C.c_void_p), ("bv", C.c_void_p), ("bo", C.c_void_p),
+                ("sinks", C.c_void_p), ("router", C.c_void_p), ("router_bias", C.c_void_p)]
+
+
+def gptoss_cfg(**kw):
+    """GPT-OSS-20B-shaped configuration; keywords override.
+    Defaults follow picchio's cfg_load (picchio.c:363-392) with the YaRN
+    fields of GPT-OSS set explicitly (factor 32, original ctx 4096)."""
+    import math
+    import numpy as np
+    d = dict(hidden=2880, n_layers=24, n_heads=64, n_kv_heads=8, head_dim=64,
+             n_experts=32, topk=4, moe_inter=5760, vocab=201088, ctx_len=1024,
+             sliding_window=128, eps=1e-5, theta=150000.0, rope_factor=32.0,
+             rope_beta_fast=32.0, rope_beta_slow=1.0, rope_original_ctx=4096,
+             rope_truncate=0, swiglu_limit=7.0, swiglu_alpha=1.702,
+             routed_scale=1.0, group_size=64, lm_head_fmt=FMT_F32)
+    lt = kw.pop("layer_type", None)
+    d.update(kw)
+    if "rope_attn_factor" not in d:
+        f = np.float32(d["rope_factor"])
+        # picchio.c:380-381: 0.1f * logf(factor) + 1.0f
+        d["rope_attn_factor"] = float(np.float32(np.float32(0.1) * np.float32(math.log(f)))
+                                      + np.float32(1.0)) if f > 1 else 1.0
+    c = PkCfg(**d)
+    for i in range(128):
+        c.layer_type[i] = lt[i] if lt is not None and i < len(lt) else i % 2
+    return c
+
+
+_lib = None
+
+
+def lib():
+    """The native library (loaded once). Raises if it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is missing: run `python -m picchio_amd.build` "
+                           "(the expert path has no CPU fallback)")
+    L = C.CDLL(LIB_PATH)
+    vp, i32, i64, f32 = C.c_void_p, C.c_int32, C.c_int64, C.c_float
+    sig = {
+        "pk_last_error": (C.c_char_p, []),
+        "pk_version": (C.c_char_p, []),
+        "pk_engine_create": (C.c_int, [C.POINTER(PkCfg), C.c_int, C.POINTER(vp)]),
+        "pk_engine_destroy": (C.c_int, [vp]),
+        "pk_engine_stream": (vp, [vp]),
+        "pk_engine_sync": (C.c_int, [vp]),
+        "pk_engine_device_bytes": (i64, [vp]),
+        "pk_store_expert": (C.c_int, [vp, C.c_int, C.c_int, C.POINTER(PkQtHost),
+                                      C.POINTER(PkQtHost), vp, vp]),
+        "pk_store_layer": (C.c_int, [vp, C.c_int, C.POINTER(PkLayerHost)]),
+        "pk_store_globals": (C.c_int, [vp, C.POINTER(PkQtHost), C.POINTER(PkQtHost), vp]),
+        "pk_engine_build_synthetic": (C.c_int, [vp, C.c_uint64, C.c_int, C.c_int]),
+        "pk_quantize_int4_gs": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
+        "pk_qt_upload": (C.c_int, [vp, C.POINTER(PkQtHost), C.POINTER(vp)]),
+        "pk_qt_free": (C.c_int, [vp, vp]),
+        "pk_matmul_qt": (C.c_int, [vp, vp, vp, vp, C.c_int]),
+        "pk_expert_apply": (C.c_int, [vp, C.c_int, C.c_int, vp, vp, f32]),
+        "pk_moe_forward": (C.c_int, [vp, C.c_int, vp, vp, vp, vp]),
+        "pk_moe_forward_batch": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
+        "pk_gqa_attention": (C.c_int, [vp, C.c_int, vp, C.c_int, vp]),
+        "pk_forward_token": (C.c_int, [vp, C.c_int, C.c_int, vp, vp]),
+        "pk_prefill_tokens": (C.c_int, [vp, vp, C.c_int, C.c_int, vp]),
+        "pk_generate": (C.c_int, [vp, vp, C.c_int, C.c_int, vp]),
+        "pk_engine_profile": (C.c_int, [vp, C.c_int]),
+        "pk_engine_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(i64)]),
+        "pk_engine_stall": (C.c_int, [vp, C.c_int]),
+        "pk_capture_begin": (C.c_int, [vp]),
+        "pk_capture_end": (C.c_int, [vp, C.POINTER(vp)]),
+        "pk_graph_launch": (C.c_int, [vp, vp]),
+        "pk_graph_destroy": (C.c_int, [vp]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def check(rc):
+    if rc != PK_OK:
+        raise PkError(rc, lib().pk_last_error().decode())
+    return rc
+
+
+def ptr(a):
+    """Raw address of a numpy array or torch tensor."""
+    if hasattr(a, "data_ptr"):
+        return C.c_void_p(a.data_ptr())
+    return C.c_void_p(a.ctypes.data)
+
+
+class Engine:
+    """One pk_engine: GPU, stream and HBM store. Device buffers are torch
+    tensors allocated on the engine's stream so that the order of torch
+    copies and library kernels is the stream order."""
+
+    def __init__(self, cfg, device=0):
+        import torch
+        self.cfg = cfg
+        self.L = lib()
+        h = C.c_void_p()
+        check(self.L.pk_engine_create(C.byref(cfg), device, C.byref(h)))
+        self.h = h
+        self.device = torch.device("cuda", device)
+        self.stream = torch.cuda.ExternalStream(self.L.pk_engine_stream(h), device=self.device)
+
+    def close(self):
+        if self.h:
+            self.L.pk_engine_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def sync(self):
+        check(self.L.pk_engine_sync(self.h))
+
+    def device_bytes(self):
+        return self.L.pk_engine_device_bytes(self.h)
+
+    def profile(self, enable):
+        check(self.L.pk_engine_profile(self.h, 1 if enable else 0))
+
+    def profile_read(self, kernel):
+        ms = C.c_double()
+        n = C.c_int64()
+        check(self.L.pk_engine_profile_read(self.h, kernel, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
+    def stall(self, usec):
+        check(self.L.pk_engine_stall(self.h, int(usec)))
+
+    def capture_begin(self):
+        check(self.L.pk_capture_begin(self.h))
+
+    def capture_end(self):
+        g = C.c_void_p()
+        check(self.L.pk_capture_end(self.h, C.byref(g)))
+        return g
+
+    def graph_launch(self, g):
+        check(self.L.pk_graph_launch(self.h, g))
+
+    def graph_destroy(self, g):
+        check(self.L.pk_graph_destroy(g))
+
+    # torch helpers on the engine stream
+    def to_dev(self, arr, dtype=None):
+        import torch
+        with torch.cuda.stream(self.stream):
+            t = torch.as_tensor(arr).to(self.device, non_blocking=False)
+            if dtype is not None:
+                t = t.to(dtype)
+        self.stream.synchronize()
+        return t.contiguous()
+
+    def empty(self, shape, dtype):
+        import torch
+        with torch.cuda.stream(self.stream):
+            return torch.empty(shape, dtype=dtype, device=self.device)
+
+    def to_host(self, t):
+        self.sync()
+        return t.cpu().numpy()
+
+    # library calls
+    def build_synthetic(self, seed, what=7, threads=0):
+        check(self.L.pk_engine_build_synthetic(self.h, seed, what, threads))
+
+    def store_expert(self, layer, eid, gu_q4, gu_s, d_q4, d_s, gu_b, d_b):
+        c = self.cfg
+        gu = PkQtHost(FMT_INT4, gu_q4.ctypes.data, gu_s.ctypes.data, c.moe_inter, c.hidden, c.group_size)
+        dn = PkQtHost(FMT_INT4, d_q4.ctypes.data, d_s.ctypes.data, c.hidden, c.moe_inter // 2, c.group_size)
+        check(self.L.pk_store_expert(self.h, layer, eid, C.byref(gu), C.byref(dn),
+                                     ptr(gu_b), ptr(d_b)))
+
+    def store_router(self, layer, router, bias):
+        lh = PkLayerHost()
+        lh.router = router.ctypes.data
+        lh.router_bias = bias.ctypes.data
+        check(self.L.pk_store_layer(self.h, layer, C.byref(lh)))
+
+    def moe_forward(self, layer, x_dev, out_dev, want_routing=False):
+        import numpy as np
+        if want_routing:
+            sel = np.empty(self.cfg.topk, np.int32)
+            w = np.empty(self.cfg.topk, np.float32)
+            check(self.L.pk_moe_forward(self.h, layer, ptr(x_dev), ptr(out_dev), ptr(sel), ptr(w)))
+            return sel, w
+        check(self.L.pk_moe_forward(self.h, layer, ptr(x_dev), ptr(out_dev), None, None))
+        return None
+
+    def expert_apply(self, layer, eid, x_dev, dst_dev, w):
+        check(self.L.pk_expert_apply(self.h, layer, eid, ptr(x_dev), ptr(dst_dev), w))
+
+    def qt_upload(self, fmt, data, scales, O, I, block_size=0):
+        q = PkQtHost(fmt, data.ctypes.data, scales.ctypes.data if scales is not None else None,
+                     O, I, block_size)
+        h = C.c_void_p()
+        check(self.L.pk_qt_upload(self.h, C.byref(q), C.byref(h)))
+        return h
+
+    def qt_free(self, h):
+        check(self.L.pk_qt_free(self.h, h))
+
+    def matmul_qt(self, y_dev, x_dev, qt, S):
+        check(self.L.pk_matmul_qt(self.h, ptr(y_dev), ptr(x_dev), qt, S))
+
+    def quantize_int4_gs(self, w_dev, O, I, gs, packed_dev, scales_dev):
+        check(self.L.pk_quantize_int4_gs(self.h, ptr(w_dev), O, I, gs, ptr(packed_dev), ptr(scales_dev)))

@@ -1,0 +1,318 @@
+// pk_dense.hip — fp32 / int8 GEMV, RMSNorm, router top-k, combine, and the
+// on-device synthetic weight generator.
+#include "pk_internal.h"
+#include "pk_synth.h"
+
+// ───────────────────────── wave reductions ─────────────────────────
+__device__ __forceinline__ float pk_wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double pk_wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+// ───────────────────────── fp32 GEMV ─────────────────────────
+// y[s][o] = x[s] . W[o] (+ bias[o]), matmul_f32 (quant.h:117-148). One wave
+// per row; lanes stride the row in float4 so each load instruction reads
+// 1 KiB contiguous. fp32 sum in tree order (not the reference's 8-lane
+// order: within 1e-6 relative, checked against the oracle at 1e-4).
+template <int RPW>
+__global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const float *__restrict__ x,
+                                                  const float *__restrict__ W,
+                                                  const float *__restrict__ bias, int S, int I, int O) {
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * RPW;
+    const int s = blockIdx.y;
+    const float *xs = x + (int64_t)s * I;
+    const int n4 = I >> 2;
+    float acc[RPW];
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    for (int i = lane; i < n4; i += 64) {
+        const float4 xv = x4[i];
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int o = row0 + r;
+            if (o < O) {
+                const pk_f32x4 wv = __builtin_nontemporal_load(
+                    reinterpret_cast<const pk_f32x4 *>(W + (int64_t)o * I) + i);
+                acc[r] = __builtin_fmaf(xv.x, wv.x, acc[r]);
+                acc[r] = __builtin_fmaf(xv.y, wv.y, acc[r]);
+                acc[r] = __builtin_fmaf(xv.z, wv.z, acc[r]);
+                acc[r] = __builtin_fmaf(xv.w, wv.w, acc[r]);
+            }
+        }
+    }
+    for (int i = (n4 << 2) + lane; i < I; i += 64) {
+#pragma unroll
+        for (int r = 0; r < RPW; ++r) {
+            const int o = row0 + r;
+            if (o < O) acc[r] = __builtin_fmaf(xs[i], W[(int64_t)o * I + i], acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+        const float v = pk_wave_sum(acc[r]);
+        const int o = row0 + r;
+        if (lane == 0 && o < O) y[(int64_t)s * O + o] = bias ? v + bias[o] : v;
+    }
+}
+
+int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
+                       int S, int I, int O, hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv f32: bad shape");
+    PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0,
+             PK_ERR_UNSUPPORTED, "gemv f32: needs 16-byte aligned rows (I=%d)", I);
+    constexpr int RPW = 2;
+    const int rows_per_block = 4 * RPW;
+    hipLaunchKernelGGL((k_gemv_f32<RPW>), dim3((O + rows_per_block - 1) / rows_per_block, S),
+                       dim3(256), 0, st, y, x, W, bias, S, I, O);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── int8 GEMV ─────────────────────────
+// matmul_q8 (quant.h:152-186): fp32 accumulation of x*q, times the row scale.
+__global__ __launch_bounds__(256) void k_gemv_q8(float *__restrict__ y, const float *__restrict__ x,
+                                                 const int8_t *__restrict__ q,
+                                                 const float *__restrict__ sc, int S, int I, int O) {
+    const int lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int s = blockIdx.y;
+    if (o >= O) return;
+    const float *xs = x + (int64_t)s * I;
+    const int8_t *w = q + (int64_t)o * I;
+    float acc = 0.0f;
+    const int n16 = I >> 4;
+    for (int i = lane; i < n16; i += 64) {
+        const pk_i32x4 v = __builtin_nontemporal_load(reinterpret_cast<const pk_i32x4 *>(w) + i);
+        const int32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                acc = __builtin_fmaf(xs[i * 16 + k * 4 + b], (float)(int8_t)(d[k] >> (8 * b)), acc);
+    }
+    for (int i = (n16 << 4) + lane; i < I; i += 64) acc = __builtin_fmaf(xs[i], (float)w[i], acc);
+    const float v = pk_wave_sum(acc);
+    if (lane == 0) y[(int64_t)s * O + o] = v * sc[o];
+}
+
+int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
+                      int S, int I, int O, hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv q8: bad shape");
+    PK_CHECK(((uintptr_t)q & 15) == 0 && (I & 15) == 0, PK_ERR_UNSUPPORTED,
+             "gemv q8: needs I %% 16 == 0 and 16-byte aligned rows");
+    hipLaunchKernelGGL(k_gemv_q8, dim3((O + 3) / 4, S), dim3(256), 0, st, y, x, q, s, S, I, O);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// Per-row INT4 (quant.h:191-253): fp32 sum of x*(nib-8), times the row scale.
+__global__ __launch_bounds__(256) void k_gemv_i4_row(float *__restrict__ y, const float *__restrict__ x,
+                                                     const uint8_t *__restrict__ q4,
+                                                     const float *__restrict__ sc, int S, int I, int O) {
+    const int lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int s = blockIdx.y;
+    if (o >= O) return;
+    const float *xs = x + (int64_t)s * I;
+    const uint8_t *w = q4 + (int64_t)o * ((I + 1) / 2);
+    float acc = 0.0f;
+    for (int i = lane; i < I; i += 64) {
+        const uint8_t b = w[i >> 1];
+        const int nib = (i & 1) ? (b >> 4) : (b & 15);
+        acc = __builtin_fmaf(xs[i], (float)(nib - 8), acc);
+    }
+    const float v = pk_wave_sum(acc);
+    if (lane == 0) y[(int64_t)s * O + o] = v * sc[o];
+}
+
+int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, const float *s,
+                               int S, int I, int O, hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv i4 row: bad shape");
+    hipLaunchKernelGGL(k_gemv_i4_row, dim3((O + 3) / 4, S), dim3(256), 0, st, y, x, q4, s, S, I, O);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── RMSNorm ─────────────────────────
+// rmsnorm (quant.h:396-402): sum of x^2 in double (each term exact), one
+// float rsqrt, out = (x * r) * w. Only the summation order of the double
+// accumulator differs from the reference, far below float resolution.
+__global__ __launch_bounds__(256) void k_rmsnorm(float *out, const float *x, const float *w, int D,
+                                                 float eps) {
+    __shared__ double part[4];
+    __shared__ float rs;
+    const int t = blockIdx.x;
+    const float *xr = x + (int64_t)t * D;
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < D; i += 256) acc += (double)xr[i] * (double)xr[i];
+    acc = pk_wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double ms = ((part[0] + part[1]) + (part[2] + part[3]));
+        rs = 1.0f / sqrtf((float)(ms / D) + eps);
+    }
+    __syncthreads();
+    const float r = rs;
+    float *o = out + (int64_t)t * D;
+    for (int i = threadIdx.x; i < D; i += 256) o[i] = xr[i] * r * w[i];
+}
+
+int pk_launch_rmsnorm(float *out, const float *x, const float *w, int D, float eps, int T,
+                      hipStream_t st) {
+    PK_CHECK(D > 0 && T > 0, PK_ERR_ARG, "rmsnorm: bad shape");
+    hipLaunchKernelGGL(k_rmsnorm, dim3(T), dim3(256), 0, st, out, x, w, D, eps);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── router top-k ─────────────────────────
+// picchio.c:1330-1355: K rounds of argmax with strict '>' (ties -> lowest
+// index, already-chosen experts skipped), softmax over the K raw logits
+// (quant.h:406-412), weight_k * routed_scale for the combine (:1445).
+// One wave per token; logits [T][E] -> sel [T][K], w [T][K].
+__global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E, int K,
+                                                     float routed_scale, int32_t *sel,
+                                                     float *w_scaled, float *w_soft) {
+    const int t = blockIdx.x;
+    const int lane = threadIdx.x;
+    const float *lg = logits + (int64_t)t * E;
+    // each lane holds experts lane, lane+64 (E <= 128)
+    float v0 = lane < E ? lg[lane] : -INFINITY;
+    float v1 = lane + 64 < E ? lg[lane + 64] : -INFINITY;
+    bool t0 = lane >= E, t1 = lane + 64 >= E;
+    int chosen[16];
+    float val[16];
+    for (int k = 0; k < K; ++k) {
+        // best of this lane (lower index first on ties)
+        float bv = -1e30f;
+        int bi = 0x7fffffff;
+        if (!t0 && v0 > bv) { bv = v0; bi = lane; }
+        if (!t1 && v1 > bv) { bv = v1; bi = lane + 64; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        chosen[k] = bi;
+        val[k] = bv;
+        if (bi == lane) t0 = true;
+        if (bi == lane + 64) t1 = true;
+    }
+    if (lane == 0) {
+        float m = -1e30f;
+        for (int k = 0; k < K; ++k) if (val[k] > m) m = val[k];
+        float e[16], s = 0.0f;
+        for (int k = 0; k < K; ++k) { e[k] = expf(val[k] - m); s += e[k]; }
+        for (int k = 0; k < K; ++k) {
+            const float p = e[k] / s;
+            sel[(int64_t)t * K + k] = chosen[k];
+            if (w_soft) w_soft[(int64_t)t * K + k] = p;
+            w_scaled[(int64_t)t * K + k] = p * routed_scale;
+        }
+    }
+}
+
+int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D, int K,
+                          float routed_scale, float *logits, int32_t *sel, float *w_scaled,
+                          float *w_soft, uint32_t *counter, hipStream_t st) {
+    (void)counter;
+    PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
+             "router: E=%d K=%d outside 1..128 / 1..16", E, K);
+    PK_TRY(pk_launch_gemv_f32(logits, x, R, b, 1, D, E, st));
+    hipLaunchKernelGGL(k_topk_softmax, dim3(1), dim3(64), 0, st, logits, E, K, routed_scale,
+                       sel, w_scaled, w_soft);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// Batched router: logits [T][E] already computed.
+int pk_launch_topk_batch(const float *logits, int T, int E, int K, float routed_scale,
+                         int32_t *sel, float *w_scaled, float *w_soft, hipStream_t st) {
+    PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
+             "router: E=%d K=%d outside 1..128 / 1..16", E, K);
+    hipLaunchKernelGGL(k_topk_softmax, dim3(T), dim3(64), 0, st, logits, E, K, routed_scale,
+                       sel, w_scaled, w_soft);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── combine ─────────────────────────
+// moe_forward's accumulation (picchio.c:1387, :1445-1454): out = 0, then
+// out = fma(w_k, eo_k, out) for k in routing order; optional residual add
+// afterwards (forward_token, picchio.c:1714-1716): res + out.
+__global__ void k_combine(float *out, const float *eo, const float *w, int K, int D,
+                          const float *residual, float *res_out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= D) return;
+    float o = 0.0f;
+    for (int k = 0; k < K; ++k) o = __builtin_fmaf(w[k], eo[(int64_t)k * D + i], o);
+    if (out) out[i] = o;
+    if (res_out) res_out[i] = residual[i] + o;
+}
+
+int pk_launch_combine(float *out, const float *eo, const float *w, int K, int D,
+                      const float *residual, float *res_out, hipStream_t st) {
+    hipLaunchKernelGGL(k_combine, dim3((D + 255) / 256), dim3(256), 0, st, out, eo, w, K, D,
+                       residual, res_out);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// dst += w * eo (expert_apply, picchio.c:1788); w read from device memory.
+__global__ void k_axpy_dev(float *dst, const float *eo, const float *w, int D) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < D) dst[i] = __builtin_fmaf(w[0], eo[i], dst[i]);
+}
+__global__ void k_axpy(float *dst, const float *eo, float w, int D) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < D) dst[i] = __builtin_fmaf(w, eo[i], dst[i]);
+}
+
+int pk_launch_axpy(float *dst, const float *eo, float w, int D, hipStream_t st) {
+    hipLaunchKernelGGL(k_axpy, dim3((D + 255) / 256), dim3(256), 0, st, dst, eo, w, D);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────── synthetic N(0,1)*std on the GPU ─────────────────────
+// Same counter formula as pk_synth.h (SplitMix64 + Box-Muller in double);
+// device log/sqrt/sin/cos may differ from glibc in the last double bit, which
+// changes the rounded float in about one element per 10^9.
+__global__ void k_fill_normal(float *out, int64_t n, uint64_t s, float std) {
+    const int64_t pair = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (2 * pair >= n) return;
+    double n0, n1;
+    pk_normal_pair(s, (uint64_t)pair, &n0, &n1);
+    out[2 * pair] = (float)(n0 * (double)std);
+    if (2 * pair + 1 < n) out[2 * pair + 1] = (float)(n1 * (double)std);
+}
+
+int pk_launch_fill_normal(float *out, int64_t n, uint64_t stream_seed, float std, hipStream_t st) {
+    const int64_t pairs = (n + 1) / 2;
+    hipLaunchKernelGGL(k_fill_normal, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, st,
+                       out, n, stream_seed, std);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+__global__ void k_fill_const(float *out, int64_t n, float v) {
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = v;
+}
+
+int pk_launch_fill_const(float *out, int64_t n, float v, hipStream_t st) {
+    hipLaunchKernelGGL(k_fill_const, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, out, n, v);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}

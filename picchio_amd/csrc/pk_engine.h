@@ -1,0 +1,87 @@
+// pk_engine.h — engine state shared by the host-side translation units.
+#pragma once
+
+#include "pk_internal.h"
+
+struct pk_layer_dev {
+    float *in_ln = nullptr, *post_ln = nullptr;
+    float *wqkv = nullptr, *bqkv = nullptr;   // [(H + 2 KVH) hd][D], bias
+    float *wo = nullptr, *bo = nullptr;       // [D][H hd], bias
+    float *sinks = nullptr;                   // [H]
+    float *router = nullptr, *router_b = nullptr;  // [E][D], [E]
+    bool have_attn = false, have_router = false;
+};
+
+struct pk_engine {
+    pk_cfg c{};
+    int device = 0;
+    hipStream_t stream = nullptr;
+    int64_t device_bytes = 0;
+
+    // expert store: n_layers * n_experts slots of `ex.stride` bytes
+    pk_expert_layout ex{};
+    uint8_t *store = nullptr;
+    uint8_t *expert_ready = nullptr;          // host flags [L*E]
+
+    pk_layer_dev *L = nullptr;                // host array of device pointers
+    float *embed = nullptr;                   // [vocab][D] fp32
+    float *lm_f32 = nullptr;                  // [vocab][D]
+    int8_t *lm_q8 = nullptr;                  // [vocab][D]
+    float *lm_s = nullptr;                    // [vocab]
+    float *final_norm = nullptr;
+    bool have_globals = false;
+
+    float *rope = nullptr;                    // [ctx][hd/2][2] (cos, sin) * attn_factor
+    float *K = nullptr, *V = nullptr;         // [L][ctx][kv_dim]
+
+    // staging for uploads / synthetic builds
+    uint8_t *stage = nullptr;
+    int64_t stage_bytes = 0;
+
+    // decode scratch
+    float *x_in = nullptr, *h = nullptr, *hn = nullptr, *attn_out = nullptr;
+    float *qkv = nullptr, *att = nullptr, *logits = nullptr;
+    float *r_logits = nullptr, *w_scaled = nullptr, *w_soft = nullptr;
+    int32_t *sel = nullptr;
+    float *act = nullptr, *eo = nullptr;
+    float *attn_part = nullptr;               // split-K attention partials
+    int32_t *argmax_out = nullptr;
+    uint32_t *counters = nullptr;
+
+    bool capturing = false;                  // inside pk_capture_begin/end
+
+    // opt-in per-kernel timing (pk_engine_profile)
+    bool prof = false;
+    static constexpr int PROF_CAP = 16384;
+    hipEvent_t *prof_ev = nullptr;           // [PROF_CAP][2]
+    int *prof_kind = nullptr;                // [PROF_CAP]
+    int prof_n = 0;
+    double prof_ms[PK_PROF_N] = {0};
+    int64_t prof_cnt[PK_PROF_N] = {0};
+
+    // batched scratch (grown on demand)
+    int64_t batch_cap = 0;
+    float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
+    int32_t *b_sel = nullptr;
+};
+
+int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes);
+void pk_dev_free(pk_engine *e, void *p);
+int pk_stage_reserve(pk_engine *e, int64_t bytes);
+
+// kernels defined in pk_dense.hip / pk_attn.hip without a launcher above
+int pk_launch_topk_batch(const float *logits, int T, int E, int K, float routed_scale,
+                         int32_t *sel, float *w_scaled, float *w_soft, hipStream_t st);
+int pk_launch_combine(float *out, const float *eo, const float *w, int K, int D,
+                      const float *residual, float *res_out, hipStream_t st);
+int pk_launch_axpy(float *dst, const float *eo, float w, int D, hipStream_t st);
+int pk_launch_fill_normal(float *out, int64_t n, uint64_t stream_seed, float std, hipStream_t st);
+int pk_launch_fill_const(float *out, int64_t n, float v, hipStream_t st);
+
+// profiling brackets around a launch (no-ops unless profiling is on)
+int pk_prof_begin(pk_engine *e, int kind);
+int pk_prof_end(pk_engine *e, int slot);
+
+// internal MoE pieces reused by the decode driver
+int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
+                 const float *residual, float *res_out);

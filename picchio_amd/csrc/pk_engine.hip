@@ -1,0 +1,816 @@
+// pk_engine.hip — host side of the C ABI: engine, HBM expert store, uploads,
+// matmul_qt and the MoE call chain.
+#include "pk_engine.h"
+#include "pk_synth.h"
+
+#include <math.h>
+#include <stdarg.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <vector>
+
+// ───────────────────────── errors ─────────────────────────
+static thread_local char g_err[512] = "";
+
+void pk_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+}
+
+extern "C" const char *pk_last_error(void) { return g_err; }
+extern "C" const char *pk_version(void) { return "picchio-amd 0.1 (gfx950)"; }
+
+// ───────────────────────── memory ─────────────────────────
+int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes) {
+    *p = nullptr;
+    if (bytes <= 0) return PK_OK;
+    hipError_t rc = hipMalloc(p, (size_t)bytes);
+    if (rc != hipSuccess) {
+        *p = nullptr;
+        (void)hipGetLastError();
+        pk_set_error("hipMalloc(%lld bytes) failed: %s", (long long)bytes, hipGetErrorString(rc));
+        return PK_ERR_OOM;
+    }
+    e->device_bytes += bytes;
+    return PK_OK;
+}
+
+void pk_dev_free(pk_engine *e, void *p) {
+    (void)e;
+    if (p) (void)hipFree(p);
+}
+
+int pk_stage_reserve(pk_engine *e, int64_t bytes) {
+    if (bytes <= e->stage_bytes) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "uploads are not available while capturing a graph");
+    PK_HIP(hipStreamSynchronize(e->stream));
+    if (e->stage) {
+        pk_dev_free(e, e->stage);
+        e->device_bytes -= e->stage_bytes;
+        e->stage = nullptr;
+        e->stage_bytes = 0;
+    }
+    PK_TRY(pk_dev_alloc(e, (void **)&e->stage, bytes));
+    e->stage_bytes = bytes;
+    return PK_OK;
+}
+
+#define ALLOC(ptr, bytes) PK_TRY(pk_dev_alloc(e, (void **)&(ptr), (int64_t)(bytes)))
+
+// ───────────────────────── configuration ─────────────────────────
+static int cfg_check(const pk_cfg *c) {
+    PK_CHECK(c, PK_ERR_ARG, "cfg is null");
+    PK_CHECK(c->hidden > 0 && c->n_layers > 0 && c->n_experts > 0 && c->topk > 0, PK_ERR_ARG,
+             "cfg: non-positive dimension");
+    PK_CHECK(c->topk <= c->n_experts && c->topk <= 16 && c->n_experts <= 128, PK_ERR_UNSUPPORTED,
+             "cfg: topk=%d n_experts=%d (supported: topk <= 16, experts <= 128)", c->topk,
+             c->n_experts);
+    PK_CHECK(c->moe_inter > 0 && c->moe_inter % 2 == 0, PK_ERR_ARG, "cfg: moe_inter must be even");
+    PK_CHECK(c->group_size == PK_GS, PK_ERR_UNSUPPORTED,
+             "cfg: expert group_size %d (the HBM store holds gs64 experts)", c->group_size);
+    PK_CHECK(c->hidden % PK_GS == 0 && (c->moe_inter / 2) % PK_GS == 0, PK_ERR_UNSUPPORTED,
+             "cfg: hidden and moe_inter/2 must be multiples of 64");
+    PK_CHECK(c->n_layers <= 128, PK_ERR_UNSUPPORTED, "cfg: more than 128 layers");
+    PK_CHECK(c->n_heads > 0 && c->n_kv_heads > 0 && c->n_heads % c->n_kv_heads == 0, PK_ERR_ARG,
+             "cfg: n_heads must be a multiple of n_kv_heads");
+    PK_CHECK(c->head_dim > 0 && c->head_dim <= 128 && c->head_dim % 2 == 0, PK_ERR_UNSUPPORTED,
+             "cfg: head_dim %d (supported: even, <= 128)", c->head_dim);
+    PK_CHECK(c->ctx_len > 0 && c->vocab > 0, PK_ERR_ARG, "cfg: ctx_len / vocab must be positive");
+    PK_CHECK(c->lm_head_fmt == PK_FMT_F32 || c->lm_head_fmt == PK_FMT_INT8, PK_ERR_UNSUPPORTED,
+             "cfg: lm_head_fmt %d", c->lm_head_fmt);
+    return PK_OK;
+}
+
+static pk_expert_layout make_layout(const pk_cfg *c) {
+    pk_expert_layout L{};
+    L.gu = pk_i4_make_shape(c->moe_inter, c->hidden);
+    L.dn = pk_i4_make_shape(c->hidden, c->moe_inter / 2);
+    int64_t off = 0;
+    L.off_gu_tiles = off;   off = pk_align256(off + L.gu.tile_bytes);
+    L.off_dn_tiles = off;   off = pk_align256(off + L.dn.tile_bytes);
+    L.off_gu_scales = off;  off = pk_align256(off + L.gu.scale_bytes);
+    L.off_dn_scales = off;  off = pk_align256(off + L.dn.scale_bytes);
+    L.off_gu_bias = off;    off = pk_align256(off + (int64_t)c->moe_inter * 4);
+    L.off_dn_bias = off;    off = pk_align256(off + (int64_t)c->hidden * 4);
+    L.stride = off;
+    return L;
+}
+
+// RoPE table: cos/sin(pos * yarn_inv_freq(j)) * attn_factor in host libm,
+// exactly as rope_apply computes them (picchio.c:431-466).
+static float yarn_inv_freq(const pk_cfg *c, int j) {
+    const int dim = c->head_dim;
+    const float pos_freq = powf(c->theta, 2.0f * (float)j / (float)dim);
+    const float extrap = 1.0f / pos_freq;
+    if (c->rope_factor <= 1.0f) return extrap;
+    const float pi = (float)M_PI;
+    float low = (float)dim * logf((float)c->rope_original_ctx / (c->rope_beta_fast * 2.0f * pi)) /
+                (2.0f * logf(c->theta));
+    float high = (float)dim * logf((float)c->rope_original_ctx / (c->rope_beta_slow * 2.0f * pi)) /
+                 (2.0f * logf(c->theta));
+    if (c->rope_truncate) { low = floorf(low); high = ceilf(high); }
+    if (low < 0) low = 0;
+    if (high > dim - 1) high = (float)(dim - 1);
+    if (low == high) high += 0.001f;
+    float ramp = ((float)j - low) / (high - low);
+    if (ramp < 0) ramp = 0;
+    if (ramp > 1) ramp = 1;
+    const float ef = 1.0f - ramp;
+    const float interp = extrap / c->rope_factor;
+    return fmaf(interp, 1.0f - ef, extrap * ef);   // contracted as in the reference build
+}
+
+static int build_rope_table(pk_engine *e) {
+    const pk_cfg *c = &e->c;
+    const int half = c->head_dim / 2;
+    std::vector<float> inv(half), tab((size_t)c->ctx_len * half * 2);
+    for (int j = 0; j < half; ++j) inv[j] = yarn_inv_freq(c, j);
+    for (int p = 0; p < c->ctx_len; ++p)
+        for (int j = 0; j < half; ++j) {
+            const float ang = (float)p * inv[j];
+            tab[((size_t)p * half + j) * 2 + 0] = cosf(ang) * c->rope_attn_factor;
+            tab[((size_t)p * half + j) * 2 + 1] = sinf(ang) * c->rope_attn_factor;
+        }
+    PK_HIP(hipMemcpy(e->rope, tab.data(), tab.size() * sizeof(float), hipMemcpyHostToDevice));
+    return PK_OK;
+}
+
+static void engine_free(pk_engine *e) {
+    if (!e) return;
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    void *ptrs[] = {e->store, e->embed, e->lm_f32, e->lm_q8, e->lm_s, e->final_norm, e->rope,
+                    e->K, e->V, e->stage, e->x_in, e->h, e->hn, e->attn_out, e->qkv, e->att,
+                    e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
+                    e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
+                    e->b_eo, e->b_sel};
+    for (void *p : ptrs) pk_dev_free(e, p);
+    if (e->L) {
+        for (int l = 0; l < e->c.n_layers; ++l) {
+            pk_layer_dev &d = e->L[l];
+            void *lp[] = {d.in_ln, d.post_ln, d.wqkv, d.bqkv, d.wo, d.bo, d.sinks, d.router, d.router_b};
+            for (void *p : lp) pk_dev_free(e, p);
+        }
+        delete[] e->L;
+    }
+    free(e->expert_ready);
+    if (e->prof_ev) {
+        for (int i = 0; i < 2 * pk_engine::PROF_CAP; ++i) (void)hipEventDestroy(e->prof_ev[i]);
+        delete[] e->prof_ev;
+        delete[] e->prof_kind;
+    }
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+}
+
+static int engine_init(pk_engine *e) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, E = c->n_experts, L = c->n_layers;
+    const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, K = c->topk;
+    const int half = c->moe_inter / 2;
+    e->ex = make_layout(c);
+    ALLOC(e->store, e->ex.stride * (int64_t)L * E);
+    e->expert_ready = (uint8_t *)calloc((size_t)L * E, 1);
+    PK_CHECK(e->expert_ready, PK_ERR_OOM, "host allocation failed");
+    e->L = new pk_layer_dev[L];
+    const int64_t kv = (int64_t)L * c->ctx_len * KVH * hd * 4;
+    ALLOC(e->K, kv);
+    ALLOC(e->V, kv);
+    PK_HIP(hipMemsetAsync(e->K, 0, kv, e->stream));
+    PK_HIP(hipMemsetAsync(e->V, 0, kv, e->stream));
+    ALLOC(e->rope, (int64_t)c->ctx_len * hd * 4);
+    PK_TRY(build_rope_table(e));
+    const int qkv_rows = (H + 2 * KVH) * hd;
+    ALLOC(e->x_in, D * 4);
+    ALLOC(e->h, D * 4);
+    ALLOC(e->hn, D * 4);
+    ALLOC(e->attn_out, D * 4);
+    ALLOC(e->qkv, qkv_rows * 4);
+    ALLOC(e->att, H * hd * 4);
+    ALLOC(e->logits, (int64_t)c->vocab * 4);
+    ALLOC(e->r_logits, E * 4);
+    ALLOC(e->w_scaled, K * 4);
+    ALLOC(e->w_soft, K * 4);
+    ALLOC(e->sel, K * 4);
+    ALLOC(e->act, (int64_t)K * half * 4);
+    ALLOC(e->eo, (int64_t)K * D * 4);
+    ALLOC(e->argmax_out, 64);
+    ALLOC(e->counters, 4096);
+    PK_HIP(hipMemsetAsync(e->counters, 0, 4096, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_engine_create(const pk_cfg *cfg, int device, pk_engine **out) {
+    PK_CHECK(out, PK_ERR_ARG, "out is null");
+    *out = nullptr;
+    PK_TRY(cfg_check(cfg));
+    int n = 0;
+    PK_HIP(hipGetDeviceCount(&n));
+    PK_CHECK(device >= 0 && device < n, PK_ERR_ARG, "device %d not present (%d devices)", device, n);
+    PK_HIP(hipSetDevice(device));
+    pk_engine *e = new pk_engine();
+    e->c = *cfg;
+    e->device = device;
+    hipError_t rc = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+    if (rc != hipSuccess) {
+        pk_set_error("hipStreamCreate: %s", hipGetErrorString(rc));
+        delete e;
+        return PK_ERR_HIP;
+    }
+    int st = engine_init(e);
+    if (st != PK_OK) {
+        char msg[512];
+        snprintf(msg, sizeof(msg), "%s", pk_last_error());
+        engine_free(e);
+        pk_set_error("%s", msg);
+        return st;
+    }
+    *out = e;
+    return PK_OK;
+}
+
+extern "C" int pk_engine_destroy(pk_engine *e) {
+    engine_free(e);
+    return PK_OK;
+}
+
+extern "C" void *pk_engine_stream(pk_engine *e) { return e ? (void *)e->stream : nullptr; }
+
+extern "C" int pk_engine_sync(pk_engine *e) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+extern "C" int64_t pk_engine_device_bytes(pk_engine *e) { return e ? e->device_bytes : -1; }
+
+// ───────────────────────── profiling ─────────────────────────
+static int prof_flush(pk_engine *e) {
+    if (!e->prof_n) return PK_OK;
+    PK_HIP(hipStreamSynchronize(e->stream));
+    for (int i = 0; i < e->prof_n; ++i) {
+        float ms = 0.f;
+        PK_HIP(hipEventElapsedTime(&ms, e->prof_ev[2 * i], e->prof_ev[2 * i + 1]));
+        e->prof_ms[e->prof_kind[i]] += ms;
+        e->prof_cnt[e->prof_kind[i]] += 1;
+    }
+    e->prof_n = 0;
+    return PK_OK;
+}
+
+int pk_prof_begin(pk_engine *e, int kind) {
+    if (!e->prof || e->capturing) return -1;
+    if (e->prof_n == pk_engine::PROF_CAP && prof_flush(e) != PK_OK) return -1;
+    const int slot = e->prof_n++;
+    e->prof_kind[slot] = kind;
+    if (hipEventRecord(e->prof_ev[2 * slot], e->stream) != hipSuccess) return -1;
+    return slot;
+}
+
+int pk_prof_end(pk_engine *e, int slot) {
+    if (slot < 0) return PK_OK;
+    PK_HIP(hipEventRecord(e->prof_ev[2 * slot + 1], e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_engine_profile(pk_engine *e, int enable) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    if (enable && !e->prof_ev) {
+        e->prof_ev = new hipEvent_t[2 * pk_engine::PROF_CAP];
+        e->prof_kind = new int[pk_engine::PROF_CAP];
+        for (int i = 0; i < 2 * pk_engine::PROF_CAP; ++i) PK_HIP(hipEventCreate(&e->prof_ev[i]));
+    }
+    PK_TRY(prof_flush(e));
+    for (int k = 0; k < PK_PROF_N; ++k) { e->prof_ms[k] = 0.0; e->prof_cnt[k] = 0; }
+    e->prof = enable != 0;
+    return PK_OK;
+}
+
+extern "C" int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches) {
+    PK_CHECK(e && kernel >= 0 && kernel < PK_PROF_N, PK_ERR_ARG, "bad argument");
+    PK_TRY(prof_flush(e));
+    if (total_ms) *total_ms = e->prof_ms[kernel];
+    if (launches) *launches = e->prof_cnt[kernel];
+    return PK_OK;
+}
+
+// One wave sleeping in bounded steps: s_sleep 127 is ~8k cycles (~3.4 us).
+__global__ void k_stall(int iters) {
+    for (int i = 0; i < iters; ++i) __builtin_amdgcn_s_sleep(127);
+}
+
+extern "C" int pk_engine_stall(pk_engine *e, int usec) {
+    PK_CHECK(e && usec >= 0, PK_ERR_ARG, "bad argument");
+    if (usec > 1000000) usec = 1000000;
+    hipLaunchKernelGGL(k_stall, dim3(1), dim3(64), 0, e->stream, usec / 3 + 1);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── graphs ─────────────────────────
+struct pk_graph {
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+};
+
+extern "C" int pk_capture_begin(pk_engine *e) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "already capturing");
+    PK_HIP(hipStreamSynchronize(e->stream));
+    PK_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+    e->capturing = true;
+    return PK_OK;
+}
+
+extern "C" int pk_capture_end(pk_engine *e, pk_graph **out) {
+    PK_CHECK(e && out, PK_ERR_ARG, "null argument");
+    PK_CHECK(e->capturing, PK_ERR_ARG, "not capturing");
+    *out = nullptr;
+    e->capturing = false;
+    pk_graph *g = new pk_graph();
+    hipError_t rc = hipStreamEndCapture(e->stream, &g->graph);
+    if (rc == hipSuccess) rc = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+    if (rc != hipSuccess) {
+        pk_set_error("graph capture failed: %s", hipGetErrorString(rc));
+        if (g->graph) (void)hipGraphDestroy(g->graph);
+        delete g;
+        return PK_ERR_HIP;
+    }
+    *out = g;
+    return PK_OK;
+}
+
+extern "C" int pk_graph_launch(pk_engine *e, pk_graph *g) {
+    PK_CHECK(e && g && g->exec, PK_ERR_ARG, "null argument");
+    PK_HIP(hipGraphLaunch(g->exec, e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_graph_destroy(pk_graph *g) {
+    if (!g) return PK_OK;
+    if (g->exec) (void)hipGraphExecDestroy(g->exec);
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+    return PK_OK;
+}
+
+// ───────────────────────── expert store ─────────────────────────
+static int check_i4_host(const pk_qt_host *t, int O, int I, int gs, const char *what) {
+    PK_CHECK(t && t->data && t->s, PK_ERR_ARG, "%s: null tensor", what);
+    PK_CHECK(t->fmt == PK_FMT_INT4, PK_ERR_UNSUPPORTED, "%s: fmt %d (store holds INT4)", what, t->fmt);
+    PK_CHECK(t->O == O && t->I == I, PK_ERR_ARG, "%s: shape [%d,%d], expected [%d,%d]", what, t->O,
+             t->I, O, I);
+    PK_CHECK(t->block_size == gs, PK_ERR_UNSUPPORTED, "%s: block_size %d, expected %d", what,
+             t->block_size, gs);
+    return PK_OK;
+}
+
+// host ref layout -> staging -> tiles in the slot
+static int upload_i4(pk_engine *e, const pk_qt_host *t, uint8_t *tiles, float *sc16) {
+    const int64_t qbytes = (int64_t)t->O * ((t->I + 1) / 2);
+    const int64_t sbytes = (int64_t)t->O * (t->I / PK_GS) * 4;
+    PK_TRY(pk_stage_reserve(e, pk_align256(qbytes) + sbytes));
+    uint8_t *dq = e->stage;
+    float *ds = (float *)(e->stage + pk_align256(qbytes));
+    PK_HIP(hipMemcpyAsync(dq, t->data, qbytes, hipMemcpyHostToDevice, e->stream));
+    PK_HIP(hipMemcpyAsync(ds, t->s, sbytes, hipMemcpyHostToDevice, e->stream));
+    PK_TRY(pk_launch_i4_repack(dq, ds, t->O, t->I, tiles, sc16, e->stream));
+    return PK_OK;
+}
+
+static uint8_t *slot_ptr(pk_engine *e, int layer, int eid) {
+    return e->store + ((int64_t)layer * e->c.n_experts + eid) * e->ex.stride;
+}
+
+extern "C" int pk_store_expert(pk_engine *e, int layer, int eid, const pk_qt_host *gu,
+                               const pk_qt_host *dn, const float *gu_bias, const float *d_bias) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(layer >= 0 && layer < c->n_layers && eid >= 0 && eid < c->n_experts, PK_ERR_ARG,
+             "expert (%d,%d) out of range", layer, eid);
+    PK_CHECK(gu_bias && d_bias, PK_ERR_ARG, "expert biases are null");
+    PK_TRY(check_i4_host(gu, c->moe_inter, c->hidden, c->group_size, "gate_up"));
+    PK_TRY(check_i4_host(dn, c->hidden, c->moe_inter / 2, c->group_size, "down"));
+    uint8_t *s = slot_ptr(e, layer, eid);
+    PK_TRY(upload_i4(e, gu, s + e->ex.off_gu_tiles, (float *)(s + e->ex.off_gu_scales)));
+    PK_TRY(upload_i4(e, dn, s + e->ex.off_dn_tiles, (float *)(s + e->ex.off_dn_scales)));
+    PK_HIP(hipMemcpyAsync(s + e->ex.off_gu_bias, gu_bias, (size_t)c->moe_inter * 4,
+                          hipMemcpyHostToDevice, e->stream));
+    PK_HIP(hipMemcpyAsync(s + e->ex.off_dn_bias, d_bias, (size_t)c->hidden * 4,
+                          hipMemcpyHostToDevice, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    e->expert_ready[(int64_t)layer * c->n_experts + eid] = 1;
+    return PK_OK;
+}
+
+static int upload_f32(pk_engine *e, float **dst, const float *src, int64_t n) {
+    if (!*dst) ALLOC(*dst, n * 4);
+    PK_HIP(hipMemcpyAsync(*dst, src, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l) {
+    PK_CHECK(e && l, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(layer >= 0 && layer < c->n_layers, PK_ERR_ARG, "layer %d out of range", layer);
+    const int D = c->hidden, H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, E = c->n_experts;
+    pk_layer_dev &d = e->L[layer];
+    if (l->in_ln) PK_TRY(upload_f32(e, &d.in_ln, l->in_ln, D));
+    if (l->post_ln) PK_TRY(upload_f32(e, &d.post_ln, l->post_ln, D));
+    if (l->router) {
+        PK_CHECK(l->router_bias, PK_ERR_ARG, "router bias is null");
+        PK_TRY(upload_f32(e, &d.router, l->router, (int64_t)E * D));
+        PK_TRY(upload_f32(e, &d.router_b, l->router_bias, E));
+        d.have_router = true;
+    }
+    if (l->wq.data) {
+        const pk_qt_host *ws[3] = {&l->wq, &l->wk, &l->wv};
+        const int rows[3] = {H * hd, KVH * hd, KVH * hd};
+        const float *bs[3] = {l->bq, l->bk, l->bv};
+        for (int i = 0; i < 3; ++i) {
+            PK_CHECK(ws[i]->fmt == PK_FMT_F32 && ws[i]->O == rows[i] && ws[i]->I == D && ws[i]->data,
+                     PK_ERR_UNSUPPORTED, "attention projection %d: need F32 [%d,%d]", i, rows[i], D);
+            PK_CHECK(bs[i], PK_ERR_ARG, "attention bias %d is null", i);
+        }
+        PK_CHECK(l->wo.fmt == PK_FMT_F32 && l->wo.O == D && l->wo.I == H * hd && l->wo.data && l->bo,
+                 PK_ERR_UNSUPPORTED, "wo: need F32 [%d,%d] and bias", D, H * hd);
+        PK_CHECK(l->sinks && l->in_ln && l->post_ln, PK_ERR_ARG, "sinks / norms are null");
+        const int64_t nq = (int64_t)H * hd * D, nk = (int64_t)KVH * hd * D;
+        if (!d.wqkv) ALLOC(d.wqkv, (nq + 2 * nk) * 4);
+        if (!d.bqkv) ALLOC(d.bqkv, (int64_t)(H + 2 * KVH) * hd * 4);
+        PK_HIP(hipMemcpyAsync(d.wqkv, l->wq.data, nq * 4, hipMemcpyHostToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(d.wqkv + nq, l->wk.data, nk * 4, hipMemcpyHostToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(d.wqkv + nq + nk, l->wv.data, nk * 4, hipMemcpyHostToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(d.bqkv, l->bq, (size_t)H * hd * 4, hipMemcpyHostToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(d.bqkv + H * hd, l->bk, (size_t)KVH * hd * 4, hipMemcpyHostToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(d.bqkv + (H + KVH) * hd, l->bv, (size_t)KVH * hd * 4, hipMemcpyHostToDevice,
+                              e->stream));
+        PK_TRY(upload_f32(e, &d.wo, (const float *)l->wo.data, (int64_t)D * H * hd));
+        PK_TRY(upload_f32(e, &d.bo, l->bo, D));
+        PK_TRY(upload_f32(e, &d.sinks, l->sinks, H));
+        d.have_attn = true;
+    }
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_store_globals(pk_engine *e, const pk_qt_host *embed, const pk_qt_host *lm_head,
+                                const float *final_norm) {
+    PK_CHECK(e && embed && lm_head && final_norm, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden;
+    PK_CHECK(embed->fmt == PK_FMT_F32 && embed->O == c->vocab && embed->I == D && embed->data,
+             PK_ERR_UNSUPPORTED, "embedding: need F32 [%d,%d]", c->vocab, D);
+    PK_CHECK(lm_head->fmt == c->lm_head_fmt && lm_head->O == c->vocab && lm_head->I == D &&
+                 lm_head->data, PK_ERR_UNSUPPORTED, "lm_head: need fmt %d [%d,%d]", c->lm_head_fmt,
+             c->vocab, D);
+    PK_TRY(upload_f32(e, &e->embed, (const float *)embed->data, (int64_t)c->vocab * D));
+    if (c->lm_head_fmt == PK_FMT_F32) {
+        PK_TRY(upload_f32(e, &e->lm_f32, (const float *)lm_head->data, (int64_t)c->vocab * D));
+    } else {
+        PK_CHECK(lm_head->s, PK_ERR_ARG, "lm_head scales are null");
+        if (!e->lm_q8) ALLOC(e->lm_q8, (int64_t)c->vocab * D);
+        PK_HIP(hipMemcpyAsync(e->lm_q8, lm_head->data, (size_t)c->vocab * D, hipMemcpyHostToDevice, e->stream));
+        PK_TRY(upload_f32(e, &e->lm_s, lm_head->s, c->vocab));
+    }
+    PK_TRY(upload_f32(e, &e->final_norm, final_norm, D));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    e->have_globals = true;
+    return PK_OK;
+}
+
+// ───────────────────────── synthetic build ─────────────────────────
+static int synth_fill(pk_engine *e, float *dst, int64_t n, uint64_t seed, uint32_t kind,
+                      uint32_t layer, uint32_t idx, float std) {
+    return pk_launch_fill_normal(dst, n, pk_stream(seed, kind, layer, idx), std, e->stream);
+}
+
+static int synth_expert_matrix(pk_engine *e, int O, int I, uint64_t seed, uint32_t kind, int layer,
+                               int eid, uint8_t *tiles, float *sc16) {
+    const int64_t n = (int64_t)O * I;
+    const int64_t qbytes = (int64_t)O * (I / 2), sbytes = (int64_t)O * (I / PK_GS) * 4;
+    const int64_t need = pk_align256(n * 4) + pk_align256(qbytes) + sbytes;
+    PK_TRY(pk_stage_reserve(e, need));
+    float *w = (float *)e->stage;
+    uint8_t *q = e->stage + pk_align256(n * 4);
+    float *s = (float *)(q + pk_align256(qbytes));
+    PK_TRY(synth_fill(e, w, n, seed, kind, layer, eid, 0.02f));
+    PK_TRY(pk_launch_quantize_i4(w, O, I, PK_GS, q, s, e->stream));
+    PK_TRY(pk_launch_i4_repack(q, s, O, I, tiles, sc16, e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, int n_threads) {
+    (void)n_threads;
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, E = c->n_experts, H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim;
+    const int inter = c->moe_inter, half = inter / 2;
+    for (int l = 0; l < c->n_layers; ++l) {
+        pk_layer_dev &d = e->L[l];
+        if (!d.in_ln) { ALLOC(d.in_ln, D * 4); PK_TRY(pk_launch_fill_const(d.in_ln, D, 1.0f, e->stream)); }
+        if (!d.post_ln) { ALLOC(d.post_ln, D * 4); PK_TRY(pk_launch_fill_const(d.post_ln, D, 1.0f, e->stream)); }
+        if (what & 1) {
+            if (!d.router) ALLOC(d.router, (int64_t)E * D * 4);
+            if (!d.router_b) ALLOC(d.router_b, E * 4);
+            PK_TRY(synth_fill(e, d.router, (int64_t)E * D, seed, PK_T_ROUTER, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.router_b, E, seed, PK_T_ROUTER_B, l, 0, 0.02f));
+            d.have_router = true;
+            for (int x = 0; x < E; ++x) {
+                uint8_t *s = slot_ptr(e, l, x);
+                PK_TRY(synth_expert_matrix(e, inter, D, seed, PK_T_GU, l, x, s + e->ex.off_gu_tiles,
+                                           (float *)(s + e->ex.off_gu_scales)));
+                PK_TRY(synth_expert_matrix(e, D, half, seed, PK_T_DOWN, l, x, s + e->ex.off_dn_tiles,
+                                           (float *)(s + e->ex.off_dn_scales)));
+                PK_TRY(synth_fill(e, (float *)(s + e->ex.off_gu_bias), inter, seed, PK_T_GU_B, l, x, 0.02f));
+                PK_TRY(synth_fill(e, (float *)(s + e->ex.off_dn_bias), D, seed, PK_T_DOWN_B, l, x, 0.02f));
+                e->expert_ready[(int64_t)l * E + x] = 1;
+            }
+        }
+        if (what & 2) {
+            const int64_t nq = (int64_t)H * hd * D, nk = (int64_t)KVH * hd * D;
+            if (!d.wqkv) ALLOC(d.wqkv, (nq + 2 * nk) * 4);
+            if (!d.bqkv) ALLOC(d.bqkv, (int64_t)(H + 2 * KVH) * hd * 4);
+            if (!d.wo) ALLOC(d.wo, (int64_t)D * H * hd * 4);
+            if (!d.bo) ALLOC(d.bo, D * 4);
+            if (!d.sinks) ALLOC(d.sinks, H * 4);
+            PK_TRY(synth_fill(e, d.wqkv, nq, seed, PK_T_WQ, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.wqkv + nq, nk, seed, PK_T_WK, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.wqkv + nq + nk, nk, seed, PK_T_WV, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.bqkv, H * hd, seed, PK_T_BQ, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.bqkv + H * hd, KVH * hd, seed, PK_T_BK, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.bqkv + (H + KVH) * hd, KVH * hd, seed, PK_T_BV, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.wo, (int64_t)D * H * hd, seed, PK_T_WO, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.bo, D, seed, PK_T_BO, l, 0, 0.02f));
+            PK_TRY(synth_fill(e, d.sinks, H, seed, PK_T_SINKS, l, 0, 0.02f));
+            d.have_attn = true;
+        }
+    }
+    if (what & 4) {
+        const int64_t n = (int64_t)c->vocab * D;
+        if (!e->embed) ALLOC(e->embed, n * 4);
+        PK_TRY(synth_fill(e, e->embed, n, seed, PK_T_EMBED, 0, 0, 0.02f));
+        if (c->lm_head_fmt == PK_FMT_F32) {
+            if (!e->lm_f32) ALLOC(e->lm_f32, n * 4);
+            PK_TRY(synth_fill(e, e->lm_f32, n, seed, PK_T_LM_HEAD, 0, 0, 0.02f));
+        } else {
+            pk_set_error("synthetic INT8 lm_head is built by the host loader");
+            return PK_ERR_UNSUPPORTED;
+        }
+        if (!e->final_norm) ALLOC(e->final_norm, D * 4);
+        PK_TRY(pk_launch_fill_const(e->final_norm, D, 1.0f, e->stream));
+        e->have_globals = true;
+    }
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+// ───────────────────────── quantizer ─────────────────────────
+extern "C" int pk_quantize_int4_gs(pk_engine *e, const float *w_dev, int O, int I, int gs,
+                                   uint8_t *packed_dev, float *scales_dev) {
+    PK_CHECK(e && w_dev && packed_dev && scales_dev, PK_ERR_ARG, "null argument");
+    PK_TRY(pk_launch_quantize_i4(w_dev, O, I, gs, packed_dev, scales_dev, e->stream));
+    return PK_OK;
+}
+
+// ───────────────────────── tensors / matmul_qt ─────────────────────────
+extern "C" int pk_qt_upload(pk_engine *e, const pk_qt_host *h, pk_qt **out) {
+    PK_CHECK(e && h && out && h->data, PK_ERR_ARG, "null argument");
+    PK_CHECK(h->O > 0 && h->I > 0, PK_ERR_ARG, "tensor shape [%d,%d]", h->O, h->I);
+    *out = nullptr;
+    pk_qt *t = new pk_qt();
+    t->fmt = h->fmt; t->O = h->O; t->I = h->I; t->gs = h->block_size; t->tiled = 0;
+    int rc = PK_OK;
+    const int64_t n = (int64_t)h->O * h->I;
+    if (h->fmt == PK_FMT_F32) {
+        rc = pk_dev_alloc(e, &t->data, n * 4);
+        if (rc == PK_OK) rc = hipMemcpy(t->data, h->data, n * 4, hipMemcpyHostToDevice) == hipSuccess ? PK_OK : PK_ERR_HIP;
+    } else if (h->fmt == PK_FMT_INT8) {
+        rc = h->s ? pk_dev_alloc(e, &t->data, n) : PK_ERR_ARG;
+        if (rc == PK_OK) rc = pk_dev_alloc(e, (void **)&t->s, (int64_t)h->O * 4);
+        if (rc == PK_OK) rc = hipMemcpy(t->data, h->data, n, hipMemcpyHostToDevice) == hipSuccess ? PK_OK : PK_ERR_HIP;
+        if (rc == PK_OK) rc = hipMemcpy(t->s, h->s, (size_t)h->O * 4, hipMemcpyHostToDevice) == hipSuccess ? PK_OK : PK_ERR_HIP;
+    } else if (h->fmt == PK_FMT_INT4) {
+        const int64_t qb = (int64_t)h->O * ((h->I + 1) / 2);
+        const int gs = h->block_size;
+        const int64_t nsc = gs > 0 ? (int64_t)h->O * ((h->I + gs - 1) / gs) : h->O;
+        if (!h->s) rc = PK_ERR_ARG;
+        else if (gs == PK_GS && h->I % PK_GS == 0) {
+            t->tiled = 1;
+            t->sh = pk_i4_make_shape(h->O, h->I);
+            rc = pk_dev_alloc(e, &t->data, t->sh.tile_bytes);
+            if (rc == PK_OK) rc = pk_dev_alloc(e, (void **)&t->s, t->sh.scale_bytes);
+            if (rc == PK_OK) {
+                pk_qt_host hh = *h;
+                rc = upload_i4(e, &hh, (uint8_t *)t->data, t->s);
+                if (rc == PK_OK) rc = hipStreamSynchronize(e->stream) == hipSuccess ? PK_OK : PK_ERR_HIP;
+            }
+        } else {
+            rc = pk_dev_alloc(e, &t->data, qb);
+            if (rc == PK_OK) rc = pk_dev_alloc(e, (void **)&t->s, nsc * 4);
+            if (rc == PK_OK) rc = hipMemcpy(t->data, h->data, qb, hipMemcpyHostToDevice) == hipSuccess ? PK_OK : PK_ERR_HIP;
+            if (rc == PK_OK) rc = hipMemcpy(t->s, h->s, nsc * 4, hipMemcpyHostToDevice) == hipSuccess ? PK_OK : PK_ERR_HIP;
+        }
+    } else {
+        rc = PK_ERR_UNSUPPORTED;
+    }
+    if (rc != PK_OK) {
+        if (rc == PK_ERR_UNSUPPORTED) pk_set_error("matmul_qt: format %d not supported", h->fmt);
+        else if (rc == PK_ERR_ARG) pk_set_error("tensor: scales are null");
+        else if (rc == PK_ERR_HIP) pk_set_error("tensor upload failed");
+        pk_dev_free(e, t->data);
+        pk_dev_free(e, t->s);
+        delete t;
+        return rc;
+    }
+    *out = t;
+    return PK_OK;
+}
+
+extern "C" int pk_qt_free(pk_engine *e, pk_qt *t) {
+    if (!t) return PK_OK;
+    if (e) (void)hipStreamSynchronize(e->stream);
+    pk_dev_free(e, t->data);
+    pk_dev_free(e, t->s);
+    delete t;
+    return PK_OK;
+}
+
+extern "C" int pk_matmul_qt(pk_engine *e, float *y, const float *x, const pk_qt *w, int S) {
+    PK_CHECK(e && y && x && w, PK_ERR_ARG, "null argument");
+    PK_CHECK(S > 0, PK_ERR_ARG, "S=%d", S);
+    switch (w->fmt) {
+    case PK_FMT_F32:
+        return pk_launch_gemv_f32(y, x, (const float *)w->data, nullptr, S, w->I, w->O, e->stream);
+    case PK_FMT_INT8:
+        return pk_launch_gemv_q8(y, x, (const int8_t *)w->data, w->s, S, w->I, w->O, e->stream);
+    case PK_FMT_INT4:
+        if (w->gs <= 0)
+            return pk_launch_i4_rowscale_gemv(y, x, (const uint8_t *)w->data, w->s, S, w->I, w->O, e->stream);
+        if (w->tiled) {
+            pk_i4_items it{};
+            it.base = (const uint8_t *)w->data;
+            it.slot_stride = 0;
+            it.off_tiles = 0;
+            it.off_scales = (const uint8_t *)w->s - (const uint8_t *)w->data;
+            it.off_bias = -1;
+            it.slots = nullptr;
+            it.x = x; it.x_stride = w->I;
+            it.y = y; it.y_stride = w->O;
+            it.n_items = S;
+            return pk_launch_i4_gemv(it, w->sh, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream);
+        }
+        return pk_launch_i4_gemv_ref(y, x, (const uint8_t *)w->data, w->s, S, w->I, w->O, w->gs, e->stream);
+    default:
+        pk_set_error("matmul_qt: format %d not supported", w->fmt);
+        return PK_ERR_UNSUPPORTED;
+    }
+}
+
+// ───────────────────────── expert path ─────────────────────────
+static pk_i4_items expert_items(pk_engine *e, int layer, bool down) {
+    pk_i4_items it{};
+    it.base = e->store;
+    it.slot_stride = e->ex.stride;
+    it.off_tiles = down ? e->ex.off_dn_tiles : e->ex.off_gu_tiles;
+    it.off_scales = down ? e->ex.off_dn_scales : e->ex.off_gu_scales;
+    it.off_bias = down ? e->ex.off_dn_bias : e->ex.off_gu_bias;
+    it.slot_base = layer * e->c.n_experts;
+    return it;
+}
+
+static int check_layer_experts(pk_engine *e, int layer) {
+    const pk_cfg *c = &e->c;
+    PK_CHECK(layer >= 0 && layer < c->n_layers, PK_ERR_ARG, "layer %d out of range", layer);
+    PK_CHECK(e->L[layer].have_router, PK_ERR_MISSING, "layer %d: router not loaded", layer);
+    for (int x = 0; x < c->n_experts; ++x)
+        PK_CHECK(e->expert_ready[(int64_t)layer * c->n_experts + x], PK_ERR_MISSING,
+                 "layer %d expert %d not loaded", layer, x);
+    return PK_OK;
+}
+
+// FFN of the experts listed in sel (device, n entries): act <- SwiGLU(gate_up x + b),
+// eo <- down act + b.
+static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, const float *x,
+                       int64_t x_stride, float *act, float *eo) {
+    const pk_cfg *c = &e->c;
+    pk_i4_items gu = expert_items(e, layer, false);
+    gu.slots = sel_dev;
+    gu.x = x; gu.x_stride = x_stride;
+    gu.y = act; gu.y_stride = c->moe_inter / 2;
+    gu.n_items = n;
+    int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
+    PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
+                             nullptr, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    pk_i4_items dn = expert_items(e, layer, true);
+    dn.slots = sel_dev;
+    dn.x = act; dn.x_stride = c->moe_inter / 2;
+    dn.y = eo; dn.y_stride = c->hidden;
+    dn.n_items = n;
+    ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
+    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    return PK_OK;
+}
+
+int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
+                 const float *residual, float *res_out) {
+    const pk_cfg *c = &e->c;
+    const pk_layer_dev &d = e->L[layer];
+    int ps = pk_prof_begin(e, PK_PROF_ROUTER);
+    PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
+                                 c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
+                                 e->counters, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, x_dev, 0, e->act, e->eo));
+    ps = pk_prof_begin(e, PK_PROF_COMBINE);
+    PK_TRY(pk_launch_combine(out_dev, e->eo, e->w_scaled, c->topk, c->hidden, residual, res_out,
+                             e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    return PK_OK;
+}
+
+extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
+                              int32_t *sel_host, float *w_host) {
+    PK_CHECK(e && x_dev && out_dev, PK_ERR_ARG, "null argument");
+    PK_TRY(check_layer_experts(e, layer));
+    PK_CHECK(!(e->capturing && (sel_host || w_host)), PK_ERR_ARG,
+             "moe_forward: host routing outputs are not available while capturing a graph");
+    PK_TRY(pk_moe_layer(e, layer, x_dev, out_dev, nullptr, nullptr));
+    if (sel_host || w_host) {
+        if (sel_host)
+            PK_HIP(hipMemcpyAsync(sel_host, e->sel, e->c.topk * 4, hipMemcpyDeviceToHost, e->stream));
+        if (w_host)
+            PK_HIP(hipMemcpyAsync(w_host, e->w_soft, e->c.topk * 4, hipMemcpyDeviceToHost, e->stream));
+        PK_HIP(hipStreamSynchronize(e->stream));
+    }
+    return PK_OK;
+}
+
+extern "C" int pk_expert_apply(pk_engine *e, int layer, int eid, const float *x_dev, float *dst_dev,
+                               float w) {
+    PK_CHECK(e && x_dev && dst_dev, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(layer >= 0 && layer < c->n_layers && eid >= 0 && eid < c->n_experts, PK_ERR_ARG,
+             "expert (%d,%d) out of range", layer, eid);
+    PK_CHECK(e->expert_ready[(int64_t)layer * c->n_experts + eid], PK_ERR_MISSING,
+             "layer %d expert %d not loaded", layer, eid);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "expert_apply: not available while capturing a graph");
+    // a one-entry slot list in device scratch (sel[0] is free outside moe_forward)
+    PK_HIP(hipMemcpyAsync(e->sel, &eid, 4, hipMemcpyHostToDevice, e->stream));
+    PK_TRY(experts_ffn(e, layer, e->sel, 1, x_dev, 0, e->act, e->eo));
+    PK_TRY(pk_launch_axpy(dst_dev, e->eo, w, c->hidden, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+static int batch_reserve(pk_engine *e, int T) {
+    if (T <= e->batch_cap) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "batch buffers must be sized before capturing a graph");
+    PK_HIP(hipStreamSynchronize(e->stream));
+    const pk_cfg *c = &e->c;
+    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel};
+    for (void *p : ptrs) pk_dev_free(e, p);
+    e->b_logits = e->b_w = e->b_act = e->b_eo = nullptr;
+    e->b_sel = nullptr;
+    e->batch_cap = 0;
+    const int64_t TK = (int64_t)T * c->topk;
+    ALLOC(e->b_logits, (int64_t)T * c->n_experts * 4);
+    ALLOC(e->b_w, TK * 4);
+    ALLOC(e->b_sel, TK * 4);
+    ALLOC(e->b_act, TK * (c->moe_inter / 2) * 4);
+    ALLOC(e->b_eo, TK * c->hidden * 4);
+    e->batch_cap = T;
+    return PK_OK;
+}
+
+// Batched MoE: every token runs the decode arithmetic (same bits as
+// pk_moe_forward token by token).
+extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
+                                    float *out_dev, int32_t *sel_dev, float *w_dev) {
+    PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
+    PK_TRY(check_layer_experts(e, layer));
+    PK_TRY(batch_reserve(e, T));
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, K = c->topk;
+    const pk_layer_dev &d = e->L[layer];
+    PK_TRY(pk_launch_gemv_f32(e->b_logits, x_dev, d.router, d.router_b, T, D, c->n_experts, e->stream));
+    PK_TRY(pk_launch_topk_batch(e->b_logits, T, c->n_experts, K, c->routed_scale, e->b_sel, e->b_w,
+                                nullptr, e->stream));
+    for (int t = 0; t < T; ++t) {
+        PK_TRY(experts_ffn(e, layer, e->b_sel + (int64_t)t * K, K, x_dev + (int64_t)t * D, 0,
+                           e->b_act, e->b_eo));
+        PK_TRY(pk_launch_combine(out_dev + (int64_t)t * D, e->b_eo, e->b_w + (int64_t)t * K, K, D,
+                                 nullptr, nullptr, e->stream));
+    }
+    if (sel_dev)
+        PK_HIP(hipMemcpyAsync(sel_dev, e->b_sel, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    if (w_dev)
+        PK_HIP(hipMemcpyAsync(w_dev, e->b_w, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    return PK_OK;
+}

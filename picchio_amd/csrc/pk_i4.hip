@@ -1,0 +1,312 @@
+// pk_i4.hip — INT4 group-scaled kernels for gfx950.
+//
+// Replaces quant.h:259-319 (matmul_i4_gs) and the gs64 converter
+// convert.py:45-93. Results are bit-identical to the reference:
+//
+//  * Each lane owns one (row, 64-column group) of a tile and runs the eight
+//    fp32 FMA chains of quant.h's AVX2 loop in the same order: chain j takes
+//    columns j, 8+j, ..., 56+j of the group. The chains are folded with
+//    hsum256's tree ((c0+c4)+(c2+c6))+((c1+c5)+(c3+c7)) (quant.h:94-103).
+//  * The per-group partial sums of a row are folded in group order,
+//    a = fma(partial_g, scale_g, a), the contraction gcc applies to
+//    quant.h:313 `a += ga * group_sc`.
+//  * A nibble is decoded with one v_cvt_off_f32_i4 (SDWA byte select), which
+//    yields q/16 exactly; the 1/16 is folded into the stored scales (x16),
+//    and all scaling by 16 is exact, so every rounding matches the reference.
+#include "pk_internal.h"
+
+typedef uint32_t pk_u32x4 __attribute__((ext_vector_type(4)));
+
+// Streaming 16-byte load (weights are read once per token: non-temporal).
+__device__ __forceinline__ uint4 pk_load_nt(const uint4 *p) {
+    const pk_u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const pk_u32x4 *>(p));
+    return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// ───────────────────────── nibble decode ─────────────────────────
+// Low nibble of byte B of w, read as a signed 4-bit value, divided by 16.
+template <int B>
+__device__ __forceinline__ float pk_q16(uint32_t w) {
+    float r;
+    if constexpr (B == 0)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_0"
+            : "=v"(r) : "v"(w));
+    else if constexpr (B == 1)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_1"
+            : "=v"(r) : "v"(w));
+    else if constexpr (B == 2)
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_2"
+            : "=v"(r) : "v"(w));
+    else
+        asm("v_cvt_off_f32_i4_sdwa %0, %1 dst_sel:DWORD dst_unused:UNUSED_PAD src0_sel:BYTE_3"
+            : "=v"(r) : "v"(w));
+    return r;
+}
+
+// One 64-column group of one row: 32 stored bytes in two uint4 (columns 0..31
+// and 32..63), x = the group's 64 inputs (wave-uniform). Returns partial/16.
+__device__ __forceinline__ float pk_group_dot(uint4 a, uint4 b, const float *__restrict__ xg) {
+    float c[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) c[j] = 0.0f;
+    const uint32_t wd[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+        // dword d holds columns 8d..8d+7: byte k -> columns 8d+2k (low), 8d+2k+1 (high)
+        const uint32_t w = wd[d], h = w >> 4;
+        const float *xs = xg + 8 * d;
+        c[0] = __builtin_fmaf(xs[0], pk_q16<0>(w), c[0]);
+        c[1] = __builtin_fmaf(xs[1], pk_q16<0>(h), c[1]);
+        c[2] = __builtin_fmaf(xs[2], pk_q16<1>(w), c[2]);
+        c[3] = __builtin_fmaf(xs[3], pk_q16<1>(h), c[3]);
+        c[4] = __builtin_fmaf(xs[4], pk_q16<2>(w), c[4]);
+        c[5] = __builtin_fmaf(xs[5], pk_q16<2>(h), c[5]);
+        c[6] = __builtin_fmaf(xs[6], pk_q16<3>(w), c[6]);
+        c[7] = __builtin_fmaf(xs[7], pk_q16<3>(h), c[7]);
+    }
+    const float b0 = c[0] + c[4], b1 = c[1] + c[5], b2 = c[2] + c[6], b3 = c[3] + c[7];
+    return (b0 + b2) + (b1 + b3);
+}
+
+__device__ __forceinline__ float pk_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+
+// GPT-OSS clamped SwiGLU of one (gate, up) pair (picchio.c:1416-1424).
+__device__ __forceinline__ float pk_swiglu(float gate, float up, float lim, float alpha) {
+    if (gate > lim) gate = lim;
+    if (up > lim) up = lim;
+    if (up < -lim) up = -lim;
+    return (up + 1.0f) * gate * pk_sigmoid(alpha * gate);
+}
+
+// ───────────────────────── tiled GEMV ─────────────────────────
+// grid = (RB, n_items); block = NW waves. Wave w handles groups w, w+NW, ...
+// (GPW groups per pass, loads issued before the math); partial sums and
+// scales meet in LDS; wave 0 folds the groups of its 64 rows in order.
+template <int NW, int GPW, int EPI>
+__global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int NG,
+                                                     float lim, float alpha) {
+    extern __shared__ float lds[];            // part[NG][64], scl[NG][64]
+    float *part = lds;
+    float *scl = lds + NG * 64;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = blockIdx.x;
+    const int item = blockIdx.y;
+
+    int slot = it.slot_base + (it.slots ? it.slots[item] : 0);
+    slot = __builtin_amdgcn_readfirstlane(slot);
+    const uint8_t *base = it.base + (int64_t)slot * it.slot_stride;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(base + it.off_tiles) +
+                         (int64_t)rb * NG * (PK_TILE_BYTES / 16);
+    const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
+    const float *__restrict__ x = it.x + (int64_t)item * it.x_stride;
+
+    for (int g0 = wave; g0 < NG; g0 += NW * GPW) {
+        uint4 wa[GPW], wb[GPW];
+        float s[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = g0 + u * NW;
+            if (g < NG) {
+                wa[u] = pk_load_nt(&tiles[g * 128 + lane]);
+                wb[u] = pk_load_nt(&tiles[g * 128 + 64 + lane]);
+                s[u] = sc[g * 64 + lane];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = g0 + u * NW;
+            if (g < NG) {
+                part[g * 64 + lane] = pk_group_dot(wa[u], wb[u], x + g * 64);
+                scl[g * 64 + lane] = s[u];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+
+    float acc = 0.0f;
+    for (int g = 0; g < NG; ++g) acc = __builtin_fmaf(part[g * 64 + lane], scl[g * 64 + lane], acc);
+    const int row = rb * 64 + lane;
+    if (it.off_bias >= 0 && row < O)
+        acc = acc + reinterpret_cast<const float *>(base + it.off_bias)[row];
+    float *y = it.y + (int64_t)item * it.y_stride;
+    if constexpr (EPI == PK_EPI_SWIGLU) {
+        const float up = __shfl_down(acc, 1, 64);
+        if ((lane & 1) == 0 && row + 1 < O) y[row >> 1] = pk_swiglu(acc, up, lim, alpha);
+    } else {
+        if (row < O) y[row] = acc;
+    }
+}
+
+int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
+                      float lim, float alpha, const pk_combine_args *comb, hipStream_t st) {
+    (void)comb;
+    PK_CHECK(sh.NG > 0 && sh.RB > 0 && it.n_items > 0, PK_ERR_ARG, "i4 gemv: empty shape");
+    PK_CHECK(sh.NG <= 128, PK_ERR_UNSUPPORTED, "i4 gemv: I=%d above 8192", sh.I);
+    const dim3 grid(sh.RB, it.n_items);
+    const size_t lds = (size_t)sh.NG * 64 * 2 * sizeof(float);
+    // 15 waves x 3 groups covers the 45 groups of a 2880-wide row in one pass.
+    constexpr int NW = 15, GPW = 3;
+    if (epilogue == PK_EPI_SWIGLU)
+        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_SWIGLU>), grid, dim3(NW * 64), lds, st,
+                           it, sh.O, sh.NG, lim, alpha);
+    else
+        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_PLAIN>), grid, dim3(NW * 64), lds, st,
+                           it, sh.O, sh.NG, lim, alpha);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────── reference-layout GEMV (any shape / group) ─────────────────
+// One thread per (s, row). Same arithmetic as quant.h:259-319 including the
+// scalar tail of a short last group; used for shapes the tiled layout does
+// not cover (I % 64 != 0, group size != 64).
+__global__ void k_i4_gemv_ref(float *y, const float *x, const uint8_t *q4, const float *s,
+                              int S, int I, int O, int gs) {
+    const int o = blockIdx.x * blockDim.x + threadIdx.x;
+    const int si = blockIdx.y;
+    if (o >= O || si >= S) return;
+    const int rb = (I + 1) / 2, ng = (I + gs - 1) / gs;
+    const uint8_t *w = q4 + (int64_t)o * rb;
+    const float *xs = x + (int64_t)si * I;
+    float a = 0.0f;
+    for (int g = 0; g < ng; ++g) {
+        const int g0 = g * gs, g1 = min(g0 + gs, I);
+        int gi = g0;
+        float c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (; gi + 16 <= g1; gi += 16) {
+            const uint8_t *p = w + (gi >> 1);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint8_t bt = p[j >> 1];
+                const int nib = (j & 1) ? (bt >> 4) : (bt & 15);
+                c[j] = __builtin_fmaf(xs[gi + j], (float)(nib - 8), c[j]);
+            }
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+                const uint8_t bt = p[4 + (j >> 1)];
+                const int nib = (j & 1) ? (bt >> 4) : (bt & 15);
+                c[j] = __builtin_fmaf(xs[gi + 8 + j], (float)(nib - 8), c[j]);
+            }
+        }
+        const float b0 = c[0] + c[4], b1 = c[1] + c[5], b2 = c[2] + c[6], b3 = c[3] + c[7];
+        float ga = (b0 + b2) + (b1 + b3);
+        for (; gi < g1; gi += 2) {
+            const uint8_t bt = w[gi >> 1];
+            ga = __builtin_fmaf(xs[gi], (float)((int)(bt & 15) - 8), ga);
+            if (gi + 1 < g1) ga = __builtin_fmaf(xs[gi + 1], (float)((int)(bt >> 4) - 8), ga);
+        }
+        a = __builtin_fmaf(ga, s[(int64_t)o * ng + g], a);
+    }
+    y[(int64_t)si * O + o] = a;
+}
+
+int pk_launch_i4_gemv_ref(float *y, const float *x, const uint8_t *q4, const float *s,
+                          int S, int I, int O, int gs, hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0 && gs > 0, PK_ERR_ARG, "i4 gemv ref: bad shape");
+    PK_CHECK(S <= 65535, PK_ERR_ARG, "i4 gemv ref: S=%d too large", S);
+    hipLaunchKernelGGL(k_i4_gemv_ref, dim3((O + 127) / 128, S), dim3(128), 0, st,
+                       y, x, q4, s, S, I, O, gs);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── repack ─────────────────────────
+// Reference layout (q4 [O][I/2], s [O][I/64]) -> tiles + 16*scale.
+// One thread per (row of the padded block, group).
+__global__ void k_i4_repack(const uint8_t *q4, const float *s, int O, int I, int RB, int NG,
+                            uint8_t *tiles, float *sc16) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= (int64_t)RB * 64 * NG) return;
+    const int g = (int)(t % NG);
+    const int row = (int)(t / NG);
+    const int rb = row >> 6, r = row & 63;
+    uint4 lo = make_uint4(0, 0, 0, 0), hi = make_uint4(0, 0, 0, 0);
+    float scv = 0.0f;
+    if (row < O) {
+        const uint32_t *src = reinterpret_cast<const uint32_t *>(q4 + (int64_t)row * (I / 2) + g * 32);
+        uint32_t v[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) v[k] = src[k] ^ 0x88888888u;
+        lo = make_uint4(v[0], v[1], v[2], v[3]);
+        hi = make_uint4(v[4], v[5], v[6], v[7]);
+        scv = 16.0f * s[(int64_t)row * NG + g];
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(tiles + ((int64_t)rb * NG + g) * PK_TILE_BYTES);
+    dst[r] = lo;
+    dst[64 + r] = hi;
+    sc16[((int64_t)rb * NG + g) * 64 + r] = scv;
+}
+
+int pk_launch_i4_repack(const uint8_t *q4, const float *s, int O, int I,
+                        uint8_t *tiles, float *sc16, hipStream_t st) {
+    PK_CHECK(I % 64 == 0 && O > 0, PK_ERR_UNSUPPORTED, "repack: I=%d not a multiple of 64", I);
+    PK_CHECK(((uintptr_t)q4 & 3) == 0, PK_ERR_ARG, "repack: q4 not 4-byte aligned");
+    const pk_i4_shape sh = pk_i4_make_shape(O, I);
+    const int64_t n = (int64_t)sh.RB * 64 * sh.NG;
+    hipLaunchKernelGGL(k_i4_repack, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       q4, s, O, I, sh.RB, sh.NG, tiles, sc16);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────────────────── quantizer ─────────────────────────
+// convert.py:45-93: per (row, group) amax, scale = amax/7 (fp32, correctly
+// rounded) or 1e-8, q = clip(rint(w/scale), -8, 7), low nibble = even column.
+// One thread per (row, group); group_size <= 0 or >= I -> one group per row.
+// Groups of odd length could share a byte with the next group: those are
+// rare (odd gs) and handled by the per-row thread doing every group itself.
+__global__ void k_quantize_i4(const float *w, int O, int I, int glen, int ng, int per_thread_row,
+                              uint8_t *packed, float *scales) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int rbytes = (I + 1) / 2;
+    int row, g_first, g_last;
+    if (per_thread_row) {
+        if (t >= O) return;
+        row = (int)t; g_first = 0; g_last = ng;
+    } else {
+        if (t >= (int64_t)O * ng) return;
+        row = (int)(t / ng); g_first = (int)(t % ng); g_last = g_first + 1;
+    }
+    const float *wr = w + (int64_t)row * I;
+    uint8_t *pr = packed + (int64_t)row * rbytes;
+    float *sr = scales + (int64_t)row * ng;
+    for (int g = g_first; g < g_last; ++g) {
+        const int a0 = g * glen, a1 = min(a0 + glen, I);
+        float amax = 0.0f;
+        for (int i = a0; i < a1; ++i) amax = fmaxf(amax, fabsf(wr[i]));
+        sr[g] = amax > 1e-8f ? amax / 7.0f : 1e-8f;
+    }
+    // Column pairs (2c, 2c+1) -> byte c (convert.py:84-91). With an even group
+    // length a thread's columns start on an even column; with an odd one the
+    // thread owns the whole row. The last byte of an odd-width row keeps a
+    // zero high nibble (convert.py:90-91).
+    const int c0 = g_first * glen, c1 = min(g_last * glen, I);
+    for (int i = c0; i < c1; i += 2) {
+        float r0 = rintf(wr[i] / sr[i / glen]);
+        r0 = fminf(fmaxf(r0, -8.0f), 7.0f);
+        int n0 = ((int)r0 + 8) & 15, n1 = 0;
+        if (i + 1 < I) {
+            float r1 = rintf(wr[i + 1] / sr[(i + 1) / glen]);
+            r1 = fminf(fmaxf(r1, -8.0f), 7.0f);
+            n1 = ((int)r1 + 8) & 15;
+        }
+        pr[i >> 1] = (uint8_t)(n0 | (n1 << 4));
+    }
+}
+
+int pk_launch_quantize_i4(const float *w, int O, int I, int gs, uint8_t *packed,
+                          float *scales, hipStream_t st) {
+    PK_CHECK(O > 0 && I > 0, PK_ERR_ARG, "quantize: bad shape");
+    const int per_row_scale = (gs <= 0 || gs >= I);
+    const int glen = per_row_scale ? I : gs;
+    const int ng = per_row_scale ? 1 : (I + gs - 1) / gs;
+    // an odd group length puts two groups in one byte: keep a row on one thread
+    const int per_thread_row = (glen & 1) ? 1 : 0;
+    const int64_t n = per_thread_row ? (int64_t)O : (int64_t)O * ng;
+    hipLaunchKernelGGL(k_quantize_i4, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                       w, O, I, glen, ng, per_thread_row, packed, scales);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}

@@ -1,0 +1,153 @@
+// pk_internal.h — shared definitions of the gfx950 expert-path library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+#include "../../include/picchio_hip.h"
+
+// Native vector types for non-temporal (streaming) 16-byte loads.
+typedef float pk_f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t pk_i32x4 __attribute__((ext_vector_type(4)));
+
+// ───────────────────────── error plumbing ─────────────────────────
+void pk_set_error(const char *fmt, ...);
+
+#define PK_HIP(call)                                                          \
+    do {                                                                      \
+        hipError_t e_ = (call);                                               \
+        if (e_ != hipSuccess) {                                               \
+            pk_set_error("%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                         __FILE__, __LINE__);                                 \
+            return PK_ERR_HIP;                                                \
+        }                                                                     \
+    } while (0)
+
+#define PK_CHECK(cond, code, ...)                                             \
+    do {                                                                      \
+        if (!(cond)) {                                                        \
+            pk_set_error(__VA_ARGS__);                                        \
+            return (code);                                                    \
+        }                                                                     \
+    } while (0)
+
+#define PK_TRY(expr)                                                          \
+    do {                                                                      \
+        int rc_ = (expr);                                                     \
+        if (rc_ != PK_OK) return rc_;                                         \
+    } while (0)
+
+// ───────────────────── INT4 group-scaled HBM layout ─────────────────────
+//
+// The reference keeps an INT4 gs64 matrix row-major: uint8 [O][I/2] (low
+// nibble = even column, value = nib - 8) and float scales [O][I/64]
+// (convert.py:84-93). In HBM the library stores it as 64-row x 64-column
+// tiles so that one wavefront load instruction reads 1 KiB contiguous:
+//
+//   tile (rb, g), rb = row block of 64 rows, g = 64-column scale group:
+//     bytes [0, 1024):    lane r's 16 bytes = row rb*64+r, columns g*64 +  0..31
+//     bytes [1024, 2048): lane r's 16 bytes = row rb*64+r, columns g*64 + 32..63
+//   tiles ordered [rb][g]; every nibble is stored XOR 8, i.e. as the 4-bit
+//   two's complement of (nib - 8), which v_cvt_off_f32_i4 reads as q/16.
+//   scales: float [rb][g][64], each stored as 16 * scale (exact), so that
+//   (partial sum of x*q/16) * (16*scale) == (partial sum of x*q) * scale.
+//
+// Rows beyond O are zero-padded (q = 0, scale = 0).
+constexpr int PK_TILE_ROWS = 64;
+constexpr int PK_GS = 64;
+constexpr int PK_TILE_BYTES = PK_TILE_ROWS * PK_GS / 2;   // 2048
+
+struct pk_i4_shape {
+    int O, I;        // logical shape
+    int RB, NG;      // row blocks of 64, groups of 64
+    int64_t tile_bytes;   // RB*NG*2048
+    int64_t scale_bytes;  // RB*NG*64*4
+};
+
+inline pk_i4_shape pk_i4_make_shape(int O, int I) {
+    pk_i4_shape s;
+    s.O = O; s.I = I;
+    s.RB = (O + PK_TILE_ROWS - 1) / PK_TILE_ROWS;
+    s.NG = I / PK_GS;
+    s.tile_bytes = (int64_t)s.RB * s.NG * PK_TILE_BYTES;
+    s.scale_bytes = (int64_t)s.RB * s.NG * PK_TILE_ROWS * 4;
+    return s;
+}
+
+inline int64_t pk_align256(int64_t v) { return (v + 255) & ~(int64_t)255; }
+
+// Expert slot layout inside the store (all experts of a model share it).
+struct pk_expert_layout {
+    pk_i4_shape gu, dn;          // gate_up [moe_inter][hidden], down [hidden][moe_inter/2]
+    int64_t off_gu_tiles, off_gu_scales, off_dn_tiles, off_dn_scales;
+    int64_t off_gu_bias, off_dn_bias;
+    int64_t stride;              // bytes per expert slot
+};
+
+// ───────────────────────── device tensors ─────────────────────────
+struct pk_qt {
+    int fmt;           // PK_FMT_*
+    int O, I;
+    int gs;            // INT4 group size (0 = per-row)
+    int tiled;         // INT4 gs64 in the tiled layout
+    pk_i4_shape sh;
+    void *data;        // F32 [O][I] / INT8 [O][I] / INT4 tiles or ref layout
+    float *s;          // scales (INT8 per row, INT4 ref or tiled)
+};
+
+// ───────────────────────── kernel launchers ─────────────────────────
+// All launchers queue on `st` and return PK_OK / PK_ERR_*.
+
+// One INT4 GEMV "item" = one matrix applied to one input vector.
+struct pk_i4_items {
+    const uint8_t *base;       // store base (or matrix base when slots == null)
+    int64_t slot_stride;       // bytes between expert slots
+    int64_t off_tiles, off_scales, off_bias;  // offsets inside a slot (bias < 0: none)
+    const int32_t *slots;      // [n_items] slot index (device), or null -> slot 0
+    int32_t slot_base;         // added to every slot index (layer * n_experts)
+    const float *x;            // input of item i at x + i * x_stride
+    int64_t x_stride;
+    float *y;                  // output of item i at y + i * y_stride
+    int64_t y_stride;
+    int n_items;
+};
+
+enum pk_i4_epilogue { PK_EPI_PLAIN = 0, PK_EPI_SWIGLU = 1, PK_EPI_COMBINE = 2 };
+
+struct pk_combine_args {
+    const float *w;           // [n_items] routing weights (already * routed_scale)
+    float *out;               // [O] combined output
+    const float *residual;    // optional: out = residual + combine
+    uint32_t *counters;       // [RB] zero-initialised arrival counters
+};
+
+int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
+                      float swiglu_limit, float swiglu_alpha,
+                      const pk_combine_args *comb, hipStream_t st);
+
+// Reference-layout INT4 gs GEMV, any I / group size (exact quant.h order).
+int pk_launch_i4_gemv_ref(float *y, const float *x, const uint8_t *q4, const float *s,
+                          int S, int I, int O, int gs, hipStream_t st);
+
+int pk_launch_i4_repack(const uint8_t *q4, const float *s, int O, int I,
+                        uint8_t *tiles, float *sc16, hipStream_t st);
+
+int pk_launch_quantize_i4(const float *w, int O, int I, int gs, uint8_t *packed,
+                          float *scales, hipStream_t st);
+
+int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
+                       int S, int I, int O, hipStream_t st);
+int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
+                      int S, int I, int O, hipStream_t st);
+int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, const float *s,
+                               int S, int I, int O, hipStream_t st);
+
+// Router for one token: logits = R x + b, top-k by repeated argmax, softmax.
+int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D,
+                          int K, float routed_scale, float *logits, int32_t *sel,
+                          float *w_scaled, float *w_soft, uint32_t *counter,
+                          hipStream_t st);
+
+int pk_launch_rmsnorm(float *out, const float *x, const float *w, int D, float eps,
+                      int T, hipStream_t st);

@@ -14,11 +14,18 @@
 #include <stdint.h>
 #include <math.h>
 
+/* Callable from device code too when compiled by hipcc. */
+#if defined(__HIPCC__)
+#define PK_SYNTH_FN static inline __host__ __device__
+#else
+#define PK_SYNTH_FN static inline
+#endif
+
 #ifdef __cplusplus
 extern "C" {
 #endif
 
-static inline uint64_t pk_mix64(uint64_t z) {
+PK_SYNTH_FN uint64_t pk_mix64(uint64_t z) {
     z += 0x9E3779B97F4A7C15ull;
     z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
     z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
@@ -42,14 +49,14 @@ enum {
     PK_T_IDS = 19        /* uniform token ids                 */
 };
 
-static inline uint64_t pk_stream(uint64_t seed, uint32_t kind, uint32_t layer,
+PK_SYNTH_FN uint64_t pk_stream(uint64_t seed, uint32_t kind, uint32_t layer,
                                  uint32_t index) {
     uint64_t tag = ((uint64_t)kind << 56) ^ ((uint64_t)layer << 36) ^ (uint64_t)index;
     return pk_mix64(seed ^ pk_mix64(tag));
 }
 
 /* Samples 2c and 2c+1 of stream `s`. */
-static inline void pk_normal_pair(uint64_t s, uint64_t c, double *n0, double *n1) {
+PK_SYNTH_FN void pk_normal_pair(uint64_t s, uint64_t c, double *n0, double *n1) {
     uint64_t a = pk_mix64(s ^ pk_mix64(2 * c));
     uint64_t b = pk_mix64(s ^ pk_mix64(2 * c + 1));
     double u1 = (double)((a >> 11) + 1) * 0x1p-53;   /* (0, 1] */
@@ -61,7 +68,7 @@ static inline void pk_normal_pair(uint64_t s, uint64_t c, double *n0, double *n1
 }
 
 /* out[i] = (float)(std * N_{first+i}) for i in [0, n). */
-static inline void pk_fill_normal(float *out, int64_t n, uint64_t s, float std,
+PK_SYNTH_FN void pk_fill_normal(float *out, int64_t n, uint64_t s, float std,
                                   int64_t first) {
     int64_t i = 0;
     while (i < n) {
@@ -78,7 +85,7 @@ static inline void pk_fill_normal(float *out, int64_t n, uint64_t s, float std,
 }
 
 /* Uniform integer in [0, m). */
-static inline int pk_uniform_int(uint64_t s, uint64_t c, int m) {
+PK_SYNTH_FN int pk_uniform_int(uint64_t s, uint64_t c, int m) {
     uint64_t a = pk_mix64(s ^ pk_mix64(c));
     return (int)((a >> 11) % (uint64_t)m);
 }

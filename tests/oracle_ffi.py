@@ -21,42 +21,12 @@ i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
 i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 
 
-class PkCfg(C.Structure):
-    """pk_cfg of include/picchio_hip.h (field order and types must match)."""
-    _fields_ = [
-        ("hidden", C.c_int32), ("n_layers", C.c_int32), ("n_heads", C.c_int32),
-        ("n_kv_heads", C.c_int32), ("head_dim", C.c_int32), ("n_experts", C.c_int32),
-        ("topk", C.c_int32), ("moe_inter", C.c_int32), ("vocab", C.c_int32),
-        ("ctx_len", C.c_int32), ("sliding_window", C.c_int32),
-        ("eps", C.c_float), ("theta", C.c_float), ("rope_factor", C.c_float),
-        ("rope_beta_fast", C.c_float), ("rope_beta_slow", C.c_float),
-        ("rope_original_ctx", C.c_int32), ("rope_truncate", C.c_int32),
-        ("rope_attn_factor", C.c_float), ("swiglu_limit", C.c_float),
-        ("swiglu_alpha", C.c_float), ("routed_scale", C.c_float),
-        ("group_size", C.c_int32), ("lm_head_fmt", C.c_int32),
-        ("layer_type", C.c_int8 * 128),
-    ]
+from picchio_amd import PkCfg, gptoss_cfg  # noqa: E402  (struct layout only)
 
 
 def make_cfg(**kw):
-    """GPT-OSS-20B-shaped defaults; keywords override."""
-    import math
-    d = dict(hidden=2880, n_layers=24, n_heads=64, n_kv_heads=8, head_dim=64,
-             n_experts=32, topk=4, moe_inter=5760, vocab=201088, ctx_len=1024,
-             sliding_window=128, eps=1e-5, theta=150000.0, rope_factor=32.0,
-             rope_beta_fast=32.0, rope_beta_slow=1.0, rope_original_ctx=4096,
-             rope_truncate=0, swiglu_limit=7.0, swiglu_alpha=1.702,
-             routed_scale=1.0, group_size=64, lm_head_fmt=0)
-    d.update(kw)
-    if "rope_attn_factor" not in d:
-        f = np.float32(d["rope_factor"])
-        d["rope_attn_factor"] = float(np.float32(0.1) * np.float32(math.log(f)) + np.float32(1.0)) \
-            if f > 1.0 else 1.0
-    lt = d.pop("layer_type", None)
-    c = PkCfg(**d)
-    for i in range(128):
-        c.layer_type[i] = (lt[i] if lt is not None and i < len(lt) else i % 2)
-    return c
+    """GPT-OSS-20B-shaped configuration; keywords override."""
+    return gptoss_cfg(**kw)
 
 
 def _bind(lib, name, res, *args):

@@ -1,0 +1,227 @@
+"""GPU parity of the INT4 expert path against the oracle (oracle/pk_oracle.c,
+itself bit-exact with picchio's quant.h / picchio.c, see test_oracle.py).
+
+Bars: INT4 group-scaled GEMV and the gs64 quantizer bit-exact; fp32 results
+of the expert FFN and MoE layer within relative L2 1e-4,
+top-k expert ids identical.
+"""
+import numpy as np
+import pytest
+
+from helpers import REL_L2_TOL, bits_equal, first_mismatch, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+
+def _engine(cfg):
+    import picchio_amd
+    return picchio_amd.Engine(cfg)
+
+
+def _rand(shape, seed, scale=1.0):
+    return (np.random.default_rng(seed).standard_normal(shape) * scale).astype(np.float32)
+
+
+# ───────────────────────── INT4 GEMV ─────────────────────────
+
+@pytest.mark.parametrize("O,I,S", [(5760, 2880, 1), (2880, 2880, 1), (2880, 2880, 3),
+                                   (100, 128, 2), (64, 64, 1), (720, 2880, 1)])
+def test_i4_gs64_gemv_tiled_bitexact(gpu, oracle, O, I, S):
+    """Tiled HBM layout + cvt_off decode reproduce matmul_i4_gs bit for bit."""
+    import picchio_amd as pa
+    import torch
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    w = _rand((O, I), 11 + O + I, 0.02)
+    q4, s = oracle.quant_gs(w, 64)
+    x = _rand((S, I), 7 + S)
+    y_ref = oracle.mm_i4_gs(x, q4, s, O, I, 64)
+    with _engine(cfg) as eng:
+        qt = eng.qt_upload(pa.FMT_INT4, q4, s, O, I, 64)
+        xd = eng.to_dev(x)
+        yd = eng.empty((S, O), torch.float32)
+        eng.matmul_qt(yd, xd, qt, S)
+        y = eng.to_host(yd)
+        eng.qt_free(qt)
+    assert bits_equal(y, y_ref), first_mismatch(y, y_ref)
+
+
+@pytest.mark.parametrize("O,I,gs,S", [(37, 200, 64, 2), (16, 101, 32, 2), (5, 50, 64, 3),
+                                      (9, 130, 48, 1), (7, 33, 33, 1), (8, 64, 16, 1)])
+def test_i4_gs_gemv_ragged_bitexact(gpu, oracle, O, I, gs, S):
+    """Shapes outside the tiled layout (short last group, odd width, other
+    group sizes) run the reference-layout kernel, still bit-exact."""
+    import picchio_amd as pa
+    import torch
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    w = _rand((O, I), 100 + O, 0.02)
+    q4, s = oracle.quant_gs(w, gs)
+    gs_eff = gs if 0 < gs < I else I
+    x = _rand((S, I), 3)
+    y_ref = oracle.mm_i4_gs(x, q4, s, O, I, gs_eff)
+    with _engine(cfg) as eng:
+        qt = eng.qt_upload(pa.FMT_INT4, q4, np.ascontiguousarray(s), O, I, gs_eff)
+        xd = eng.to_dev(x)
+        yd = eng.empty((S, O), torch.float32)
+        eng.matmul_qt(yd, xd, qt, S)
+        y = eng.to_host(yd)
+        eng.qt_free(qt)
+    assert bits_equal(y, y_ref), first_mismatch(y, y_ref)
+
+
+@pytest.mark.parametrize("O,I,gs", [(5760, 2880, 64), (37, 200, 64), (16, 101, 32),
+                                    (7, 33, 33), (6, 40, 0), (4, 10, 64)])
+def test_quantizer_bitexact(gpu, oracle, O, I, gs):
+    """GPU gs64 quantizer == convert.py restatement, bytes and scales."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    w = _rand((O, I), 5 + I, 0.02)
+    w[0, :min(I, 8)] = 0.0                      # an (almost) all-zero group
+    q_ref, s_ref = oracle.quant_gs(w, gs)
+    ng = s_ref.shape[1]
+    with _engine(cfg) as eng:
+        wd = eng.to_dev(w)
+        qd = eng.empty((O, (I + 1) // 2), torch.uint8)
+        sd = eng.empty((O, ng), torch.float32)
+        eng.quantize_int4_gs(wd, O, I, gs, qd, sd)
+        q = eng.to_host(qd)
+        s = eng.to_host(sd)
+    assert np.array_equal(q, q_ref)
+    assert bits_equal(s, s_ref)
+
+
+# ───────────────────────── dense matmul_qt ─────────────────────────
+
+@pytest.mark.parametrize("fmt", ["f32", "q8", "i4row"])
+def test_matmul_qt_formats(gpu, oracle, fmt):
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    O, I, S = 300, 2880, 2
+    x = _rand((S, I), 9)
+    y_ref = np.empty((S, O), np.float32)
+    W = _rand((O, I), 10, 0.02)
+    if fmt == "f32":
+        oracle.matmul_f32(y_ref, x, W, S, I, O)
+        args = (pa.FMT_F32, W, None, O, I, 0)
+    elif fmt == "q8":
+        q = np.empty((O, I), np.int8)
+        s = np.empty(O, np.float32)
+        oracle.quantize_int8_rows(W, O, I, q, s)
+        oracle.matmul_q8(y_ref, x, q, s, S, I, O)
+        args = (pa.FMT_INT8, q, s, O, I, 0)
+    else:
+        q = np.empty((O, (I + 1) // 2), np.uint8)
+        s = np.empty(O, np.float32)
+        oracle.quantize_rows_i4(W, O, I, q, s)
+        oracle.matmul_i4(y_ref, x, q, s, S, I, O)
+        args = (pa.FMT_INT4, q, s, O, I, 0)
+    with _engine(cfg) as eng:
+        qt = eng.qt_upload(*args)
+        xd = eng.to_dev(x)
+        yd = eng.empty((S, O), torch.float32)
+        eng.matmul_qt(yd, xd, qt, S)
+        y = eng.to_host(yd)
+        eng.qt_free(qt)
+    assert rel_l2(y, y_ref) < 1e-6
+
+
+# ───────────────────────── expert FFN / MoE layer ─────────────────────────
+
+@pytest.fixture(scope="module")
+def moe_setup(gpu, oracle):
+    """One GPT-OSS-20B-shaped MoE layer (8 experts to keep the CPU build
+    short; every expert has the full 5760x2880 / 2880x2880 shape)."""
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=8, ctx_len=16, vocab=64)
+    model = oracle.model_build(cfg, 20240601, 0)
+    eng = pa.Engine(cfg)
+    for e in range(cfg.n_experts):
+        eng.store_expert(0, e, *oracle.expert_arrays(model, 0, e, cfg))
+    D, E = cfg.hidden, cfg.n_experts
+    router = oracle.tensor(model, 6, 0, E * D)          # PK_T_ROUTER
+    rbias = oracle.tensor(model, 7, 0, E)               # PK_T_ROUTER_B
+    eng.store_router(0, router, rbias)
+    yield cfg, model, eng
+    eng.close()
+    oracle.model_free(model)
+
+
+def _token_x(oracle, cfg, t):
+    x = oracle.normal(77, 1, t, 0, cfg.hidden)
+    xn = np.empty_like(x)
+    oracle.rmsnorm(xn, x, np.ones(cfg.hidden, np.float32), cfg.hidden, 1e-5)
+    return xn
+
+
+def test_expert_apply_parity(moe_setup, oracle):
+    import torch
+    cfg, model, eng = moe_setup
+    D = cfg.hidden
+    for eid, w in [(0, 0.25), (5, 1.0), (7, -0.5)]:
+        x = _token_x(oracle, cfg, 1000 + eid)
+        dst0 = oracle.normal(78, 1, eid, 0, D)
+        ref = dst0.copy()
+        oracle.expert_apply(model, 0, eid, x, ref, w)
+        xd = eng.to_dev(x)
+        dd = eng.to_dev(dst0)
+        eng.expert_apply(0, eid, xd, dd, w)
+        got = eng.to_host(dd)
+        assert rel_l2(got - dst0, ref - dst0) < 1e-6
+
+
+def test_moe_forward_parity(moe_setup, oracle):
+    import torch
+    cfg, model, eng = moe_setup
+    D, K, E = cfg.hidden, cfg.topk, cfg.n_experts
+    worst = 0.0
+    for t in range(12):
+        x = _token_x(oracle, cfg, t)
+        out_ref = np.empty(D, np.float32)
+        sel_ref = np.empty(K, np.int32)
+        w_ref = np.empty(K, np.float32)
+        logits = np.empty(E, np.float32)
+        oracle.moe_forward(model, 0, x, out_ref, sel_ref, w_ref, logits)
+        xd = eng.to_dev(x)
+        od = eng.empty(D, torch.float32)
+        sel, w = eng.moe_forward(0, xd, od, want_routing=True)
+        out = eng.to_host(od)
+        srt = np.sort(logits)[::-1]
+        margin = float(srt[K - 1] - srt[K])           # 4th vs 5th logit
+        if margin > 1e-5:
+            assert list(sel) == list(sel_ref), (t, sel, sel_ref, margin)
+            assert np.allclose(w, w_ref, rtol=1e-5, atol=0)
+            err = rel_l2(out, out_ref)
+            worst = max(worst, err)
+            assert err < REL_L2_TOL, (t, err)
+    assert worst < 1e-5
+
+
+def test_moe_forward_batch_matches_decode(moe_setup, oracle):
+    import torch
+    cfg, model, eng = moe_setup
+    D, K, T = cfg.hidden, cfg.topk, 5
+    xs = np.stack([_token_x(oracle, cfg, 50 + t) for t in range(T)])
+    xd = eng.to_dev(xs)
+    ob = eng.empty((T, D), torch.float32)
+    import picchio_amd as pa
+    pa.check(eng.L.pk_moe_forward_batch(eng.h, 0, pa.ptr(xd), T, pa.ptr(ob), None, None))
+    got = eng.to_host(ob)
+    for t in range(T):
+        od = eng.empty(D, torch.float32)
+        eng.moe_forward(0, eng.to_dev(xs[t]), od)
+        assert bits_equal(got[t], eng.to_host(od))
+
+
+def test_missing_expert_is_an_error(gpu, oracle):
+    """picchio skips a missing expert silently (picchio.c:1394); the library
+    refuses the call instead."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    with _engine(cfg) as eng:
+        xd = eng.to_dev(np.zeros(cfg.hidden, np.float32))
+        od = eng.empty(cfg.hidden, torch.float32)
+        with pytest.raises(pa.PkError) as ei:
+            eng.moe_forward(0, xd, od)
+        assert ei.value.code in (-5,)
