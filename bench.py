@@ -66,8 +66,8 @@ def cpu_baseline(x, seed, budget_s):
     out = np.empty(D, np.float32)
     run(x[0], out)                                   # warm-up (page in)
     n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s and n < len(x):
-        run(x[n], out)
+    while time.perf_counter() - t0 < budget_s:
+        run(x[n % len(x)], out)
         n += 1
     dt = time.perf_counter() - t0
     o.model_free(model)
@@ -87,6 +87,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=400)
+    ap.add_argument("--mode", choices=["seq", "kernels"], default="seq",
+                    help="seq: one persistent kernel per sequence; kernels: five kernels per step in a HIP graph")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
@@ -109,57 +111,89 @@ def main():
     x = token_inputs(n_tok, 1000 + args.seed)
     xd = eng.to_dev(x)
     od = eng.empty((n_tok, D), torch.float32)
-
-    def enqueue(t):
-        eng.moe_forward(t % L, xd[t], od[t])
-
-    # HIP graphs: one for the warm-up tokens, one for the timed tokens
-    eng.capture_begin()
-    for t in range(args.warmup):
-        enqueue(t)
-    g_warm = eng.capture_end()
-    eng.capture_begin()
-    for t in range(args.warmup, n_tok):
-        enqueue(t)
-    g_run = eng.capture_end()
-
-    eng.graph_launch(g_warm)
-    eng.sync()
-    torch.cuda.synchronize()
+    layers = np.array([t % L for t in range(n_tok)], np.int32)
+    ld = eng.to_dev(layers)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
-    ev0.record(eng.stream)
-    eng.graph_launch(g_run)
-    ev1.record(eng.stream)
-    ev1.synchronize()
-    torch.cuda.synchronize()
-    ms = ev0.elapsed_time(ev1)
-    ms_tok = ms / args.steps
+    W, S = args.warmup, args.steps
+
+    if args.mode == "seq":
+        # one persistent launch per sequence; chained steps = batch-1 decode
+        eng.moe_seq_reserve(max(W, S))
+        eng.moe_forward_seq(ld[:W], xd[:W], od[:W], W, chain=True)
+        eng.moe_seq_status()
+        torch.cuda.synchronize()
+        ev0.record(eng.stream)
+        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=True)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        eng.moe_seq_status()
+        ms = ev0.elapsed_time(ev1)
+        # the same launch bracketed by the engine's per-kernel events
+        eng.profile(True)
+        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=True)
+        eng.moe_seq_status()
+        tot, cnt = eng.profile_read(pa.PROF_MOE_SEQ)
+        eng.profile(False)
+        kern_ms = tot / max(cnt, 1)
+        # independent steps (no chain): the throughput bound of the same kernel
+        ev0.record(eng.stream)
+        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=False)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        eng.moe_seq_status()
+        ms_nochain = ev0.elapsed_time(ev1)
+        prof = {"moe_seq_launch": kern_ms}
+        roof_bytes = S * TOKEN_BYTES
+        roof_ms = kern_ms
+        roof_kernel = "k_moe_seq (persistent: router+top-4+gate_up+SwiGLU+down+combine, chained steps)"
+        extra = {"unchained_us_per_token": round(ms_nochain / S * 1e3, 3),
+                 "unchained_gbps": round(S * TOKEN_BYTES / (ms_nochain * 1e-3) / 1e9, 1)}
+    else:
+        def enqueue(t):
+            eng.moe_forward(t % L, xd[t], od[t])
+        eng.capture_begin()
+        for t in range(W):
+            enqueue(t)
+        g_warm = eng.capture_end()
+        eng.capture_begin()
+        for t in range(W, n_tok):
+            enqueue(t)
+        g_run = eng.capture_end()
+        eng.graph_launch(g_warm)
+        eng.sync()
+        torch.cuda.synchronize()
+        ev0.record(eng.stream)
+        eng.graph_launch(g_run)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        ms = ev0.elapsed_time(ev1)
+        # per-kernel durations: event brackets per launch, queue pre-filled
+        # behind a bounded idle kernel so host launch latency stays outside
+        n_prof = min(args.profile_tokens, n_tok)
+        eng.profile(True)
+        eng.stall(60000)
+        for t in range(n_prof):
+            enqueue(t)
+        eng.sync()
+        prof = {}
+        for name, kid in (("gate_up", pa.PROF_EXPERT_GATE_UP), ("down", pa.PROF_EXPERT_DOWN),
+                          ("router", pa.PROF_ROUTER), ("combine", pa.PROF_COMBINE)):
+            tot, cnt = eng.profile_read(kid)
+            prof[name] = tot / max(cnt, 1)
+        eng.profile(False)
+        eng.graph_destroy(g_warm)
+        eng.graph_destroy(g_run)
+        roof_bytes = GATE_UP_LAUNCH_BYTES
+        roof_ms = prof["gate_up"]
+        roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up, 4 experts/launch)"
+        extra = {}
+
+    ms_tok = ms / S
     gbps = TOKEN_BYTES / (ms_tok * 1e-3) / 1e9
-    print(f"[bench] {args.steps} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, "
-          f"{gbps:.1f} GB/s", file=sys.stderr, flush=True)
-
-    # per-kernel durations: event brackets per launch, queue pre-filled behind
-    # a bounded idle kernel so host launch latency never lands inside a bracket
-    n_prof = min(args.profile_tokens, n_tok)
-    eng.profile(True)
-    eng.stall(60000)
-    for t in range(n_prof):
-        enqueue(t)
-    eng.sync()
-    prof = {}
-    for name, kid in (("gate_up", pa.PROF_EXPERT_GATE_UP), ("down", pa.PROF_EXPERT_DOWN),
-                      ("router", pa.PROF_ROUTER), ("combine", pa.PROF_COMBINE)):
-        tot, cnt = eng.profile_read(kid)
-        prof[name] = tot / max(cnt, 1)
-    eng.profile(False)
-    gu_us = prof["gate_up"] * 1e3
-    achieved = GATE_UP_LAUNCH_BYTES / (prof["gate_up"] * 1e-3) / 1e9
-    print("[bench] mean kernel us: " + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in prof.items()),
-          file=sys.stderr, flush=True)
-
-    eng.graph_destroy(g_warm)
-    eng.graph_destroy(g_run)
+    achieved = roof_bytes / (roof_ms * 1e-3) / 1e9
+    print(f"[bench] {S} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, {gbps:.1f} GB/s; "
+          f"kernel {achieved:.1f} GB/s; {extra}", file=sys.stderr, flush=True)
     eng.close()
 
     cpu = None
@@ -185,11 +219,12 @@ def main():
                    "layer_copies": L, "experts": E, "topk": K, "hidden": D, "weights": "int4-gs64",
                    "bytes_per_token": TOKEN_BYTES, "tokens_per_s": round(1e3 / ms_tok, 1),
                    "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-                   "kernel_us": {k: round(v * 1e3, 3) for k, v in prof.items()}},
+                   "mode": args.mode, "chained": True,
+                   "kernel_us": {k: round(v * 1e3, 3) for k, v in prof.items()}, **extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
-                     "kernel": "k_i4_gemv<15,3,SWIGLU> (gate_up, 4 experts/launch)",
-                     "bytes_per_launch": GATE_UP_LAUNCH_BYTES, "mean_us": round(gu_us, 3)},
+                     "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
+                     "mean_us": round(roof_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(line))

@@ -168,6 +168,26 @@ int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
 int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
                          float *out_dev, int32_t *sel_dev, float *w_dev);
 
+/* A sequence of T batch-1 MoE steps in one persistent kernel: step t runs
+ * moe_forward on layer layers_dev[t] with input x_dev[t][hidden] into
+ * out_dev[t][hidden]. chain != 0 makes step t+1 wait for step t (the layer
+ * dependency of decode); chain == 0 lets independent steps overlap.
+ * Results equal pk_moe_forward step by step. Errors raised inside the kernel
+ * (a bounded dependency wait that timed out) are reported by
+ * pk_moe_seq_status, which synchronises the stream. */
+int pk_moe_forward_seq(pk_engine *e, const int32_t *layers_dev, const float *x_dev, int T,
+                       float *out_dev, int chain);
+int pk_moe_seq_status(pk_engine *e);
+/* Sizes the per-step buffers for sequences of up to T steps (allocates;
+ * call before capturing or timing). */
+int pk_moe_seq_reserve(pk_engine *e, int T);
+/* Tracing: with trace_dev != NULL, later sequence launches record four
+ * 100 MHz timestamps per task (start, dependencies ready, math done, end)
+ * into trace_dev[task][4]; tasks are numbered step-major: per step
+ * n_experts router rows, then topk x gate_up row blocks, then topk x down
+ * row blocks. NULL turns tracing off. */
+int pk_moe_seq_trace(pk_engine *e, uint64_t *trace_dev);
+
 /* gqa_attention (picchio.c:504-623) for one token at `pos`; writes K/V. */
 int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
                      float *out_dev);
@@ -194,6 +214,7 @@ int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
 #define PK_PROF_EXPERT_DOWN    1   /* INT4 down GEMV                                 */
 #define PK_PROF_ROUTER         2   /* router GEMV + top-k                            */
 #define PK_PROF_COMBINE        3   /* weighted combine                               */
+#define PK_PROF_MOE_SEQ        4   /* persistent MoE sequence kernel (whole launch)  */
 #define PK_PROF_N              8
 int pk_engine_profile(pk_engine *e, int enable);
 int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);

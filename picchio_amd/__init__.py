@@ -16,7 +16,7 @@ PK_OK = 0
 ERRORS = {-1: "PK_ERR_ARG", -2: "PK_ERR_HIP", -3: "PK_ERR_OOM", -4: "PK_ERR_UNSUPPORTED",
           -5: "PK_ERR_MISSING", -6: "PK_ERR_CONTEXT_FULL"}
 FMT_F32, FMT_INT8, FMT_INT4 = 0, 1, 2
-PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE = 0, 1, 2, 3
+PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE, PROF_MOE_SEQ = 0, 1, 2, 3, 4
 
 
 class PkError(RuntimeError):
@@ -120,6 +120,10 @@ def lib():
         "pk_engine_profile": (C.c_int, [vp, C.c_int]),
         "pk_engine_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(i64)]),
         "pk_engine_stall": (C.c_int, [vp, C.c_int]),
+        "pk_moe_forward_seq": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_int]),
+        "pk_moe_seq_status": (C.c_int, [vp]),
+        "pk_moe_seq_reserve": (C.c_int, [vp, C.c_int]),
+        "pk_moe_seq_trace": (C.c_int, [vp, vp]),
         "pk_capture_begin": (C.c_int, [vp]),
         "pk_capture_end": (C.c_int, [vp, C.POINTER(vp)]),
         "pk_graph_launch": (C.c_int, [vp, vp]),
@@ -249,6 +253,16 @@ class Engine:
             return sel, w
         check(self.L.pk_moe_forward(self.h, layer, ptr(x_dev), ptr(out_dev), None, None))
         return None
+
+    def moe_forward_seq(self, layers_dev, x_dev, out_dev, T, chain=True):
+        check(self.L.pk_moe_forward_seq(self.h, ptr(layers_dev), ptr(x_dev), T, ptr(out_dev),
+                                        1 if chain else 0))
+
+    def moe_seq_reserve(self, T):
+        check(self.L.pk_moe_seq_reserve(self.h, T))
+
+    def moe_seq_status(self):
+        check(self.L.pk_moe_seq_status(self.h))
 
     def expert_apply(self, layer, eid, x_dev, dst_dev, w):
         check(self.L.pk_expert_apply(self.h, layer, eid, ptr(x_dev), ptr(dst_dev), w))

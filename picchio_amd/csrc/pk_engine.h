@@ -59,6 +59,19 @@ struct pk_engine {
     double prof_ms[PK_PROF_N] = {0};
     int64_t prof_cnt[PK_PROF_N] = {0};
 
+    int n_cu = 256;                          // compute units of the device
+
+    // persistent MoE sequence (pk_moe_forward_seq): per-step exchange buffers
+    int seq_cap = 0;
+    bool seq_ready = false;
+    float *s_logits = nullptr, *s_act = nullptr, *s_eo = nullptr, *s_w = nullptr;
+    int32_t *s_sel = nullptr;
+    uint32_t *s_ctr = nullptr;
+    int64_t s_ctr_n = 0, s_act_stride = 0, s_eo_stride = 0;
+    void *router_tab = nullptr;               // device [2L] router / bias pointers
+    uint64_t *seq_trace = nullptr;            // optional task timeline (pk_moe_seq_trace)
+    bool router_tab_dirty = true;
+
     // batched scratch (grown on demand)
     int64_t batch_cap = 0;
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;

@@ -146,7 +146,8 @@ static void engine_free(pk_engine *e) {
                     e->K, e->V, e->stage, e->x_in, e->h, e->hn, e->attn_out, e->qkv, e->att,
                     e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
-                    e->b_eo, e->b_sel};
+                    e->b_eo, e->b_sel, e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
+                    e->s_sel, e->s_w};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -172,6 +173,7 @@ static int engine_init(pk_engine *e) {
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, K = c->topk;
     const int half = c->moe_inter / 2;
     e->ex = make_layout(c);
+    PK_HIP(hipDeviceGetAttribute(&e->n_cu, hipDeviceAttributeMultiprocessorCount, e->device));
     ALLOC(e->store, e->ex.stride * (int64_t)L * E);
     e->expert_ready = (uint8_t *)calloc((size_t)L * E, 1);
     PK_CHECK(e->expert_ready, PK_ERR_OOM, "host allocation failed");
@@ -426,6 +428,7 @@ extern "C" int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l) {
         PK_TRY(upload_f32(e, &d.router, l->router, (int64_t)E * D));
         PK_TRY(upload_f32(e, &d.router_b, l->router_bias, E));
         d.have_router = true;
+        e->router_tab_dirty = true;
     }
     if (l->wq.data) {
         const pk_qt_host *ws[3] = {&l->wq, &l->wk, &l->wv};
@@ -520,6 +523,7 @@ extern "C" int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, 
             PK_TRY(synth_fill(e, d.router, (int64_t)E * D, seed, PK_T_ROUTER, l, 0, 0.02f));
             PK_TRY(synth_fill(e, d.router_b, E, seed, PK_T_ROUTER_B, l, 0, 0.02f));
             d.have_router = true;
+            e->router_tab_dirty = true;
             for (int x = 0; x < E; ++x) {
                 uint8_t *s = slot_ptr(e, l, x);
                 PK_TRY(synth_expert_matrix(e, inter, D, seed, PK_T_GU, l, x, s + e->ex.off_gu_tiles,

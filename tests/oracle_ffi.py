@@ -15,10 +15,21 @@ ORACLE_DIR = os.path.join(ROOT, "oracle")
 ORACLE_SO = os.path.join(ORACLE_DIR, "liboracle.so")
 REF_SO = os.path.join(ORACLE_DIR, "_ref", "libpicchio_ref.so")
 
-f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
-u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
-i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
-i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+def _nd(dtype):
+    """ndpointer that also accepts None (optional outputs)."""
+    base = np.ctypeslib.ndpointer(dtype, flags="C_CONTIGUOUS")
+
+    def from_param(cls, obj):
+        if obj is None:
+            return None
+        return base.from_param(obj)
+    return type(f"nd_{np.dtype(dtype).name}", (base,), {"from_param": classmethod(from_param)})
+
+
+f32p = _nd(np.float32)
+u8p = _nd(np.uint8)
+i8p = _nd(np.int8)
+i32p = _nd(np.int32)
 
 
 from picchio_amd import PkCfg, gptoss_cfg  # noqa: E402  (struct layout only)
