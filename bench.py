@@ -87,8 +87,10 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=400)
-    ap.add_argument("--mode", choices=["seq", "kernels"], default="seq",
-                    help="seq: one persistent kernel per sequence; kernels: five kernels per step in a HIP graph")
+    ap.add_argument("--mode", choices=["seq", "kernels"], default="kernels",
+                    help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
+                         "down+combine) replayed from a HIP graph; seq: one block-ordered "
+                         "kernel per sequence of steps")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "

@@ -202,9 +202,16 @@ int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host,
 int pk_prefill_tokens(pk_engine *e, const int32_t *ids_host, int n, int pos_base,
                       int32_t *next_host);
 
-/* Greedy decode of n_steps after a prompt: out_host[n_steps] token ids. */
+/* Greedy decode of n_steps after a prompt: out_host[n_steps] token ids.
+ * The prompt runs position by position (prefill_tokens with PREFILL_BATCH=1,
+ * picchio.c:1946-1954), then one captured decode step is replayed n_steps
+ * times with the token and position carried on the device. */
 int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
                 int n_steps, int32_t *out_host);
+
+/* n_steps greedy decode steps from (tok, pos) over the existing KV cache,
+ * replaying the captured step (for timing); out_host[n_steps] token ids. */
+int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out_host);
 
 /* ── measurement (no reference counterpart: benchmark plumbing) ──
  * With profiling on, the engine brackets each launch of the listed kernels

@@ -124,6 +124,7 @@ def lib():
         "pk_moe_seq_status": (C.c_int, [vp]),
         "pk_moe_seq_reserve": (C.c_int, [vp, C.c_int]),
         "pk_moe_seq_trace": (C.c_int, [vp, vp]),
+        "pk_decode_replay": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
         "pk_capture_begin": (C.c_int, [vp]),
         "pk_capture_end": (C.c_int, [vp, C.POINTER(vp)]),
         "pk_graph_launch": (C.c_int, [vp, vp]),
@@ -253,6 +254,63 @@ class Engine:
             return sel, w
         check(self.L.pk_moe_forward(self.h, layer, ptr(x_dev), ptr(out_dev), None, None))
         return None
+
+    def store_layer(self, layer, in_ln, post_ln, wq, wk, wv, wo, bq, bk, bv, bo, sinks,
+                    router=None, router_bias=None):
+        """Dense tensors of one layer (host fp32 numpy arrays)."""
+        c = self.cfg
+        H, KVH, hd, D = c.n_heads, c.n_kv_heads, c.head_dim, c.hidden
+        lh = PkLayerHost()
+        keep = [in_ln, post_ln, wq, wk, wv, wo, bq, bk, bv, bo, sinks, router, router_bias]
+        lh.in_ln, lh.post_ln = in_ln.ctypes.data, post_ln.ctypes.data
+        lh.wq = PkQtHost(FMT_F32, wq.ctypes.data, None, H * hd, D, 0)
+        lh.wk = PkQtHost(FMT_F32, wk.ctypes.data, None, KVH * hd, D, 0)
+        lh.wv = PkQtHost(FMT_F32, wv.ctypes.data, None, KVH * hd, D, 0)
+        lh.wo = PkQtHost(FMT_F32, wo.ctypes.data, None, D, H * hd, 0)
+        lh.bq, lh.bk, lh.bv, lh.bo = bq.ctypes.data, bk.ctypes.data, bv.ctypes.data, bo.ctypes.data
+        lh.sinks = sinks.ctypes.data
+        if router is not None:
+            lh.router, lh.router_bias = router.ctypes.data, router_bias.ctypes.data
+        check(self.L.pk_store_layer(self.h, layer, C.byref(lh)))
+        del keep
+
+    def store_globals(self, embed, lm_head, final_norm, lm_scales=None):
+        c = self.cfg
+        emb = PkQtHost(FMT_F32, embed.ctypes.data, None, c.vocab, c.hidden, 0)
+        if lm_scales is None:
+            lm = PkQtHost(FMT_F32, lm_head.ctypes.data, None, c.vocab, c.hidden, 0)
+        else:
+            lm = PkQtHost(FMT_INT8, lm_head.ctypes.data, lm_scales.ctypes.data, c.vocab, c.hidden, 0)
+        check(self.L.pk_store_globals(self.h, C.byref(emb), C.byref(lm), ptr(final_norm)))
+
+    def forward_token(self, tok, pos, logits_dev=None):
+        nxt = C.c_int32()
+        check(self.L.pk_forward_token(self.h, tok, pos, C.byref(nxt),
+                                      ptr(logits_dev) if logits_dev is not None else None))
+        return nxt.value
+
+    def gqa_attention(self, layer, x_dev, pos, out_dev):
+        check(self.L.pk_gqa_attention(self.h, layer, ptr(x_dev), pos, ptr(out_dev)))
+
+    def generate(self, prompt, n_steps):
+        import numpy as np
+        p = np.ascontiguousarray(prompt, np.int32)
+        out = np.empty(max(n_steps, 1), np.int32)
+        check(self.L.pk_generate(self.h, ptr(p), len(p), n_steps, ptr(out)))
+        return out[:n_steps]
+
+    def prefill_tokens(self, ids, pos_base=0):
+        import numpy as np
+        p = np.ascontiguousarray(ids, np.int32)
+        nxt = C.c_int32()
+        check(self.L.pk_prefill_tokens(self.h, ptr(p), len(p), pos_base, C.byref(nxt)))
+        return nxt.value
+
+    def decode_replay(self, tok, pos, n_steps):
+        import numpy as np
+        out = np.empty(n_steps, np.int32)
+        check(self.L.pk_decode_replay(self.h, tok, pos, n_steps, ptr(out)))
+        return out
 
     def moe_forward_seq(self, layers_dev, x_dev, out_dev, T, chain=True):
         check(self.L.pk_moe_forward_seq(self.h, ptr(layers_dev), ptr(x_dev), T, ptr(out_dev),

@@ -1,30 +1,536 @@
 // pk_decode.hip — GQA decode attention and the forward_token driver.
+//
+// One decode step (forward_token, picchio.c:1655-1756) on the GPU:
+//   embed + RMSNorm -> per layer: QKV GEMV + bias, RoPE/YaRN + KV store,
+//   sink/sliding-window attention (split over position chunks), O GEMV + bias
+//   + residual, RMSNorm, MoE (router+top-k, gate_up+SwiGLU, down+combine+
+//   residual) -> final RMSNorm -> lm_head GEMV with a fused greedy argmax.
+// The token and position live in device memory (pk_dstate), so a captured
+// step can be replayed for every token: the argmax writes the next token,
+// appends it to the output list and advances the position.
 #include "pk_engine.h"
 
-extern "C" int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
-                                float *out_dev) {
-    (void)e; (void)layer; (void)x_dev; (void)pos; (void)out_dev;
-    pk_set_error("gqa_attention: not built yet");
-    return PK_ERR_UNSUPPORTED;
+#include <math.h>
+#include <vector>
+
+namespace {
+
+constexpr int ATT_CHUNK = 128;         // positions per attention partial
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
 }
 
-extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host,
-                                float *logits_dev) {
-    (void)e; (void)tok; (void)pos; (void)next_host; (void)logits_dev;
-    pk_set_error("forward_token: not built yet");
-    return PK_ERR_UNSUPPORTED;
+// Token row -> h (zeros for an out-of-range id, picchio.c:1476-1480), and
+// hn = rmsnorm(h) (quant.h:396-402: double sum of squares).
+__global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, const float *embed, int vocab,
+                                                       float *h, float *hn, const float *w, int D,
+                                                       float eps) {
+    __shared__ double part[4];
+    __shared__ float rs;
+    const int tok = st->tok;
+    const bool ok = tok >= 0 && tok < vocab;
+    const float *row = embed + (int64_t)(ok ? tok : 0) * D;
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < D; i += 256) {
+        const float v = ok ? row[i] : 0.0f;
+        h[i] = v;
+        acc += (double)v * (double)v;
+    }
+    acc = wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) rs = 1.0f / sqrtf((float)(((part[0] + part[1]) + (part[2] + part[3])) / D) + eps);
+    __syncthreads();
+    const float r = rs;
+    for (int i = threadIdx.x; i < D; i += 256) hn[i] = (ok ? row[i] : 0.0f) * r * w[i];
 }
 
-extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int pos_base,
-                                 int32_t *next_host) {
-    (void)e; (void)ids; (void)n; (void)pos_base; (void)next_host;
-    pk_set_error("prefill_tokens: not built yet");
-    return PK_ERR_UNSUPPORTED;
+// RoPE (picchio.c:455-473) on q [H][hd] and k [KVH][hd] at position pos with
+// the host-built cos/sin table (attn_factor folded in), then kv_store
+// (picchio.c:492-498): K/V rows of this layer at pos.
+__global__ void k_rope_kv(const pk_dstate *st, float *qkv, const float *rope, int H, int KVH, int hd,
+                          float *Kl, float *Vl) {
+    const int pos = st->pos;
+    const int half = hd / 2;
+    const int n_pairs = (H + KVH) * half;
+    const int kv_dim = KVH * hd;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n_pairs) {
+        const int head = i / half, j = i - head * half;
+        float *v = qkv + head * hd;                     // q heads then k heads
+        const float cs = rope[((int64_t)pos * half + j) * 2 + 0];
+        const float sn = rope[((int64_t)pos * half + j) * 2 + 1];
+        const float a = v[j], b = v[j + half];
+        const float r0 = __builtin_fmaf(a, cs, -(b * sn));   // a*cs - b*sn (contracted)
+        const float r1 = __builtin_fmaf(a, sn, b * cs);      // a*sn + b*cs (contracted)
+        v[j] = r0;
+        v[j + half] = r1;
+        if (head >= H) {
+            float *kr = Kl + (int64_t)pos * kv_dim + (head - H) * hd;
+            kr[j] = r0;
+            kr[j + half] = r1;
+        }
+    } else if (i < n_pairs + kv_dim) {
+        const int c = i - n_pairs;
+        Vl[(int64_t)pos * kv_dim + c] = qkv[(H + KVH) * hd + c];
+    }
 }
 
-extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, int n_steps,
-                           int32_t *out) {
-    (void)e; (void)prompt; (void)n_prompt; (void)n_steps; (void)out;
-    pk_set_error("generate: not built yet");
-    return PK_ERR_UNSUPPORTED;
+// Window of picchio.c:556-567 for this layer at pos.
+__device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int window, int &start, int &end) {
+    end = pos < ctx ? pos : ctx - 1;
+    start = 0;
+    if (sliding) {
+        start = end - window + 1;
+        if (start < 0) start = 0;
+    }
+}
+
+// Attention partials: block (h, c) scores positions start+128c .. +127 of
+// head h against its KV head (h / group). Scores are the reference's
+// in-order dot (uncontracted products added one by one, picchio.c:573-577 as
+// gcc builds it) times 1/sqrt(hd). Writes the chunk max, sum of exp(s - max)
+// and the exp-weighted V sum (flash-decoding partials).
+__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, const float *qkv,
+                                                         const float *Kl, const float *Vl, int H, int KVH,
+                                                         int hd, int ctx, int sliding, int window,
+                                                         float *part, int max_chunks) {
+    __shared__ float q[128];
+    __shared__ float p[ATT_CHUNK];
+    __shared__ float red[2];
+    const int h = blockIdx.x, c = blockIdx.y;
+    int start, end;
+    att_window(st->pos, ctx, sliding, window, start, end);
+    const int t0 = start + c * ATT_CHUNK;
+    const int n = min(ATT_CHUNK, end - t0 + 1);
+    if (n <= 0) return;
+    const int kv_dim = KVH * hd, kvh = h / (H / KVH);
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) q[i] = qkv[h * hd + i];
+    __syncthreads();
+    const float scale = 1.0f / sqrtf((float)hd);
+    float s = -INFINITY;
+    if ((int)threadIdx.x < n) {
+        const float *kt = Kl + (int64_t)(t0 + threadIdx.x) * kv_dim + kvh * hd;
+        float dot = 0.0f;
+        int i = 0;
+        const int n4 = hd & ~3;
+        for (; i < n4; ++i) { const float pr = q[i] * kt[i]; dot = dot + pr; }
+        for (; i < hd; ++i) dot = __builtin_fmaf(q[i], kt[i], dot);
+        s = dot * scale;
+    }
+    // chunk max (wave 0 / wave 1 halves), then p = exp(s - m)
+    float m = s;
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(red[0], red[1]);
+    const float e = (int)threadIdx.x < n ? expf(s - m) : 0.0f;
+    p[threadIdx.x] = e;
+    __syncthreads();
+    float* out = part + ((int64_t)h * max_chunks + c) * (hd + 2);
+    if (threadIdx.x < 64) {
+        float sum = 0.0f;
+        for (int t = threadIdx.x; t < n; t += 64) sum += p[t];
+        sum = wave_sum(sum);
+        if (threadIdx.x == 0) { out[0] = m; out[1] = sum; }
+    }
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        float o = 0.0f;
+        const float *vt = Vl + (int64_t)t0 * kv_dim + kvh * hd + i;
+        for (int t = 0; t < n; ++t) o = __builtin_fmaf(p[t], vt[(int64_t)t * kv_dim], o);
+        out[2 + i] = o;
+    }
+}
+
+// Combine the chunk partials of head h with the learned sink (picchio.c:586-604):
+// the sink joins the max and the denominator, not the value sum.
+__global__ void k_attn_combine(const pk_dstate *st, const float *part, const float *sinks, int hd, int ctx,
+                               int sliding, int window, int max_chunks, float *att) {
+    const int h = blockIdx.x;
+    int start, end;
+    att_window(st->pos, ctx, sliding, window, start, end);
+    const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+    const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
+    float M = sinks[h];
+    for (int c = 0; c < nc; ++c) M = fmaxf(M, ph[c * (hd + 2)]);
+    float S = expf(sinks[h] - M);
+    for (int c = 0; c < nc; ++c) S += ph[c * (hd + 2) + 1] * expf(ph[c * (hd + 2)] - M);
+    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+        float o = 0.0f;
+        for (int c = 0; c < nc; ++c) o = __builtin_fmaf(ph[c * (hd + 2) + 2 + i], expf(ph[c * (hd + 2)] - M), o);
+        att[h * hd + i] = o / S;
+    }
+}
+
+// y[o] += (W[o] . x + b[o])  — attention output projection + residual
+// (picchio.c:615-616, :1690). One workgroup per 4 rows (one per wave).
+__global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restrict__ x,
+                                                  const float *__restrict__ W,
+                                                  const float *__restrict__ b, int I, int O) {
+    const int lane = threadIdx.x & 63;
+    const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (o >= O) return;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const float4 *w4 = reinterpret_cast<const float4 *>(W + (int64_t)o * I);
+    const int n4 = I >> 2;
+    float acc = 0.0f;
+    for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
+        float4 xv[4], wv[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 64;
+            xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            acc = __builtin_fmaf(xv[u].x, wv[u].x, acc);
+            acc = __builtin_fmaf(xv[u].y, wv[u].y, acc);
+            acc = __builtin_fmaf(xv[u].z, wv[u].z, acc);
+            acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
+        }
+    }
+    for (int i = (n4 << 2) + lane; i < I; i += 64) acc = __builtin_fmaf(x[i], W[(int64_t)o * I + i], acc);
+    acc = wave_sum(acc);
+    if (lane == 0) y[o] = y[o] + (acc + b[o]);
+}
+
+// lm_head GEMV (fp32 or INT8 rows) fused with the greedy argmax of
+// sample_logits (first maximum, picchio.c:1555-1560): each block reduces its
+// rows to (value, lowest index); the last block to arrive reduces the block
+// results, writes the token, appends it to the output list and advances the
+// position. Blocks exchange results through device-coherent stores.
+constexpr int LM_ROWS_PER_BLOCK = 8;      // 4 waves x 2 rows
+
+__device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
+    if (v > bv || (v == bv && i < bi)) { bv = v; bi = i; }
+}
+
+template <bool Q8>
+__global__ __launch_bounds__(256) void k_lm_head_argmax(const float *__restrict__ x, const void *__restrict__ Wv,
+                                                        const float *__restrict__ sc, int I, int O,
+                                                        float *logits, float *bval, int32_t *bidx,
+                                                        uint32_t *counter, pk_dstate *st, int32_t *out_toks,
+                                                        int out_cap) {
+    __shared__ float rv[4];
+    __shared__ int ri[4];
+    __shared__ int last;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    const float4 *x4 = reinterpret_cast<const float4 *>(x);
+    const int n4 = I >> 2;
+    for (int r = 0; r < 2; ++r) {
+        const int o = blockIdx.x * LM_ROWS_PER_BLOCK + wave * 2 + r;
+        if (o >= O) break;
+        float acc = 0.0f;
+        if (Q8) {
+            const int8_t *w = reinterpret_cast<const int8_t *>(Wv) + (int64_t)o * I;
+            for (int i = lane; i < I; i += 64) acc = __builtin_fmaf(x[i], (float)w[i], acc);
+        } else {
+            const float4 *w4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Wv) + (int64_t)o * I);
+            for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
+                float4 xv[4];
+                pk_f32x4 wv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int i = i0 + u * 64;
+                    xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                    wv[u] = i < n4 ? __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4) + i)
+                                   : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+                }
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    acc = __builtin_fmaf(xv[u].x, wv[u].x, acc);
+                    acc = __builtin_fmaf(xv[u].y, wv[u].y, acc);
+                    acc = __builtin_fmaf(xv[u].z, wv[u].z, acc);
+                    acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
+                }
+            }
+            const float *wr = reinterpret_cast<const float *>(Wv) + (int64_t)o * I;
+            for (int i = (n4 << 2) + lane; i < I; i += 64) acc = __builtin_fmaf(x[i], wr[i], acc);
+        }
+        acc = wave_sum(acc);
+        if (Q8) acc = acc * sc[o];
+        if (lane == 0 && logits) logits[o] = acc;
+        better(bv, bi, acc, o);
+    }
+    if (lane == 0) { rv[wave] = bv; ri[wave] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w) better(bv, bi, rv[w], ri[w]);
+        __hip_atomic_store(bval + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(bidx + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               gridDim.x - 1;
+    }
+    __syncthreads();
+    if (!last || wave != 0) return;
+    bv = -INFINITY;
+    bi = 0x7fffffff;
+    for (int b = lane; b < (int)gridDim.x; b += 64)
+        better(bv, bi, __hip_atomic_load(bval + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+               __hip_atomic_load(bidx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(bv, o, 64);
+        const int oi = __shfl_xor(bi, o, 64);
+        better(bv, bi, ov, oi);
+    }
+    if (lane == 0) {
+        const int tok = bi == 0x7fffffff ? 0 : bi;
+        if (st->n_out < out_cap) out_toks[st->n_out] = tok;
+        st->n_out = st->n_out + 1;
+        st->next = tok;
+        st->tok = tok;
+        st->pos = st->pos + 1;
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+}  // namespace
+
+// ───────────────────────── host side ─────────────────────────
+
+static int decode_reserve(pk_engine *e) {
+    if (e->dec_ready) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "decode buffers must exist before capturing a graph");
+    const pk_cfg *c = &e->c;
+    const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->attn_part, (int64_t)c->n_heads * max_chunks * (c->head_dim + 2) * 4));
+    const int lm_blocks = (c->vocab + LM_ROWS_PER_BLOCK - 1) / LM_ROWS_PER_BLOCK;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->lm_bval, (int64_t)lm_blocks * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->lm_bidx, (int64_t)lm_blocks * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->dstate, sizeof(pk_dstate)));
+    PK_HIP(hipMemsetAsync(e->dstate, 0, sizeof(pk_dstate), e->stream));
+    // one pinned staging entry per position: host-set (tok, pos) copies stay
+    // valid until the stream reaches them
+    PK_HIP(hipHostMalloc((void **)&e->pin_state, (size_t)c->ctx_len * sizeof(pk_dstate), hipHostMallocDefault));
+    e->dec_ready = true;
+    return PK_OK;
+}
+
+static int check_model(pk_engine *e) {
+    const pk_cfg *c = &e->c;
+    PK_CHECK(e->have_globals, PK_ERR_MISSING, "embedding / lm_head / final norm not loaded");
+    for (int l = 0; l < c->n_layers; ++l) {
+        PK_CHECK(e->L[l].have_attn, PK_ERR_MISSING, "layer %d: attention weights not loaded", l);
+        PK_CHECK(e->L[l].have_router, PK_ERR_MISSING, "layer %d: router not loaded", l);
+        for (int x = 0; x < c->n_experts; ++x)
+            PK_CHECK(e->expert_ready[(int64_t)l * c->n_experts + x], PK_ERR_MISSING,
+                     "layer %d expert %d not loaded", l, x);
+    }
+    PK_CHECK(((c->n_heads + 2 * c->n_kv_heads) * c->head_dim) % 4 == 0 && c->hidden % 4 == 0,
+             PK_ERR_UNSUPPORTED, "dimensions must be multiples of 4");
+    return PK_OK;
+}
+
+// Attention of one layer for the token in e->hn at dstate->pos: e->qkv,
+// e->att; adds the projection into e->h (residual).
+static int attention_layer(pk_engine *e, int l) {
+    const pk_cfg *c = &e->c;
+    const pk_layer_dev &d = e->L[l];
+    const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
+    const int kv_dim = KVH * hd;
+    float *Kl = e->K + (int64_t)l * c->ctx_len * kv_dim;
+    float *Vl = e->V + (int64_t)l * c->ctx_len * kv_dim;
+    PK_TRY(pk_launch_gemv_f32(e->qkv, e->hn, d.wqkv, d.bqkv, 1, D, (H + 2 * KVH) * hd, e->stream));
+    const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
+    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256), dim3(256), 0, e->stream, e->dstate, e->qkv,
+                       e->rope, H, KVH, hd, Kl, Vl);
+    PK_HIP(hipGetLastError());
+    const int sliding = c->layer_type[l] == 0;
+    const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
+    const int chunks = sliding ? std::min(max_chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK) : max_chunks;
+    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks), dim3(ATT_CHUNK), 0, e->stream, e->dstate, e->qkv, Kl,
+                       Vl, H, KVH, hd, c->ctx_len, sliding, c->sliding_window, e->attn_part, max_chunks);
+    PK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(64), 0, e->stream, e->dstate, e->attn_part, d.sinks,
+                       hd, c->ctx_len, sliding, c->sliding_window, max_chunks, e->att);
+    PK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4), dim3(256), 0, e->stream, e->h, e->att, d.wo, d.bo,
+                       H * hd, D);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// One forward_token step with tok/pos in device state; logits optional.
+static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int out_cap) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden;
+    hipLaunchKernelGGL(k_embed_rmsnorm, dim3(1), dim3(256), 0, e->stream, e->dstate, e->embed, c->vocab,
+                       e->h, e->hn, e->L[0].in_ln, D, c->eps);
+    PK_HIP(hipGetLastError());
+    for (int l = 0; l < c->n_layers; ++l) {
+        if (l > 0) PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->L[l].in_ln, D, c->eps, 1, e->stream));
+        PK_TRY(attention_layer(e, l));
+        PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->L[l].post_ln, D, c->eps, 1, e->stream));
+        PK_TRY(pk_moe_layer(e, l, e->hn, nullptr, e->h, e->h));      // h += moe(hn)
+    }
+    PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->final_norm, D, c->eps, 1, e->stream));
+    const int lm_blocks = (c->vocab + LM_ROWS_PER_BLOCK - 1) / LM_ROWS_PER_BLOCK;
+    float *lg = logits_dev ? logits_dev : e->logits;
+    if (c->lm_head_fmt == PK_FMT_INT8)
+        hipLaunchKernelGGL(k_lm_head_argmax<true>, dim3(lm_blocks), dim3(256), 0, e->stream, e->hn,
+                           (const void *)e->lm_q8, e->lm_s, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
+                           e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
+    else
+        hipLaunchKernelGGL(k_lm_head_argmax<false>, dim3(lm_blocks), dim3(256), 0, e->stream, e->hn,
+                           (const void *)e->lm_f32, nullptr, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
+                           e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// tok / pos (and n_out = 0) for position pos through its pinned staging slot
+static int set_state(pk_engine *e, int tok, int pos) {
+    pk_dstate &s = e->pin_state[pos];
+    s.tok = tok;
+    s.pos = pos;
+    s.n_out = 0;
+    s.next = 0;
+    PK_HIP(hipMemcpyAsync(e->dstate, &s, sizeof(s), hipMemcpyHostToDevice, e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos, float *out_dev) {
+    PK_CHECK(e && x_dev && out_dev, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(layer >= 0 && layer < c->n_layers, PK_ERR_ARG, "layer %d out of range", layer);
+    PK_CHECK(e->L[layer].have_attn, PK_ERR_MISSING, "layer %d: attention weights not loaded", layer);
+    PK_CHECK(pos >= 0, PK_ERR_ARG, "pos %d", pos);
+    PK_CHECK(pos < c->ctx_len, PK_ERR_CONTEXT_FULL, "pos %d >= context %d", pos, c->ctx_len);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "gqa_attention: host position; not available while capturing");
+    PK_TRY(decode_reserve(e));
+    PK_TRY(set_state(e, 0, pos));
+    PK_HIP(hipMemcpyAsync(e->hn, x_dev, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
+    PK_HIP(hipMemsetAsync(e->h, 0, (size_t)c->hidden * 4, e->stream));
+    PK_TRY(attention_layer(e, layer));               // h = 0 + attn(x)
+    PK_HIP(hipMemcpyAsync(out_dev, e->h, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host, float *logits_dev) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(pos >= 0, PK_ERR_ARG, "pos %d", pos);
+    PK_CHECK(pos < e->c.ctx_len, PK_ERR_CONTEXT_FULL, "pos %d >= context %d", pos, e->c.ctx_len);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "forward_token: use pk_generate inside graphs");
+    PK_TRY(check_model(e));
+    PK_TRY(decode_reserve(e));
+    PK_TRY(set_state(e, tok, pos));
+    PK_TRY(decode_step(e, logits_dev, nullptr, 0));
+    if (next_host) {
+        pk_dstate s{};
+        PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
+        PK_HIP(hipStreamSynchronize(e->stream));
+        *next_host = s.next;
+    }
+    return PK_OK;
+}
+
+extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *next_host) {
+    PK_CHECK(e && ids && n > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(pos_base >= 0 && pos_base + n <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
+             "positions %d..%d exceed context %d", pos_base, pos_base + n - 1, e->c.ctx_len);
+    PK_TRY(check_model(e));
+    PK_TRY(decode_reserve(e));
+    for (int i = 0; i < n; ++i) {
+        PK_TRY(set_state(e, ids[i], pos_base + i));
+        PK_TRY(decode_step(e, nullptr, nullptr, 0));
+    }
+    pk_dstate s{};
+    PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    if (next_host) *next_host = s.next;
+    return PK_OK;
+}
+
+// Greedy generation: prompt through the step graph (token overridden per
+// position), then n_steps decode steps replayed from the same graph with the
+// token and position carried on the device.
+extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, int n_steps, int32_t *out) {
+    PK_CHECK(e && prompt && out && n_prompt > 0 && n_steps >= 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(n_prompt + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
+             "%d prompt + %d steps exceed context %d", n_prompt, n_steps, e->c.ctx_len);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "generate: not available while capturing");
+    PK_TRY(check_model(e));
+    PK_TRY(decode_reserve(e));
+    int32_t *out_dev = nullptr;
+    PK_TRY(pk_dev_alloc(e, (void **)&out_dev, (int64_t)(n_steps + 1) * 4));
+    int rc = PK_OK;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    do {
+        if ((rc = set_state(e, prompt[0], 0)) != PK_OK) break;
+        // capture one step (writes the next token into the output list)
+        if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { rc = PK_ERR_HIP; break; }
+        e->capturing = true;
+        rc = decode_step(e, nullptr, out_dev, n_steps + 1);
+        e->capturing = false;
+        hipError_t hr = hipStreamEndCapture(e->stream, &graph);
+        if (rc != PK_OK) break;
+        if (hr != hipSuccess || hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+            pk_set_error("generate: graph capture failed"); rc = PK_ERR_HIP; break;
+        }
+        // prompt: each position with its own token; n_out counts from the last one
+        for (int i = 0; i < n_prompt && rc == PK_OK; ++i) {
+            rc = set_state(e, prompt[i], i);
+            if (rc == PK_OK && hipGraphLaunch(exec, e->stream) != hipSuccess) rc = PK_ERR_HIP;
+        }
+        // decode: the graph feeds itself (tok = last argmax, pos += 1)
+        for (int i = 0; i < n_steps - 1 && rc == PK_OK; ++i)
+            if (hipGraphLaunch(exec, e->stream) != hipSuccess) rc = PK_ERR_HIP;
+        if (rc != PK_OK) { pk_set_error("generate: launch failed"); break; }
+        if (n_steps > 0 &&
+            hipMemcpyAsync(out, out_dev, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess) {
+            rc = PK_ERR_HIP; break;
+        }
+        if (hipStreamSynchronize(e->stream) != hipSuccess) { rc = PK_ERR_HIP; break; }
+    } while (0);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    (void)hipStreamSynchronize(e->stream);
+    pk_dev_free(e, out_dev);
+    e->device_bytes -= (int64_t)(n_steps + 1) * 4;
+    return rc;
+}
+
+// Timed decode: n_steps replays of the step graph from (tok, pos); the
+// caller brackets the call with events. Returns tokens into out (host).
+extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out) {
+    PK_CHECK(e && out && n_steps > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(pos + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL, "positions exceed context");
+    PK_TRY(check_model(e));
+    PK_TRY(decode_reserve(e));
+    if (!e->step_exec) {
+        int32_t *od = nullptr;
+        PK_TRY(pk_dev_alloc(e, (void **)&od, (int64_t)e->c.ctx_len * 4));
+        e->step_out = od;
+        hipGraph_t g = nullptr;
+        PK_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
+        e->capturing = true;
+        int rc = decode_step(e, nullptr, e->step_out, e->c.ctx_len);
+        e->capturing = false;
+        hipError_t hr = hipStreamEndCapture(e->stream, &g);
+        PK_TRY(rc);
+        PK_HIP(hr);
+        PK_HIP(hipGraphInstantiate(&e->step_exec, g, nullptr, nullptr, 0));
+        (void)hipGraphDestroy(g);
+    }
+    PK_TRY(set_state(e, tok, pos));
+    for (int i = 0; i < n_steps; ++i) PK_HIP(hipGraphLaunch(e->step_exec, e->stream));
+    PK_HIP(hipMemcpyAsync(out, e->step_out, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
 }

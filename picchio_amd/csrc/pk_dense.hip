@@ -16,10 +16,15 @@ __device__ __forceinline__ double pk_wave_sum_d(double v) {
 }
 
 // ───────────────────────── fp32 GEMV ─────────────────────────
-// y[s][o] = x[s] . W[o] (+ bias[o]), matmul_f32 (quant.h:117-148). One wave
-// per row; lanes stride the row in float4 so each load instruction reads
-// 1 KiB contiguous. fp32 sum in tree order (not the reference's 8-lane
-// order: within 1e-6 relative, checked against the oracle at 1e-4).
+// y[s][o] = x[s] . W[o] (+ bias[o]), matmul_f32 (quant.h:117-148). fp32 sum
+// in a fixed tree order (not the reference's 8-lane order: within 1e-6
+// relative, checked against the oracle). Every lane issues its loads for a
+// chunk before the FMAs that consume them, so a row costs one or two memory
+// round trips rather than one per float4.
+constexpr int GEMV_U = 4;           // float4 per lane per chunk
+
+// Large O: one wave per RPW rows, lanes stride the row in float4 (each load
+// instruction reads 1 KiB contiguous).
 template <int RPW>
 __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const float *__restrict__ x,
                                                   const float *__restrict__ W,
@@ -30,30 +35,40 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
     const int s = blockIdx.y;
     const float *xs = x + (int64_t)s * I;
     const int n4 = I >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
-    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
-    for (int i = lane; i < n4; i += 64) {
-        const float4 xv = x4[i];
+    for (int i0 = lane; i0 < n4; i0 += 64 * GEMV_U) {
+        float4 xv[GEMV_U];
+        pk_f32x4 wv[RPW][GEMV_U];
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-            const int o = row0 + r;
-            if (o < O) {
-                const pk_f32x4 wv = __builtin_nontemporal_load(
-                    reinterpret_cast<const pk_f32x4 *>(W + (int64_t)o * I) + i);
-                acc[r] = __builtin_fmaf(xv.x, wv.x, acc[r]);
-                acc[r] = __builtin_fmaf(xv.y, wv.y, acc[r]);
-                acc[r] = __builtin_fmaf(xv.z, wv.z, acc[r]);
-                acc[r] = __builtin_fmaf(xv.w, wv.w, acc[r]);
+        for (int u = 0; u < GEMV_U; ++u) {
+            const int i = i0 + u * 64;
+            xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                const int o = min(row0 + r, O - 1);
+                wv[r][u] = i < n4 ? __builtin_nontemporal_load(
+                                        reinterpret_cast<const pk_f32x4 *>(W + (int64_t)o * I) + i)
+                                  : pk_f32x4{0.f, 0.f, 0.f, 0.f};
             }
         }
+#pragma unroll
+        for (int u = 0; u < GEMV_U; ++u)
+#pragma unroll
+            for (int r = 0; r < RPW; ++r) {
+                acc[r] = __builtin_fmaf(xv[u].x, wv[r][u].x, acc[r]);
+                acc[r] = __builtin_fmaf(xv[u].y, wv[r][u].y, acc[r]);
+                acc[r] = __builtin_fmaf(xv[u].z, wv[r][u].z, acc[r]);
+                acc[r] = __builtin_fmaf(xv[u].w, wv[r][u].w, acc[r]);
+            }
     }
     for (int i = (n4 << 2) + lane; i < I; i += 64) {
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
-            const int o = row0 + r;
-            if (o < O) acc[r] = __builtin_fmaf(xs[i], W[(int64_t)o * I + i], acc[r]);
+            const int o = min(row0 + r, O - 1);
+            acc[r] = __builtin_fmaf(xs[i], W[(int64_t)o * I + i], acc[r]);
         }
     }
 #pragma unroll
@@ -64,15 +79,58 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
     }
 }
 
+// Small O: one workgroup per row, 256 threads split the row.
+__device__ __forceinline__ float pk_row_dot_block(const float *__restrict__ xs,
+                                                  const float *__restrict__ w, int I, float *red) {
+    const int n4 = I >> 2;
+    const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    float acc = 0.0f;
+    for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
+        float4 xv[GEMV_U], wv[GEMV_U];
+#pragma unroll
+        for (int u = 0; u < GEMV_U; ++u) {
+            const int i = i0 + u * 256;
+            xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            wv[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < GEMV_U; ++u) {
+            acc = __builtin_fmaf(xv[u].x, wv[u].x, acc);
+            acc = __builtin_fmaf(xv[u].y, wv[u].y, acc);
+            acc = __builtin_fmaf(xv[u].z, wv[u].z, acc);
+            acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
+        }
+    }
+    for (int i = (n4 << 2) + threadIdx.x; i < I; i += 256) acc = __builtin_fmaf(xs[i], w[i], acc);
+    acc = pk_wave_sum(acc);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+__global__ __launch_bounds__(256) void k_gemv_f32_rows(float *__restrict__ y, const float *__restrict__ x,
+                                                       const float *__restrict__ W,
+                                                       const float *__restrict__ bias, int S, int I, int O) {
+    __shared__ float red[4];
+    const int o = blockIdx.x, s = blockIdx.y;
+    const float v = pk_row_dot_block(x + (int64_t)s * I, W + (int64_t)o * I, I, red);
+    if (threadIdx.x == 0) y[(int64_t)s * O + o] = bias ? v + bias[o] : v;
+}
+
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
                        int S, int I, int O, hipStream_t st) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv f32: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0,
              PK_ERR_UNSUPPORTED, "gemv f32: needs 16-byte aligned rows (I=%d)", I);
-    constexpr int RPW = 2;
-    const int rows_per_block = 4 * RPW;
-    hipLaunchKernelGGL((k_gemv_f32<RPW>), dim3((O + rows_per_block - 1) / rows_per_block, S),
-                       dim3(256), 0, st, y, x, W, bias, S, I, O);
+    if (O <= 2048) {
+        hipLaunchKernelGGL(k_gemv_f32_rows, dim3(O, S), dim3(256), 0, st, y, x, W, bias, S, I, O);
+    } else {
+        constexpr int RPW = 2;
+        const int rows_per_block = 4 * RPW;
+        hipLaunchKernelGGL((k_gemv_f32<RPW>), dim3((O + rows_per_block - 1) / rows_per_block, S),
+                           dim3(256), 0, st, y, x, W, bias, S, I, O);
+    }
     PK_HIP(hipGetLastError());
     return PK_OK;
 }
@@ -223,15 +281,78 @@ __global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E,
     }
 }
 
+// Router + top-k in one launch: block e computes logit e (one row per
+// block), stores it device-coherently and counts itself in; the last block
+// to arrive runs top-k + softmax (same arithmetic as k_topk_softmax) and
+// re-arms the counter. (picchio.c:1316-1355)
+__device__ __forceinline__ void pk_st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float pk_ld_dev(float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x, const float *__restrict__ R,
+                                                     const float *__restrict__ b, int E, int D, int K,
+                                                     float routed_scale, float *logits, int32_t *sel,
+                                                     float *w_scaled, float *w_soft, uint32_t *counter) {
+    __shared__ float red[4];
+    __shared__ int last;
+    const int e = blockIdx.x;
+    const float v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
+    if (threadIdx.x == 0) {
+        pk_st_dev(logits + e, v + b[e]);
+        __builtin_amdgcn_s_waitcnt(0);
+        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               (uint32_t)(E - 1);
+    }
+    __syncthreads();
+    if (!last || threadIdx.x >= 64) return;
+    const int lane = threadIdx.x;
+    float v0 = lane < E ? pk_ld_dev(logits + lane) : -INFINITY;
+    float v1 = lane + 64 < E ? pk_ld_dev(logits + lane + 64) : -INFINITY;
+    bool t0 = lane >= E, t1 = lane + 64 >= E;
+    __shared__ int ci[16];
+    __shared__ float cv[16];
+    for (int k = 0; k < K; ++k) {
+        float bv = -1e30f;
+        int bi = 0x7fffffff;
+        if (!t0 && v0 > bv) { bv = v0; bi = lane; }
+        if (!t1 && v1 > bv) { bv = v1; bi = lane + 64; }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) {
+            const float ov = __shfl_xor(bv, o, 64);
+            const int oi = __shfl_xor(bi, o, 64);
+            if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
+        }
+        if (lane == 0) { ci[k] = bi; cv[k] = bv; }
+        if (bi == lane) t0 = true;
+        if (bi == lane + 64) t1 = true;
+    }
+    if (lane == 0) {
+        float m = -1e30f;
+        for (int k = 0; k < K; ++k) if (cv[k] > m) m = cv[k];
+        float s = 0.0f;
+        for (int k = 0; k < K; ++k) { cv[k] = expf(cv[k] - m); s += cv[k]; }
+        for (int k = 0; k < K; ++k) {
+            const float p = cv[k] / s;
+            sel[k] = ci[k];
+            if (w_soft) w_soft[k] = p;
+            w_scaled[k] = p * routed_scale;
+        }
+        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D, int K,
                           float routed_scale, float *logits, int32_t *sel, float *w_scaled,
                           float *w_soft, uint32_t *counter, hipStream_t st) {
-    (void)counter;
     PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
              "router: E=%d K=%d outside 1..128 / 1..16", E, K);
-    PK_TRY(pk_launch_gemv_f32(logits, x, R, b, 1, D, E, st));
-    hipLaunchKernelGGL(k_topk_softmax, dim3(1), dim3(64), 0, st, logits, E, K, routed_scale,
-                       sel, w_scaled, w_soft);
+    PK_CHECK(((uintptr_t)R & 15) == 0 && ((uintptr_t)x & 15) == 0 && (D & 3) == 0, PK_ERR_UNSUPPORTED,
+             "router: needs 16-byte aligned rows");
+    hipLaunchKernelGGL(k_router_topk, dim3(E), dim3(256), 0, st, x, R, b, E, D, K, routed_scale, logits,
+                       sel, w_scaled, w_soft, counter);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

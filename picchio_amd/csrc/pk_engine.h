@@ -12,6 +12,18 @@ struct pk_layer_dev {
     bool have_attn = false, have_router = false;
 };
 
+// Decode state in device memory: the step reads tok/pos and its argmax
+// writes next, appends to the output list (n_out) and advances pos.
+struct pk_dstate {
+    int32_t tok, pos, n_out, next;
+};
+
+// counters[] layout (uint32, zero-initialised, re-armed by their users)
+constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
+constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
+constexpr int PK_CTR_LM_HEAD = 2048;      // lm_head+argmax arrivals
+constexpr int PK_CTR_N = 4096;
+
 struct pk_engine {
     pk_cfg c{};
     int device = 0;
@@ -49,6 +61,15 @@ struct pk_engine {
     uint32_t *counters = nullptr;
 
     bool capturing = false;                  // inside pk_capture_begin/end
+
+    // decode step (pk_decode.hip)
+    bool dec_ready = false;
+    pk_dstate *dstate = nullptr;              // device
+    pk_dstate *pin_state = nullptr;           // pinned host staging [ctx_len]
+    float *lm_bval = nullptr;                 // lm_head block maxima
+    int32_t *lm_bidx = nullptr;
+    hipGraphExec_t step_exec = nullptr;       // captured decode step (pk_decode_replay)
+    int32_t *step_out = nullptr;
 
     // opt-in per-kernel timing (pk_engine_profile)
     bool prof = false;

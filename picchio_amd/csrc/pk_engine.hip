@@ -147,7 +147,7 @@ static void engine_free(pk_engine *e) {
                     e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
                     e->b_eo, e->b_sel, e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
-                    e->s_sel, e->s_w};
+                    e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -158,6 +158,8 @@ static void engine_free(pk_engine *e) {
         delete[] e->L;
     }
     free(e->expert_ready);
+    if (e->step_exec) (void)hipGraphExecDestroy(e->step_exec);
+    if (e->pin_state) (void)hipHostFree(e->pin_state);
     if (e->prof_ev) {
         for (int i = 0; i < 2 * pk_engine::PROF_CAP; ++i) (void)hipEventDestroy(e->prof_ev[i]);
         delete[] e->prof_ev;
@@ -200,8 +202,8 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->act, (int64_t)K * half * 4);
     ALLOC(e->eo, (int64_t)K * D * 4);
     ALLOC(e->argmax_out, 64);
-    ALLOC(e->counters, 4096);
-    PK_HIP(hipMemsetAsync(e->counters, 0, 4096, e->stream));
+    ALLOC(e->counters, PK_CTR_N * 4);
+    PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
 }
@@ -698,9 +700,10 @@ static int check_layer_experts(pk_engine *e, int layer) {
 }
 
 // FFN of the experts listed in sel (device, n entries): act <- SwiGLU(gate_up x + b),
-// eo <- down act + b.
+// eo <- down act + b; with comb, the down launch also combines the n outputs
+// (weights comb->w) into comb->out (+ residual).
 static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, const float *x,
-                       int64_t x_stride, float *act, float *eo) {
+                       int64_t x_stride, float *act, float *eo, const pk_combine_args *comb) {
     const pk_cfg *c = &e->c;
     pk_i4_items gu = expert_items(e, layer, false);
     gu.slots = sel_dev;
@@ -717,7 +720,8 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     dn.y = eo; dn.y_stride = c->hidden;
     dn.n_items = n;
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
-    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
+    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, comb ? PK_EPI_COMBINE : PK_EPI_PLAIN, 0.f, 0.f, comb,
+                             e->stream));
     PK_TRY(pk_prof_end(e, ps));
     return PK_OK;
 }
@@ -729,13 +733,15 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
-                                 e->counters, e->stream));
+                                 e->counters + PK_CTR_ROUTER, e->stream));
     PK_TRY(pk_prof_end(e, ps));
-    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, x_dev, 0, e->act, e->eo));
-    ps = pk_prof_begin(e, PK_PROF_COMBINE);
-    PK_TRY(pk_launch_combine(out_dev, e->eo, e->w_scaled, c->topk, c->hidden, residual, res_out,
-                             e->stream));
-    PK_TRY(pk_prof_end(e, ps));
+    // the down launch combines the top-k outputs (routing order) + residual
+    pk_combine_args cb{};
+    cb.w = e->w_scaled;
+    cb.out = residual ? res_out : out_dev;
+    cb.residual = residual;
+    cb.counters = e->counters + PK_CTR_COMBINE;
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, x_dev, 0, e->act, e->eo, &cb));
     return PK_OK;
 }
 
@@ -767,7 +773,7 @@ extern "C" int pk_expert_apply(pk_engine *e, int layer, int eid, const float *x_
     PK_CHECK(!e->capturing, PK_ERR_ARG, "expert_apply: not available while capturing a graph");
     // a one-entry slot list in device scratch (sel[0] is free outside moe_forward)
     PK_HIP(hipMemcpyAsync(e->sel, &eid, 4, hipMemcpyHostToDevice, e->stream));
-    PK_TRY(experts_ffn(e, layer, e->sel, 1, x_dev, 0, e->act, e->eo));
+    PK_TRY(experts_ffn(e, layer, e->sel, 1, x_dev, 0, e->act, e->eo, nullptr));
     PK_TRY(pk_launch_axpy(dst_dev, e->eo, w, c->hidden, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -808,7 +814,7 @@ extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev,
                                 nullptr, e->stream));
     for (int t = 0; t < T; ++t) {
         PK_TRY(experts_ffn(e, layer, e->b_sel + (int64_t)t * K, K, x_dev + (int64_t)t * D, 0,
-                           e->b_act, e->b_eo));
+                           e->b_act, e->b_eo, nullptr));
         PK_TRY(pk_launch_combine(out_dev + (int64_t)t * D, e->b_eo, e->b_w + (int64_t)t * K, K, D,
                                  nullptr, nullptr, e->stream));
     }

@@ -23,7 +23,7 @@
 // scales meet in LDS; wave 0 folds the groups of its 64 rows in order.
 template <int NW, int GPW, int EPI>
 __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int NG,
-                                                     float lim, float alpha) {
+                                                     float lim, float alpha, pk_combine_args cb) {
     extern __shared__ float lds[];            // part[NG][64], scl[NG][64]
     float *part = lds;
     float *scl = lds + NG * 64;
@@ -73,6 +73,32 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     if constexpr (EPI == PK_EPI_SWIGLU) {
         const float up = __shfl_down(acc, 1, 64);
         if ((lane & 1) == 0 && row + 1 < O) y[row >> 1] = pk_swiglu(acc, up, lim, alpha);
+    } else if constexpr (EPI == PK_EPI_COMBINE) {
+        // moe_forward's accumulation (picchio.c:1387, :1445-1454) fused: each
+        // item's rows go out device-coherently; the last item to finish this
+        // row block adds them up in routing order, out = fma(w_k, eo_k, out),
+        // then the residual (forward_token, picchio.c:1716), and re-arms the
+        // block's arrival counter.
+        if (row < O)
+            __hip_atomic_store(y + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __builtin_amdgcn_s_waitcnt(0);
+        uint32_t arrived = 0;
+        if (lane == 0)
+            arrived = __hip_atomic_fetch_add(cb.counters + rb, 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+        arrived = __shfl(arrived, 0, 64);
+        if (arrived != (uint32_t)(it.n_items - 1)) return;
+        if (row < O) {
+            float o = 0.0f;
+            for (int k = 0; k < it.n_items; ++k)
+                o = __builtin_fmaf(cb.w[k],
+                                   __hip_atomic_load(it.y + (int64_t)k * it.y_stride + row,
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                   o);
+            cb.out[row] = cb.residual ? cb.residual[row] + o : o;
+        }
+        if (lane == 0)
+            __hip_atomic_store(cb.counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     } else {
         if (row < O) y[row] = acc;
     }
@@ -80,7 +106,12 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
 
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
                       float lim, float alpha, const pk_combine_args *comb, hipStream_t st) {
-    (void)comb;
+    pk_combine_args cb{};
+    if (epilogue == PK_EPI_COMBINE) {
+        PK_CHECK(comb && comb->w && comb->out && comb->counters, PK_ERR_ARG, "combine: missing buffers");
+        PK_CHECK(sh.RB <= 1024, PK_ERR_UNSUPPORTED, "combine: %d row blocks", sh.RB);
+        cb = *comb;
+    }
     PK_CHECK(sh.NG > 0 && sh.RB > 0 && it.n_items > 0, PK_ERR_ARG, "i4 gemv: empty shape");
     PK_CHECK(sh.NG <= 128, PK_ERR_UNSUPPORTED, "i4 gemv: I=%d above 8192", sh.I);
     const dim3 grid(sh.RB, it.n_items);
@@ -89,10 +120,13 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
     constexpr int NW = 15, GPW = 3;
     if (epilogue == PK_EPI_SWIGLU)
         hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_SWIGLU>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha);
+                           it, sh.O, sh.NG, lim, alpha, cb);
+    else if (epilogue == PK_EPI_COMBINE)
+        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_COMBINE>), grid, dim3(NW * 64), lds, st,
+                           it, sh.O, sh.NG, lim, alpha, cb);
     else
         hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_PLAIN>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha);
+                           it, sh.O, sh.NG, lim, alpha, cb);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

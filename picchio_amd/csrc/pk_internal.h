@@ -116,10 +116,10 @@ struct pk_i4_items {
 enum pk_i4_epilogue { PK_EPI_PLAIN = 0, PK_EPI_SWIGLU = 1, PK_EPI_COMBINE = 2 };
 
 struct pk_combine_args {
-    const float *w;           // [n_items] routing weights (already * routed_scale)
+    const float *w;           // [n_items] routing weights (already * routed_scale), device
     float *out;               // [O] combined output
     const float *residual;    // optional: out = residual + combine
-    uint32_t *counters;       // [RB] zero-initialised arrival counters
+    uint32_t *counters;       // [RB] zero-initialised arrival counters (re-armed after use)
 };
 
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
