@@ -33,7 +33,43 @@ D, INTER, HALF, E, K = 2880, 5760, 2880, 32, 4
 EXPERT_BYTES = 12441600 + 1555200 + 34560          # packed + scales + biases
 ROUTER_BYTES = E * D * 4 + E * 4
 TOKEN_BYTES = K * EXPERT_BYTES + ROUTER_BYTES + 2 * D * 4      # 56,517,248
-GATE_UP_LAUNCH_BYTES = K * (INTER * D // 2 + INTER * (D // 64) * 4 + INTER * 4) + D * 4 + K * HALF * 4
+
+# HBM bytes per 4-expert gate_up launch measured by rocprofv3 --pmc (profiles/
+# k_i4_gemv_gate_up_moe_config1.txt): FETCH_SIZE 18406.14 KiB x 2.000 +
+# WRITE_SIZE 45.00 KiB x 1.000, the factors being what the two counters read
+# for a plain copy kernel over 1 GiB.
+GATE_UP_TRAFFIC = 37740032
+
+
+def gate_up_bytes(n):
+    """Algorithmic bytes of one gate_up launch over n experts: packed nibbles,
+    scales, bias of each, x in, SwiGLU activations out."""
+    return n * (INTER * D // 2 + INTER * (D // 64) * 4 + INTER * 4) + D * 4 + n * HALF * 4
+
+
+def down_bytes(n):
+    """One down launch over n experts: weights + scales + bias, activations in, outputs out."""
+    return n * (D * HALF // 2 + D * (HALF // 64) * 4 + D * 4) + n * HALF * 4 + n * D * 4
+
+
+def replay_ms(eng, ev0, ev1, n, enqueue, reps=3):
+    """Mean duration of one of n launches captured in a graph and replayed
+    back to back (events on the engine stream around each replay)."""
+    eng.capture_begin()
+    for t in range(n):
+        enqueue(t)
+    g = eng.capture_end()
+    eng.graph_launch(g)
+    eng.sync()
+    tot = 0.0
+    for _ in range(reps):
+        ev0.record(eng.stream)
+        eng.graph_launch(g)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        tot += ev0.elapsed_time(ev1)
+    eng.graph_destroy(g)
+    return tot / (reps * n)
 
 
 def token_inputs(n, seed):
@@ -87,6 +123,9 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=400)
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="after the timed region, run a plain read+write kernel over this many "
+                         "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--mode", choices=["seq", "kernels"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "
@@ -149,6 +188,7 @@ def main():
         roof_bytes = S * TOKEN_BYTES
         roof_ms = kern_ms
         roof_kernel = "k_moe_seq (persistent: router+top-4+gate_up+SwiGLU+down+combine, chained steps)"
+        traffic = None
         extra = {"unchained_us_per_token": round(ms_nochain / S * 1e3, 3),
                  "unchained_gbps": round(S * TOKEN_BYTES / (ms_nochain * 1e-3) / 1e9, 1)}
     else:
@@ -170,26 +210,43 @@ def main():
         ev1.record(eng.stream)
         ev1.synchronize()
         ms = ev0.elapsed_time(ev1)
-        # per-kernel durations: event brackets per launch, queue pre-filled
-        # behind a bounded idle kernel so host launch latency stays outside
-        n_prof = min(args.profile_tokens, n_tok)
-        eng.profile(True)
-        eng.stall(60000)
-        for t in range(n_prof):
-            enqueue(t)
-        eng.sync()
-        prof = {}
-        for name, kid in (("gate_up", pa.PROF_EXPERT_GATE_UP), ("down", pa.PROF_EXPERT_DOWN),
-                          ("router", pa.PROF_ROUTER), ("combine", pa.PROF_COMBINE)):
-            tot, cnt = eng.profile_read(kid)
-            prof[name] = tot / max(cnt, 1)
-        eng.profile(False)
         eng.graph_destroy(g_warm)
         eng.graph_destroy(g_run)
-        roof_bytes = GATE_UP_LAUNCH_BYTES
-        roof_ms = prof["gate_up"]
-        roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up, 4 experts/launch)"
-        extra = {}
+        # The dominant kernel alone: each token's gate_up launch (4 experts of
+        # its layer copy, the same k_i4_gemv<SWIGLU> the MoE step runs)
+        # replayed back to back from a graph; HIP events on the engine stream
+        # around the replay / launches = the mean launch duration.
+        n_prof = min(args.profile_tokens, S)
+        rng = np.random.default_rng(7)
+        eids = np.stack([rng.choice(E, K, replace=False) for _ in range(n_prof)]).astype(np.int32)
+        eids_d = eng.to_dev(eids)
+        act = eng.empty((E, HALF), torch.float32)
+        eo = eng.empty((E, D), torch.float32)
+        all_e = eng.to_dev(np.arange(E, dtype=np.int32))
+        gu_ms = replay_ms(eng, ev0, ev1, n_prof,
+                          lambda t: eng.expert_gate_up(t % L, eids_d[t], xd[t], act))
+        dn_ms = replay_ms(eng, ev0, ev1, n_prof,
+                          lambda t: eng.expert_down(t % L, eids_d[t], act, eo))
+        # streaming shape: all 32 experts of a layer copy in one gate_up launch
+        st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act))
+        prof = {"gate_up": gu_ms, "down": dn_ms, "gate_up_32_experts": st_ms}
+        roof_bytes = gate_up_bytes(K)
+        roof_ms = gu_ms
+        roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up + bias + SwiGLU, 4 experts/launch)"
+        traffic = GATE_UP_TRAFFIC
+        extra = {"down_gbps": round(down_bytes(K) / (dn_ms * 1e-3) / 1e9, 1),
+                 "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
+                 "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
+                                                      / HBM_PEAK_GBPS, 4)}
+
+    if args.calib_copy_mib:
+        n = args.calib_copy_mib << 18                       # fp32 elements
+        src = torch.ones(n, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            torch.neg(src, out=dst)                         # reads n*4 B, writes n*4 B
+        torch.cuda.synchronize()
+        del src, dst
 
     ms_tok = ms / S
     gbps = TOKEN_BYTES / (ms_tok * 1e-3) / 1e9
@@ -224,7 +281,7 @@ def main():
                    "mode": args.mode, "chained": True,
                    "kernel_us": {k: round(v * 1e3, 3) for k, v in prof.items()}, **extra},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
                      "mean_us": round(roof_ms * 1e3, 3)},
         "cpu_baseline": cpu,

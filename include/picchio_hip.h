@@ -156,6 +156,18 @@ int pk_matmul_qt(pk_engine *e, float *y_dev, const float *x_dev, const pk_qt *w,
 int pk_expert_apply(pk_engine *e, int layer, int eid, const float *x_dev,
                     float *dst_dev, float w);
 
+/* The two expert matmul_qt call sites of moe_forward, each batched over n
+ * experts of one layer in a single launch (eids_dev: n device int32 ids):
+ *  gate_up (picchio.c:1399, bias :1400-1402, clamped SwiGLU :1415-1424):
+ *    act_dev[n][moe_inter/2] = SwiGLU(gate_up_k · x_dev + b)
+ *  down (picchio.c:1431, bias :1432-1434):
+ *    eo_dev[n][hidden] = down_k · act_dev[k] + b
+ * Same bits as the matching steps of pk_moe_forward. */
+int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                      const float *x_dev, float *act_dev);
+int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                   const float *act_dev, float *eo_dev);
+
 /* moe_forward (picchio.c:1309-1466): out_dev = Σ_k (w_k·routed_scale)·expert_k(x).
  * Optional host outputs: sel_host[topk], w_host[topk] (softmaxed weights) —
  * passing either forces a stream sync. */

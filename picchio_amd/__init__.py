@@ -111,6 +111,8 @@ def lib():
         "pk_qt_free": (C.c_int, [vp, vp]),
         "pk_matmul_qt": (C.c_int, [vp, vp, vp, vp, C.c_int]),
         "pk_expert_apply": (C.c_int, [vp, C.c_int, C.c_int, vp, vp, f32]),
+        "pk_expert_gate_up": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
+        "pk_expert_down": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
         "pk_moe_forward": (C.c_int, [vp, C.c_int, vp, vp, vp, vp]),
         "pk_moe_forward_batch": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
         "pk_gqa_attention": (C.c_int, [vp, C.c_int, vp, C.c_int, vp]),
@@ -324,6 +326,14 @@ class Engine:
 
     def expert_apply(self, layer, eid, x_dev, dst_dev, w):
         check(self.L.pk_expert_apply(self.h, layer, eid, ptr(x_dev), ptr(dst_dev), w))
+
+    def expert_gate_up(self, layer, eids_dev, x_dev, act_dev):
+        check(self.L.pk_expert_gate_up(self.h, layer, ptr(eids_dev), eids_dev.numel(),
+                                       ptr(x_dev), ptr(act_dev)))
+
+    def expert_down(self, layer, eids_dev, act_dev, eo_dev):
+        check(self.L.pk_expert_down(self.h, layer, ptr(eids_dev), eids_dev.numel(),
+                                    ptr(act_dev), ptr(eo_dev)))
 
     def qt_upload(self, fmt, data, scales, O, I, block_size=0):
         q = PkQtHost(fmt, data.ctypes.data, scales.ctypes.data if scales is not None else None,

@@ -779,6 +779,46 @@ extern "C" int pk_expert_apply(pk_engine *e, int layer, int eid, const float *x_
     return PK_OK;
 }
 
+static int check_expert_batch(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                              const void *in, const void *out) {
+    const pk_cfg *c = &e->c;
+    PK_CHECK(eids_dev && in && out, PK_ERR_ARG, "null argument");
+    PK_CHECK(n > 0 && n <= c->n_experts, PK_ERR_ARG, "%d experts per launch (1..%d)", n, c->n_experts);
+    PK_TRY(check_layer_experts(e, layer));
+    return PK_OK;
+}
+
+extern "C" int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                                 const float *x_dev, float *act_dev) {
+    PK_CHECK(e, PK_ERR_ARG, "null engine");
+    PK_TRY(check_expert_batch(e, layer, eids_dev, n, x_dev, act_dev));
+    const pk_cfg *c = &e->c;
+    pk_i4_items gu = expert_items(e, layer, false);
+    gu.slots = eids_dev;
+    gu.x = x_dev; gu.x_stride = 0;
+    gu.y = act_dev; gu.y_stride = c->moe_inter / 2;
+    gu.n_items = n;
+    int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
+    PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
+                             nullptr, e->stream));
+    return pk_prof_end(e, ps);
+}
+
+extern "C" int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                              const float *act_dev, float *eo_dev) {
+    PK_CHECK(e, PK_ERR_ARG, "null engine");
+    PK_TRY(check_expert_batch(e, layer, eids_dev, n, act_dev, eo_dev));
+    const pk_cfg *c = &e->c;
+    pk_i4_items dn = expert_items(e, layer, true);
+    dn.slots = eids_dev;
+    dn.x = act_dev; dn.x_stride = c->moe_inter / 2;
+    dn.y = eo_dev; dn.y_stride = c->hidden;
+    dn.n_items = n;
+    int ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
+    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
+    return pk_prof_end(e, ps);
+}
+
 static int batch_reserve(pk_engine *e, int T) {
     if (T <= e->batch_cap) return PK_OK;
     PK_CHECK(!e->capturing, PK_ERR_ARG, "batch buffers must be sized before capturing a graph");

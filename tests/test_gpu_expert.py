@@ -170,6 +170,31 @@ def test_expert_apply_parity(moe_setup, oracle):
         assert rel_l2(got - dst0, ref - dst0) < 1e-6
 
 
+def test_expert_gate_up_down_batched(moe_setup, oracle):
+    """gate_up and down over three experts in one launch each give the same
+    bits as expert_apply of each expert alone (w = 1 into zeros is exact),
+    and match the oracle's expert FFN."""
+    import torch
+    cfg, model, eng = moe_setup
+    D, H = cfg.hidden, cfg.moe_inter // 2
+    eids = np.array([6, 1, 3], np.int32)
+    x = _token_x(oracle, cfg, 2024)
+    xd = eng.to_dev(x)
+    act = eng.empty((3, H), torch.float32)
+    eo = eng.empty((3, D), torch.float32)
+    ed = eng.to_dev(eids)
+    eng.expert_gate_up(0, ed, xd, act)
+    eng.expert_down(0, ed, act, eo)
+    got = eng.to_host(eo)
+    for k, eid in enumerate(eids):
+        one = eng.to_dev(np.zeros(D, np.float32))
+        eng.expert_apply(0, int(eid), xd, one, 1.0)
+        assert bits_equal(got[k], eng.to_host(one)), k
+        ref = np.zeros(D, np.float32)
+        oracle.expert_apply(model, 0, int(eid), x, ref, 1.0)
+        assert rel_l2(got[k], ref) < 1e-6
+
+
 def test_moe_forward_parity(moe_setup, oracle):
     import torch
     cfg, model, eng = moe_setup
