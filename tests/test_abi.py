@@ -1,0 +1,117 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point that
+include/picchio_hip.h declares, its structs have the header's layout on the
+Python side, and its argument checks return error codes (no device work)."""
+import ctypes as C
+import os
+import re
+import subprocess
+import tempfile
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "picchio_hip.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(pk_[a-z0-9_]+)\s*\(", src)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    import picchio_amd
+    return picchio_amd.lib()
+
+
+def test_exports_every_declared_symbol(lib):
+    names = declared_functions()
+    assert len(names) >= 30
+    missing = [n for n in names if not hasattr(lib, n)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_declared_symbols():
+    import picchio_amd
+    src = open(picchio_amd.__file__).read()
+    bound = set(re.findall(r'"(pk_[a-z0-9_]+)"', src))
+    assert set(declared_functions()) <= bound | {"pk_version", "pk_last_error"}
+
+
+def _c_layout():
+    prog = r"""
+#include <stdio.h>
+#include <stddef.h>
+#include "picchio_hip.h"
+#define F(T, m) printf(#T " " #m " %zu\n", offsetof(T, m));
+int main(void) {
+  printf("pk_cfg size %zu\n", sizeof(pk_cfg));
+  printf("pk_qt_host size %zu\n", sizeof(pk_qt_host));
+  printf("pk_layer_host size %zu\n", sizeof(pk_layer_host));
+  F(pk_cfg, eps) F(pk_cfg, rope_original_ctx) F(pk_cfg, rope_attn_factor)
+  F(pk_cfg, group_size) F(pk_cfg, lm_head_fmt) F(pk_cfg, layer_type)
+  F(pk_qt_host, data) F(pk_qt_host, s) F(pk_qt_host, O) F(pk_qt_host, block_size)
+  F(pk_layer_host, wq) F(pk_layer_host, wo) F(pk_layer_host, bq) F(pk_layer_host, sinks)
+  F(pk_layer_host, router_bias)
+  return 0;
+}
+"""
+    with tempfile.TemporaryDirectory() as d:
+        c = os.path.join(d, "l.c")
+        open(c, "w").write(prog)
+        exe = os.path.join(d, "l")
+        subprocess.check_call(["gcc", "-I", os.path.join(ROOT, "include"), c, "-o", exe])
+        out = subprocess.check_output([exe], text=True)
+    return {(a, b): int(v) for a, b, v in (l.split() for l in out.splitlines())}
+
+
+def test_struct_layout_matches_header():
+    import picchio_amd as pa
+    lay = _c_layout()
+    assert lay[("pk_cfg", "size")] == C.sizeof(pa.PkCfg)
+    assert lay[("pk_qt_host", "size")] == C.sizeof(pa.PkQtHost)
+    assert lay[("pk_layer_host", "size")] == C.sizeof(pa.PkLayerHost)
+    for (t, m), off in lay.items():
+        if m == "size":
+            continue
+        cls = {"pk_cfg": pa.PkCfg, "pk_qt_host": pa.PkQtHost, "pk_layer_host": pa.PkLayerHost}[t]
+        assert getattr(cls, m).offset == off, (t, m)
+
+
+def test_version_and_error_strings(lib):
+    assert b"gfx950" in lib.pk_version()
+    assert lib.pk_last_error() is not None
+
+
+def test_null_arguments_are_errors_not_crashes(lib):
+    import picchio_amd as pa
+    h = C.c_void_p()
+    assert lib.pk_engine_create(None, 0, C.byref(h)) == -1
+    assert b"null" in lib.pk_last_error().lower() or lib.pk_last_error()
+    for fn, args in (("pk_moe_forward", [None, 0, None, None, None, None]),
+                     ("pk_forward_token", [None, 0, 0, None, None]),
+                     ("pk_gqa_attention", [None, 0, None, 0, None]),
+                     ("pk_expert_apply", [None, 0, 0, None, None, 1.0]),
+                     ("pk_expert_gate_up", [None, 0, None, 1, None, None]),
+                     ("pk_matmul_qt", [None, None, None, None, 1])):
+        assert getattr(lib, fn)(*args) == -1, fn
+    assert lib.pk_engine_destroy(None) in (0, -1)
+
+
+def test_bad_config_is_rejected(lib):
+    import picchio_amd as pa
+    h = C.c_void_p()
+    for kw in ({"group_size": 32}, {"hidden": 2890}, {"topk": 0}, {"head_dim": 256},
+               {"n_experts": 129}):
+        cfg = pa.gptoss_cfg(n_layers=1, **kw)
+        rc = lib.pk_engine_create(C.byref(cfg), 0, C.byref(h))
+        assert rc in (-1, -4), (kw, rc)
+
+
+def test_rope_attn_factor_default():
+    """picchio.c:380-381: attn_factor = 0.1 * ln(factor) + 1 for factor > 1."""
+    import math
+    import picchio_amd as pa
+    assert abs(pa.gptoss_cfg().rope_attn_factor - (0.1 * math.log(32.0) + 1.0)) < 1e-6
+    assert pa.gptoss_cfg(rope_factor=1.0).rope_attn_factor == 1.0

@@ -107,3 +107,34 @@ def test_context_full_is_an_error(dec_setup):
     with pytest.raises(pa.PkError) as ei:
         eng.forward_token(1, cfg.ctx_len, None)
     assert ei.value.code == -6
+
+
+def test_reference_golden_tiny_model(gpu, oracle):
+    """The GPU path against picchio's own outputs (tests/golden/model_tiny.npz,
+    recorded from the reference build): moe_forward and gqa_attention outputs,
+    and the greedy token stream of forward_token."""
+    import os
+    import torch
+    import picchio_amd as pa
+    from test_oracle import cfg_from, load
+    z = load("model_tiny.npz")
+    cfg = cfg_from(z)
+    model = oracle.model_build(cfg, int(z["seed"]), 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg)
+        D = cfg.hidden
+        od = eng.empty(D, torch.float32)
+        for layer in range(2):
+            for t in range(z["moe_x"].shape[1]):
+                eng.moe_forward(layer, eng.to_dev(z["moe_x"][layer, t]), od)
+                assert rel_l2(eng.to_host(od), z["moe_out"][layer, t]) < REL_L2_TOL, (layer, t)
+        for pos in range(z["att_x"].shape[0]):
+            for layer in range(2):
+                eng.gqa_attention(layer, eng.to_dev(z["att_x"][pos, layer]), pos, od)
+                assert rel_l2(eng.to_host(od), z["att_out"][pos, layer]) < REL_L2_TOL, (pos, layer)
+        got = list(eng.generate([int(v) for v in z["prompt"]], len(z["stream"])))
+        assert got == [int(v) for v in z["stream"]]
+    finally:
+        eng.close()
+        oracle.model_free(model)
