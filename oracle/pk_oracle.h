@@ -11,16 +11,28 @@
  * -ffp-contract=fast): matmuls keep quant.h's 8-lane accumulators and hsum256
  * tree, and every `a += b * c` the compiler contracts is an explicit fmaf here.
  *
- * Parity status per function (what pins it):
- *   po_quantize_int4_gs    closed forms + exhaustive small cases (tests/)
- *   po_quantize_int8_rows  closed forms (tests/)
- *   po_quantize_rows_i4    golden vectors from quant.h (tests/golden)
- *   po_matmul_*            golden vectors from quant.h (bit-exact)
- *   po_rmsnorm/po_softmax  golden vectors + KATs from picchio.c self-test
- *   po_swiglu_clamped      golden vectors from picchio.c (moe_forward)
- *   po_moe_forward/po_expert_apply   golden vectors from picchio.c
- *   po_gqa_attention/rope  golden vectors from picchio.c
- *   po_forward_token/po_forward_prefill  golden token streams from picchio.c
+ * Parity status per function (what pins it; all checks in tests/test_oracle.py,
+ * golden vectors recorded from picchio's own C build by tests/golden/make_golden.py):
+ *   po_quantize_int4_gs    convert.py's algorithm restated in numpy (bit-equal on
+ *                          ragged, odd, zero and sub-1e-8 groups) + known answers
+ *                          for ties / zero groups; nibble decode exhaustive
+ *   po_quantize_int8_rows  convert.py's algorithm restated in numpy + known answers
+ *   po_quantize_rows_i4    golden vectors (quant.h) + the self-test KAT
+ *   po_matmul_*            golden vectors (quant.h), bit-identical; float64 brute force
+ *   po_rmsnorm/po_softmax  golden vectors + the self-test KATs
+ *   po_swiglu_clamped      float64 closed form incl. both clamps; inside moe golden
+ *   po_moe_forward/po_expert_apply   golden vectors (picchio.c) + float64
+ *                          restatement of router, top-k tie rule, softmax, combine
+ *   po_gqa_attention/rope/yarn  golden vectors + float64 restatement (window, sinks,
+ *                          sink = -inf reducing to plain softmax, YaRN closed form)
+ *   po_forward_token/po_prefill_tokens  golden token streams (picchio.c)
+ *   po_model_build / po_fill_normal     the synthetic-input generator (not a
+ *                          reference function); the GPU generator is checked
+ *                          against it bit-for-bit in the GPU tests.
+ * Nothing here is "parity unpinned". Transcendentals (expf, cosf, sinf, powf,
+ * logf) are glibc's, as in the reference build, so the oracle matches the
+ * reference bit-for-bit on this image; the GPU path's own transcendentals are
+ * compared within relative L2 1e-4 instead.
  */
 #ifndef PK_ORACLE_H
 #define PK_ORACLE_H

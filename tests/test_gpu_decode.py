@@ -138,3 +138,37 @@ def test_reference_golden_tiny_model(gpu, oracle):
     finally:
         eng.close()
         oracle.model_free(model)
+
+
+def test_synthetic_build_matches_oracle_model(gpu, oracle):
+    """pk_engine_build_synthetic (generator + INT4 quantizer on the GPU) gives
+    the model po_model_build gives on the CPU for the same seed: MoE outputs
+    match an engine loaded from the oracle's tensors (the device libm may
+    round about one generated weight in 1e9 differently, hence a relative
+    bar rather than bits), and logits match the oracle within the fp32 bar."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=4, ctx_len=32, vocab=512)
+    model = oracle.model_build(cfg, 31, 0)
+    a, b = pa.Engine(cfg), pa.Engine(cfg)
+    try:
+        a.build_synthetic(31, what=7)
+        upload_model(b, oracle, model, cfg)
+        D = cfg.hidden
+        oa, ob = a.empty(D, torch.float32), b.empty(D, torch.float32)
+        for t in range(4):
+            x = _x(oracle, cfg, 500 + t)
+            a.moe_forward(1, a.to_dev(x), oa)
+            b.moe_forward(1, b.to_dev(x), ob)
+            assert rel_l2(a.to_host(oa), b.to_host(ob)) < 1e-6
+        oracle.model_reset_kv(model)
+        ref = np.empty(cfg.vocab, np.float32)
+        lg = a.empty(cfg.vocab, torch.float32)
+        for pos, tok in enumerate([3, 77, 400, 12]):
+            nref = oracle.forward_token(model, tok, pos, ref.ctypes.data)
+            n = a.forward_token(tok, pos, lg)
+            assert rel_l2(a.to_host(lg), ref) < REL_L2_TOL
+    finally:
+        a.close()
+        b.close()
+        oracle.model_free(model)

@@ -264,6 +264,24 @@ def test_quantizer_known_answers(oracle):
     assert np.all(p[0, 4:] == 0x88) and np.all(p[1] == 0x88)    # zero -> nibble 8
 
 
+def test_int8_row_quantizer_matches_numpy_restatement(oracle):
+    """convert.py:106-126: per-row fp32 amax/127 (1.0 for an all-zero row),
+    round half to even, clip [-127, 127]."""
+    rng = np.random.default_rng(12)
+    w = (rng.standard_normal((9, 333)) * 0.05).astype(np.float32)
+    w[3] = 0.0
+    w[4, :3] = [127.0, 0.5, -1.5]                  # scale exactly 1: ties to even
+    w[4, 3:] = 0.0
+    amax = np.abs(w).max(axis=1)
+    s_ref = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
+    q_ref = np.clip(np.rint(w / s_ref[:, None]), -127, 127).astype(np.int8)
+    q = np.empty_like(q_ref)
+    s = np.empty(9, np.float32)
+    oracle.quantize_int8_rows(w, 9, 333, q, s)
+    assert np.array_equal(q, q_ref) and bits_equal(s, s_ref)
+    assert list(q[4, :3]) == [127, 0, -2] and s[3] == 1.0 and np.all(q[3] == 0)
+
+
 def test_nibble_decode_exhaustive(oracle):
     """Every byte value, both nibbles: matmul_i4_gs with x = identity gives
     (nib - 8) * scale exactly, low nibble = even column."""
