@@ -53,12 +53,19 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
     for (int i = threadIdx.x; i < D; i += 256) hn[i] = (ok ? row[i] : 0.0f) * r * w[i];
 }
 
-// RoPE (picchio.c:455-473) on q [H][hd] and k [KVH][hd] at position pos with
-// the host-built cos/sin table (attn_factor folded in), then kv_store
-// (picchio.c:492-498): K/V rows of this layer at pos.
-__global__ void k_rope_kv(const pk_dstate *st, float *qkv, const float *rope, int H, int KVH, int hd,
-                          float *Kl, float *Vl) {
-    const int pos = st->pos;
+// Position of row r: the decode step's (device state) or pos_base + r for a
+// batch of consecutive prompt positions.
+__device__ __forceinline__ int row_pos(const pk_dstate *st, int pos_base, int r) {
+    return st ? st->pos : pos_base + r;
+}
+
+// RoPE (picchio.c:455-473) on q [H][hd] and k [KVH][hd] at the row's position
+// with the host-built cos/sin table (attn_factor folded in), then kv_store
+// (picchio.c:492-498): K/V rows of this layer at that position. grid.y = row.
+__global__ void k_rope_kv(const pk_dstate *st, int pos_base, float *qkv, int64_t qkv_stride,
+                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl) {
+    const int pos = row_pos(st, pos_base, blockIdx.y);
+    qkv += (int64_t)blockIdx.y * qkv_stride;
     const int half = hd / 2;
     const int n_pairs = (H + KVH) * half;
     const int kv_dim = KVH * hd;
@@ -99,16 +106,19 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 // in-order dot (uncontracted products added one by one, picchio.c:573-577 as
 // gcc builds it) times 1/sqrt(hd). Writes the chunk max, sum of exp(s - max)
 // and the exp-weighted V sum (flash-decoding partials).
-__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, const float *qkv,
-                                                         const float *Kl, const float *Vl, int H, int KVH,
-                                                         int hd, int ctx, int sliding, int window,
-                                                         float *part, int max_chunks) {
+__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, const float *qkv,
+                                                         int64_t qkv_stride, const float *Kl,
+                                                         const float *Vl, int H, int KVH, int hd, int ctx,
+                                                         int sliding, int window, float *part,
+                                                         int max_chunks) {
     __shared__ float q[128];
     __shared__ float p[ATT_CHUNK];
     __shared__ float red[2];
-    const int h = blockIdx.x, c = blockIdx.y;
+    const int h = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
+    qkv += (int64_t)r * qkv_stride;
+    part += (int64_t)r * H * max_chunks * (hd + 2);
     int start, end;
-    att_window(st->pos, ctx, sliding, window, start, end);
+    att_window(row_pos(st, pos_base, r), ctx, sliding, window, start, end);
     const int t0 = start + c * ATT_CHUNK;
     const int n = min(ATT_CHUNK, end - t0 + 1);
     if (n <= 0) return;
@@ -153,11 +163,13 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, co
 
 // Combine the chunk partials of head h with the learned sink (picchio.c:586-604):
 // the sink joins the max and the denominator, not the value sum.
-__global__ void k_attn_combine(const pk_dstate *st, const float *part, const float *sinks, int hd, int ctx,
-                               int sliding, int window, int max_chunks, float *att) {
-    const int h = blockIdx.x;
+__global__ void k_attn_combine(const pk_dstate *st, int pos_base, const float *part, const float *sinks,
+                               int H, int hd, int ctx, int sliding, int window, int max_chunks, float *att) {
+    const int h = blockIdx.x, r = blockIdx.y;
+    part += (int64_t)r * H * max_chunks * (hd + 2);
+    att += (int64_t)r * H * hd;
     int start, end;
-    att_window(st->pos, ctx, sliding, window, start, end);
+    att_window(row_pos(st, pos_base, r), ctx, sliding, window, start, end);
     const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
     const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
     float M = sinks[h];
@@ -172,11 +184,14 @@ __global__ void k_attn_combine(const pk_dstate *st, const float *part, const flo
 }
 
 // y[o] += (W[o] . x + b[o])  — attention output projection + residual
-// (picchio.c:615-616, :1690). One workgroup per 4 rows (one per wave).
+// (picchio.c:615-616, :1690). One workgroup per 4 outputs (one per wave);
+// grid.y = row of a batch (x [rows][I], y [rows][O]).
 __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restrict__ x,
                                                   const float *__restrict__ W,
                                                   const float *__restrict__ b, int I, int O) {
     const int lane = threadIdx.x & 63;
+    y += (int64_t)blockIdx.y * O;
+    x += (int64_t)blockIdx.y * I;
     const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (o >= O) return;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
@@ -302,7 +317,7 @@ __global__ __launch_bounds__(256) void k_lm_head_argmax(const float *__restrict_
 
 // ───────────────────────── host side ─────────────────────────
 
-static int decode_reserve(pk_engine *e) {
+int pk_decode_reserve(pk_engine *e) {
     if (e->dec_ready) return PK_OK;
     PK_CHECK(!e->capturing, PK_ERR_ARG, "decode buffers must exist before capturing a graph");
     const pk_cfg *c = &e->c;
@@ -320,7 +335,7 @@ static int decode_reserve(pk_engine *e) {
     return PK_OK;
 }
 
-static int check_model(pk_engine *e) {
+int pk_check_model(pk_engine *e) {
     const pk_cfg *c = &e->c;
     PK_CHECK(e->have_globals, PK_ERR_MISSING, "embedding / lm_head / final norm not loaded");
     for (int l = 0; l < c->n_layers; ++l) {
@@ -335,33 +350,43 @@ static int check_model(pk_engine *e) {
     return PK_OK;
 }
 
-// Attention of one layer for the token in e->hn at dstate->pos: e->qkv,
-// e->att; adds the projection into e->h (residual).
-static int attention_layer(pk_engine *e, int l) {
+// Attention of layer l for n rows of normalised input xn: the decode token
+// (st = device state, n = 1) or prompt positions pos_base .. pos_base+n-1
+// (st = null). Writes K/V, qkv [n][(H+2KVH)hd], att [n][H hd] and adds the
+// output projection into h [n][D] (residual).
+int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int n, const float *xn,
+                      float *qkv, float *part, float *att, float *h) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[l];
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
-    const int kv_dim = KVH * hd;
+    const int kv_dim = KVH * hd, qkv_dim = (H + 2 * KVH) * hd;
     float *Kl = e->K + (int64_t)l * c->ctx_len * kv_dim;
     float *Vl = e->V + (int64_t)l * c->ctx_len * kv_dim;
-    PK_TRY(pk_launch_gemv_f32(e->qkv, e->hn, d.wqkv, d.bqkv, 1, D, (H + 2 * KVH) * hd, e->stream));
+    PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
     const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
-    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256), dim3(256), 0, e->stream, e->dstate, e->qkv,
-                       e->rope, H, KVH, hd, Kl, Vl);
+    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, qkv,
+                       (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl);
     PK_HIP(hipGetLastError());
     const int sliding = c->layer_type[l] == 0;
     const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
-    const int chunks = sliding ? std::min(max_chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK) : max_chunks;
-    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks), dim3(ATT_CHUNK), 0, e->stream, e->dstate, e->qkv, Kl,
-                       Vl, H, KVH, hd, c->ctx_len, sliding, c->sliding_window, e->attn_part, max_chunks);
+    int chunks = st ? max_chunks : (pos_base + n + ATT_CHUNK - 1) / ATT_CHUNK;
+    if (sliding) chunks = std::min(chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK);
+    chunks = std::min(chunks, max_chunks);
+    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks, n), dim3(ATT_CHUNK), 0, e->stream, st, pos_base, qkv,
+                       (int64_t)qkv_dim, Kl, Vl, H, KVH, hd, c->ctx_len, sliding, c->sliding_window, part,
+                       max_chunks);
     PK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_attn_combine, dim3(H), dim3(64), 0, e->stream, e->dstate, e->attn_part, d.sinks,
-                       hd, c->ctx_len, sliding, c->sliding_window, max_chunks, e->att);
+    hipLaunchKernelGGL(k_attn_combine, dim3(H, n), dim3(64), 0, e->stream, st, pos_base, part, d.sinks, H,
+                       hd, c->ctx_len, sliding, c->sliding_window, max_chunks, att);
     PK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4), dim3(256), 0, e->stream, e->h, e->att, d.wo, d.bo,
+    hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4, n), dim3(256), 0, e->stream, h, att, d.wo, d.bo,
                        H * hd, D);
     PK_HIP(hipGetLastError());
     return PK_OK;
+}
+
+static int attention_layer(pk_engine *e, int l) {
+    return pk_attention_rows(e, l, e->dstate, 0, 1, e->hn, e->qkv, e->attn_part, e->att, e->h);
 }
 
 // One forward_token step with tok/pos in device state; logits optional.
@@ -378,14 +403,22 @@ static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int o
         PK_TRY(pk_moe_layer(e, l, e->hn, nullptr, e->h, e->h));      // h += moe(hn)
     }
     PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->final_norm, D, c->eps, 1, e->stream));
+    return pk_lm_head_step(e, e->hn, logits_dev, out_toks, out_cap);
+}
+
+// lm_head GEMV + greedy argmax of the normalised state hn for the token at
+// dstate->pos: writes next/tok, advances pos, appends to out_toks.
+int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden;
     const int lm_blocks = (c->vocab + LM_ROWS_PER_BLOCK - 1) / LM_ROWS_PER_BLOCK;
     float *lg = logits_dev ? logits_dev : e->logits;
     if (c->lm_head_fmt == PK_FMT_INT8)
-        hipLaunchKernelGGL(k_lm_head_argmax<true>, dim3(lm_blocks), dim3(256), 0, e->stream, e->hn,
+        hipLaunchKernelGGL(k_lm_head_argmax<true>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
                            (const void *)e->lm_q8, e->lm_s, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
                            e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
     else
-        hipLaunchKernelGGL(k_lm_head_argmax<false>, dim3(lm_blocks), dim3(256), 0, e->stream, e->hn,
+        hipLaunchKernelGGL(k_lm_head_argmax<false>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
                            (const void *)e->lm_f32, nullptr, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
                            e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
     PK_HIP(hipGetLastError());
@@ -393,7 +426,7 @@ static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int o
 }
 
 // tok / pos (and n_out = 0) for position pos through its pinned staging slot
-static int set_state(pk_engine *e, int tok, int pos) {
+int pk_set_state(pk_engine *e, int tok, int pos) {
     pk_dstate &s = e->pin_state[pos];
     s.tok = tok;
     s.pos = pos;
@@ -411,8 +444,8 @@ extern "C" int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int
     PK_CHECK(pos >= 0, PK_ERR_ARG, "pos %d", pos);
     PK_CHECK(pos < c->ctx_len, PK_ERR_CONTEXT_FULL, "pos %d >= context %d", pos, c->ctx_len);
     PK_CHECK(!e->capturing, PK_ERR_ARG, "gqa_attention: host position; not available while capturing");
-    PK_TRY(decode_reserve(e));
-    PK_TRY(set_state(e, 0, pos));
+    PK_TRY(pk_decode_reserve(e));
+    PK_TRY(pk_set_state(e, 0, pos));
     PK_HIP(hipMemcpyAsync(e->hn, x_dev, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
     PK_HIP(hipMemsetAsync(e->h, 0, (size_t)c->hidden * 4, e->stream));
     PK_TRY(attention_layer(e, layer));               // h = 0 + attn(x)
@@ -426,9 +459,9 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
     PK_CHECK(pos >= 0, PK_ERR_ARG, "pos %d", pos);
     PK_CHECK(pos < e->c.ctx_len, PK_ERR_CONTEXT_FULL, "pos %d >= context %d", pos, e->c.ctx_len);
     PK_CHECK(!e->capturing, PK_ERR_ARG, "forward_token: use pk_generate inside graphs");
-    PK_TRY(check_model(e));
-    PK_TRY(decode_reserve(e));
-    PK_TRY(set_state(e, tok, pos));
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
+    PK_TRY(pk_set_state(e, tok, pos));
     PK_TRY(decode_step(e, logits_dev, nullptr, 0));
     if (next_host) {
         pk_dstate s{};
@@ -439,70 +472,54 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
     return PK_OK;
 }
 
-extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *next_host) {
-    PK_CHECK(e && ids && n > 0, PK_ERR_ARG, "bad argument");
-    PK_CHECK(pos_base >= 0 && pos_base + n <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
-             "positions %d..%d exceed context %d", pos_base, pos_base + n - 1, e->c.ctx_len);
-    PK_TRY(check_model(e));
-    PK_TRY(decode_reserve(e));
-    for (int i = 0; i < n; ++i) {
-        PK_TRY(set_state(e, ids[i], pos_base + i));
-        PK_TRY(decode_step(e, nullptr, nullptr, 0));
-    }
-    pk_dstate s{};
-    PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
-    PK_HIP(hipStreamSynchronize(e->stream));
-    if (next_host) *next_host = s.next;
-    return PK_OK;
+int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap) {
+    PK_TRY(pk_set_state(e, tok, pos));
+    return decode_step(e, nullptr, out_toks, out_cap);
 }
 
-// Greedy generation: prompt through the step graph (token overridden per
-// position), then n_steps decode steps replayed from the same graph with the
-// token and position carried on the device.
+// Greedy generation as picchio runs a turn: the prompt through prefill_tokens
+// (batched chunks, picchio.c:1936-1975), then n_steps - 1 forward_token steps
+// replayed from one captured step graph that feeds itself (tok = last argmax,
+// pos += 1). out[0] is the prompt's next token.
 extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, int n_steps, int32_t *out) {
     PK_CHECK(e && prompt && out && n_prompt > 0 && n_steps >= 0, PK_ERR_ARG, "bad argument");
     PK_CHECK(n_prompt + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
              "%d prompt + %d steps exceed context %d", n_prompt, n_steps, e->c.ctx_len);
     PK_CHECK(!e->capturing, PK_ERR_ARG, "generate: not available while capturing");
-    PK_TRY(check_model(e));
-    PK_TRY(decode_reserve(e));
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
+    if (n_steps == 0) return PK_OK;
     int32_t *out_dev = nullptr;
-    PK_TRY(pk_dev_alloc(e, (void **)&out_dev, (int64_t)(n_steps + 1) * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&out_dev, (int64_t)n_steps * 4));
     int rc = PK_OK;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     do {
-        if ((rc = set_state(e, prompt[0], 0)) != PK_OK) break;
-        // capture one step (writes the next token into the output list)
-        if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) { rc = PK_ERR_HIP; break; }
-        e->capturing = true;
-        rc = decode_step(e, nullptr, out_dev, n_steps + 1);
-        e->capturing = false;
-        hipError_t hr = hipStreamEndCapture(e->stream, &graph);
-        if (rc != PK_OK) break;
-        if (hr != hipSuccess || hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
-            pk_set_error("generate: graph capture failed"); rc = PK_ERR_HIP; break;
+        if (n_steps > 1) {
+            if (hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+                rc = PK_ERR_HIP; break;
+            }
+            e->capturing = true;
+            rc = decode_step(e, nullptr, out_dev, n_steps);
+            e->capturing = false;
+            hipError_t hr = hipStreamEndCapture(e->stream, &graph);
+            if (rc != PK_OK) break;
+            if (hr != hipSuccess || hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+                pk_set_error("generate: graph capture failed"); rc = PK_ERR_HIP; break;
+            }
         }
-        // prompt: each position with its own token; n_out counts from the last one
-        for (int i = 0; i < n_prompt && rc == PK_OK; ++i) {
-            rc = set_state(e, prompt[i], i);
-            if (rc == PK_OK && hipGraphLaunch(exec, e->stream) != hipSuccess) rc = PK_ERR_HIP;
-        }
-        // decode: the graph feeds itself (tok = last argmax, pos += 1)
+        if ((rc = pk_prefill_run(e, prompt, n_prompt, 0, out_dev, n_steps)) != PK_OK) break;
         for (int i = 0; i < n_steps - 1 && rc == PK_OK; ++i)
-            if (hipGraphLaunch(exec, e->stream) != hipSuccess) rc = PK_ERR_HIP;
-        if (rc != PK_OK) { pk_set_error("generate: launch failed"); break; }
-        if (n_steps > 0 &&
-            hipMemcpyAsync(out, out_dev, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess) {
-            rc = PK_ERR_HIP; break;
-        }
-        if (hipStreamSynchronize(e->stream) != hipSuccess) { rc = PK_ERR_HIP; break; }
+            if (hipGraphLaunch(exec, e->stream) != hipSuccess) { pk_set_error("generate: launch failed"); rc = PK_ERR_HIP; }
+        if (rc != PK_OK) break;
+        if (hipMemcpyAsync(out, out_dev, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
+            hipStreamSynchronize(e->stream) != hipSuccess) { rc = PK_ERR_HIP; break; }
     } while (0);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     (void)hipStreamSynchronize(e->stream);
     pk_dev_free(e, out_dev);
-    e->device_bytes -= (int64_t)(n_steps + 1) * 4;
+    e->device_bytes -= (int64_t)n_steps * 4;
     return rc;
 }
 
@@ -511,8 +528,8 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
 extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out) {
     PK_CHECK(e && out && n_steps > 0, PK_ERR_ARG, "bad argument");
     PK_CHECK(pos + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL, "positions exceed context");
-    PK_TRY(check_model(e));
-    PK_TRY(decode_reserve(e));
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
     if (!e->step_exec) {
         int32_t *od = nullptr;
         PK_TRY(pk_dev_alloc(e, (void **)&od, (int64_t)e->c.ctx_len * 4));
@@ -528,7 +545,7 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
         PK_HIP(hipGraphInstantiate(&e->step_exec, g, nullptr, nullptr, 0));
         (void)hipGraphDestroy(g);
     }
-    PK_TRY(set_state(e, tok, pos));
+    PK_TRY(pk_set_state(e, tok, pos));
     for (int i = 0; i < n_steps; ++i) PK_HIP(hipGraphLaunch(e->step_exec, e->stream));
     PK_HIP(hipMemcpyAsync(out, e->step_out, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));

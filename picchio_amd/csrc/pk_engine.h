@@ -93,10 +93,14 @@ struct pk_engine {
     uint64_t *seq_trace = nullptr;            // optional task timeline (pk_moe_seq_trace)
     bool router_tab_dirty = true;
 
-    // batched scratch (grown on demand)
+    // batched MoE scratch for up to batch_cap tokens (pk_prefill.hip)
     int64_t batch_cap = 0;
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
-    int32_t *b_sel = nullptr;
+    int32_t *b_sel = nullptr, *b_perm = nullptr;
+    // prompt-chunk scratch for up to p_cap positions (pk_prefill.hip)
+    int p_cap = 0;
+    float *p_H = nullptr, *p_XN = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_part = nullptr;
+    int32_t *p_ids = nullptr;
 };
 
 int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes);
@@ -116,6 +120,20 @@ int pk_launch_fill_const(float *out, int64_t n, float v, hipStream_t st);
 int pk_prof_begin(pk_engine *e, int kind);
 int pk_prof_end(pk_engine *e, int slot);
 
-// internal MoE pieces reused by the decode driver
+// internal MoE pieces reused by the decode and prompt drivers
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out);
+int pk_check_layer_experts(pk_engine *e, int layer);
+pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
+
+// decode driver pieces (pk_decode.hip) reused by the prompt driver
+int pk_decode_reserve(pk_engine *e);
+int pk_check_model(pk_engine *e);
+int pk_set_state(pk_engine *e, int tok, int pos);
+int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int n, const float *xn,
+                      float *qkv, float *part, float *att, float *h);
+int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap);
+// one forward_token step for (tok, pos), greedy id appended to out_toks
+int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap);
+// prefill_tokens (pk_prefill.hip): the prompt, next id into the decode state / out_toks
+int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *out_toks, int out_cap);

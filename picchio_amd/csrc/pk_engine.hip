@@ -146,7 +146,8 @@ static void engine_free(pk_engine *e) {
                     e->K, e->V, e->stage, e->x_in, e->h, e->hn, e->attn_out, e->qkv, e->att,
                     e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
-                    e->b_eo, e->b_sel, e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
+                    e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
+                    e->p_part, e->p_ids, e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
@@ -678,7 +679,7 @@ extern "C" int pk_matmul_qt(pk_engine *e, float *y, const float *x, const pk_qt 
 }
 
 // ───────────────────────── expert path ─────────────────────────
-static pk_i4_items expert_items(pk_engine *e, int layer, bool down) {
+pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down) {
     pk_i4_items it{};
     it.base = e->store;
     it.slot_stride = e->ex.stride;
@@ -689,7 +690,7 @@ static pk_i4_items expert_items(pk_engine *e, int layer, bool down) {
     return it;
 }
 
-static int check_layer_experts(pk_engine *e, int layer) {
+int pk_check_layer_experts(pk_engine *e, int layer) {
     const pk_cfg *c = &e->c;
     PK_CHECK(layer >= 0 && layer < c->n_layers, PK_ERR_ARG, "layer %d out of range", layer);
     PK_CHECK(e->L[layer].have_router, PK_ERR_MISSING, "layer %d: router not loaded", layer);
@@ -705,7 +706,7 @@ static int check_layer_experts(pk_engine *e, int layer) {
 static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, const float *x,
                        int64_t x_stride, float *act, float *eo, const pk_combine_args *comb) {
     const pk_cfg *c = &e->c;
-    pk_i4_items gu = expert_items(e, layer, false);
+    pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = sel_dev;
     gu.x = x; gu.x_stride = x_stride;
     gu.y = act; gu.y_stride = c->moe_inter / 2;
@@ -714,7 +715,7 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
                              nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));
-    pk_i4_items dn = expert_items(e, layer, true);
+    pk_i4_items dn = pk_expert_items(e, layer, true);
     dn.slots = sel_dev;
     dn.x = act; dn.x_stride = c->moe_inter / 2;
     dn.y = eo; dn.y_stride = c->hidden;
@@ -748,7 +749,7 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
 extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                               int32_t *sel_host, float *w_host) {
     PK_CHECK(e && x_dev && out_dev, PK_ERR_ARG, "null argument");
-    PK_TRY(check_layer_experts(e, layer));
+    PK_TRY(pk_check_layer_experts(e, layer));
     PK_CHECK(!(e->capturing && (sel_host || w_host)), PK_ERR_ARG,
              "moe_forward: host routing outputs are not available while capturing a graph");
     PK_TRY(pk_moe_layer(e, layer, x_dev, out_dev, nullptr, nullptr));
@@ -784,7 +785,7 @@ static int check_expert_batch(pk_engine *e, int layer, const int32_t *eids_dev, 
     const pk_cfg *c = &e->c;
     PK_CHECK(eids_dev && in && out, PK_ERR_ARG, "null argument");
     PK_CHECK(n > 0 && n <= c->n_experts, PK_ERR_ARG, "%d experts per launch (1..%d)", n, c->n_experts);
-    PK_TRY(check_layer_experts(e, layer));
+    PK_TRY(pk_check_layer_experts(e, layer));
     return PK_OK;
 }
 
@@ -793,7 +794,7 @@ extern "C" int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_de
     PK_CHECK(e, PK_ERR_ARG, "null engine");
     PK_TRY(check_expert_batch(e, layer, eids_dev, n, x_dev, act_dev));
     const pk_cfg *c = &e->c;
-    pk_i4_items gu = expert_items(e, layer, false);
+    pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = eids_dev;
     gu.x = x_dev; gu.x_stride = 0;
     gu.y = act_dev; gu.y_stride = c->moe_inter / 2;
@@ -809,7 +810,7 @@ extern "C" int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, 
     PK_CHECK(e, PK_ERR_ARG, "null engine");
     PK_TRY(check_expert_batch(e, layer, eids_dev, n, act_dev, eo_dev));
     const pk_cfg *c = &e->c;
-    pk_i4_items dn = expert_items(e, layer, true);
+    pk_i4_items dn = pk_expert_items(e, layer, true);
     dn.slots = eids_dev;
     dn.x = act_dev; dn.x_stride = c->moe_inter / 2;
     dn.y = eo_dev; dn.y_stride = c->hidden;
@@ -819,48 +820,3 @@ extern "C" int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, 
     return pk_prof_end(e, ps);
 }
 
-static int batch_reserve(pk_engine *e, int T) {
-    if (T <= e->batch_cap) return PK_OK;
-    PK_CHECK(!e->capturing, PK_ERR_ARG, "batch buffers must be sized before capturing a graph");
-    PK_HIP(hipStreamSynchronize(e->stream));
-    const pk_cfg *c = &e->c;
-    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel};
-    for (void *p : ptrs) pk_dev_free(e, p);
-    e->b_logits = e->b_w = e->b_act = e->b_eo = nullptr;
-    e->b_sel = nullptr;
-    e->batch_cap = 0;
-    const int64_t TK = (int64_t)T * c->topk;
-    ALLOC(e->b_logits, (int64_t)T * c->n_experts * 4);
-    ALLOC(e->b_w, TK * 4);
-    ALLOC(e->b_sel, TK * 4);
-    ALLOC(e->b_act, TK * (c->moe_inter / 2) * 4);
-    ALLOC(e->b_eo, TK * c->hidden * 4);
-    e->batch_cap = T;
-    return PK_OK;
-}
-
-// Batched MoE: every token runs the decode arithmetic (same bits as
-// pk_moe_forward token by token).
-extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
-                                    float *out_dev, int32_t *sel_dev, float *w_dev) {
-    PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
-    PK_TRY(check_layer_experts(e, layer));
-    PK_TRY(batch_reserve(e, T));
-    const pk_cfg *c = &e->c;
-    const int D = c->hidden, K = c->topk;
-    const pk_layer_dev &d = e->L[layer];
-    PK_TRY(pk_launch_gemv_f32(e->b_logits, x_dev, d.router, d.router_b, T, D, c->n_experts, e->stream));
-    PK_TRY(pk_launch_topk_batch(e->b_logits, T, c->n_experts, K, c->routed_scale, e->b_sel, e->b_w,
-                                nullptr, e->stream));
-    for (int t = 0; t < T; ++t) {
-        PK_TRY(experts_ffn(e, layer, e->b_sel + (int64_t)t * K, K, x_dev + (int64_t)t * D, 0,
-                           e->b_act, e->b_eo, nullptr));
-        PK_TRY(pk_launch_combine(out_dev + (int64_t)t * D, e->b_eo, e->b_w + (int64_t)t * K, K, D,
-                                 nullptr, nullptr, e->stream));
-    }
-    if (sel_dev)
-        PK_HIP(hipMemcpyAsync(sel_dev, e->b_sel, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
-    if (w_dev)
-        PK_HIP(hipMemcpyAsync(w_dev, e->b_w, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
-    return PK_OK;
-}

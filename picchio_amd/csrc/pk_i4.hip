@@ -38,7 +38,7 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     const uint4 *tiles = reinterpret_cast<const uint4 *>(base + it.off_tiles) +
                          (int64_t)rb * NG * (PK_TILE_BYTES / 16);
     const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
-    const float *__restrict__ x = it.x + (int64_t)item * it.x_stride;
+    const float *__restrict__ x = it.x + (int64_t)(item / it.x_div) * it.x_stride;
 
     for (int g0 = wave; g0 < NG; g0 += NW * GPW) {
         uint4 wa[GPW], wb[GPW];

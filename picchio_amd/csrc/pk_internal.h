@@ -106,8 +106,9 @@ struct pk_i4_items {
     int64_t off_tiles, off_scales, off_bias;  // offsets inside a slot (bias < 0: none)
     const int32_t *slots;      // [n_items] slot index (device), or null -> slot 0
     int32_t slot_base;         // added to every slot index (layer * n_experts)
-    const float *x;            // input of item i at x + i * x_stride
+    const float *x;            // input of item i at x + (i / x_div) * x_stride
     int64_t x_stride;
+    int x_div = 1;             // items sharing one input row (token-major item lists)
     float *y;                  // output of item i at y + i * y_stride
     int64_t y_stride;
     int n_items;

@@ -1,0 +1,225 @@
+// pk_prefill.hip — the prompt path: prefill_tokens / forward_prefill
+// (picchio.c:1795-1975) and the batched MoE of a chunk of tokens.
+//
+// A prompt runs in chunks of PREFILL_BATCH positions (64 unless the
+// environment says otherwise, read as picchio.c:1937-1938 reads it; 1 selects
+// the position-by-position path). Per chunk and layer, on n positions at once:
+//   RMSNorm -> QKV GEMV -> RoPE + KV store of every position -> causal /
+//   sliding attention of every position (each sees its own window) -> O
+//   projection + residual -> RMSNorm -> router logits -> top-k + softmax ->
+//   gate_up + SwiGLU and down over all n*K (token, expert) pairs, one launch
+//   each -> per-token sum in the chunk's expert order + residual.
+// Then the last position's final norm, lm_head and greedy argmax.
+#include "pk_engine.h"
+
+#include <stdlib.h>
+
+namespace {
+
+__global__ __launch_bounds__(256) void k_embed_rows(const int32_t *ids, const float *embed, int vocab,
+                                                    float *H, int D) {
+    const int p = blockIdx.x;
+    const int tok = ids[p];
+    const bool ok = tok >= 0 && tok < vocab;           // embed_token, picchio.c:1476-1480
+    const float *row = embed + (int64_t)(ok ? tok : 0) * D;
+    float *h = H + (int64_t)p * D;
+    for (int i = threadIdx.x; i < D; i += 256) h[i] = ok ? row[i] : 0.0f;
+}
+
+// forward_prefill's expert order (picchio.c:1846-1852, :1885-1902): experts are
+// ranked by first request, scanning positions, then k; each token adds its
+// experts in rank order. perm[p][j] = k of the token's j-th expert.
+__global__ __launch_bounds__(64) void k_uniq_perm(const int32_t *sel, int n, int K, int E, int32_t *perm) {
+    __shared__ int rank[128];
+    if (threadIdx.x == 0) {
+        for (int e = 0; e < E; ++e) rank[e] = -1;
+        int r = 0;
+        for (int i = 0; i < n * K; ++i) {
+            const int e = sel[i];
+            if (e >= 0 && e < E && rank[e] < 0) rank[e] = r++;
+        }
+    }
+    __syncthreads();
+    for (int p = threadIdx.x; p < n; p += blockDim.x) {
+        int ks[16], rk[16];
+        for (int k = 0; k < K; ++k) {
+            const int e = sel[p * K + k];
+            ks[k] = k;
+            rk[k] = (e >= 0 && e < E) ? rank[e] : 0x7fffffff;
+        }
+        for (int a = 1; a < K; ++a) {
+            const int kk = ks[a], rr = rk[a];
+            int b = a - 1;
+            while (b >= 0 && rk[b] > rr) { ks[b + 1] = ks[b]; rk[b + 1] = rk[b]; --b; }
+            ks[b + 1] = kk;
+            rk[b + 1] = rr;
+        }
+        for (int j = 0; j < K; ++j) perm[p * K + j] = ks[j];
+    }
+}
+
+// moe = 0; moe = fma(w_k, eo_k, moe) in rank order (expert_apply's
+// dst += w * eo, picchio.c:1788); out = residual + moe (picchio.c:1910-1914)
+// or moe alone.
+__global__ __launch_bounds__(256) void k_combine_rows(float *out, const float *residual, const float *eo,
+                                                      const float *w, const int32_t *perm, int K, int D) {
+    const int p = blockIdx.y;
+    const int i = blockIdx.x * 256 + threadIdx.x;
+    if (i >= D) return;
+    float acc = 0.0f;
+    for (int j = 0; j < K; ++j) {
+        const int k = perm[p * K + j];
+        acc = __builtin_fmaf(w[p * K + k], eo[((int64_t)p * K + k) * D + i], acc);
+    }
+    const int64_t o = (int64_t)p * D + i;
+    out[o] = residual ? residual[o] + acc : acc;
+}
+
+}  // namespace
+
+static int batch_reserve(pk_engine *e, int T) {
+    if (T <= e->batch_cap) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "batch buffers must be sized before capturing a graph");
+    const pk_cfg *c = &e->c;
+    PK_CHECK((int64_t)T * c->topk <= 65535, PK_ERR_UNSUPPORTED, "batched MoE: %d tokens x top-%d", T,
+             c->topk);
+    PK_HIP(hipStreamSynchronize(e->stream));
+    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm};
+    for (void *p : ptrs) pk_dev_free(e, p);
+    e->b_logits = e->b_w = e->b_act = e->b_eo = nullptr;
+    e->b_sel = e->b_perm = nullptr;
+    e->batch_cap = 0;
+    const int64_t TK = (int64_t)T * c->topk;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_logits, (int64_t)T * c->n_experts * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_w, TK * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_sel, TK * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_perm, TK * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_act, TK * (c->moe_inter / 2) * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_eo, TK * c->hidden * 4));
+    e->batch_cap = T;
+    return PK_OK;
+}
+
+// The MoE of forward_prefill (picchio.c:1829-1916) for T tokens x [T][D]:
+// out[t] = (residual ? residual[t] : 0) + sum over the token's experts, in the
+// batch's expert order, of (w_k * routed_scale) * expert_k(x[t]).
+static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
+    PK_TRY(batch_reserve(e, T));
+    const pk_layer_dev &d = e->L[layer];
+    PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
+    PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr, e->stream));
+    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(64), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+    PK_HIP(hipGetLastError());
+    pk_i4_items gu = pk_expert_items(e, layer, false);
+    gu.slots = e->b_sel;
+    gu.x = x; gu.x_stride = D; gu.x_div = K;
+    gu.y = e->b_act; gu.y_stride = half;
+    gu.n_items = T * K;
+    int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
+    PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, nullptr,
+                             e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    pk_i4_items dn = pk_expert_items(e, layer, true);
+    dn.slots = e->b_sel;
+    dn.x = e->b_act; dn.x_stride = half;
+    dn.y = e->b_eo; dn.y_stride = D;
+    dn.n_items = T * K;
+    ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
+    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
+                       e->b_eo, e->b_w, e->b_perm, K, D);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
+                                    float *out_dev, int32_t *sel_dev, float *w_dev) {
+    PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
+    PK_TRY(pk_check_layer_experts(e, layer));
+    PK_TRY(moe_rows(e, layer, x_dev, T, out_dev, nullptr));
+    const int K = e->c.topk;
+    if (sel_dev)
+        PK_HIP(hipMemcpyAsync(sel_dev, e->b_sel, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    if (w_dev)
+        PK_HIP(hipMemcpyAsync(w_dev, e->b_w, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    return PK_OK;
+}
+
+static int prefill_reserve(pk_engine *e, int B) {
+    if (B <= e->p_cap) return PK_OK;
+    PK_HIP(hipStreamSynchronize(e->stream));
+    void *ptrs[] = {e->p_H, e->p_XN, e->p_qkv, e->p_att, e->p_part, e->p_ids};
+    for (void *p : ptrs) pk_dev_free(e, p);
+    e->p_H = e->p_XN = e->p_qkv = e->p_att = e->p_part = nullptr;
+    e->p_ids = nullptr;
+    e->p_cap = 0;
+    const pk_cfg *c = &e->c;
+    const int64_t qkv_dim = (int64_t)(c->n_heads + 2 * c->n_kv_heads) * c->head_dim;
+    const int max_chunks = (c->ctx_len + 127) / 128;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_H, (int64_t)B * c->hidden * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_XN, (int64_t)B * c->hidden * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_qkv, B * qkv_dim * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_att, (int64_t)B * c->n_heads * c->head_dim * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_part,
+                        (int64_t)B * c->n_heads * max_chunks * (c->head_dim + 2) * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->p_ids, (int64_t)c->ctx_len * 4));
+    e->p_cap = B;
+    return PK_OK;
+}
+
+// forward_prefill (picchio.c:1795-1932) of ids_dev[0..n) at positions
+// pos_base..pos_base+n-1; the greedy next token goes to the decode state
+// (and to out_toks when given).
+static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int n, int pos_base,
+                         int32_t *out_toks, int out_cap) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden;
+    hipLaunchKernelGGL(k_embed_rows, dim3(n), dim3(256), 0, e->stream, ids_dev, e->embed, c->vocab, e->p_H, D);
+    PK_HIP(hipGetLastError());
+    for (int l = 0; l < c->n_layers; ++l) {
+        PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].in_ln, D, c->eps, n, e->stream));
+        PK_TRY(pk_attention_rows(e, l, nullptr, pos_base, n, e->p_XN, e->p_qkv, e->p_part, e->p_att, e->p_H));
+        PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n, e->stream));
+        PK_TRY(moe_rows(e, l, e->p_XN, n, e->p_H, e->p_H));
+    }
+    PK_TRY(pk_launch_rmsnorm(e->hn, e->p_H + (int64_t)(n - 1) * D, e->final_norm, D, c->eps, 1, e->stream));
+    PK_TRY(pk_set_state(e, last_tok, pos_base + n - 1));
+    return pk_lm_head_step(e, e->hn, nullptr, out_toks, out_cap);
+}
+
+int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *out_toks, int out_cap) {
+    int batch = 64;
+    if (const char *v = getenv("PREFILL_BATCH")) batch = atoi(v);
+    if (batch <= 1 || n <= 1) {
+        for (int i = 0; i < n; ++i) PK_TRY(pk_decode_token(e, ids[i], pos_base + i, out_toks, out_cap));
+        return PK_OK;
+    }
+    const int B = batch < n ? batch : n;
+    PK_TRY(prefill_reserve(e, B));
+    PK_TRY(batch_reserve(e, B));
+    PK_HIP(hipMemcpyAsync(e->p_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+    for (int off = 0; off < n; off += B) {
+        const int len = n - off < B ? n - off : B;
+        PK_TRY(prefill_chunk(e, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap));
+    }
+    PK_HIP(hipStreamSynchronize(e->stream));           // ids is the caller's pageable memory
+    return PK_OK;
+}
+
+extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *next_host) {
+    PK_CHECK(e && ids && n > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(pos_base >= 0 && pos_base + n <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
+             "positions %d..%d exceed context %d", pos_base, pos_base + n - 1, e->c.ctx_len);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "prefill_tokens: not available while capturing");
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
+    PK_TRY(pk_prefill_run(e, ids, n, pos_base, nullptr, 0));
+    pk_dstate s{};
+    PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    if (next_host) *next_host = s.next;
+    return PK_OK;
+}

@@ -85,20 +85,37 @@ def test_out_of_range_token_embeds_zero(dec_setup, oracle):
 
 
 def test_generate_stream_matches_oracle(dec_setup, oracle):
-    """Prompt position by position, then greedy decode from the replayed
-    step graph: the same token stream as the oracle's forward_token loop."""
+    """The prompt through prefill_tokens (chunks of 64, as picchio runs it),
+    then greedy decode from the replayed step graph: the oracle's stream."""
     cfg, model, eng = dec_setup
-    prompt = [int(v) for v in np.random.default_rng(11).integers(0, cfg.vocab, 12)]
+    prompt = np.random.default_rng(11).integers(0, cfg.vocab, 70).astype(np.int32)
     n = 20
     oracle.model_reset_kv(model)
-    nxt = None
-    for pos, tok in enumerate(prompt):
-        nxt = oracle.forward_token(model, tok, pos, None)
-    ref = [nxt]
+    ref = [oracle.prefill_tokens(model, prompt, len(prompt), 0, 64)]
     for i in range(n - 1):
         ref.append(oracle.forward_token(model, ref[-1], len(prompt) + i, None))
     got = list(eng.generate(prompt, n))
     assert got == ref
+
+
+def test_prefill_chunks_match_oracle(dec_setup, oracle, monkeypatch):
+    """prefill_tokens over 150 positions in chunks of 64 (crossing the
+    128-position window), then forward_token: next id and logits as the
+    oracle's prefill_tokens + forward_token (the KV written by the prompt
+    path is what the decode step reads)."""
+    import torch
+    cfg, model, eng = dec_setup
+    monkeypatch.setenv("PREFILL_BATCH", "64")
+    prompt = np.random.default_rng(21).integers(0, cfg.vocab, 150).astype(np.int32)
+    oracle.model_reset_kv(model)
+    nref = oracle.prefill_tokens(model, prompt, len(prompt), 0, 64)
+    assert eng.prefill_tokens(prompt) == nref
+    ref = np.empty(cfg.vocab, np.float32)
+    lg = eng.empty(cfg.vocab, torch.float32)
+    for i, tok in enumerate([nref, 7, 1999]):
+        oracle.forward_token(model, int(tok), 150 + i, ref.ctypes.data)
+        eng.forward_token(int(tok), 150 + i, lg)
+        assert rel_l2(eng.to_host(lg), ref) < REL_L2_TOL, i
 
 
 def test_context_full_is_an_error(dec_setup):
@@ -133,9 +150,14 @@ def test_reference_golden_tiny_model(gpu, oracle):
             for layer in range(2):
                 eng.gqa_attention(layer, eng.to_dev(z["att_x"][pos, layer]), pos, od)
                 assert rel_l2(eng.to_host(od), z["att_out"][pos, layer]) < REL_L2_TOL, (pos, layer)
-        got = list(eng.generate([int(v) for v in z["prompt"]], len(z["stream"])))
-        assert got == [int(v) for v in z["stream"]]
+        prompt = [int(v) for v in z["prompt"]]
+        os.environ["PREFILL_BATCH"] = "1"            # position by position
+        assert list(eng.generate(prompt, len(z["stream"]))) == [int(v) for v in z["stream"]]
+        os.environ["PREFILL_BATCH"] = "4"            # forward_prefill in chunks of 4
+        got = list(eng.generate(prompt, len(z["prefill_stream"])))
+        assert got == [int(v) for v in z["prefill_stream"]]
     finally:
+        os.environ.pop("PREFILL_BATCH", None)
         eng.close()
         oracle.model_free(model)
 

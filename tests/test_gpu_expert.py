@@ -222,20 +222,32 @@ def test_moe_forward_parity(moe_setup, oracle):
     assert worst < 1e-5
 
 
-def test_moe_forward_batch_matches_decode(moe_setup, oracle):
+def test_moe_forward_batch_prefill_order(moe_setup, oracle):
+    """Batched MoE = forward_prefill's MoE (picchio.c:1829-1916): same routing
+    as decode per token; each token sums its experts in the order the batch
+    first requested them (restated here with the oracle's expert_apply)."""
     import torch
+    import picchio_amd as pa
     cfg, model, eng = moe_setup
-    D, K, T = cfg.hidden, cfg.topk, 5
+    D, K, T = cfg.hidden, cfg.topk, 7
     xs = np.stack([_token_x(oracle, cfg, 50 + t) for t in range(T)])
     xd = eng.to_dev(xs)
     ob = eng.empty((T, D), torch.float32)
-    import picchio_amd as pa
-    pa.check(eng.L.pk_moe_forward_batch(eng.h, 0, pa.ptr(xd), T, pa.ptr(ob), None, None))
-    got = eng.to_host(ob)
+    sd = eng.empty((T, K), torch.int32)
+    wd = eng.empty((T, K), torch.float32)
+    pa.check(eng.L.pk_moe_forward_batch(eng.h, 0, pa.ptr(xd), T, pa.ptr(ob), pa.ptr(sd), pa.ptr(wd)))
+    got, sel, w = eng.to_host(ob), eng.to_host(sd), eng.to_host(wd)
+    rank = {}
+    for e in sel.ravel():
+        rank.setdefault(int(e), len(rank))
+    od = eng.empty(D, torch.float32)
     for t in range(T):
-        od = eng.empty(D, torch.float32)
-        eng.moe_forward(0, eng.to_dev(xs[t]), od)
-        assert bits_equal(got[t], eng.to_host(od))
+        s1, w1 = eng.moe_forward(0, xd[t], od, want_routing=True)
+        assert list(s1) == list(sel[t])
+        acc = np.zeros(D, np.float32)
+        for k in sorted(range(K), key=lambda k: rank[int(sel[t, k])]):
+            oracle.expert_apply(model, 0, int(sel[t, k]), xs[t], acc, float(w[t, k]))
+        assert rel_l2(got[t], acc) < 1e-6, t
 
 
 def test_missing_expert_is_an_error(gpu, oracle):
