@@ -113,6 +113,126 @@ def cpu_baseline(x, seed, budget_s):
                       f"{dt:.1f} s, OpenMP {threads} threads"}
 
 
+def decode_bytes_per_token(cfg, pos):
+    """Algorithmic HBM bytes of one forward_token at position pos: top-k
+    experts, router, attention weights and biases, the KV rows each layer's
+    window reads, the embedding row and the fp32 lm_head (+ logits out)."""
+    D, H, KVH, hd = cfg.hidden, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim
+    E, K, V = cfg.n_experts, cfg.topk, cfg.vocab
+    half = cfg.moe_inter // 2
+    ng_d, ng_h = D // 64, half // 64
+    expert = (cfg.moe_inter * D // 2 + cfg.moe_inter * ng_d * 4 + cfg.moe_inter * 4
+              + D * half // 2 + D * ng_h * 4 + D * 4)
+    qkv = (H + 2 * KVH) * hd
+    attn = 4 * (qkv * D + D * H * hd + qkv + D + H) + 4 * 2 * D          # + two norms
+    kv_dim = KVH * hd
+    total = 0
+    for l in range(cfg.n_layers):
+        n_pos = min(pos + 1, cfg.sliding_window) if cfg.layer_type[l] == 0 else pos + 1
+        total += K * expert + 4 * (E * D + E) + attn + 2 * 4 * n_pos * kv_dim + 4 * kv_dim * 2
+    lm = V * D * (4 if cfg.lm_head_fmt == 0 else 1) + (0 if cfg.lm_head_fmt == 0 else 4 * V)
+    return total + 4 * D + lm + 4 * D
+
+
+def cpu_decode_baseline(cfg, seed, budget_s, prompt):
+    """picchio's forward_token on the host cores for the same model shape
+    (time-bounded sample)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle, Reference, reference_available
+    o = Oracle()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    t0 = time.perf_counter()
+    model = o.model_build(cfg, seed, threads)
+    build_s = time.perf_counter() - t0
+    if reference_available():
+        ref = Reference()
+        ref.attach(model, cfg)
+        ref.reset_kv()
+        step = lambda tok, pos: ref.forward_token(tok, pos)
+        kind = "reference"
+    else:
+        step = lambda tok, pos: o.forward_token(model, tok, pos, None)
+        kind = "port"
+    tok = int(prompt[0])
+    tok = step(tok, 0)                                  # warm-up (page in)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        tok = step(int(prompt[(n + 1) % len(prompt)]), n + 1)
+        n += 1
+    dt = time.perf_counter() - t0
+    o.model_free(model)
+    return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "sample": f"{n} forward_token steps at positions 1..{n} of the same 20B-shaped model "
+                      f"(all experts resident in RAM, fp32 lm_head), {dt:.1f} s, OpenMP {threads} "
+                      f"threads; model build {build_s:.0f} s"}
+
+
+def run_decode(args):
+    """GPT-OSS-20B-shaped model, 512-token prompt through
+    prefill_tokens, then `steps` greedy decode steps replayed from the
+    captured step graph. value = decode tokens/s."""
+    import torch
+    import picchio_amd as pa
+    n_prompt, steps = 512, args.steps
+    cfg = pa.gptoss_cfg(ctx_len=n_prompt + steps + 1)
+    eng = pa.Engine(cfg)
+    t0 = time.perf_counter()
+    eng.build_synthetic(args.seed, what=7)
+    eng.sync()
+    print(f"[bench] 20B model built on the GPU: {eng.device_bytes() / 1e9:.2f} GB in "
+          f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    prompt = np.random.default_rng(args.seed + 100).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    t0 = time.perf_counter()
+    nxt = eng.prefill_tokens(prompt)
+    prefill_s = time.perf_counter() - t0
+    # warm-up: captures the step graph and runs `warmup` steps from the same state
+    warm = eng.decode_replay(nxt, n_prompt, max(args.warmup, 1))
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(eng.stream)
+    toks = eng.decode_replay(nxt, n_prompt, steps)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    assert list(toks[:len(warm)]) == list(warm), "decode is not deterministic"
+    # per-kernel event brackets on one eager step (lm_head, attention)
+    eng.profile(True)
+    eng.forward_token(int(toks[-1]), n_prompt + steps, None)     # ctx_len leaves this position free
+    lm_ms, _ = eng.profile_read(pa.PROF_LM_HEAD)
+    att_ms, att_n = eng.profile_read(pa.PROF_ATTENTION)
+    eng.profile(False)
+    eng.close()
+    tok_s = steps / (ms * 1e-3)
+    bpt = sum(decode_bytes_per_token(cfg, n_prompt + i) for i in range(steps)) / steps
+    lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    line = {
+        "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms / steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config2: GPT-OSS-20B-shaped greedy decode, batch 1, 512-token "
+                               "random-id prompt then 256 steps, all experts HBM-resident",
+                   "layers": cfg.n_layers, "experts": cfg.n_experts, "vocab": cfg.vocab,
+                   "lm_head": "fp32", "bytes_per_token": int(bpt),
+                   "hbm_gbps": round(bpt * tok_s / 1e9, 1),
+                   "hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
+                   "prefill_s": round(prefill_s, 3), "prefill_tok_s": round(n_prompt / prefill_s, 1),
+                   "attention_us_per_layer": round(att_ms / max(att_n, 1) * 1e3, 2),
+                   "first_tokens": [int(nxt)] + [int(t) for t in toks[:8]]},
+        "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(lm_bytes / (lm_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
+                     "traffic": None, "kernel": "k_lm_head_argmax<fp32> (201088 x 2880 GEMV + argmax)",
+                     "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -126,15 +246,19 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain read+write kernel over this many "
                          "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--mode", choices=["seq", "kernels"], default="kernels",
+    ap.add_argument("--mode", choices=["seq", "kernels", "decode"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "
-                         "kernel per sequence of steps")
+                         "kernel per sequence of steps; decode: config 2, the whole 20B-shaped "
+                         "model (use --steps 256)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
         sys.exit(2)
+    if args.mode == "decode":
+        run_decode(args)
+        return
 
     import torch
     import picchio_amd as pa

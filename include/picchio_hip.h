@@ -234,6 +234,8 @@ int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out_h
 #define PK_PROF_ROUTER         2   /* router GEMV + top-k                            */
 #define PK_PROF_COMBINE        3   /* weighted combine                               */
 #define PK_PROF_MOE_SEQ        4   /* persistent MoE sequence kernel (whole launch)  */
+#define PK_PROF_LM_HEAD        5   /* lm_head GEMV + greedy argmax                   */
+#define PK_PROF_ATTENTION      6   /* QKV .. O-projection of one layer (5 launches)  */
 #define PK_PROF_N              8
 int pk_engine_profile(pk_engine *e, int enable);
 int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);

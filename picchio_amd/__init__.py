@@ -17,6 +17,7 @@ ERRORS = {-1: "PK_ERR_ARG", -2: "PK_ERR_HIP", -3: "PK_ERR_OOM", -4: "PK_ERR_UNSU
           -5: "PK_ERR_MISSING", -6: "PK_ERR_CONTEXT_FULL"}
 FMT_F32, FMT_INT8, FMT_INT4 = 0, 1, 2
 PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE, PROF_MOE_SEQ = 0, 1, 2, 3, 4
+PROF_LM_HEAD, PROF_ATTENTION = 5, 6
 
 
 class PkError(RuntimeError):

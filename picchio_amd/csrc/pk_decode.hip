@@ -362,6 +362,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     const int kv_dim = KVH * hd, qkv_dim = (H + 2 * KVH) * hd;
     float *Kl = e->K + (int64_t)l * c->ctx_len * kv_dim;
     float *Vl = e->V + (int64_t)l * c->ctx_len * kv_dim;
+    const int ps = pk_prof_begin(e, PK_PROF_ATTENTION);
     PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
     const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
     hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, qkv,
@@ -382,7 +383,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4, n), dim3(256), 0, e->stream, h, att, d.wo, d.bo,
                        H * hd, D);
     PK_HIP(hipGetLastError());
-    return PK_OK;
+    return pk_prof_end(e, ps);
 }
 
 static int attention_layer(pk_engine *e, int l) {
@@ -413,6 +414,7 @@ int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *o
     const int D = c->hidden;
     const int lm_blocks = (c->vocab + LM_ROWS_PER_BLOCK - 1) / LM_ROWS_PER_BLOCK;
     float *lg = logits_dev ? logits_dev : e->logits;
+    const int ps = pk_prof_begin(e, PK_PROF_LM_HEAD);
     if (c->lm_head_fmt == PK_FMT_INT8)
         hipLaunchKernelGGL(k_lm_head_argmax<true>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
                            (const void *)e->lm_q8, e->lm_s, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
@@ -422,7 +424,7 @@ int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *o
                            (const void *)e->lm_f32, nullptr, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
                            e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
     PK_HIP(hipGetLastError());
-    return PK_OK;
+    return pk_prof_end(e, ps);
 }
 
 // tok / pos (and n_out = 0) for position pos through its pinned staging slot
