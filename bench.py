@@ -233,6 +233,132 @@ def run_decode(args):
     print(json.dumps(line))
 
 
+def zipf_routing(T, E, K, seed, s=1.1, lo=16, hi=512):
+    """BASELINE config 3 routing: per-expert pair counts proportional to
+    (e+1)^-s, clipped to [lo, hi] and summing to T*K; slot i of the
+    expert-sorted list goes to token i % T (an expert's run is shorter than T,
+    so every token gets K distinct experts); tokens shuffled; combine weights
+    = softmax of K random logits."""
+    P = T * K
+    x = (np.arange(E) + 1.0) ** -s
+    a, b = 0.0, 1e9
+    for _ in range(200):
+        c = (a + b) / 2
+        a, b = (c, b) if np.clip(c * x, lo, hi).sum() < P else (a, c)
+    f = np.clip(c * x, lo, hi)
+    counts = np.floor(f).astype(np.int64)
+    for e in np.argsort(-(f - counts)):
+        if counts.sum() >= P:
+            break
+        if counts[e] < hi:
+            counts[e] += 1
+    slots = np.repeat(np.arange(E), counts)[:P]
+    sel = slots.reshape(K, T).T.copy()
+    rng = np.random.default_rng(seed)
+    sel = sel[rng.permutation(T)].astype(np.int32)
+    lg = rng.standard_normal((T, K))
+    w = np.exp(lg - lg.max(axis=1, keepdims=True))
+    w = (w / w.sum(axis=1, keepdims=True)).astype(np.float32)
+    return sel, w, counts
+
+
+def cpu_pairs_baseline(seed, budget_s, x, sel, w):
+    """picchio's expert_apply (the per-pair work of forward_prefill's MoE,
+    picchio.c:1885-1905) on the host cores, time-bounded sample of the pairs."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle, Reference, reference_available, make_cfg
+    o = Oracle()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    cfg = make_cfg(n_layers=1, n_experts=E, ctx_len=16, vocab=64)
+    model = o.model_build(cfg, seed, threads)
+    if reference_available():
+        ref = Reference()
+        ref.attach(model, cfg)
+        run = lambda e, xt, dst, wt: ref.expert_apply(0, e, xt, dst, wt)
+        kind = "reference"
+    else:
+        run = lambda e, xt, dst, wt: o.expert_apply(model, 0, e, xt, dst, wt)
+        kind = "port"
+    dst = np.zeros(D, np.float32)
+    T = x.shape[0]
+    run(int(sel[0, 0]), x[0], dst, 1.0)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        t, k = divmod(n % (T * K), K)
+        run(int(sel[t, k]), x[t], dst, float(w[t, k]))
+        n += 1
+    dt = time.perf_counter() - t0
+    o.model_free(model)
+    flops = 2.0 * (INTER * D + D * HALF)
+    return {"value": round(n * flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": threads, "kind": kind,
+            "pairs_per_s": round(n / dt, 1),
+            "sample": f"{n} (token, expert) pairs of the config-3 routing through expert_apply, "
+                      f"{dt:.1f} s, OpenMP {threads} threads"}
+
+
+def run_prefill(args):
+    """T=2048 tokens through one GPT-OSS-20B MoE layer as
+    expert-grouped INT4 GEMMs on the int8 matrix cores (8192 pairs, Zipf 1.1
+    routing). value = algorithmic TFLOP/s (2 x pairs x (5760x2880 + 2880x2880))."""
+    import torch
+    import picchio_amd as pa
+    T = 2048
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=E, ctx_len=16, vocab=64)
+    eng = pa.Engine(cfg)
+    eng.build_synthetic(args.seed, what=1)
+    sel, w, counts = zipf_routing(T, E, K, args.seed)
+    x = np.random.default_rng(args.seed + 7).standard_normal((T, D)).astype(np.float32)
+    xd, sd, wd = eng.to_dev(x), eng.to_dev(sel), eng.to_dev(w)
+    out = eng.empty((T, D), torch.float32)
+    for _ in range(max(args.warmup, 1)):
+        eng.moe_forward_grouped(0, xd, out, sd, wd)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    ev0.record(eng.stream)
+    for _ in range(args.steps):
+        eng.moe_forward_grouped(0, xd, out, sd, wd)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms = ev0.elapsed_time(ev1) / args.steps
+    eng.profile(True)
+    for _ in range(5):
+        eng.moe_forward_grouped(0, xd, out, sd, wd)
+    gu_ms, gu_n = eng.profile_read(pa.PROF_EXPERT_GATE_UP)
+    dn_ms, dn_n = eng.profile_read(pa.PROF_EXPERT_DOWN)
+    eng.profile(False)
+    gu_ms, dn_ms = gu_ms / gu_n, dn_ms / dn_n
+    eng.close()
+    P = T * K
+    flops = 2.0 * P * (INTER * D + D * HALF)
+    gu_flops = 2.0 * P * INTER * D
+    tiles = int(sum((c + 31) // 32 for c in counts))
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_pairs_baseline(args.seed, args.cpu_seconds, x, sel, w)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    tfs = flops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(tfs, 2), "unit": "TFLOP/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8x3 (int4 weights)",
+        "data": "synthetic",
+        "config": {"workload": "config3: prefill MoE layer, T=2048 tokens, 8192 (token, expert) pairs "
+                               "over 32 INT4 gs64 experts (Zipf 1.1, 16..512 per expert), expert-grouped "
+                               "int8 MFMA GEMMs (3 activation limbs)",
+                   "tokens": T, "pairs": P, "tiles_of_32": tiles,
+                   "pairs_per_expert": [int(c) for c in counts],
+                   "flops": flops, "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4),
+                   "int8_mfma_ops_executed": 3 * 2 * tiles * 32 * (INTER * D + D * HALF)},
+        "roofline": {"bound": "mfma", "achieved": round(gu_flops / (gu_ms * 1e-3) / 1e12, 1),
+                     "peak": 5000.0, "unit": "TFLOP/s",
+                     "frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / 5000.0, 4), "traffic": None,
+                     "kernel": "k_moe_mfma<SWIGLU> (gate_up, algorithmic flops vs the int8 dense peak)",
+                     "flops_per_launch": gu_flops, "mean_us": round(gu_ms * 1e3, 2)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,11 +372,11 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain read+write kernel over this many "
                          "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--mode", choices=["seq", "kernels", "decode"], default="kernels",
+    ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "
                          "kernel per sequence of steps; decode: config 2, the whole 20B-shaped "
-                         "model (use --steps 256)")
+                         "model (use --steps 256); prefill: config 3, grouped MFMA MoE (--steps 20)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
@@ -258,6 +384,9 @@ def main():
         sys.exit(2)
     if args.mode == "decode":
         run_decode(args)
+        return
+    if args.mode == "prefill":
+        run_prefill(args)
         return
 
     import torch

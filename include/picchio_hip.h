@@ -174,6 +174,29 @@ int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
 int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                    int32_t *sel_host, float *w_host);
 
+/* Expert-grouped prefill MoE on the int8 matrix cores (forward_prefill's
+ * MoE, picchio.c:1829-1916, as one grouped GEMM per projection): the T*topk
+ * (token, expert) pairs are grouped by expert; activations are quantized by
+ * pk_quantize_act_i8x3; per 64-column scale group the int32 dot products are
+ * exact, then folded in fp32 (within ~1e-6 of the reference's fp32 path).
+ * sel_dev [T][topk] / w_dev [T][topk] (combine weights, softmax x
+ * routed_scale): the routing to use, both or neither (null: the layer's
+ * router). out_dev [T][hidden] = each token's weighted sum in the batch's
+ * first-request expert order. act_dev [T*topk][moe_inter/2] and eo_dev
+ * [T*topk][hidden] (pair p = t*topk + k) optionally receive the SwiGLU
+ * activations and expert outputs. */
+int pk_moe_forward_grouped(pk_engine *e, int layer, const float *x_dev, int T,
+                           const int32_t *sel_dev, const float *w_dev, float *out_dev,
+                           float *act_dev, float *eo_dev);
+
+/* Integer activation quantization of the grouped path: per row, k = binary
+ * exponent of max|x| (x = m 2^k, m in [0.5,1)), A = rint(x 2^(20-k)), split
+ * as A = a0 2^14 + a1 2^7 + a2 into limbs_dev[3][rows][cols] (int8, column
+ * order as x); exps_dev[rows] = k. No reference counterpart: the reference
+ * keeps fp32 activations; this is the exact integer form the MFMA path uses. */
+int pk_quantize_act_i8x3(pk_engine *e, const float *x_dev, int rows, int cols,
+                         int8_t *limbs_dev, int32_t *exps_dev);
+
 /* Batched form for T tokens at once (the expert-grouped prefill of
  * forward_prefill, picchio.c:1829-1916): x_dev[T][hidden] -> out_dev[T][hidden];
  * sel_dev[T][topk] / w_dev[T][topk] optional device outputs. */

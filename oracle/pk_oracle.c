@@ -827,3 +827,48 @@ int po_prefill_tokens(po_model *m, const int *ids, int n, int pos_base, int batc
     }
     return last;
 }
+
+/* ═══════════════ the grouped int8 path's arithmetic (not a reference function) ═══════════════ */
+
+void po_act_limbs(const float *x, int rows, int cols, int8_t *limbs, int32_t *exps) {
+    const int64_t plane = (int64_t)rows * cols;
+    for (int r = 0; r < rows; r++) {
+        const float *xr = x + (int64_t)r * cols;
+        float m = 0.0f;
+        for (int i = 0; i < cols; i++) m = fmaxf(m, fabsf(xr[i]));
+        int k = 0;
+        if (m > 0.0f) (void)frexpf(m, &k);
+        exps[r] = k;
+        for (int i = 0; i < cols; i++) {
+            int A = (int)rintf(ldexpf(xr[i], 20 - k));
+            int a0 = (A + 8192) >> 14;
+            int rem = A - a0 * 16384;
+            int a1 = (rem + 64) >> 7;
+            int a2 = rem - a1 * 128;
+            int64_t o = (int64_t)r * cols + i;
+            limbs[o] = (int8_t)a0;
+            limbs[plane + o] = (int8_t)a1;
+            limbs[2 * plane + o] = (int8_t)a2;
+        }
+    }
+}
+
+void po_mfma_matvec(const uint8_t *q4, const float *s, const float *bias, int O, int I,
+                    const int8_t *l0, const int8_t *l1, const int8_t *l2, int k, float *y) {
+    const int ng = I / 64, rb = (I + 1) / 2;
+    for (int o = 0; o < O; o++) {
+        const uint8_t *w = q4 + (int64_t)o * rb;
+        float acc = 0.0f;
+        for (int g = 0; g < ng; g++) {
+            int32_t C = 0;
+            for (int i = g * 64; i < g * 64 + 64; i++) {
+                const int nib = (i & 1) ? (w[i >> 1] >> 4) : (w[i >> 1] & 15);
+                const int A = l0[i] * 16384 + l1[i] * 128 + l2[i];
+                C += A * (nib - 8);
+            }
+            acc = fmaf(16.0f * s[(int64_t)o * ng + g], (float)C, acc);
+        }
+        y[o] = ldexpf(acc, k - 24);
+        if (bias) y[o] = y[o] + bias[o];
+    }
+}

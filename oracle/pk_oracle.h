@@ -108,6 +108,18 @@ int po_prefill_tokens(po_model *m, const int *ids, int n, int pos_base, int batc
 /* greedy branch of sample_logits (picchio.c:1555-1560). */
 int po_argmax(const float *logits, int n);
 
+/* ── the GPU's expert-grouped (int8 matrix core) path, restated ──
+ * Not a reference function: the exact arithmetic the library's grouped
+ * prefill uses, so its integer parts and fold order can be checked bit for
+ * bit. Per row: k = binary exponent of max|x| (0 if all zero),
+ * A = rint(x 2^(20-k)) = a0 2^14 + a1 2^7 + a2, limbs[3][rows][cols]. */
+void po_act_limbs(const float *x, int rows, int cols, int8_t *limbs, int32_t *exps);
+/* y[o] = (sum_g fma-fold of (16 s[o][g]) * (float) C_g) 2^(k-24) + bias[o],
+ * C_g = sum over the group of A q (exact int32), for one activation row
+ * given as its three limb rows (l0, l1, l2) and exponent k. */
+void po_mfma_matvec(const uint8_t *q4, const float *s, const float *bias, int O, int I,
+                    const int8_t *l0, const int8_t *l1, const int8_t *l2, int k, float *y);
+
 #ifdef __cplusplus
 }
 #endif

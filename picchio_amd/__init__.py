@@ -116,6 +116,8 @@ def lib():
         "pk_expert_down": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
         "pk_moe_forward": (C.c_int, [vp, C.c_int, vp, vp, vp, vp]),
         "pk_moe_forward_batch": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
+        "pk_moe_forward_grouped": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp, vp, vp]),
+        "pk_quantize_act_i8x3": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
         "pk_gqa_attention": (C.c_int, [vp, C.c_int, vp, C.c_int, vp]),
         "pk_forward_token": (C.c_int, [vp, C.c_int, C.c_int, vp, vp]),
         "pk_prefill_tokens": (C.c_int, [vp, vp, C.c_int, C.c_int, vp]),
@@ -327,6 +329,23 @@ class Engine:
 
     def expert_apply(self, layer, eid, x_dev, dst_dev, w):
         check(self.L.pk_expert_apply(self.h, layer, eid, ptr(x_dev), ptr(dst_dev), w))
+
+    def moe_forward_batch(self, layer, x_dev, out_dev, sel_dev=None, w_dev=None):
+        T = x_dev.shape[0]
+        check(self.L.pk_moe_forward_batch(self.h, layer, ptr(x_dev), T, ptr(out_dev),
+                                          ptr(sel_dev) if sel_dev is not None else None,
+                                          ptr(w_dev) if w_dev is not None else None))
+
+    def moe_forward_grouped(self, layer, x_dev, out_dev, sel_dev=None, w_dev=None, act_dev=None,
+                            eo_dev=None):
+        T = x_dev.shape[0]
+        opt = lambda t: ptr(t) if t is not None else None
+        check(self.L.pk_moe_forward_grouped(self.h, layer, ptr(x_dev), T, opt(sel_dev), opt(w_dev),
+                                            ptr(out_dev), opt(act_dev), opt(eo_dev)))
+
+    def quantize_act_i8x3(self, x_dev, limbs_dev, exps_dev):
+        rows, cols = x_dev.shape
+        check(self.L.pk_quantize_act_i8x3(self.h, ptr(x_dev), rows, cols, ptr(limbs_dev), ptr(exps_dev)))
 
     def expert_gate_up(self, layer, eids_dev, x_dev, act_dev):
         check(self.L.pk_expert_gate_up(self.h, layer, ptr(eids_dev), eids_dev.numel(),

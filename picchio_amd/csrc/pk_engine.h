@@ -101,6 +101,10 @@ struct pk_engine {
     int p_cap = 0;
     float *p_H = nullptr, *p_XN = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_part = nullptr;
     int32_t *p_ids = nullptr;
+    // grouped MFMA scratch for up to g_cap pairs (pk_prefill.hip)
+    int64_t g_cap = 0;
+    int8_t *g_limbs = nullptr;
+    int32_t *g_exps = nullptr, *g_pairs = nullptr, *g_tiles = nullptr;
 };
 
 int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes);
@@ -125,6 +129,29 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out);
 int pk_check_layer_experts(pk_engine *e, int layer);
 pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
+
+// ── expert-grouped MFMA GEMM (pk_mfma.hip) ──
+struct pk_mfma_args {
+    const uint8_t *base;                       // expert store
+    int64_t slot_stride, off_tiles, off_scales, off_bias;
+    int32_t slot_base;                         // layer * n_experts
+    int O, NG;                                 // output rows, 64-column groups
+    const int8_t *limbs;                       // 3 planes of activation limbs (permuted columns)
+    int64_t plane;                             // bytes between limb planes
+    int lrow;                                  // bytes per activation row (= its columns)
+    const int32_t *exps;                       // per activation row: scale exponent
+    const int32_t *pairs;                      // pair ids grouped by expert
+    int x_div;                                 // activation row of pair p = p / x_div
+    const int32_t *tile_exp, *tile_beg, *tile_cnt, *n_tiles;
+    float *y;                                  // output rows by pair id
+    int64_t y_stride;
+    float lim, alpha;                          // SwiGLU clamp / slope
+};
+int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, int8_t *limbs, int64_t plane,
+                        int32_t *exps, int permuted, hipStream_t st);
+int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int32_t *tile_exp,
+                          int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st);
+int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
 
 // decode driver pieces (pk_decode.hip) reused by the prompt driver
 int pk_decode_reserve(pk_engine *e);

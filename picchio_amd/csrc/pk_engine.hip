@@ -147,7 +147,8 @@ static void engine_free(pk_engine *e) {
                     e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
-                    e->p_part, e->p_ids, e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
+                    e->p_part, e->p_ids, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
+                    e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {

@@ -14,6 +14,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 namespace {
 
 __global__ __launch_bounds__(256) void k_embed_rows(const int32_t *ids, const float *embed, int vocab,
@@ -135,6 +137,110 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     return PK_OK;
 }
 
+static int grouped_reserve(pk_engine *e, int T) {
+    const pk_cfg *c = &e->c;
+    const int64_t P = (int64_t)T * c->topk;
+    if (P <= e->g_cap) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "grouped buffers must be sized before capturing a graph");
+    PK_HIP(hipStreamSynchronize(e->stream));
+    void *ptrs[] = {e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles};
+    for (void *p : ptrs) pk_dev_free(e, p);
+    e->g_limbs = nullptr;
+    e->g_exps = e->g_pairs = e->g_tiles = nullptr;
+    e->g_cap = 0;
+    const int64_t plane = std::max((int64_t)T * c->hidden, P * (c->moe_inter / 2));
+    const int64_t max_tiles = (P + 31) / 32 + c->n_experts;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_limbs, 3 * plane));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_exps, std::max((int64_t)T, P) * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_pairs, P * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_tiles, (3 * max_tiles + 1) * 4));
+    e->g_cap = P;
+    return PK_OK;
+}
+
+// The same MoE as moe_rows on the int8 matrix cores: pairs grouped by expert,
+// activations as three int8 limbs, gate_up (+SwiGLU) and down as grouped
+// GEMMs over 32-pair tiles (pk_mfma.hip), then the per-token sum in the
+// batch's expert order. sel_in / w_in: routing supplied by the caller
+// (device [T][K], combine weights already x routed_scale), else the router's.
+static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
+                         const int32_t *sel_in, const float *w_in) {
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
+    const int P = T * K;
+    PK_TRY(batch_reserve(e, T));
+    PK_TRY(grouped_reserve(e, T));
+    if (sel_in) {
+        PK_HIP(hipMemcpyAsync(e->b_sel, sel_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
+        PK_HIP(hipMemcpyAsync(e->b_w, w_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
+    } else {
+        const pk_layer_dev &d = e->L[layer];
+        PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
+        PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr,
+                                    e->stream));
+    }
+    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(64), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+    PK_HIP(hipGetLastError());
+    const int max_tiles = (P + 31) / 32 + E;
+    int32_t *tile_exp = e->g_tiles, *tile_beg = tile_exp + max_tiles, *tile_cnt = tile_beg + max_tiles;
+    int32_t *n_tiles = tile_cnt + max_tiles;
+    PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->g_pairs, tile_exp, tile_beg, tile_cnt, n_tiles, e->stream));
+    const int64_t plane = std::max((int64_t)T * D, (int64_t)P * half);
+    pk_mfma_args a{};
+    a.base = e->store;
+    a.slot_stride = e->ex.stride;
+    a.slot_base = layer * E;
+    a.limbs = e->g_limbs;
+    a.plane = plane;
+    a.exps = e->g_exps;
+    a.pairs = e->g_pairs;
+    a.tile_exp = tile_exp; a.tile_beg = tile_beg; a.tile_cnt = tile_cnt; a.n_tiles = n_tiles;
+    a.lim = c->swiglu_limit;
+    a.alpha = c->swiglu_alpha;
+    // gate_up + SwiGLU: activation rows are the T tokens
+    PK_TRY(pk_launch_act_limbs(x, D, T, D, e->g_limbs, plane, e->g_exps, 1, e->stream));
+    a.off_tiles = e->ex.off_gu_tiles; a.off_scales = e->ex.off_gu_scales; a.off_bias = e->ex.off_gu_bias;
+    a.O = c->moe_inter; a.NG = D / 64; a.lrow = D; a.x_div = K;
+    a.y = e->b_act; a.y_stride = half;
+    int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
+    PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_SWIGLU, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    // down: activation rows are the P pairs' SwiGLU outputs
+    PK_TRY(pk_launch_act_limbs(e->b_act, half, P, half, e->g_limbs, plane, e->g_exps, 1, e->stream));
+    a.off_tiles = e->ex.off_dn_tiles; a.off_scales = e->ex.off_dn_scales; a.off_bias = e->ex.off_dn_bias;
+    a.O = D; a.NG = half / 64; a.lrow = half; a.x_div = 1;
+    a.y = e->b_eo; a.y_stride = D;
+    ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
+    PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_PLAIN, e->stream));
+    PK_TRY(pk_prof_end(e, ps));
+    hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
+                       e->b_eo, e->b_w, e->b_perm, K, D);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+extern "C" int pk_moe_forward_grouped(pk_engine *e, int layer, const float *x_dev, int T,
+                                      const int32_t *sel_dev, const float *w_dev, float *out_dev,
+                                      float *act_dev, float *eo_dev) {
+    PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(!sel_dev == !w_dev, PK_ERR_ARG, "sel_dev and w_dev go together");
+    PK_TRY(pk_check_layer_experts(e, layer));
+    PK_TRY(moe_rows_mfma(e, layer, x_dev, T, out_dev, nullptr, sel_dev, w_dev));
+    const pk_cfg *c = &e->c;
+    const size_t P = (size_t)T * c->topk;
+    if (act_dev)
+        PK_HIP(hipMemcpyAsync(act_dev, e->b_act, P * (c->moe_inter / 2) * 4, hipMemcpyDeviceToDevice, e->stream));
+    if (eo_dev)
+        PK_HIP(hipMemcpyAsync(eo_dev, e->b_eo, P * c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
+    return PK_OK;
+}
+
+extern "C" int pk_quantize_act_i8x3(pk_engine *e, const float *x_dev, int rows, int cols, int8_t *limbs_dev,
+                                    int32_t *exps_dev) {
+    PK_CHECK(e && x_dev && limbs_dev && exps_dev && rows > 0 && cols > 0, PK_ERR_ARG, "bad argument");
+    return pk_launch_act_limbs(x_dev, cols, rows, cols, limbs_dev, (int64_t)rows * cols, exps_dev, 0, e->stream);
+}
+
 extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
                                     float *out_dev, int32_t *sel_dev, float *w_dev) {
     PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
@@ -174,7 +280,7 @@ static int prefill_reserve(pk_engine *e, int B) {
 // pos_base..pos_base+n-1; the greedy next token goes to the decode state
 // (and to out_toks when given).
 static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int n, int pos_base,
-                         int32_t *out_toks, int out_cap) {
+                         int32_t *out_toks, int out_cap, bool mfma) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden;
     hipLaunchKernelGGL(k_embed_rows, dim3(n), dim3(256), 0, e->stream, ids_dev, e->embed, c->vocab, e->p_H, D);
@@ -183,7 +289,10 @@ static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].in_ln, D, c->eps, n, e->stream));
         PK_TRY(pk_attention_rows(e, l, nullptr, pos_base, n, e->p_XN, e->p_qkv, e->p_part, e->p_att, e->p_H));
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n, e->stream));
-        PK_TRY(moe_rows(e, l, e->p_XN, n, e->p_H, e->p_H));
+        if (mfma)
+            PK_TRY(moe_rows_mfma(e, l, e->p_XN, n, e->p_H, e->p_H, nullptr, nullptr));
+        else
+            PK_TRY(moe_rows(e, l, e->p_XN, n, e->p_H, e->p_H));
     }
     PK_TRY(pk_launch_rmsnorm(e->hn, e->p_H + (int64_t)(n - 1) * D, e->final_norm, D, c->eps, 1, e->stream));
     PK_TRY(pk_set_state(e, last_tok, pos_base + n - 1));
@@ -198,12 +307,16 @@ int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_
         return PK_OK;
     }
     const int B = batch < n ? batch : n;
+    // PK_PREFILL_MFMA=1: the chunk's MoE on the int8 matrix cores (grouped GEMM)
+    const char *mv = getenv("PK_PREFILL_MFMA");
+    const bool mfma = mv && atoi(mv) != 0;
     PK_TRY(prefill_reserve(e, B));
     PK_TRY(batch_reserve(e, B));
     PK_HIP(hipMemcpyAsync(e->p_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
     for (int off = 0; off < n; off += B) {
         const int len = n - off < B ? n - off : B;
-        PK_TRY(prefill_chunk(e, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap));
+        PK_TRY(prefill_chunk(e, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap,
+                             mfma));
     }
     PK_HIP(hipStreamSynchronize(e->stream));           // ids is the caller's pageable memory
     return PK_OK;

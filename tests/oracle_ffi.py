@@ -82,6 +82,9 @@ class Oracle:
         self.forward_prefill = _bind(L, "po_forward_prefill", C.c_int, vp, i32p, C.c_int, C.c_int)
         self.prefill_tokens = _bind(L, "po_prefill_tokens", C.c_int, vp, i32p, C.c_int, C.c_int, C.c_int)
         self.argmax = _bind(L, "po_argmax", C.c_int, f32p, C.c_int)
+        self.act_limbs = _bind(L, "po_act_limbs", None, f32p, C.c_int, C.c_int, i8p, i32p)
+        self.mfma_matvec = _bind(L, "po_mfma_matvec", None, u8p, f32p, _nd(np.float32), C.c_int, C.c_int,
+                                 i8p, i8p, i8p, C.c_int, f32p)
 
     def normal(self, seed, kind, layer, idx, n, std=1.0, first=0):
         out = np.empty(n, np.float32)
