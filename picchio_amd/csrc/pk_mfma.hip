@@ -27,7 +27,8 @@ typedef int pk_v4i __attribute__((ext_vector_type(4)));
 typedef int pk_v16i __attribute__((ext_vector_type(16)));
 
 constexpr int TT = 32;        // tokens per tile (MFMA N)
-constexpr int NWAVE = 4;      // waves per workgroup, 32 output rows each
+constexpr int NWAVE = 8;      // waves per workgroup, 32 output rows each
+constexpr int NTHR = NWAVE * 64;
 constexpr int WG_ROWS = NWAVE * 32;
 
 // Position of column u (0..15) of a 16-column chunk in the operand byte order
@@ -69,22 +70,25 @@ __global__ __launch_bounds__(256) void k_act_limbs(const float *__restrict__ x, 
 }
 
 // Stable grouping of the P = T*K (token, expert) pairs by expert, and the
-// tile list: tile j = up to 32 consecutive pairs of one expert.
+// tile list: tile j = up to 32 consecutive pairs of one expert. One
+// workgroup: counts by LDS atomics, then each wave places the pairs of its
+// experts in order with ballots (routing staged in LDS when it fits).
+constexpr int GP_LDS = 16384;
 __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict__ sel, int P, int E,
                                                       int32_t *__restrict__ pairs, int32_t *__restrict__ tile_exp,
                                                       int32_t *__restrict__ tile_beg,
                                                       int32_t *__restrict__ tile_cnt, int32_t *n_tiles) {
     __shared__ int cnt[128], off[129];
+    __shared__ int s_sel[GP_LDS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    for (int e = wave; e < E; e += nw) {
-        int run = 0;
-        for (int b = 0; b < P; b += 64) {
-            const int i = b + lane;
-            const bool hit = i < P && sel[i] == e;
-            run += __popcll(__ballot(hit));
-        }
-        if (lane == 0) cnt[e] = run;
+    const bool staged = P <= GP_LDS;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        const int e = sel[i];
+        if (staged) s_sel[i] = e;
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
     if (threadIdx.x == 0) {
@@ -105,7 +109,7 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
         int run = off[e];
         for (int b = 0; b < P; b += 64) {
             const int i = b + lane;
-            const bool hit = i < P && sel[i] == e;
+            const bool hit = i < P && (staged ? s_sel[i] : sel[i]) == e;
             const uint64_t m = __ballot(hit);
             if (hit) pairs[run + __popcll(m & lt)] = i;
             run += __popcll(m);
@@ -124,11 +128,70 @@ __device__ __forceinline__ void expand_w(uint4 w, pk_v4i &o0, pk_v4i &o1) {
 }  // namespace
 
 // Grouped expert GEMM (pk_mfma_args in pk_engine.h): grid (max tiles,
-// ceil(O / 128)), 256 threads. Tile j of expert e holds its up to 32 pairs;
-// the activation row of pair p is p / x_div.
+// ceil(O / 256)), 512 threads. Tile j of expert e holds its up to 32 pairs;
+// the activation row of pair p is p / x_div. Wave w computes output rows
+// row0 .. row0+31 for the tile's 32 pairs. The K loop runs in stages of G
+// scale groups: the stage's activation limbs and scales are staged in LDS
+// (double-buffered, one barrier per stage) while the next stage's operands
+// are fetched into registers.
+constexpr int G = 3;                      // scale groups per stage (45 = 15 x 3)
+constexpr int BROW = G * 64 + 16;         // LDS bytes per token row (padded: no bank conflicts)
+constexpr int BCH = 3 * TT * G * 4;       // 16-byte activation chunks per stage
+
+// Operands of stage st into registers: activation chunks (limb, token,
+// 16-byte quarter of the stage's G groups), the stage's scales of the
+// workgroup's 128 rows, and this lane's weight bytes of the G groups.
+static_assert(G == 3 && NTHR == 512 && BCH == 2 * 512 + 128, "stage loads assume 3 groups, 512 threads");
+
+__device__ __forceinline__ const uint4 *chunk_src(const pk_mfma_args &a, int st, const int *tok_row, int c) {
+    const int l = c / (TT * G * 4), r = c - l * (TT * G * 4), t = r / (G * 4), q = r - t * (G * 4);
+    return reinterpret_cast<const uint4 *>(a.limbs + l * a.plane + (int64_t)tok_row[t] * a.lrow +
+                                           st * (G * 64) + q * 16);
+}
+__device__ __forceinline__ int chunk_dst(int c) {              // byte offset in one stage buffer
+    const int l = c / (TT * G * 4), r = c - l * (TT * G * 4), t = r / (G * 4), q = r - t * (G * 4);
+    return (l * TT + t) * BROW + q * 16;
+}
+
+// Operands of stage st into registers: activation chunks c = tid + 512 u
+// (limb, token, 16-byte quarter of the stage's G groups; u = 2 only for
+// tid < 128), the stage's scales of the workgroup's 256 rows (tid < 192),
+// and this lane's weight bytes of the G groups.
+#define MFMA_LOAD_STAGE(st)                                                                          \
+    do {                                                                                             \
+        const int t0_ = threadIdx.x;                                                                 \
+        rb0 = *chunk_src(a, (st), tok_row, t0_);                                                     \
+        rb1 = *chunk_src(a, (st), tok_row, t0_ + NTHR);                                              \
+        if (t0_ < 128) rb2 = *chunk_src(a, (st), tok_row, t0_ + 2 * NTHR);                           \
+        if (t0_ < G * (WG_ROWS / 4)) {                                                               \
+            const int rr_ = rowW + (t0_ % (WG_ROWS / 4)) * 4;                                        \
+            if (rr_ < a.O)                                                                           \
+                rsv = *reinterpret_cast<const float4 *>(                                             \
+                    scw + ((int64_t)(rr_ >> 6) * a.NG + (st) * G + t0_ / (WG_ROWS / 4)) * 64 +       \
+                    (rr_ & 63));                                                                     \
+        }                                                                                            \
+        if (active) {                                                                                \
+            rw0 = wt[(int64_t)((st) * G + 0) * 128];                                                 \
+            rw1 = wt[(int64_t)((st) * G + 1) * 128];                                                 \
+            rw2 = wt[(int64_t)((st) * G + 2) * 128];                                                 \
+        }                                                                                            \
+    } while (0)
+
+#define MFMA_STORE_STAGE(buf)                                                                        \
+    do {                                                                                             \
+        const int t0_ = threadIdx.x;                                                                 \
+        int8_t *bb_ = &bsh[buf][0][0][0];                                                            \
+        *reinterpret_cast<uint4 *>(bb_ + chunk_dst(t0_)) = rb0;                                      \
+        *reinterpret_cast<uint4 *>(bb_ + chunk_dst(t0_ + NTHR)) = rb1;                               \
+        if (t0_ < 128) *reinterpret_cast<uint4 *>(bb_ + chunk_dst(t0_ + 2 * NTHR)) = rb2;            \
+        if (t0_ < G * (WG_ROWS / 4))                                                                 \
+            *reinterpret_cast<float4 *>(&ssh[buf][t0_ / (WG_ROWS / 4)][(t0_ % (WG_ROWS / 4)) * 4]) = rsv; \
+    } while (0)
+
 template <int EPI>
-__global__ __launch_bounds__(256) void k_moe_mfma(pk_mfma_args a) {
-    __shared__ __attribute__((aligned(16))) int8_t bsh[3][TT][64];
+__global__ __launch_bounds__(NTHR) void k_moe_mfma(pk_mfma_args a) {
+    __shared__ __attribute__((aligned(16))) int8_t bsh[2][3][TT][BROW];
+    __shared__ __attribute__((aligned(16))) float ssh[2][G][WG_ROWS];
     __shared__ int tok_row[TT];
     __shared__ int tok_exp[TT];
     const int j = blockIdx.x;
@@ -143,70 +206,57 @@ __global__ __launch_bounds__(256) void k_moe_mfma(pk_mfma_args a) {
         tok_exp[n] = a.exps[row];
     }
     const uint8_t *base = a.base + (int64_t)(a.slot_base + e) * a.slot_stride;
-    const int row0 = blockIdx.y * WG_ROWS + wave * 32;      // this wave's first output row
+    const int rowW = blockIdx.y * WG_ROWS;                   // workgroup's first output row
+    const int row0 = rowW + wave * 32;                       // this wave's first output row
     const bool active = row0 < a.O;
-    const int rb = row0 >> 6, r64 = (row0 & 63);             // HBM tile row block, offset in it
+    const int rb = row0 >> 6, r64 = (row0 & 63);
     const int h = lane >> 5, n = lane & 31;
     const uint4 *wt = reinterpret_cast<const uint4 *>(base + a.off_tiles + (int64_t)rb * a.NG * 2048 +
                                                       h * 1024 + 16 * (r64 + n));
-    const float *sc = reinterpret_cast<const float *>(base + a.off_scales) + (int64_t)rb * a.NG * 64 +
-                      r64 + 4 * h;
+    const float *scw = reinterpret_cast<const float *>(base + a.off_scales);
+    const int n_stage = a.NG / G;
     __syncthreads();
 
+    const uint4 z4 = make_uint4(0, 0, 0, 0);
+    uint4 rb0 = z4, rb1 = z4, rb2 = z4, rw0 = z4, rw1 = z4, rw2 = z4;
+    float4 rsv = make_float4(0.f, 0.f, 0.f, 0.f);
     float acc[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) acc[v] = 0.0f;
-    // cooperative activation-tile load: 384 chunks of 16 B (limb, token, quarter)
-    const int c0 = threadIdx.x, c1 = threadIdx.x + 256;
-    auto src = [&](int c, int g) -> const uint4 * {
-        const int l = c >> 7, t = (c >> 2) & 31, q = c & 3;
-        return reinterpret_cast<const uint4 *>(a.limbs + l * a.plane + (int64_t)tok_row[t] * a.lrow + g * 64 +
-                                               q * 16);
-    };
-    // operands of group g are fetched while group g-1 computes
-    uint4 v0 = *src(c0, 0), v1 = make_uint4(0, 0, 0, 0), w = make_uint4(0, 0, 0, 0);
-    if (c1 < 384) v1 = *src(c1, 0);
-    float4 s4[4];
-    if (active) {
-        w = wt[0];
-#pragma unroll
-        for (int b = 0; b < 4; ++b) s4[b] = *reinterpret_cast<const float4 *>(sc + 8 * b);
-    }
-    for (int g = 0; g < a.NG; ++g) {
-        __syncthreads();                                     // previous group's LDS reads done
-        reinterpret_cast<uint4 *>(&bsh[0][0][0])[c0] = v0;
-        if (c1 < 384) reinterpret_cast<uint4 *>(&bsh[0][0][0])[c1] = v1;
+    MFMA_LOAD_STAGE(0);
+    for (int st = 0; st < n_stage; ++st) {
+        const int buf = st & 1;
+        MFMA_STORE_STAGE(buf);
+        const uint4 wc0 = rw0, wc1 = rw1, wc2 = rw2;
         __syncthreads();
-        const uint4 wc = w;
-        float sc_g[16];
-#pragma unroll
-        for (int v = 0; v < 16; ++v) sc_g[v] = (&s4[v >> 2].x)[v & 3];
-        if (g + 1 < a.NG) {
-            v0 = *src(c0, g + 1);
-            if (c1 < 384) v1 = *src(c1, g + 1);
-            if (active) {
-                w = wt[(int64_t)(g + 1) * 128];
-#pragma unroll
-                for (int b = 0; b < 4; ++b)
-                    s4[b] = *reinterpret_cast<const float4 *>(sc + (g + 1) * 64 + 8 * b);
-            }
-        }
+        if (st + 1 < n_stage) MFMA_LOAD_STAGE(st + 1);
         if (!active) continue;
-        pk_v4i A0, A1;
-        expand_w(wc, A0, A1);
-        pk_v16i P[3];
 #pragma unroll
-        for (int l = 0; l < 3; ++l) {
-            const pk_v4i B0 = *reinterpret_cast<const pk_v4i *>(&bsh[l][n][32 * h]);
-            const pk_v4i B1 = *reinterpret_cast<const pk_v4i *>(&bsh[l][n][32 * h + 16]);
-            pk_v16i z = {};
-            z = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, z, 0, 0, 0);
-            P[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, z, 0, 0, 0);
-        }
+        for (int gi = 0; gi < G; ++gi) {
+            pk_v4i A0, A1;
+            expand_w(gi == 0 ? wc0 : gi == 1 ? wc1 : wc2, A0, A1);
+            pk_v16i P[3];
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-            const int C = (P[0][v] << 10) + (P[1][v] << 3) + (P[2][v] >> 4);
-            acc[v] = __builtin_fmaf(sc_g[v], (float)C, acc[v]);
+            for (int l = 0; l < 3; ++l) {
+                const int8_t *bp = &bsh[buf][l][n][gi * 64 + 32 * h];
+                const pk_v4i B0 = *reinterpret_cast<const pk_v4i *>(bp);
+                const pk_v4i B1 = *reinterpret_cast<const pk_v4i *>(bp + 16);
+                pk_v16i z = {};
+                z = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, z, 0, 0, 0);
+                P[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, z, 0, 0, 0);
+            }
+            const float *sp = &ssh[buf][gi][wave * 32 + 4 * h];
+#pragma unroll
+            for (int b4 = 0; b4 < 4; ++b4) {
+                const float4 s4 = *reinterpret_cast<const float4 *>(sp + 8 * b4);
+                const float sv4[4] = {s4.x, s4.y, s4.z, s4.w};
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int v = 4 * b4 + i;
+                    const int C = (P[0][v] << 10) + (P[1][v] << 3) + (P[2][v] >> 4);
+                    acc[v] = __builtin_fmaf(sv4[i], (float)C, acc[v]);
+                }
+            }
         }
     }
     if (!active || n >= cnt) return;
@@ -254,13 +304,13 @@ int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int3
 }
 
 int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st) {
-    PK_CHECK(a.O % 64 == 0 && a.NG > 0 && max_tiles > 0 && a.lrow % 64 == 0, PK_ERR_UNSUPPORTED,
-             "mfma gemm: O=%d NG=%d", a.O, a.NG);
+    PK_CHECK(a.O % 64 == 0 && a.NG > 0 && a.NG % G == 0 && max_tiles > 0 && a.lrow % 64 == 0,
+             PK_ERR_UNSUPPORTED, "mfma gemm: O=%d NG=%d (groups must be a multiple of %d)", a.O, a.NG, G);
     const dim3 grid(max_tiles, (a.O + WG_ROWS - 1) / WG_ROWS);
     if (epilogue == PK_EPI_SWIGLU)
-        hipLaunchKernelGGL(k_moe_mfma<PK_EPI_SWIGLU>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_moe_mfma<PK_EPI_SWIGLU>, grid, dim3(NTHR), 0, st, a);
     else
-        hipLaunchKernelGGL(k_moe_mfma<PK_EPI_PLAIN>, grid, dim3(256), 0, st, a);
+        hipLaunchKernelGGL(k_moe_mfma<PK_EPI_PLAIN>, grid, dim3(NTHR), 0, st, a);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

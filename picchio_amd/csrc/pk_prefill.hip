@@ -30,33 +30,38 @@ __global__ __launch_bounds__(256) void k_embed_rows(const int32_t *ids, const fl
 
 // forward_prefill's expert order (picchio.c:1846-1852, :1885-1902): experts are
 // ranked by first request, scanning positions, then k; each token adds its
-// experts in rank order. perm[p][j] = k of the token's j-th expert.
-__global__ __launch_bounds__(64) void k_uniq_perm(const int32_t *sel, int n, int K, int E, int32_t *perm) {
-    __shared__ int rank[128];
-    if (threadIdx.x == 0) {
-        for (int e = 0; e < E; ++e) rank[e] = -1;
+// experts in rank order. perm[p][j] = k of the token's j-th expert. One
+// workgroup: first request of each expert by atomic min, rank = number of
+// experts requested earlier, then each token orders its k by rank.
+__global__ __launch_bounds__(1024) void k_uniq_perm(const int32_t *sel, int n, int K, int E, int32_t *perm) {
+    __shared__ int first[128], rank[128];
+    const int P = n * K;
+    for (int e = threadIdx.x; e < E; e += blockDim.x) first[e] = 0x7fffffff;
+    __syncthreads();
+    for (int i = threadIdx.x; i < P; i += blockDim.x) {
+        const int e = sel[i];
+        if (e >= 0 && e < E) atomicMin(&first[e], i);
+    }
+    __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x) {
         int r = 0;
-        for (int i = 0; i < n * K; ++i) {
-            const int e = sel[i];
-            if (e >= 0 && e < E && rank[e] < 0) rank[e] = r++;
-        }
+        for (int f = 0; f < E; ++f) r += first[f] < first[e];
+        rank[e] = first[e] == 0x7fffffff ? 0x7fffffff : r;
     }
     __syncthreads();
     for (int p = threadIdx.x; p < n; p += blockDim.x) {
-        int ks[16], rk[16];
+        const int32_t *sp = sel + (int64_t)p * K;
         for (int k = 0; k < K; ++k) {
-            const int e = sel[p * K + k];
-            ks[k] = k;
-            rk[k] = (e >= 0 && e < E) ? rank[e] : 0x7fffffff;
+            const int ek = sp[k];
+            const int rk = (ek >= 0 && ek < E) ? rank[ek] : 0x7fffffff;
+            int pos = 0;
+            for (int k2 = 0; k2 < K; ++k2) {
+                const int e2 = sp[k2];
+                const int r2 = (e2 >= 0 && e2 < E) ? rank[e2] : 0x7fffffff;
+                pos += (r2 < rk) || (r2 == rk && k2 < k);
+            }
+            perm[(int64_t)p * K + pos] = k;
         }
-        for (int a = 1; a < K; ++a) {
-            const int kk = ks[a], rr = rk[a];
-            int b = a - 1;
-            while (b >= 0 && rk[b] > rr) { ks[b + 1] = ks[b]; rk[b + 1] = rk[b]; --b; }
-            ks[b + 1] = kk;
-            rk[b + 1] = rr;
-        }
-        for (int j = 0; j < K; ++j) perm[p * K + j] = ks[j];
     }
 }
 
@@ -112,7 +117,7 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     const pk_layer_dev &d = e->L[layer];
     PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
     PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr, e->stream));
-    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(64), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
     PK_HIP(hipGetLastError());
     pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = e->b_sel;
@@ -179,7 +184,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
         PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr,
                                     e->stream));
     }
-    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(64), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
     PK_HIP(hipGetLastError());
     const int max_tiles = (P + 31) / 32 + E;
     int32_t *tile_exp = e->g_tiles, *tile_beg = tile_exp + max_tiles, *tile_cnt = tile_beg + max_tiles;
