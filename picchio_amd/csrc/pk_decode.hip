@@ -380,9 +380,16 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     hipLaunchKernelGGL(k_attn_combine, dim3(H, n), dim3(64), 0, e->stream, st, pos_base, part, d.sinks, H,
                        hd, c->ctx_len, sliding, c->sliding_window, max_chunks, att);
     PK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4, n), dim3(256), 0, e->stream, h, att, d.wo, d.bo,
-                       H * hd, D);
-    PK_HIP(hipGetLastError());
+    if (n >= 4) {
+        // several rows: one read of wo per 32 rows
+        for (int r0 = 0; r0 < n; r0 += 32)
+            PK_TRY(pk_launch_gemm_skinny(h + (int64_t)r0 * D, att + (int64_t)r0 * H * hd, d.wo, d.bo,
+                                         n - r0 < 32 ? n - r0 : 32, H * hd, D, 1, e->stream));
+    } else {
+        hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4, n), dim3(256), 0, e->stream, h, att, d.wo, d.bo,
+                           H * hd, D);
+        PK_HIP(hipGetLastError());
+    }
     return pk_prof_end(e, ps);
 }
 

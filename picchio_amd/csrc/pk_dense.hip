@@ -118,11 +118,115 @@ __global__ __launch_bounds__(256) void k_gemv_f32_rows(float *__restrict__ y, co
     if (threadIdx.x == 0) y[(int64_t)s * O + o] = bias ? v + bias[o] : v;
 }
 
+// ───────────────── skinny fp32 GEMM: several inputs per weight read ─────────────────
+// Y[s][o] = (residual ? Y[s][o] : 0) + (X[s] . W[o] + bias[o]) for s < S <= SB.
+// A wave owns 4 rows of W and all SB inputs: per 256-column chunk each lane
+// takes one float4 of each row (read once from HBM) against the chunk's SB
+// inputs staged in LDS (4 x SB accumulators per lane). The 64 lanes' partial
+// sums are then reduce-scattered in 6 exchange steps, leaving each lane two
+// finished (row, input) sums. grid = ceil(O / 16) workgroups of 4 waves.
+constexpr int SK_KC = 256;                 // columns per staged chunk
+
+template <int SB>
+__global__ __launch_bounds__(256) void k_gemm_skinny(float *__restrict__ Y, const float *__restrict__ X,
+                                                     const float *__restrict__ W,
+                                                     const float *__restrict__ bias, int S, int I, int O,
+                                                     int residual) {
+    __shared__ __attribute__((aligned(16))) float xs[SB][SK_KC];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = blockIdx.x * 16 + wave * 4;
+    float acc[4 * SB];
+#pragma unroll
+    for (int i = 0; i < 4 * SB; ++i) acc[i] = 0.0f;
+    const float4 *w4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int row = min(row0 + r, O - 1);
+        w4[r] = reinterpret_cast<const float4 *>(W + (int64_t)row * I);
+    }
+    for (int k0 = 0; k0 < I; k0 += SK_KC) {
+        const int kc = min(SK_KC, I - k0);
+        __syncthreads();
+        for (int idx = threadIdx.x; idx < SB * (SK_KC / 4); idx += 256) {
+            const int s = idx / (SK_KC / 4), c4 = idx - s * (SK_KC / 4);
+            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (s < S && 4 * c4 < kc) v = *reinterpret_cast<const float4 *>(X + (int64_t)s * I + k0 + 4 * c4);
+            *reinterpret_cast<float4 *>(&xs[s][4 * c4]) = v;
+        }
+        __syncthreads();
+        float4 wv[4];
+        const bool in = 4 * lane < kc;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pk_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            if (in) t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4[r] + (k0 >> 2) + lane));
+            wv[r] = make_float4(t.x, t.y, t.z, t.w);
+        }
+#pragma unroll
+        for (int s = 0; s < SB; ++s) {
+            const float4 xv = *reinterpret_cast<const float4 *>(&xs[s][4 * lane]);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float a = acc[r * SB + s];
+                a = __builtin_fmaf(wv[r].x, xv.x, a);
+                a = __builtin_fmaf(wv[r].y, xv.y, a);
+                a = __builtin_fmaf(wv[r].z, xv.z, a);
+                a = __builtin_fmaf(wv[r].w, xv.w, a);
+                acc[r * SB + s] = a;
+            }
+        }
+    }
+    // reduce-scatter over the 64 lanes: at the step exchanging with lane ^ m
+    // the lane keeps the upper half of its c values if (lane & m), else the
+    // lower half, adding the partner's copy; after the six steps it holds the
+    // full sums of values 2*lane and 2*lane + 1 (value index = r * SB + s).
+    static_assert(SB == 32, "the exchange leaves 2 of 4 x 32 values per lane");
+#pragma unroll
+    for (int m = 32, c = 4 * SB; m >= 1; m >>= 1, c >>= 1) {
+        const bool upper = (lane & m) != 0;
+#pragma unroll
+        for (int i = 0; i < c / 2; ++i) {
+            const float lo = acc[i], hi = acc[i + c / 2];
+            acc[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, m, 64);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int idx = 2 * lane + j;
+        const int r = idx / SB, s = idx - r * SB;
+        const int row = row0 + r;
+        if (s < S && row < O) {
+            float v = acc[j];
+            if (bias) v = v + bias[row];
+            float *yp = Y + (int64_t)s * O + row;
+            *yp = residual ? *yp + v : v;
+        }
+    }
+}
+
+int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
+                          int residual, hipStream_t st) {
+    PK_CHECK(S > 0 && S <= 32 && I > 0 && O > 0, PK_ERR_ARG, "skinny gemm: bad shape");
+    PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0, PK_ERR_UNSUPPORTED,
+             "skinny gemm: needs 16-byte aligned rows (I=%d)", I);
+    hipLaunchKernelGGL(k_gemm_skinny<32>, dim3((O + 15) / 16), dim3(256), 0, st, y, x, W, bias, S, I, O,
+                       residual);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
                        int S, int I, int O, hipStream_t st) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv f32: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0,
              PK_ERR_UNSUPPORTED, "gemv f32: needs 16-byte aligned rows (I=%d)", I);
+    if (S >= 4 && O >= 256) {
+        // several inputs: one weight read per block of up to 32 inputs
+        for (int s0 = 0; s0 < S; s0 += 32)
+            PK_TRY(pk_launch_gemm_skinny(y + (int64_t)s0 * O, x + (int64_t)s0 * I, W, bias,
+                                         S - s0 < 32 ? S - s0 : 32, I, O, 0, st));
+        return PK_OK;
+    }
     if (O <= 2048) {
         hipLaunchKernelGGL(k_gemv_f32_rows, dim3(O, S), dim3(256), 0, st, y, x, W, bias, S, I, O);
     } else {

@@ -92,12 +92,13 @@ def test_quantizer_bitexact(gpu, oracle, O, I, gs):
 
 # ───────────────────────── dense matmul_qt ─────────────────────────
 
-@pytest.mark.parametrize("fmt", ["f32", "q8", "i4row"])
-def test_matmul_qt_formats(gpu, oracle, fmt):
+@pytest.mark.parametrize("fmt,S", [("f32", 2), ("f32", 7), ("f32", 37), ("q8", 2), ("i4row", 2)])
+def test_matmul_qt_formats(gpu, oracle, fmt, S):
+    """S >= 4 fp32 rows run the skinny GEMM (one weight read per 32 inputs)."""
     import torch
     import picchio_amd as pa
     cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
-    O, I, S = 300, 2880, 2
+    O, I = 300, (2900 if fmt == "f32" else 2880)      # f32: a ragged last 256-column chunk
     x = _rand((S, I), 9)
     y_ref = np.empty((S, O), np.float32)
     W = _rand((O, I), 10, 0.02)
