@@ -233,6 +233,96 @@ def run_decode(args):
     print(json.dumps(line))
 
 
+def run_decode120b(args):
+    """GPT-OSS-120B-shaped model (36 layers, 128 INT4 experts
+    per layer, ~65 GB of experts resident in HBM), a 4096-position KV context
+    filled with synthetic rows, then `steps` greedy decode steps at batch 1
+    (captured step graph) and at batch 32 (32 independent sequences in
+    lockstep). value = batch-1 tokens/s."""
+    import torch
+    import picchio_amd as pa
+    ctx, steps, B = 4096, args.steps, 32
+    cfg = pa.gptoss_cfg(n_layers=36, n_experts=128, ctx_len=ctx + steps + 1)
+    eng = pa.Engine(cfg)
+    t0 = time.perf_counter()
+    eng.build_synthetic(args.seed, what=7)
+    eng.sync()
+    print(f"[bench] 120B model built on the GPU: {eng.device_bytes() / 1e9:.2f} GB in "
+          f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
+    ev0 = torch.cuda.Event(enable_timing=True)
+    ev1 = torch.cuda.Event(enable_timing=True)
+    rng = np.random.default_rng(args.seed + 200)
+    # batch 1
+    eng.kv_fill_synthetic(0, ctx, args.seed)
+    tok = int(rng.integers(0, cfg.vocab))
+    warm = eng.decode_replay(tok, ctx, max(args.warmup, 1))
+    ev0.record(eng.stream)
+    toks1 = eng.decode_replay(tok, ctx, steps)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms1 = ev0.elapsed_time(ev1)
+    assert list(toks1[:len(warm)]) == list(warm), "decode is not deterministic"
+    eng.profile(True)
+    eng.forward_token(int(toks1[-1]), ctx + steps, None)
+    lm_ms, _ = eng.profile_read(pa.PROF_LM_HEAD)
+    eng.profile(False)
+    # batch 32
+    eng.batch_reserve(B)
+    for sq in range(B):
+        eng.kv_fill_synthetic(sq, ctx, args.seed + sq)
+    first = rng.integers(0, cfg.vocab, B).astype(np.int32)
+    eng.decode_batch(first, ctx, max(args.warmup, 1))
+    ev0.record(eng.stream)
+    out32 = eng.decode_batch(first, ctx, steps)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms32 = ev0.elapsed_time(ev1)
+    eng.close()
+    tok1 = steps / (ms1 * 1e-3)
+    tok32 = B * steps / (ms32 * 1e-3)
+    bpt1 = sum(decode_bytes_per_token(cfg, ctx + i) for i in range(steps)) / steps
+    # batch 32: expected distinct experts per layer under uniform routing
+    E, Kk = cfg.n_experts, cfg.topk
+    uniq = E * (1.0 - (1.0 - Kk / E) ** B)
+    expert = (cfg.moe_inter * D // 2 + cfg.moe_inter * (D // 64) * 4 + cfg.moe_inter * 4
+                           + D * HALF // 2 + D * (HALF // 64) * 4 + D * 4)
+    kv_bytes = lambda pos: sum(2 * 4 * (min(pos + 1, 128) if cfg.layer_type[l] == 0 else pos + 1) * 512
+                               for l in range(cfg.n_layers))
+    dense = bpt1 - cfg.n_layers * Kk * expert - kv_bytes(ctx + steps // 2)
+    bstep32 = dense + cfg.n_layers * uniq * expert + B * kv_bytes(ctx + steps // 2)
+    lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, first)
+        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    line = {
+        "metric": METRIC, "value": round(tok1, 2), "unit": "tok/s", "n_gpus": 1,
+        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms1 / steps, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "config4: GPT-OSS-120B-shaped greedy decode (36 layers, 128 INT4 experts, "
+                               "fp32 attention and lm_head), 4096-position synthetic KV context, "
+                               f"{steps} steps at batch 1 and at batch 32",
+                   "layers": cfg.n_layers, "experts": E, "vocab": cfg.vocab,
+                   "batch1_tok_s": round(tok1, 2), "batch1_bytes_per_token": int(bpt1),
+                   "batch1_hbm_gbps": round(bpt1 * tok1 / 1e9, 1),
+                   "batch32_tok_s": round(tok32, 2), "batch32_ms_per_step": round(ms32 / steps, 4),
+                   "batch32_bytes_per_step": int(bstep32),
+                   "batch32_hbm_gbps": round(bstep32 * steps / (ms32 * 1e-3) / 1e9, 1),
+                   "batch32_distinct_experts_per_layer": round(uniq, 1),
+                   "kv_context": "synthetic N(0,1) rows for positions 0..4095 of every sequence",
+                   "first_tokens_batch1": [int(t) for t in toks1[:6]],
+                   "first_tokens_batch32_seq0": [int(t) for t in out32[:6, 0]]},
+        "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(lm_bytes / (lm_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_lm_head_argmax<fp32> (201088 x 2880 GEMV + argmax)",
+                     "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line))
+
+
 def zipf_routing(T, E, K, seed, s=1.1, lo=16, hi=512):
     """BASELINE config 3 routing: per-expert pair counts proportional to
     (e+1)^-s, clipped to [lo, hi] and summing to T*K; slot i of the
@@ -372,11 +462,12 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain read+write kernel over this many "
                          "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill"], default="kernels",
+    ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill", "decode120b"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "
                          "kernel per sequence of steps; decode: config 2, the whole 20B-shaped "
-                         "model (use --steps 256); prefill: config 3, grouped MFMA MoE (--steps 20)")
+                         "model (use --steps 256); prefill: config 3, grouped MFMA MoE (--steps 20); "
+                         "decode120b: config 4, 120B shape at batch 1 and 32 (--steps 128)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
@@ -387,6 +478,9 @@ def main():
         return
     if args.mode == "prefill":
         run_prefill(args)
+        return
+    if args.mode == "decode120b":
+        run_decode120b(args)
         return
 
     import torch

@@ -174,6 +174,30 @@ int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
 int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                    int32_t *sel_host, float *w_host);
 
+/* ── several independent sequences ──
+ * picchio decodes one sequence; these run its forward_token arithmetic for
+ * n_seq sequences in lockstep (BASELINE config 4's batch-32 decode), each
+ * sequence with its own KV cache, every weight read once per step for all
+ * of them. Per sequence the result is forward_token's within the fp32 bar
+ * (fp32 dot products in a different order; MoE GEMVs bit-identical). */
+
+/* KV caches for n_seq sequences (sequence 0 is the one pk_forward_token,
+ * pk_prefill_tokens and pk_generate use). Growing the count clears every
+ * cache. */
+int pk_batch_reserve(pk_engine *e, int n_seq);
+/* Positions 0..n_pos-1 of sequence seq's cache, every layer, filled with
+ * deterministic N(0,1) rows (a synthetic prefilled context for decode
+ * benchmarks; no reference counterpart). */
+int pk_kv_fill_synthetic(pk_engine *e, int seq, int n_pos, uint64_t seed);
+/* prefill_tokens (picchio.c:1936-1975) into sequence seq's cache. */
+int pk_prefill_seq(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base,
+                   int32_t *next_host);
+/* n_steps greedy steps of sequences 0..n_seq-1 at positions pos..pos+n_steps-1,
+ * starting from toks_host[n_seq]; out_host[n_steps][n_seq] = the tokens
+ * produced (each step feeds the next on the device). */
+int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host, int pos, int n_steps,
+                    int32_t *out_host);
+
 /* Expert-grouped prefill MoE on the int8 matrix cores (forward_prefill's
  * MoE, picchio.c:1829-1916, as one grouped GEMM per projection): the T*topk
  * (token, expert) pairs are grouped by expert; activations are quantized by

@@ -130,6 +130,10 @@ def lib():
         "pk_moe_seq_reserve": (C.c_int, [vp, C.c_int]),
         "pk_moe_seq_trace": (C.c_int, [vp, vp]),
         "pk_decode_replay": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
+        "pk_batch_reserve": (C.c_int, [vp, C.c_int]),
+        "pk_kv_fill_synthetic": (C.c_int, [vp, C.c_int, C.c_int, C.c_uint64]),
+        "pk_prefill_seq": (C.c_int, [vp, C.c_int, vp, C.c_int, C.c_int, vp]),
+        "pk_decode_batch": (C.c_int, [vp, C.c_int, vp, C.c_int, C.c_int, vp]),
         "pk_capture_begin": (C.c_int, [vp]),
         "pk_capture_end": (C.c_int, [vp, C.POINTER(vp)]),
         "pk_graph_launch": (C.c_int, [vp, vp]),
@@ -310,6 +314,26 @@ class Engine:
         nxt = C.c_int32()
         check(self.L.pk_prefill_tokens(self.h, ptr(p), len(p), pos_base, C.byref(nxt)))
         return nxt.value
+
+    def batch_reserve(self, n_seq):
+        check(self.L.pk_batch_reserve(self.h, n_seq))
+
+    def kv_fill_synthetic(self, seq, n_pos, seed):
+        check(self.L.pk_kv_fill_synthetic(self.h, seq, n_pos, seed))
+
+    def prefill_seq(self, seq, ids, pos_base=0):
+        import numpy as np
+        p = np.ascontiguousarray(ids, np.int32)
+        nxt = C.c_int32()
+        check(self.L.pk_prefill_seq(self.h, seq, ptr(p), len(p), pos_base, C.byref(nxt)))
+        return nxt.value
+
+    def decode_batch(self, toks, pos, n_steps):
+        import numpy as np
+        t = np.ascontiguousarray(toks, np.int32)
+        out = np.empty((n_steps, len(t)), np.int32)
+        check(self.L.pk_decode_batch(self.h, len(t), ptr(t), pos, n_steps, ptr(out)))
+        return out
 
     def decode_replay(self, tok, pos, n_steps):
         import numpy as np

@@ -53,19 +53,22 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
     for (int i = threadIdx.x; i < D; i += 256) hn[i] = (ok ? row[i] : 0.0f) * r * w[i];
 }
 
-// Position of row r: the decode step's (device state) or pos_base + r for a
-// batch of consecutive prompt positions.
-__device__ __forceinline__ int row_pos(const pk_dstate *st, int pos_base, int r) {
-    return st ? st->pos : pos_base + r;
+// Position of row r: the decode step's (device state), or pos_base + r * step
+// (step 1: consecutive prompt positions; step 0: sequences at one position).
+__device__ __forceinline__ int row_pos(const pk_dstate *st, int pos_base, int step, int r) {
+    return st ? st->pos : pos_base + r * step;
 }
 
 // RoPE (picchio.c:455-473) on q [H][hd] and k [KVH][hd] at the row's position
 // with the host-built cos/sin table (attn_factor folded in), then kv_store
-// (picchio.c:492-498): K/V rows of this layer at that position. grid.y = row.
-__global__ void k_rope_kv(const pk_dstate *st, int pos_base, float *qkv, int64_t qkv_stride,
-                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl) {
-    const int pos = row_pos(st, pos_base, blockIdx.y);
+// (picchio.c:492-498): K/V rows of this layer at that position. grid.y = row;
+// row r's cache starts kv_row * r floats after Kl / Vl.
+__global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float *qkv, int64_t qkv_stride,
+                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl, int64_t kv_row) {
+    const int pos = row_pos(st, pos_base, pos_step, blockIdx.y);
     qkv += (int64_t)blockIdx.y * qkv_stride;
+    Kl += (int64_t)blockIdx.y * kv_row;
+    Vl += (int64_t)blockIdx.y * kv_row;
     const int half = hd / 2;
     const int n_pairs = (H + KVH) * half;
     const int kv_dim = KVH * hd;
@@ -106,10 +109,10 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 // in-order dot (uncontracted products added one by one, picchio.c:573-577 as
 // gcc builds it) times 1/sqrt(hd). Writes the chunk max, sum of exp(s - max)
 // and the exp-weighted V sum (flash-decoding partials).
-__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, const float *qkv,
-                                                         int64_t qkv_stride, const float *Kl,
-                                                         const float *Vl, int H, int KVH, int hd, int ctx,
-                                                         int sliding, int window, float *part,
+__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
+                                                         const float *qkv, int64_t qkv_stride, const float *Kl,
+                                                         const float *Vl, int64_t kv_row, int H, int KVH,
+                                                         int hd, int ctx, int sliding, int window, float *part,
                                                          int max_chunks) {
     __shared__ float q[128];
     __shared__ float p[ATT_CHUNK];
@@ -117,8 +120,10 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
     const int h = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
     qkv += (int64_t)r * qkv_stride;
     part += (int64_t)r * H * max_chunks * (hd + 2);
+    Kl += (int64_t)r * kv_row;
+    Vl += (int64_t)r * kv_row;
     int start, end;
-    att_window(row_pos(st, pos_base, r), ctx, sliding, window, start, end);
+    att_window(row_pos(st, pos_base, pos_step, r), ctx, sliding, window, start, end);
     const int t0 = start + c * ATT_CHUNK;
     const int n = min(ATT_CHUNK, end - t0 + 1);
     if (n <= 0) return;
@@ -163,13 +168,14 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
 
 // Combine the chunk partials of head h with the learned sink (picchio.c:586-604):
 // the sink joins the max and the denominator, not the value sum.
-__global__ void k_attn_combine(const pk_dstate *st, int pos_base, const float *part, const float *sinks,
-                               int H, int hd, int ctx, int sliding, int window, int max_chunks, float *att) {
+__global__ void k_attn_combine(const pk_dstate *st, int pos_base, int pos_step, const float *part,
+                               const float *sinks, int H, int hd, int ctx, int sliding, int window,
+                               int max_chunks, float *att) {
     const int h = blockIdx.x, r = blockIdx.y;
     part += (int64_t)r * H * max_chunks * (hd + 2);
     att += (int64_t)r * H * hd;
     int start, end;
-    att_window(row_pos(st, pos_base, r), ctx, sliding, window, start, end);
+    att_window(row_pos(st, pos_base, pos_step, r), ctx, sliding, window, start, end);
     const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
     const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
     float M = sinks[h];
@@ -351,34 +357,36 @@ int pk_check_model(pk_engine *e) {
 }
 
 // Attention of layer l for n rows of normalised input xn: the decode token
-// (st = device state, n = 1) or prompt positions pos_base .. pos_base+n-1
-// (st = null). Writes K/V, qkv [n][(H+2KVH)hd], att [n][H hd] and adds the
-// output projection into h [n][D] (residual).
-int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int n, const float *xn,
-                      float *qkv, float *part, float *att, float *h) {
+// (st = device state, n = 1), prompt positions pos_base .. pos_base+n-1 of
+// one sequence (pos_step 1, seq_step 0), or n sequences at one position
+// (pos_step 0, seq_step 1). Writes K/V, qkv [n][(H+2KVH)hd], att [n][H hd]
+// and adds the output projection into h [n][D] (residual).
+int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
+                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[l];
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
     const int kv_dim = KVH * hd, qkv_dim = (H + 2 * KVH) * hd;
-    float *Kl = e->K + (int64_t)l * c->ctx_len * kv_dim;
-    float *Vl = e->V + (int64_t)l * c->ctx_len * kv_dim;
+    const int64_t kv_row = (int64_t)seq_step * e->seq_stride;
+    float *Kl = e->K + seq0 * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
+    float *Vl = e->V + seq0 * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
     const int ps = pk_prof_begin(e, PK_PROF_ATTENTION);
     PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
     const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
-    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, qkv,
-                       (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl);
+    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, pos_step,
+                       qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
     PK_HIP(hipGetLastError());
     const int sliding = c->layer_type[l] == 0;
     const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
-    int chunks = st ? max_chunks : (pos_base + n + ATT_CHUNK - 1) / ATT_CHUNK;
+    int chunks = st ? max_chunks : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
     if (sliding) chunks = std::min(chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK);
     chunks = std::min(chunks, max_chunks);
-    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks, n), dim3(ATT_CHUNK), 0, e->stream, st, pos_base, qkv,
-                       (int64_t)qkv_dim, Kl, Vl, H, KVH, hd, c->ctx_len, sliding, c->sliding_window, part,
-                       max_chunks);
+    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks, n), dim3(ATT_CHUNK), 0, e->stream, st, pos_base, pos_step,
+                       qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,
+                       part, max_chunks);
     PK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_attn_combine, dim3(H, n), dim3(64), 0, e->stream, st, pos_base, part, d.sinks, H,
-                       hd, c->ctx_len, sliding, c->sliding_window, max_chunks, att);
+    hipLaunchKernelGGL(k_attn_combine, dim3(H, n), dim3(64), 0, e->stream, st, pos_base, pos_step, part, d.sinks,
+                       H, hd, c->ctx_len, sliding, c->sliding_window, max_chunks, att);
     PK_HIP(hipGetLastError());
     if (n >= 4) {
         // several rows: one read of wo per 32 rows
@@ -394,7 +402,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
 }
 
 static int attention_layer(pk_engine *e, int l) {
-    return pk_attention_rows(e, l, e->dstate, 0, 1, e->hn, e->qkv, e->attn_part, e->att, e->h);
+    return pk_attention_rows(e, l, e->dstate, 0, 0, 0, 0, 1, e->hn, e->qkv, e->attn_part, e->att, e->h);
 }
 
 // One forward_token step with tok/pos in device state; logits optional.
@@ -517,7 +525,7 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
                 pk_set_error("generate: graph capture failed"); rc = PK_ERR_HIP; break;
             }
         }
-        if ((rc = pk_prefill_run(e, prompt, n_prompt, 0, out_dev, n_steps)) != PK_OK) break;
+        if ((rc = pk_prefill_run(e, 0, prompt, n_prompt, 0, out_dev, n_steps)) != PK_OK) break;
         for (int i = 0; i < n_steps - 1 && rc == PK_OK; ++i)
             if (hipGraphLaunch(exec, e->stream) != hipSuccess) { pk_set_error("generate: launch failed"); rc = PK_ERR_HIP; }
         if (rc != PK_OK) break;

@@ -44,7 +44,9 @@ struct pk_engine {
     bool have_globals = false;
 
     float *rope = nullptr;                    // [ctx][hd/2][2] (cos, sin) * attn_factor
-    float *K = nullptr, *V = nullptr;         // [L][ctx][kv_dim]
+    float *K = nullptr, *V = nullptr;         // [n_seq][L][ctx][kv_dim]
+    int n_seq = 1;                            // sequences with a KV cache (pk_batch_reserve)
+    int64_t seq_stride = 0;                   // floats per sequence in K / V
 
     // staging for uploads / synthetic builds
     uint8_t *stage = nullptr;
@@ -101,6 +103,10 @@ struct pk_engine {
     int p_cap = 0;
     float *p_H = nullptr, *p_XN = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_part = nullptr;
     int32_t *p_ids = nullptr;
+    // batched decode (pk_decode_batch): logits [n_seq][vocab], token ring
+    int bd_cap = 0, bd_steps = 0;
+    float *bd_logits = nullptr;
+    int32_t *bd_toks = nullptr;
     // grouped MFMA scratch for up to g_cap pairs (pk_prefill.hip)
     int64_t g_cap = 0;
     int8_t *g_limbs = nullptr;
@@ -157,10 +163,13 @@ int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipSt
 int pk_decode_reserve(pk_engine *e);
 int pk_check_model(pk_engine *e);
 int pk_set_state(pk_engine *e, int tok, int pos);
-int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int n, const float *xn,
-                      float *qkv, float *part, float *att, float *h);
+// Rows r = 0..n-1 at position (st ? st->pos : pos_base + r * pos_step) of
+// sequence seq0 + r * seq_step.
+int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
+                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h);
 int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap);
 // one forward_token step for (tok, pos), greedy id appended to out_toks
 int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap);
 // prefill_tokens (pk_prefill.hip): the prompt, next id into the decode state / out_toks
-int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *out_toks, int out_cap);
+int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base, int32_t *out_toks,
+                   int out_cap);

@@ -147,7 +147,7 @@ static void engine_free(pk_engine *e) {
                     e->logits, e->r_logits, e->w_scaled, e->w_soft, e->sel, e->act, e->eo,
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
-                    e->p_part, e->p_ids, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
+                    e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out};
     for (void *p : ptrs) pk_dev_free(e, p);
@@ -182,7 +182,9 @@ static int engine_init(pk_engine *e) {
     e->expert_ready = (uint8_t *)calloc((size_t)L * E, 1);
     PK_CHECK(e->expert_ready, PK_ERR_OOM, "host allocation failed");
     e->L = new pk_layer_dev[L];
-    const int64_t kv = (int64_t)L * c->ctx_len * KVH * hd * 4;
+    e->seq_stride = (int64_t)L * c->ctx_len * KVH * hd;
+    e->n_seq = 1;
+    const int64_t kv = e->seq_stride * 4;
     ALLOC(e->K, kv);
     ALLOC(e->V, kv);
     PK_HIP(hipMemsetAsync(e->K, 0, kv, e->stream));

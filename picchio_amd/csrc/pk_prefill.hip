@@ -75,8 +75,8 @@ __global__ __launch_bounds__(256) void k_combine_rows(float *out, const float *r
     if (i >= D) return;
     float acc = 0.0f;
     for (int j = 0; j < K; ++j) {
-        const int k = perm[p * K + j];
-        acc = __builtin_fmaf(w[p * K + k], eo[((int64_t)p * K + k) * D + i], acc);
+        const int k = perm ? perm[p * K + j] : j;
+        acc = __builtin_fmaf(w[p * K + k], eo[((int64_t)p * K + k) * D + i], acc);   // perm null: k order
     }
     const int64_t o = (int64_t)p * D + i;
     out[o] = residual ? residual[o] + acc : acc;
@@ -109,16 +109,21 @@ static int batch_reserve(pk_engine *e, int T) {
 
 // The MoE of forward_prefill (picchio.c:1829-1916) for T tokens x [T][D]:
 // out[t] = (residual ? residual[t] : 0) + sum over the token's experts, in the
-// batch's expert order, of (w_k * routed_scale) * expert_k(x[t]).
-static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual) {
+// batch's expert order, of (w_k * routed_scale) * expert_k(x[t]). With
+// decode_order the sum runs in routing order instead, as moe_forward adds
+// (picchio.c:1445-1454): T independent decode tokens.
+static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
+                    bool decode_order = false) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
     PK_TRY(batch_reserve(e, T));
     const pk_layer_dev &d = e->L[layer];
     PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
     PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr, e->stream));
-    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
-    PK_HIP(hipGetLastError());
+    if (!decode_order) {
+        hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+        PK_HIP(hipGetLastError());
+    }
     pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = e->b_sel;
     gu.x = x; gu.x_stride = D; gu.x_div = K;
@@ -137,7 +142,7 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
-                       e->b_eo, e->b_w, e->b_perm, K, D);
+                       e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }
@@ -284,7 +289,7 @@ static int prefill_reserve(pk_engine *e, int B) {
 // forward_prefill (picchio.c:1795-1932) of ids_dev[0..n) at positions
 // pos_base..pos_base+n-1; the greedy next token goes to the decode state
 // (and to out_toks when given).
-static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int n, int pos_base,
+static int prefill_chunk(pk_engine *e, int seq, const int32_t *ids_dev, int last_tok, int n, int pos_base,
                          int32_t *out_toks, int out_cap, bool mfma) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden;
@@ -292,7 +297,8 @@ static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int
     PK_HIP(hipGetLastError());
     for (int l = 0; l < c->n_layers; ++l) {
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].in_ln, D, c->eps, n, e->stream));
-        PK_TRY(pk_attention_rows(e, l, nullptr, pos_base, n, e->p_XN, e->p_qkv, e->p_part, e->p_att, e->p_H));
+        PK_TRY(pk_attention_rows(e, l, nullptr, pos_base, 1, seq, 0, n, e->p_XN, e->p_qkv, e->p_part, e->p_att,
+                                 e->p_H));
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n, e->stream));
         if (mfma)
             PK_TRY(moe_rows_mfma(e, l, e->p_XN, n, e->p_H, e->p_H, nullptr, nullptr));
@@ -304,13 +310,15 @@ static int prefill_chunk(pk_engine *e, const int32_t *ids_dev, int last_tok, int
     return pk_lm_head_step(e, e->hn, nullptr, out_toks, out_cap);
 }
 
-int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_t *out_toks, int out_cap) {
+int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base, int32_t *out_toks,
+                   int out_cap) {
     int batch = 64;
     if (const char *v = getenv("PREFILL_BATCH")) batch = atoi(v);
-    if (batch <= 1 || n <= 1) {
+    if ((batch <= 1 || n <= 1) && seq == 0) {
         for (int i = 0; i < n; ++i) PK_TRY(pk_decode_token(e, ids[i], pos_base + i, out_toks, out_cap));
         return PK_OK;
     }
+    if (batch < 1) batch = 1;
     const int B = batch < n ? batch : n;
     // PK_PREFILL_MFMA=1: the chunk's MoE on the int8 matrix cores (grouped GEMM)
     const char *mv = getenv("PK_PREFILL_MFMA");
@@ -320,7 +328,7 @@ int pk_prefill_run(pk_engine *e, const int32_t *ids, int n, int pos_base, int32_
     PK_HIP(hipMemcpyAsync(e->p_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
     for (int off = 0; off < n; off += B) {
         const int len = n - off < B ? n - off : B;
-        PK_TRY(prefill_chunk(e, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap,
+        PK_TRY(prefill_chunk(e, seq, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap,
                              mfma));
     }
     PK_HIP(hipStreamSynchronize(e->stream));           // ids is the caller's pageable memory
@@ -334,10 +342,153 @@ extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int po
     PK_CHECK(!e->capturing, PK_ERR_ARG, "prefill_tokens: not available while capturing");
     PK_TRY(pk_check_model(e));
     PK_TRY(pk_decode_reserve(e));
-    PK_TRY(pk_prefill_run(e, ids, n, pos_base, nullptr, 0));
+    PK_TRY(pk_prefill_run(e, 0, ids, n, pos_base, nullptr, 0));
     pk_dstate s{};
     PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     if (next_host) *next_host = s.next;
+    return PK_OK;
+}
+
+// ───────────────────── several independent sequences ─────────────────────
+
+namespace {
+
+// Greedy id of each row of logits [rows][V] (first maximum, picchio.c:1555-1560).
+__global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int V, int32_t *out) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float *lg = logits + (int64_t)blockIdx.x * V;
+    float v = -INFINITY;
+    int i = 0x7fffffff;
+    for (int j = threadIdx.x; j < V; j += 256) {
+        const float x = lg[j];
+        if (x > v) { v = x; i = j; }              // j increases: first maximum within the thread
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float ov = __shfl_xor(v, o, 64);
+        const int oi = __shfl_xor(i, o, 64);
+        if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+    }
+    if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = i; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; ++w)
+            if (bv[w] > v || (bv[w] == v && bi[w] < i)) { v = bv[w]; i = bi[w]; }
+        out[blockIdx.x] = i == 0x7fffffff ? 0 : i;
+    }
+}
+
+}  // namespace
+
+extern "C" int pk_batch_reserve(pk_engine *e, int n_seq) {
+    PK_CHECK(e && n_seq > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "batch_reserve: not available while capturing");
+    if (n_seq <= e->n_seq) return PK_OK;
+    PK_HIP(hipStreamSynchronize(e->stream));
+    const int64_t bytes = (int64_t)n_seq * e->seq_stride * 4;
+    pk_dev_free(e, e->K);
+    pk_dev_free(e, e->V);
+    e->K = e->V = nullptr;
+    e->device_bytes -= 2 * (int64_t)e->n_seq * e->seq_stride * 4;
+    if (e->step_exec) {                       // the captured step addresses the old cache
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+    }
+    e->n_seq = 0;
+    PK_TRY(pk_dev_alloc(e, (void **)&e->K, bytes));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->V, bytes));
+    PK_HIP(hipMemsetAsync(e->K, 0, bytes, e->stream));
+    PK_HIP(hipMemsetAsync(e->V, 0, bytes, e->stream));
+    e->n_seq = n_seq;
+    return PK_OK;
+}
+
+extern "C" int pk_kv_fill_synthetic(pk_engine *e, int seq, int n_pos, uint64_t seed) {
+    PK_CHECK(e && seq >= 0 && seq < e->n_seq && n_pos >= 0 && n_pos <= e->c.ctx_len, PK_ERR_ARG,
+             "kv fill: seq %d / %d positions", seq, n_pos);
+    const pk_cfg *c = &e->c;
+    const int64_t kv_dim = (int64_t)c->n_kv_heads * c->head_dim;
+    for (int l = 0; l < c->n_layers; ++l) {
+        const int64_t off = seq * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
+        const uint64_t s = seed * 0x9E3779B97F4A7C15ull + (uint64_t)(seq * 1024 + l) * 2;
+        PK_TRY(pk_launch_fill_normal(e->K + off, n_pos * kv_dim, s, 1.0f, e->stream));
+        PK_TRY(pk_launch_fill_normal(e->V + off, n_pos * kv_dim, s + 1, 1.0f, e->stream));
+    }
+    return PK_OK;
+}
+
+extern "C" int pk_prefill_seq(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base,
+                              int32_t *next_host) {
+    PK_CHECK(e && ids && n > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(seq >= 0 && seq < e->n_seq, PK_ERR_ARG, "sequence %d of %d", seq, e->n_seq);
+    PK_CHECK(pos_base >= 0 && pos_base + n <= e->c.ctx_len, PK_ERR_CONTEXT_FULL,
+             "positions %d..%d exceed context %d", pos_base, pos_base + n - 1, e->c.ctx_len);
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "prefill_seq: not available while capturing");
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
+    PK_TRY(pk_prefill_run(e, seq, ids, n, pos_base, nullptr, 0));
+    pk_dstate s{};
+    PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    if (next_host) *next_host = s.next;
+    return PK_OK;
+}
+
+// n_steps greedy forward_token steps of sequences 0..n_seq-1, all at
+// positions pos .. pos+n_steps-1: each step embeds the n_seq tokens, runs
+// every layer on the n_seq rows at once (weights read once per step), and
+// writes the next tokens on the device for the following step.
+extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host, int pos, int n_steps,
+                               int32_t *out_host) {
+    PK_CHECK(e && toks_host && out_host && n_seq > 0 && n_steps > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(n_seq <= e->n_seq, PK_ERR_ARG, "%d sequences, %d reserved (pk_batch_reserve)", n_seq, e->n_seq);
+    PK_CHECK(pos >= 0 && pos + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL, "positions exceed context");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "decode_batch: not available while capturing");
+    PK_TRY(pk_check_model(e));
+    PK_TRY(pk_decode_reserve(e));
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, V = c->vocab;
+    PK_TRY(prefill_reserve(e, n_seq));
+    PK_TRY(batch_reserve(e, n_seq));
+    if (n_seq > e->bd_cap || n_steps + 1 > e->bd_steps) {
+        PK_HIP(hipStreamSynchronize(e->stream));
+        pk_dev_free(e, e->bd_logits);
+        pk_dev_free(e, e->bd_toks);
+        e->bd_logits = nullptr;
+        e->bd_toks = nullptr;
+        e->bd_cap = e->bd_steps = 0;
+        PK_TRY(pk_dev_alloc(e, (void **)&e->bd_logits, (int64_t)n_seq * V * 4));
+        PK_TRY(pk_dev_alloc(e, (void **)&e->bd_toks, (int64_t)(n_steps + 1) * n_seq * 4));
+        e->bd_cap = n_seq;
+        e->bd_steps = n_steps + 1;
+    }
+    PK_HIP(hipMemcpyAsync(e->bd_toks, toks_host, (size_t)n_seq * 4, hipMemcpyHostToDevice, e->stream));
+    for (int step = 0; step < n_steps; ++step) {
+        const int32_t *tk = e->bd_toks + (int64_t)step * n_seq;
+        hipLaunchKernelGGL(k_embed_rows, dim3(n_seq), dim3(256), 0, e->stream, tk, e->embed, V, e->p_H, D);
+        PK_HIP(hipGetLastError());
+        for (int l = 0; l < c->n_layers; ++l) {
+            PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].in_ln, D, c->eps, n_seq, e->stream));
+            PK_TRY(pk_attention_rows(e, l, nullptr, pos + step, 0, 0, 1, n_seq, e->p_XN, e->p_qkv, e->p_part,
+                                     e->p_att, e->p_H));
+            PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n_seq, e->stream));
+            PK_TRY(moe_rows(e, l, e->p_XN, n_seq, e->p_H, e->p_H, true));
+        }
+        PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->final_norm, D, c->eps, n_seq, e->stream));
+        const int ps = pk_prof_begin(e, PK_PROF_LM_HEAD);
+        if (c->lm_head_fmt == PK_FMT_INT8)
+            PK_TRY(pk_launch_gemv_q8(e->bd_logits, e->p_XN, e->lm_q8, e->lm_s, n_seq, D, V, e->stream));
+        else
+            PK_TRY(pk_launch_gemv_f32(e->bd_logits, e->p_XN, e->lm_f32, nullptr, n_seq, D, V, e->stream));
+        hipLaunchKernelGGL(k_argmax_rows, dim3(n_seq), dim3(256), 0, e->stream, e->bd_logits, V,
+                           e->bd_toks + (int64_t)(step + 1) * n_seq);
+        PK_HIP(hipGetLastError());
+        PK_TRY(pk_prof_end(e, ps));
+    }
+    PK_HIP(hipMemcpyAsync(out_host, e->bd_toks + n_seq, (size_t)n_steps * n_seq * 4, hipMemcpyDeviceToHost,
+                          e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
 }

@@ -194,3 +194,31 @@ def test_synthetic_build_matches_oracle_model(gpu, oracle):
         a.close()
         b.close()
         oracle.model_free(model)
+
+
+def test_batched_sequences_match_separate_streams(gpu, oracle, monkeypatch):
+    """Three sequences with different prompts: prefill_seq into their own
+    caches, then decode_batch of all three in lockstep; each stream equals
+    the oracle's prefill_tokens + forward_token stream for that prompt."""
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=8, ctx_len=128, vocab=1000)
+    model = oracle.model_build(cfg, 1234, 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg)
+        monkeypatch.setenv("PREFILL_BATCH", "64")
+        eng.batch_reserve(3)
+        rng = np.random.default_rng(77)
+        prompts = [rng.integers(0, cfg.vocab, 40).astype(np.int32) for _ in range(3)]
+        first = [eng.prefill_seq(s, prompts[s]) for s in range(3)]
+        got = eng.decode_batch(first, 40, 12)
+        for s in range(3):
+            oracle.model_reset_kv(model)
+            ref = [oracle.prefill_tokens(model, prompts[s], 40, 0, 64)]
+            for i in range(12):
+                ref.append(oracle.forward_token(model, ref[-1], 40 + i, None))
+            assert ref[0] == first[s]
+            assert list(got[:, s]) == ref[1:], s
+    finally:
+        eng.close()
+        oracle.model_free(model)
