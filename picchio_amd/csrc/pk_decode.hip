@@ -104,19 +104,23 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
     }
 }
 
-// Attention partials: block (h, c) scores positions start+128c .. +127 of
-// head h against its KV head (h / group). Scores are the reference's
-// in-order dot (uncontracted products added one by one, picchio.c:573-577 as
-// gcc builds it) times 1/sqrt(hd). Writes the chunk max, sum of exp(s - max)
-// and the exp-weighted V sum (flash-decoding partials).
+// Attention partials: block (h, c, r) scores positions start+128c .. +127 of
+// row r's window for head h against its KV head (h / group). Scores are the
+// reference's in-order dot (uncontracted products added one by one,
+// picchio.c:573-577 as gcc builds it) times 1/sqrt(hd). Writes the chunk max,
+// the sum of exp(s - max) and the exp-weighted V sum (flash-decoding
+// partials). The V sum runs as hd/4 float4 columns x (128*4/hd) position
+// groups, each group's loads issued together, then the groups are added in
+// a fixed order.
 __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
                                                          const float *qkv, int64_t qkv_stride, const float *Kl,
                                                          const float *Vl, int64_t kv_row, int H, int KVH,
                                                          int hd, int ctx, int sliding, int window, float *part,
                                                          int max_chunks) {
-    __shared__ float q[128];
+    __shared__ __attribute__((aligned(16))) float q[128];
     __shared__ float p[ATT_CHUNK];
     __shared__ float red[2];
+    __shared__ __attribute__((aligned(16))) float vred[ATT_CHUNK * 4];
     const int h = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
     qkv += (int64_t)r * qkv_stride;
     part += (int64_t)r * H * max_chunks * (hd + 2);
@@ -133,12 +137,23 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
     const float scale = 1.0f / sqrtf((float)hd);
     float s = -INFINITY;
     if ((int)threadIdx.x < n) {
-        const float *kt = Kl + (int64_t)(t0 + threadIdx.x) * kv_dim + kvh * hd;
+        const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + threadIdx.x) * kv_dim + kvh * hd);
         float dot = 0.0f;
-        int i = 0;
-        const int n4 = hd & ~3;
-        for (; i < n4; ++i) { const float pr = q[i] * kt[i]; dot = dot + pr; }
-        for (; i < hd; ++i) dot = __builtin_fmaf(q[i], kt[i], dot);
+        for (int i0 = 0; i0 < hd; i0 += 32) {         // 32 columns: loads first, then the in-order adds
+            float4 kv[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) kv[u] = i0 + 4 * u < hd ? kt4[(i0 >> 2) + u] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                if (i0 + 4 * u >= hd) break;
+                const float *qq = q + i0 + 4 * u;
+                float pr;
+                pr = qq[0] * kv[u].x; dot = dot + pr;
+                pr = qq[1] * kv[u].y; dot = dot + pr;
+                pr = qq[2] * kv[u].z; dot = dot + pr;
+                pr = qq[3] * kv[u].w; dot = dot + pr;
+            }
+        }
         s = dot * scale;
     }
     // chunk max (wave 0 / wave 1 halves), then p = exp(s - m)
@@ -158,10 +173,35 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
         sum = wave_sum(sum);
         if (threadIdx.x == 0) { out[0] = m; out[1] = sum; }
     }
+    // V sum: thread = (column group c4 of hd/4, position group g of PG)
+    const int D4 = hd >> 2, PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
+    const int c4 = threadIdx.x % D4, g = threadIdx.x / D4;
+    const float4 *v4 = reinterpret_cast<const float4 *>(Vl + (int64_t)t0 * kv_dim + kvh * hd) + c4;
+    const int kv4 = kv_dim >> 2;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j0 = 0; j0 < PER; j0 += 16) {
+        float4 vv[16];
+        float pw[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int t = g * PER + j0 + u;
+            const bool ok = j0 + u < PER && t < n;
+            vv[u] = ok ? v4[(int64_t)t * kv4] : make_float4(0.f, 0.f, 0.f, 0.f);
+            pw[u] = ok ? p[t] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            acc.x = __builtin_fmaf(pw[u], vv[u].x, acc.x);
+            acc.y = __builtin_fmaf(pw[u], vv[u].y, acc.y);
+            acc.z = __builtin_fmaf(pw[u], vv[u].z, acc.z);
+            acc.w = __builtin_fmaf(pw[u], vv[u].w, acc.w);
+        }
+    }
+    *reinterpret_cast<float4 *>(&vred[g * hd + 4 * c4]) = acc;
+    __syncthreads();
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float o = 0.0f;
-        const float *vt = Vl + (int64_t)t0 * kv_dim + kvh * hd + i;
-        for (int t = 0; t < n; ++t) o = __builtin_fmaf(p[t], vt[(int64_t)t * kv_dim], o);
+        for (int gg = 0; gg < PG; ++gg) o += vred[gg * hd + i];
         out[2 + i] = o;
     }
 }

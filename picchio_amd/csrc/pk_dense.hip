@@ -144,6 +144,18 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(float *__restrict__ Y, cons
         const int row = min(row0 + r, O - 1);
         w4[r] = reinterpret_cast<const float4 *>(W + (int64_t)row * I);
     }
+    // this lane's float4 of each row for the chunk at k0 (zero past I)
+    auto wload = [](const float4 *const *w4p, int k0, int lane, int I, float4 *out) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pk_f32x4 t = {0.f, 0.f, 0.f, 0.f};
+            if (k0 + 4 * lane < I)
+                t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4p[r] + (k0 >> 2) + lane));
+            out[r] = make_float4(t.x, t.y, t.z, t.w);
+        }
+    };
+    float4 wv[4], wn[4];
+    wload(w4, 0, lane, I, wv);
     for (int k0 = 0; k0 < I; k0 += SK_KC) {
         const int kc = min(SK_KC, I - k0);
         __syncthreads();
@@ -154,14 +166,7 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(float *__restrict__ Y, cons
             *reinterpret_cast<float4 *>(&xs[s][4 * c4]) = v;
         }
         __syncthreads();
-        float4 wv[4];
-        const bool in = 4 * lane < kc;
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            pk_f32x4 t = {0.f, 0.f, 0.f, 0.f};
-            if (in) t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4[r] + (k0 >> 2) + lane));
-            wv[r] = make_float4(t.x, t.y, t.z, t.w);
-        }
+        if (k0 + SK_KC < I) wload(w4, k0 + SK_KC, lane, I, wn);      // next chunk's weights in flight
 #pragma unroll
         for (int s = 0; s < SB; ++s) {
             const float4 xv = *reinterpret_cast<const float4 *>(&xs[s][4 * lane]);
@@ -175,6 +180,8 @@ __global__ __launch_bounds__(256) void k_gemm_skinny(float *__restrict__ Y, cons
                 acc[r * SB + s] = a;
             }
         }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wv[r] = wn[r];
     }
     // reduce-scatter over the 64 lanes: at the step exchanging with lane ^ m
     // the lane keeps the upper half of its c values if (lane & m), else the

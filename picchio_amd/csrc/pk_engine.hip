@@ -77,8 +77,8 @@ static int cfg_check(const pk_cfg *c) {
     PK_CHECK(c->n_layers <= 128, PK_ERR_UNSUPPORTED, "cfg: more than 128 layers");
     PK_CHECK(c->n_heads > 0 && c->n_kv_heads > 0 && c->n_heads % c->n_kv_heads == 0, PK_ERR_ARG,
              "cfg: n_heads must be a multiple of n_kv_heads");
-    PK_CHECK(c->head_dim > 0 && c->head_dim <= 128 && c->head_dim % 2 == 0, PK_ERR_UNSUPPORTED,
-             "cfg: head_dim %d (supported: even, <= 128)", c->head_dim);
+    PK_CHECK(c->head_dim >= 16 && c->head_dim <= 128 && (c->head_dim & (c->head_dim - 1)) == 0,
+             PK_ERR_UNSUPPORTED, "cfg: head_dim %d (supported: 16, 32, 64, 128)", c->head_dim);
     PK_CHECK(c->ctx_len > 0 && c->vocab > 0, PK_ERR_ARG, "cfg: ctx_len / vocab must be positive");
     PK_CHECK(c->lm_head_fmt == PK_FMT_F32 || c->lm_head_fmt == PK_FMT_INT8, PK_ERR_UNSUPPORTED,
              "cfg: lm_head_fmt %d", c->lm_head_fmt);
