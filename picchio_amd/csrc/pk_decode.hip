@@ -402,7 +402,8 @@ int pk_check_model(pk_engine *e) {
 // (pos_step 0, seq_step 1). Writes K/V, qkv [n][(H+2KVH)hd], att [n][H hd]
 // and adds the output projection into h [n][D] (residual).
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
-                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h) {
+                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
+                      const float *norm_w) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[l];
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
@@ -411,7 +412,12 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     float *Kl = e->K + seq0 * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
     float *Vl = e->V + seq0 * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
     const int ps = pk_prof_begin(e, PK_PROF_ATTENTION);
-    PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
+    if (norm_w) {
+        PK_CHECK(n == 1, PK_ERR_ARG, "fused norm: one row");
+        PK_TRY(pk_launch_gemv_f32_norm(qkv, xn, norm_w, c->eps, d.wqkv, d.bqkv, D, qkv_dim, e->stream));
+    } else {
+        PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
+    }
     const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
     hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
@@ -441,8 +447,11 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     return pk_prof_end(e, ps);
 }
 
+// Decode attention of layer l on the residual row h (in_ln rmsnorm fused
+// into the QKV GEMV); adds the output projection into h.
 static int attention_layer(pk_engine *e, int l) {
-    return pk_attention_rows(e, l, e->dstate, 0, 0, 0, 0, 1, e->hn, e->qkv, e->attn_part, e->att, e->h);
+    return pk_attention_rows(e, l, e->dstate, 0, 0, 0, 0, 1, e->h, e->qkv, e->attn_part, e->att, e->h,
+                             e->L[l].in_ln);
 }
 
 // One forward_token step with tok/pos in device state; logits optional.
@@ -453,10 +462,9 @@ static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int o
                        e->h, e->hn, e->L[0].in_ln, D, c->eps);
     PK_HIP(hipGetLastError());
     for (int l = 0; l < c->n_layers; ++l) {
-        if (l > 0) PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->L[l].in_ln, D, c->eps, 1, e->stream));
         PK_TRY(attention_layer(e, l));
-        PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->L[l].post_ln, D, c->eps, 1, e->stream));
-        PK_TRY(pk_moe_layer(e, l, e->hn, nullptr, e->h, e->h));      // h += moe(hn)
+        // h += moe(rmsnorm(h)): the router normalises h and writes hn for the experts
+        PK_TRY(pk_moe_layer(e, l, e->h, nullptr, e->h, e->h, e->L[l].post_ln));
     }
     PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->final_norm, D, c->eps, 1, e->stream));
     return pk_lm_head_step(e, e->hn, logits_dev, out_toks, out_cap);
@@ -505,7 +513,8 @@ extern "C" int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int
     PK_TRY(pk_set_state(e, 0, pos));
     PK_HIP(hipMemcpyAsync(e->hn, x_dev, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
     PK_HIP(hipMemsetAsync(e->h, 0, (size_t)c->hidden * 4, e->stream));
-    PK_TRY(attention_layer(e, layer));               // h = 0 + attn(x)
+    PK_TRY(pk_attention_rows(e, layer, e->dstate, 0, 0, 0, 0, 1, e->hn, e->qkv, e->attn_part, e->att,
+                             e->h));                // h = 0 + attn(x)
     PK_HIP(hipMemcpyAsync(out_dev, e->h, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;

@@ -15,6 +15,25 @@ __device__ __forceinline__ double pk_wave_sum_d(double v) {
     return v;
 }
 
+// RMSNorm scale of x[0..D) for a 256-thread block, every thread getting it:
+// 1 / sqrtf((float)(sum x^2 / D) + eps) with k_rmsnorm's double sum (same
+// per-thread partials, wave tree and block combine, hence the same bits), so
+// a consumer can normalise its input on the fly: (x * r) * w.
+__device__ __forceinline__ float pk_block_rms_scale(const float *__restrict__ x, int D, float eps,
+                                                    double *part) {
+    double acc = 0.0;
+    for (int i = threadIdx.x; i < D; i += 256) acc += (double)x[i] * (double)x[i];
+    acc = pk_wave_sum_d(acc);
+    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
+    __syncthreads();
+    const double ms = (part[0] + part[1]) + (part[2] + part[3]);
+    return 1.0f / sqrtf((float)(ms / D) + eps);
+}
+
+__device__ __forceinline__ float4 pk_norm4(float4 h, float r, float4 w) {
+    return make_float4(h.x * r * w.x, h.y * r * w.y, h.z * r * w.z, h.w * r * w.w);
+}
+
 // ───────────────────────── fp32 GEMV ─────────────────────────
 // y[s][o] = x[s] . W[o] (+ bias[o]), matmul_f32 (quant.h:117-148). fp32 sum
 // in a fixed tree order (not the reference's 8-lane order: within 1e-6
@@ -25,10 +44,14 @@ constexpr int GEMV_U = 4;           // float4 per lane per chunk
 
 // Large O: one wave per RPW rows, lanes stride the row in float4 (each load
 // instruction reads 1 KiB contiguous).
-template <int RPW>
+// NORM: x is the raw residual row and nw the RMSNorm weight; the block
+// normalises it on the fly (pk_block_rms_scale), fusing rmsnorm into the GEMV.
+template <int RPW, bool NORM = false>
 __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const float *__restrict__ x,
                                                   const float *__restrict__ W,
-                                                  const float *__restrict__ bias, int S, int I, int O) {
+                                                  const float *__restrict__ bias, int S, int I, int O,
+                                                  const float *__restrict__ nw = nullptr, float eps = 0.f) {
+    __shared__ double npart[4];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * RPW;
@@ -36,6 +59,9 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
     const float *xs = x + (int64_t)s * I;
     const int n4 = I >> 2;
     const float4 *x4 = reinterpret_cast<const float4 *>(xs);
+    const float4 *nw4 = reinterpret_cast<const float4 *>(nw);
+    float rn = 1.0f;
+    if constexpr (NORM) rn = pk_block_rms_scale(xs, I, eps, npart);
     float acc[RPW];
 #pragma unroll
     for (int r = 0; r < RPW; ++r) acc[r] = 0.0f;
@@ -46,6 +72,7 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
         for (int u = 0; u < GEMV_U; ++u) {
             const int i = i0 + u * 64;
             xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if constexpr (NORM) xv[u] = i < n4 ? pk_norm4(xv[u], rn, nw4[i]) : xv[u];
 #pragma unroll
             for (int r = 0; r < RPW; ++r) {
                 const int o = min(row0 + r, O - 1);
@@ -65,10 +92,11 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
             }
     }
     for (int i = (n4 << 2) + lane; i < I; i += 64) {
+        const float xi = NORM ? xs[i] * rn * nw[i] : xs[i];
 #pragma unroll
         for (int r = 0; r < RPW; ++r) {
             const int o = min(row0 + r, O - 1);
-            acc[r] = __builtin_fmaf(xs[i], W[(int64_t)o * I + i], acc[r]);
+            acc[r] = __builtin_fmaf(xi, W[(int64_t)o * I + i], acc[r]);
         }
     }
 #pragma unroll
@@ -79,12 +107,15 @@ __global__ __launch_bounds__(256) void k_gemv_f32(float *__restrict__ y, const f
     }
 }
 
-// Small O: one workgroup per row, 256 threads split the row.
+// Small O: one workgroup per row, 256 threads split the row. With nw, xs is
+// the raw row and is normalised on the fly with scale rn (x * rn * nw).
 __device__ __forceinline__ float pk_row_dot_block(const float *__restrict__ xs,
-                                                  const float *__restrict__ w, int I, float *red) {
+                                                  const float *__restrict__ w, int I, float *red,
+                                                  const float *__restrict__ nw = nullptr, float rn = 1.0f) {
     const int n4 = I >> 2;
     const float4 *x4 = reinterpret_cast<const float4 *>(xs);
     const float4 *w4 = reinterpret_cast<const float4 *>(w);
+    const float4 *nw4 = reinterpret_cast<const float4 *>(nw);
     float acc = 0.0f;
     for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
         float4 xv[GEMV_U], wv[GEMV_U];
@@ -92,6 +123,7 @@ __device__ __forceinline__ float pk_row_dot_block(const float *__restrict__ xs,
         for (int u = 0; u < GEMV_U; ++u) {
             const int i = i0 + u * 256;
             xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            if (nw && i < n4) xv[u] = pk_norm4(xv[u], rn, nw4[i]);
             wv[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
@@ -102,7 +134,8 @@ __device__ __forceinline__ float pk_row_dot_block(const float *__restrict__ xs,
             acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
         }
     }
-    for (int i = (n4 << 2) + threadIdx.x; i < I; i += 256) acc = __builtin_fmaf(xs[i], w[i], acc);
+    for (int i = (n4 << 2) + threadIdx.x; i < I; i += 256)
+        acc = __builtin_fmaf(nw ? xs[i] * rn * nw[i] : xs[i], w[i], acc);
     acc = pk_wave_sum(acc);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
     __syncthreads();
@@ -111,10 +144,13 @@ __device__ __forceinline__ float pk_row_dot_block(const float *__restrict__ xs,
 
 __global__ __launch_bounds__(256) void k_gemv_f32_rows(float *__restrict__ y, const float *__restrict__ x,
                                                        const float *__restrict__ W,
-                                                       const float *__restrict__ bias, int S, int I, int O) {
+                                                       const float *__restrict__ bias, int S, int I, int O,
+                                                       const float *__restrict__ nw = nullptr, float eps = 0.f) {
     __shared__ float red[4];
+    __shared__ double npart[4];
     const int o = blockIdx.x, s = blockIdx.y;
-    const float v = pk_row_dot_block(x + (int64_t)s * I, W + (int64_t)o * I, I, red);
+    const float rn = nw ? pk_block_rms_scale(x + (int64_t)s * I, I, eps, npart) : 1.0f;
+    const float v = pk_row_dot_block(x + (int64_t)s * I, W + (int64_t)o * I, I, red, nw, rn);
     if (threadIdx.x == 0) y[(int64_t)s * O + o] = bias ? v + bias[o] : v;
 }
 
@@ -273,6 +309,22 @@ __global__ __launch_bounds__(256) void k_gemv_q8(float *__restrict__ y, const fl
     if (lane == 0) y[(int64_t)s * O + o] = v * sc[o];
 }
 
+int pk_launch_gemv_f32_norm(float *y, const float *h, const float *nw, float eps, const float *W,
+                            const float *bias, int I, int O, hipStream_t st) {
+    PK_CHECK(I > 0 && O > 0 && nw, PK_ERR_ARG, "gemv f32 norm: bad shape");
+    PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)h & 15) == 0 && ((uintptr_t)nw & 15) == 0 && (I & 3) == 0,
+             PK_ERR_UNSUPPORTED, "gemv f32 norm: needs 16-byte aligned rows (I=%d)", I);
+    if (O <= 2048) {
+        hipLaunchKernelGGL(k_gemv_f32_rows, dim3(O, 1), dim3(256), 0, st, y, h, W, bias, 1, I, O, nw, eps);
+    } else {
+        constexpr int RPW = 2;
+        hipLaunchKernelGGL((k_gemv_f32<RPW, true>), dim3((O + 4 * RPW - 1) / (4 * RPW), 1), dim3(256), 0, st, y,
+                           h, W, bias, 1, I, O, nw, eps);
+    }
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
                       int S, int I, int O, hipStream_t st) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv q8: bad shape");
@@ -403,14 +455,25 @@ __device__ __forceinline__ float pk_ld_dev(float *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// With nw, x is the raw residual row: every block normalises it on the fly
+// (rmsnorm fused, same bits) and block e also writes its slice of the
+// normalised row to hn for the expert kernels that follow.
 __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x, const float *__restrict__ R,
                                                      const float *__restrict__ b, int E, int D, int K,
                                                      float routed_scale, float *logits, int32_t *sel,
-                                                     float *w_scaled, float *w_soft, uint32_t *counter) {
+                                                     float *w_scaled, float *w_soft, uint32_t *counter,
+                                                     const float *__restrict__ nw, float eps, float *hn) {
     __shared__ float red[4];
+    __shared__ double npart[4];
     __shared__ int last;
     const int e = blockIdx.x;
-    const float v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
+    float rn = 1.0f;
+    if (nw) {
+        rn = pk_block_rms_scale(x, D, eps, npart);
+        const int span = (D + E - 1) / E;
+        for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
+    }
+    const float v = pk_row_dot_block(x, R + (int64_t)e * D, D, red, nw, rn);
     if (threadIdx.x == 0) {
         pk_st_dev(logits + e, v + b[e]);
         __builtin_amdgcn_s_waitcnt(0);
@@ -457,13 +520,15 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
 
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D, int K,
                           float routed_scale, float *logits, int32_t *sel, float *w_scaled,
-                          float *w_soft, uint32_t *counter, hipStream_t st) {
+                          float *w_soft, uint32_t *counter, hipStream_t st, const float *nw, float eps,
+                          float *hn) {
     PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
              "router: E=%d K=%d outside 1..128 / 1..16", E, K);
     PK_CHECK(((uintptr_t)R & 15) == 0 && ((uintptr_t)x & 15) == 0 && (D & 3) == 0, PK_ERR_UNSUPPORTED,
              "router: needs 16-byte aligned rows");
+    PK_CHECK(!nw || (hn && ((uintptr_t)nw & 15) == 0), PK_ERR_ARG, "router: fused norm needs hn");
     hipLaunchKernelGGL(k_router_topk, dim3(E), dim3(256), 0, st, x, R, b, E, D, K, routed_scale, logits,
-                       sel, w_scaled, w_soft, counter);
+                       sel, w_scaled, w_soft, counter, nw, eps, hn);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

@@ -132,7 +132,7 @@ int pk_prof_end(pk_engine *e, int slot);
 
 // internal MoE pieces reused by the decode and prompt drivers
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
-                 const float *residual, float *res_out);
+                 const float *residual, float *res_out, const float *norm_w = nullptr);
 int pk_check_layer_experts(pk_engine *e, int layer);
 pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
 
@@ -165,8 +165,10 @@ int pk_check_model(pk_engine *e);
 int pk_set_state(pk_engine *e, int tok, int pos);
 // Rows r = 0..n-1 at position (st ? st->pos : pos_base + r * pos_step) of
 // sequence seq0 + r * seq_step.
+// norm_w (n == 1 only): xn is the raw residual row, normalised inside the QKV GEMV.
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
-                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h);
+                      int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
+                      const float *norm_w = nullptr);
 int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap);
 // one forward_token step for (tok, pos), greedy id appended to out_toks
 int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap);

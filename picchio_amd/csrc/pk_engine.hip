@@ -730,14 +730,17 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     return PK_OK;
 }
 
+// norm_w: x_dev is the raw residual row; the router normalises it (rmsnorm
+// fused) and writes the normalised row to e->hn, which the experts read.
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
-                 const float *residual, float *res_out) {
+                 const float *residual, float *res_out, const float *norm_w) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[layer];
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
-                                 e->counters + PK_CTR_ROUTER, e->stream));
+                                 e->counters + PK_CTR_ROUTER, e->stream, norm_w, c->eps,
+                                 norm_w ? e->hn : nullptr));
     PK_TRY(pk_prof_end(e, ps));
     // the down launch combines the top-k outputs (routing order) + residual
     pk_combine_args cb{};
@@ -745,7 +748,7 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     cb.out = residual ? res_out : out_dev;
     cb.residual = residual;
     cb.counters = e->counters + PK_CTR_COMBINE;
-    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, x_dev, 0, e->act, e->eo, &cb));
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb));
     return PK_OK;
 }
 

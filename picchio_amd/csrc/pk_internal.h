@@ -148,10 +148,16 @@ int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, cons
                                int S, int I, int O, hipStream_t st);
 
 // Router for one token: logits = R x + b, top-k by repeated argmax, softmax.
+// nw (optional): x is the raw residual row, normalised in the kernel
+// (rmsnorm fused); the normalised row is also written to hn.
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D,
                           int K, float routed_scale, float *logits, int32_t *sel,
                           float *w_scaled, float *w_soft, uint32_t *counter,
-                          hipStream_t st);
+                          hipStream_t st, const float *nw = nullptr, float eps = 0.f,
+                          float *hn = nullptr);
+// y = W . rmsnorm(h; nw, eps) + bias for one row (rmsnorm fused into the GEMV).
+int pk_launch_gemv_f32_norm(float *y, const float *h, const float *nw, float eps, const float *W,
+                            const float *bias, int I, int O, hipStream_t st);
 
 int pk_launch_rmsnorm(float *out, const float *x, const float *w, int D, float eps,
                       int T, hipStream_t st);
