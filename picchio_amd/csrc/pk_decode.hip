@@ -9,6 +9,7 @@
 // step can be replayed for every token: the argmax writes the next token,
 // appends it to the output list and advances the position.
 #include "pk_engine.h"
+#include "pk_dev.h"
 
 #include <math.h>
 #include <vector>
@@ -51,6 +52,84 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
     __syncthreads();
     const float r = rs;
     for (int i = threadIdx.x; i < D; i += 256) hn[i] = (ok ? row[i] : 0.0f) * r * w[i];
+}
+
+// Decode QKV projection with the in_ln rmsnorm, the biases, RoPE
+// (picchio.c:455-473) and the KV store (picchio.c:492-498) fused: wave w
+// computes the row pair of one rotation, rows (head*hd + j, head*hd + j + hd/2)
+// of the q and k heads, or two adjacent v rows; lane 0 rotates the pair with
+// the host-built table at the decode position and writes q / K / V.
+__global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, const float *__restrict__ h,
+                                                       const float *__restrict__ nw, float eps,
+                                                       const float *__restrict__ W, const float *__restrict__ b,
+                                                       int D, int H, int KVH, int hd, const float *rope,
+                                                       float *qkv, float *Kl, float *Vl) {
+    __shared__ double npart[4];
+    const int lane = threadIdx.x & 63;
+    const int half = hd / 2;
+    const int n_rot = (H + KVH) * half, n_pairs = n_rot + KVH * half;
+    const float rn = pk_block_rms_scale(h, D, eps, npart);
+    const int pi = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (pi >= n_pairs) return;
+    int r0, r1, head = 0, j = 0;
+    if (pi < n_rot) {
+        head = pi / half;
+        j = pi - head * half;
+        r0 = head * hd + j;
+        r1 = r0 + half;
+    } else {
+        r0 = (H + KVH) * hd + 2 * (pi - n_rot);
+        r1 = r0 + 1;
+    }
+    const float4 *h4 = reinterpret_cast<const float4 *>(h);
+    const float4 *n4w = reinterpret_cast<const float4 *>(nw);
+    const pk_f32x4 *w0 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)r0 * D);
+    const pk_f32x4 *w1 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)r1 * D);
+    const int n4 = D >> 2;
+    float a0 = 0.0f, a1 = 0.0f;
+    for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
+        float4 xv[4];
+        pk_f32x4 wa[4], wb[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int i = i0 + u * 64;
+            const bool in = i < n4;
+            xv[u] = in ? pk_norm4(h4[i], rn, n4w[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
+            wa[u] = in ? __builtin_nontemporal_load(w0 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+            wb[u] = in ? __builtin_nontemporal_load(w1 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            a0 = __builtin_fmaf(xv[u].x, wa[u].x, a0); a0 = __builtin_fmaf(xv[u].y, wa[u].y, a0);
+            a0 = __builtin_fmaf(xv[u].z, wa[u].z, a0); a0 = __builtin_fmaf(xv[u].w, wa[u].w, a0);
+            a1 = __builtin_fmaf(xv[u].x, wb[u].x, a1); a1 = __builtin_fmaf(xv[u].y, wb[u].y, a1);
+            a1 = __builtin_fmaf(xv[u].z, wb[u].z, a1); a1 = __builtin_fmaf(xv[u].w, wb[u].w, a1);
+        }
+    }
+    a0 = wave_sum(a0);
+    a1 = wave_sum(a1);
+    if (lane != 0) return;
+    const float v0 = a0 + b[r0], v1 = a1 + b[r1];
+    const int pos = st->pos, kv_dim = KVH * hd;
+    if (pi < n_rot) {
+        const float cs = rope[((int64_t)pos * half + j) * 2 + 0];
+        const float sn = rope[((int64_t)pos * half + j) * 2 + 1];
+        const float q0 = __builtin_fmaf(v0, cs, -(v1 * sn));     // a*cs - b*sn (contracted)
+        const float q1 = __builtin_fmaf(v0, sn, v1 * cs);        // a*sn + b*cs (contracted)
+        qkv[r0] = q0;
+        qkv[r1] = q1;
+        if (head >= H) {
+            float *kr = Kl + (int64_t)pos * kv_dim + (head - H) * hd;
+            kr[j] = q0;
+            kr[j + half] = q1;
+        }
+    } else {
+        qkv[r0] = v0;
+        qkv[r1] = v1;
+        const int c = r0 - (H + KVH) * hd;
+        Vl[(int64_t)pos * kv_dim + c] = v0;
+        Vl[(int64_t)pos * kv_dim + c + 1] = v1;
+    }
 }
 
 // Position of row r: the decode step's (device state), or pos_base + r * step
@@ -112,15 +191,22 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 // partials). The V sum runs as hd/4 float4 columns x (128*4/hd) position
 // groups, each group's loads issued together, then the groups are added in
 // a fixed order.
+//
+// The partials are stored device-coherently; the last of the row's chunk
+// blocks to arrive at its (row, head) counter combines them with the learned
+// sink (picchio.c:586-604: the sink joins the max and the denominator, not the
+// value sum), writes att [row][h*hd..] and re-arms the counter.
 __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
                                                          const float *qkv, int64_t qkv_stride, const float *Kl,
                                                          const float *Vl, int64_t kv_row, int H, int KVH,
                                                          int hd, int ctx, int sliding, int window, float *part,
-                                                         int max_chunks) {
+                                                         int max_chunks, const float *sinks, float *att,
+                                                         uint32_t *ctr) {
     __shared__ __attribute__((aligned(16))) float q[128];
     __shared__ float p[ATT_CHUNK];
     __shared__ float red[2];
     __shared__ __attribute__((aligned(16))) float vred[ATT_CHUNK * 4];
+    __shared__ int last;
     const int h = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
     qkv += (int64_t)r * qkv_stride;
     part += (int64_t)r * H * max_chunks * (hd + 2);
@@ -171,7 +257,10 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
         float sum = 0.0f;
         for (int t = threadIdx.x; t < n; t += 64) sum += p[t];
         sum = wave_sum(sum);
-        if (threadIdx.x == 0) { out[0] = m; out[1] = sum; }
+        if (threadIdx.x == 0) {
+            __hip_atomic_store(out, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(out + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
     }
     // V sum: thread = (column group c4 of hd/4, position group g of PG)
     const int D4 = hd >> 2, PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
@@ -202,31 +291,39 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float o = 0.0f;
         for (int gg = 0; gg < PG; ++gg) o += vred[gg * hd + i];
-        out[2 + i] = o;
+        __hip_atomic_store(out + 2 + i, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-}
-
-// Combine the chunk partials of head h with the learned sink (picchio.c:586-604):
-// the sink joins the max and the denominator, not the value sum.
-__global__ void k_attn_combine(const pk_dstate *st, int pos_base, int pos_step, const float *part,
-                               const float *sinks, int H, int hd, int ctx, int sliding, int window,
-                               int max_chunks, float *att) {
-    const int h = blockIdx.x, r = blockIdx.y;
-    part += (int64_t)r * H * max_chunks * (hd + 2);
-    att += (int64_t)r * H * hd;
-    int start, end;
-    att_window(row_pos(st, pos_base, pos_step, r), ctx, sliding, window, start, end);
+    // arrival: the last of the nc chunk blocks combines
     const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    uint32_t *cnt = ctr + (int64_t)r * H + h;
+    if (threadIdx.x == 0)
+        last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nc - 1);
+    __syncthreads();
+    if (!last) return;
     const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
     float M = sinks[h];
-    for (int c = 0; c < nc; ++c) M = fmaxf(M, ph[c * (hd + 2)]);
+    for (int cc = 0; cc < nc; ++cc)
+        M = fmaxf(M, __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
     float S = expf(sinks[h] - M);
-    for (int c = 0; c < nc; ++c) S += ph[c * (hd + 2) + 1] * expf(ph[c * (hd + 2)] - M);
+    for (int cc = 0; cc < nc; ++cc) {
+        const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        S += __hip_atomic_load(ph + cc * (hd + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
+             expf(mc - M);
+    }
+    float *ar = att + (int64_t)r * H * hd + h * hd;
     for (int i = threadIdx.x; i < hd; i += blockDim.x) {
         float o = 0.0f;
-        for (int c = 0; c < nc; ++c) o = __builtin_fmaf(ph[c * (hd + 2) + 2 + i], expf(ph[c * (hd + 2)] - M), o);
-        att[h * hd + i] = o / S;
+        for (int cc = 0; cc < nc; ++cc) {
+            const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            o = __builtin_fmaf(__hip_atomic_load(ph + cc * (hd + 2) + 2 + i, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT),
+                               expf(mc - M), o);
+        }
+        ar[i] = o / S;
     }
+    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // y[o] += (W[o] . x + b[o])  — attention output projection + residual
@@ -413,26 +510,30 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     float *Vl = e->V + seq0 * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
     const int ps = pk_prof_begin(e, PK_PROF_ATTENTION);
     if (norm_w) {
-        PK_CHECK(n == 1, PK_ERR_ARG, "fused norm: one row");
-        PK_TRY(pk_launch_gemv_f32_norm(qkv, xn, norm_w, c->eps, d.wqkv, d.bqkv, D, qkv_dim, e->stream));
+        // decode row: rmsnorm + QKV + bias + RoPE + KV store in one launch
+        PK_CHECK(n == 1 && st, PK_ERR_ARG, "fused norm: the decode row");
+        PK_CHECK(((uintptr_t)xn & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && (D & 3) == 0,
+                 PK_ERR_UNSUPPORTED, "qkv: needs 16-byte aligned rows");
+        const int n_pairs = (H + 2 * KVH) * hd / 2;
+        hipLaunchKernelGGL(k_qkv_rope_norm, dim3((n_pairs + 3) / 4), dim3(256), 0, e->stream, st, xn, norm_w,
+                           c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl);
+        PK_HIP(hipGetLastError());
     } else {
         PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
+        const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
+        hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base,
+                           pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
+        PK_HIP(hipGetLastError());
     }
-    const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
-    hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base, pos_step,
-                       qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
-    PK_HIP(hipGetLastError());
     const int sliding = c->layer_type[l] == 0;
     const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
     int chunks = st ? max_chunks : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
     if (sliding) chunks = std::min(chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK);
     chunks = std::min(chunks, max_chunks);
+    PK_CHECK((int64_t)n * H <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d heads", n, H);
     hipLaunchKernelGGL(k_attn_part, dim3(H, chunks, n), dim3(ATT_CHUNK), 0, e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,
-                       part, max_chunks);
-    PK_HIP(hipGetLastError());
-    hipLaunchKernelGGL(k_attn_combine, dim3(H, n), dim3(64), 0, e->stream, st, pos_base, pos_step, part, d.sinks,
-                       H, hd, c->ctx_len, sliding, c->sliding_window, max_chunks, att);
+                       part, max_chunks, d.sinks, att, e->counters + PK_CTR_ATTN);
     PK_HIP(hipGetLastError());
     if (n >= 4) {
         // several rows: one read of wo per 32 rows
