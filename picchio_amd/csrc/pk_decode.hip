@@ -55,61 +55,77 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
 }
 
 // Decode QKV projection with the in_ln rmsnorm, the biases, RoPE
-// (picchio.c:455-473) and the KV store (picchio.c:492-498) fused: wave w
-// computes the row pair of one rotation, rows (head*hd + j, head*hd + j + hd/2)
-// of the q and k heads, or two adjacent v rows; lane 0 rotates the pair with
-// the host-built table at the decode position and writes q / K / V.
+// (picchio.c:455-473) and the KV store (picchio.c:492-498) fused. Each wave
+// computes one row; waves (0,1) and (2,3) hold the two rows of one rotation,
+// (head*hd + j, head*hd + j + hd/2) for q and k heads, or two adjacent v
+// rows, and meet in LDS, where the first of the pair rotates them with the
+// host-built table at the decode position and writes q / K / V. The first
+// weight loads are issued before the norm reduction so that they overlap it.
+__device__ __forceinline__ void qkv_fma4(float &a, float4 x, pk_f32x4 w) {
+    a = __builtin_fmaf(x.x, w.x, a);
+    a = __builtin_fmaf(x.y, w.y, a);
+    a = __builtin_fmaf(x.z, w.z, a);
+    a = __builtin_fmaf(x.w, w.w, a);
+}
+
 __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, const float *__restrict__ h,
                                                        const float *__restrict__ nw, float eps,
                                                        const float *__restrict__ W, const float *__restrict__ b,
                                                        int D, int H, int KVH, int hd, const float *rope,
                                                        float *qkv, float *Kl, float *Vl) {
     __shared__ double npart[4];
-    const int lane = threadIdx.x & 63;
+    __shared__ float pv[4];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int half = hd / 2;
     const int n_rot = (H + KVH) * half, n_pairs = n_rot + KVH * half;
-    const float rn = pk_block_rms_scale(h, D, eps, npart);
-    const int pi = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (pi >= n_pairs) return;
-    int r0, r1, head = 0, j = 0;
-    if (pi < n_rot) {
-        head = pi / half;
-        j = pi - head * half;
-        r0 = head * hd + j;
-        r1 = r0 + half;
-    } else {
-        r0 = (H + KVH) * hd + 2 * (pi - n_rot);
-        r1 = r0 + 1;
+    const int pi = blockIdx.x * 2 + (wave >> 1);
+    const bool live = pi < n_pairs;
+    int r0 = 0, head = 0, j = 0;
+    if (live) {
+        if (pi < n_rot) {
+            head = pi / half;
+            j = pi - head * half;
+            r0 = head * hd + j;
+        } else {
+            r0 = (H + KVH) * hd + 2 * (pi - n_rot);
+        }
     }
+    const int r1 = pi < n_rot ? r0 + half : r0 + 1;
+    const int row = live ? ((wave & 1) ? r1 : r0) : 0;
+    const pk_f32x4 *w4 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)row * D);
     const float4 *h4 = reinterpret_cast<const float4 *>(h);
     const float4 *n4w = reinterpret_cast<const float4 *>(nw);
-    const pk_f32x4 *w0 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)r0 * D);
-    const pk_f32x4 *w1 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)r1 * D);
     const int n4 = D >> 2;
-    float a0 = 0.0f, a1 = 0.0f;
-    for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
+    pk_f32x4 wf[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = lane + u * 64;
+        wf[u] = live && i < n4 ? __builtin_nontemporal_load(w4 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float rn = pk_block_rms_scale(h, D, eps, npart);
+    float a = 0.0f;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+        const int i = lane + u * 64;
+        if (i < n4) qkv_fma4(a, pk_norm4(h4[i], rn, n4w[i]), wf[u]);
+    }
+    for (int i0 = lane + 256; live && i0 < n4; i0 += 256) {
+        pk_f32x4 wv[4];
         float4 xv[4];
-        pk_f32x4 wa[4], wb[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int i = i0 + u * 64;
-            const bool in = i < n4;
-            xv[u] = in ? pk_norm4(h4[i], rn, n4w[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
-            wa[u] = in ? __builtin_nontemporal_load(w0 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
-            wb[u] = in ? __builtin_nontemporal_load(w1 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+            wv[u] = i < n4 ? __builtin_nontemporal_load(w4 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+            xv[u] = i < n4 ? pk_norm4(h4[i], rn, n4w[i]) : make_float4(0.f, 0.f, 0.f, 0.f);
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            a0 = __builtin_fmaf(xv[u].x, wa[u].x, a0); a0 = __builtin_fmaf(xv[u].y, wa[u].y, a0);
-            a0 = __builtin_fmaf(xv[u].z, wa[u].z, a0); a0 = __builtin_fmaf(xv[u].w, wa[u].w, a0);
-            a1 = __builtin_fmaf(xv[u].x, wb[u].x, a1); a1 = __builtin_fmaf(xv[u].y, wb[u].y, a1);
-            a1 = __builtin_fmaf(xv[u].z, wb[u].z, a1); a1 = __builtin_fmaf(xv[u].w, wb[u].w, a1);
-        }
+        for (int u = 0; u < 4; ++u) qkv_fma4(a, xv[u], wv[u]);
     }
-    a0 = wave_sum(a0);
-    a1 = wave_sum(a1);
-    if (lane != 0) return;
-    const float v0 = a0 + b[r0], v1 = a1 + b[r1];
+    a = wave_sum(a);
+    if (lane == 0) pv[wave] = a;
+    __syncthreads();
+    if (!live || (wave & 1) || lane != 0) return;
+    const float v0 = pv[wave] + b[r0], v1 = pv[wave + 1] + b[r1];
     const int pos = st->pos, kv_dim = KVH * hd;
     if (pi < n_rot) {
         const float cs = rope[((int64_t)pos * half + j) * 2 + 0];
@@ -362,11 +378,12 @@ __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restr
     if (lane == 0) y[o] = y[o] + (acc + b[o]);
 }
 
-// lm_head GEMV (fp32 or INT8 rows) fused with the greedy argmax of
-// sample_logits (first maximum, picchio.c:1555-1560): each block reduces its
-// rows to (value, lowest index); the last block to arrive reduces the block
-// results, writes the token, appends it to the output list and advances the
-// position. Blocks exchange results through device-coherent stores.
+// lm_head GEMV (fp32 or INT8 rows) and the greedy argmax of sample_logits
+// (first maximum, picchio.c:1555-1560), in two launches: every block writes
+// its rows' logits and its best (value, lowest index) pair; one workgroup
+// then reduces the block pairs, writes the token, appends it to the output
+// list and advances the position. (A single arrival counter for ~25k blocks
+// serialised at L2 and cost more than the second launch.)
 constexpr int LM_ROWS_PER_BLOCK = 8;      // 4 waves x 2 rows
 
 __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
@@ -374,85 +391,100 @@ __device__ __forceinline__ void better(float &bv, int &bi, float v, int i) {
 }
 
 template <bool Q8>
-__global__ __launch_bounds__(256) void k_lm_head_argmax(const float *__restrict__ x, const void *__restrict__ Wv,
-                                                        const float *__restrict__ sc, int I, int O,
-                                                        float *logits, float *bval, int32_t *bidx,
-                                                        uint32_t *counter, pk_dstate *st, int32_t *out_toks,
-                                                        int out_cap) {
+__global__ __launch_bounds__(256) void k_lm_head(const float *__restrict__ x, const void *__restrict__ Wv,
+                                                 const float *__restrict__ sc, int I, int O, float *logits,
+                                                 float *bval, int32_t *bidx) {
     __shared__ float rv[4];
     __shared__ int ri[4];
-    __shared__ int last;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     float bv = -INFINITY;
     int bi = 0x7fffffff;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
     const int n4 = I >> 2;
-    for (int r = 0; r < 2; ++r) {
-        const int o = blockIdx.x * LM_ROWS_PER_BLOCK + wave * 2 + r;
-        if (o >= O) break;
-        float acc = 0.0f;
-        if (Q8) {
-            const int8_t *w = reinterpret_cast<const int8_t *>(Wv) + (int64_t)o * I;
-            for (int i = lane; i < I; i += 64) acc = __builtin_fmaf(x[i], (float)w[i], acc);
-        } else {
-            const float4 *w4 = reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(Wv) + (int64_t)o * I);
-            for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
-                float4 xv[4];
-                pk_f32x4 wv[4];
+    const int o0 = blockIdx.x * LM_ROWS_PER_BLOCK + wave * 2;
+    float acc[2] = {0.0f, 0.0f};
+    if (Q8) {
 #pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    const int i = i0 + u * 64;
-                    xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-                    wv[u] = i < n4 ? __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4) + i)
-                                   : pk_f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u) {
-                    acc = __builtin_fmaf(xv[u].x, wv[u].x, acc);
-                    acc = __builtin_fmaf(xv[u].y, wv[u].y, acc);
-                    acc = __builtin_fmaf(xv[u].z, wv[u].z, acc);
-                    acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
-                }
-            }
-            const float *wr = reinterpret_cast<const float *>(Wv) + (int64_t)o * I;
-            for (int i = (n4 << 2) + lane; i < I; i += 64) acc = __builtin_fmaf(x[i], wr[i], acc);
+        for (int r = 0; r < 2; ++r) {
+            const int8_t *w = reinterpret_cast<const int8_t *>(Wv) + (int64_t)min(o0 + r, O - 1) * I;
+            for (int i = lane; i < I; i += 64) acc[r] = __builtin_fmaf(x[i], (float)w[i], acc[r]);
         }
-        acc = wave_sum(acc);
-        if (Q8) acc = acc * sc[o];
-        if (lane == 0 && logits) logits[o] = acc;
-        better(bv, bi, acc, o);
+    } else {
+        const pk_f32x4 *w4[2];
+#pragma unroll
+        for (int r = 0; r < 2; ++r)
+            w4[r] = reinterpret_cast<const pk_f32x4 *>(reinterpret_cast<const float *>(Wv) +
+                                                       (int64_t)min(o0 + r, O - 1) * I);
+        for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
+            float4 xv[4];
+            pk_f32x4 wv[2][4];
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int i = i0 + u * 64;
+                xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+                for (int r = 0; r < 2; ++r)
+                    wv[r][u] = i < n4 ? __builtin_nontemporal_load(w4[r] + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int r = 0; r < 2; ++r) {
+                    acc[r] = __builtin_fmaf(xv[u].x, wv[r][u].x, acc[r]);
+                    acc[r] = __builtin_fmaf(xv[u].y, wv[r][u].y, acc[r]);
+                    acc[r] = __builtin_fmaf(xv[u].z, wv[r][u].z, acc[r]);
+                    acc[r] = __builtin_fmaf(xv[u].w, wv[r][u].w, acc[r]);
+                }
+        }
+        for (int i = (n4 << 2) + lane; i < I; i += 64)
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+                acc[r] = __builtin_fmaf(x[i], reinterpret_cast<const float *>(Wv)[(int64_t)min(o0 + r, O - 1) * I + i],
+                                        acc[r]);
+    }
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        float v = wave_sum(acc[r]);
+        const int o = o0 + r;
+        if (o < O) {
+            if (Q8) v = v * sc[o];
+            if (lane == 0 && logits) logits[o] = v;
+            better(bv, bi, v, o);
+        }
     }
     if (lane == 0) { rv[wave] = bv; ri[wave] = bi; }
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w) better(bv, bi, rv[w], ri[w]);
-        __hip_atomic_store(bval + blockIdx.x, bv, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(bidx + blockIdx.x, bi, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
-        last = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-               gridDim.x - 1;
+        bval[blockIdx.x] = bv;
+        bidx[blockIdx.x] = bi;
     }
-    __syncthreads();
-    if (!last || wave != 0) return;
-    bv = -INFINITY;
-    bi = 0x7fffffff;
-    for (int b = lane; b < (int)gridDim.x; b += 64)
-        better(bv, bi, __hip_atomic_load(bval + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-               __hip_atomic_load(bidx + b, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+}
+
+// One workgroup: the best of the block pairs, then the decode-state update.
+__global__ __launch_bounds__(1024) void k_argmax_blocks(const float *bval, const int32_t *bidx, int nb,
+                                                        pk_dstate *st, int32_t *out_toks, int out_cap) {
+    __shared__ float rv[16];
+    __shared__ int ri[16];
+    float bv = -INFINITY;
+    int bi = 0x7fffffff;
+    for (int b = threadIdx.x; b < nb; b += blockDim.x) better(bv, bi, bval[b], bidx[b]);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
         const int oi = __shfl_xor(bi, o, 64);
         better(bv, bi, ov, oi);
     }
-    if (lane == 0) {
+    if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = bv; ri[threadIdx.x >> 6] = bi; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(bv, bi, rv[w], ri[w]);
         const int tok = bi == 0x7fffffff ? 0 : bi;
         if (st->n_out < out_cap) out_toks[st->n_out] = tok;
         st->n_out = st->n_out + 1;
         st->next = tok;
         st->tok = tok;
         st->pos = st->pos + 1;
-        __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
 }
 
@@ -515,7 +547,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
         PK_CHECK(((uintptr_t)xn & 15) == 0 && ((uintptr_t)norm_w & 15) == 0 && (D & 3) == 0,
                  PK_ERR_UNSUPPORTED, "qkv: needs 16-byte aligned rows");
         const int n_pairs = (H + 2 * KVH) * hd / 2;
-        hipLaunchKernelGGL(k_qkv_rope_norm, dim3((n_pairs + 3) / 4), dim3(256), 0, e->stream, st, xn, norm_w,
+        hipLaunchKernelGGL(k_qkv_rope_norm, dim3((n_pairs + 1) / 2), dim3(256), 0, e->stream, st, xn, norm_w,
                            c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl);
         PK_HIP(hipGetLastError());
     } else {
@@ -580,13 +612,14 @@ int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *o
     float *lg = logits_dev ? logits_dev : e->logits;
     const int ps = pk_prof_begin(e, PK_PROF_LM_HEAD);
     if (c->lm_head_fmt == PK_FMT_INT8)
-        hipLaunchKernelGGL(k_lm_head_argmax<true>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
-                           (const void *)e->lm_q8, e->lm_s, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
-                           e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
+        hipLaunchKernelGGL(k_lm_head<true>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
+                           (const void *)e->lm_q8, e->lm_s, D, c->vocab, lg, e->lm_bval, e->lm_bidx);
     else
-        hipLaunchKernelGGL(k_lm_head_argmax<false>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
-                           (const void *)e->lm_f32, nullptr, D, c->vocab, lg, e->lm_bval, e->lm_bidx,
-                           e->counters + PK_CTR_LM_HEAD, e->dstate, out_toks, out_cap);
+        hipLaunchKernelGGL(k_lm_head<false>, dim3(lm_blocks), dim3(256), 0, e->stream, hn,
+                           (const void *)e->lm_f32, nullptr, D, c->vocab, lg, e->lm_bval, e->lm_bidx);
+    PK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(k_argmax_blocks, dim3(1), dim3(1024), 0, e->stream, e->lm_bval, e->lm_bidx, lm_blocks,
+                       e->dstate, out_toks, out_cap);
     PK_HIP(hipGetLastError());
     return pk_prof_end(e, ps);
 }

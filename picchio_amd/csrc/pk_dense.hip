@@ -449,13 +449,50 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
     __shared__ double npart[4];
     __shared__ int last;
     const int e = blockIdx.x;
-    float rn = 1.0f;
+    float v;
     if (nw) {
-        rn = pk_block_rms_scale(x, D, eps, npart);
+        // the router row's loads go out before the norm reduction
+        const float4 *w4 = reinterpret_cast<const float4 *>(R + (int64_t)e * D);
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const float4 *n4w = reinterpret_cast<const float4 *>(nw);
+        const int n4 = D >> 2;
+        float4 wf[GEMV_U];
+#pragma unroll
+        for (int u = 0; u < GEMV_U; ++u) {
+            const int i = threadIdx.x + u * 256;
+            wf[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+        const float rn = pk_block_rms_scale(x, D, eps, npart);
         const int span = (D + E - 1) / E;
         for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
+        float acc = 0.0f;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
+#pragma unroll
+            for (int u = 0; u < GEMV_U; ++u) {
+                const int i = i0 + u * 256;
+                if (i0 != (int)threadIdx.x) wf[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < GEMV_U; ++u) {
+                const int i = i0 + u * 256;
+                if (i < n4) {
+                    const float4 xv = pk_norm4(x4[i], rn, n4w[i]);
+                    acc = __builtin_fmaf(xv.x, wf[u].x, acc);
+                    acc = __builtin_fmaf(xv.y, wf[u].y, acc);
+                    acc = __builtin_fmaf(xv.z, wf[u].z, acc);
+                    acc = __builtin_fmaf(xv.w, wf[u].w, acc);
+                }
+            }
+        }
+        for (int i = (n4 << 2) + threadIdx.x; i < D; i += 256)
+            acc = __builtin_fmaf(x[i] * rn * nw[i], R[(int64_t)e * D + i], acc);
+        acc = pk_wave_sum(acc);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+        __syncthreads();
+        v = (red[0] + red[1]) + (red[2] + red[3]);
+    } else {
+        v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
     }
-    const float v = pk_row_dot_block(x, R + (int64_t)e * D, D, red, nw, rn);
     if (threadIdx.x == 0) {
         pk_st_dev(logits + e, v + b[e]);
         __builtin_amdgcn_s_waitcnt(0);

@@ -21,7 +21,6 @@ struct pk_dstate {
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
-constexpr int PK_CTR_LM_HEAD = 2048;      // lm_head+argmax arrivals
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
 constexpr int PK_CTR_N = PK_CTR_ATTN + PK_CTR_ATTN_N;
