@@ -462,6 +462,9 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain read+write kernel over this many "
                          "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--fused", type=int, default=0,
+                    help="kernels mode: 1 = each MoE layer as one launch (router .. combine), "
+                         "0 = three launches")
     ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill", "decode120b"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "
@@ -539,6 +542,9 @@ def main():
         extra = {"unchained_us_per_token": round(ms_nochain / S * 1e3, 3),
                  "unchained_gbps": round(S * TOKEN_BYTES / (ms_nochain * 1e-3) / 1e9, 1)}
     else:
+        if args.fused:
+            eng.set_moe_fused(True)
+
         def enqueue(t):
             eng.moe_forward(t % L, xd[t], od[t])
         eng.capture_begin()
@@ -559,6 +565,7 @@ def main():
         ms = ev0.elapsed_time(ev1)
         eng.graph_destroy(g_warm)
         eng.graph_destroy(g_run)
+        eng.status()
         # The dominant kernel alone: each token's gate_up launch (4 experts of
         # its layer copy, the same k_i4_gemv<SWIGLU> the MoE step runs)
         # replayed back to back from a graph; HIP events on the engine stream
@@ -581,6 +588,16 @@ def main():
         roof_ms = gu_ms
         roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up + bias + SwiGLU, 4 experts/launch)"
         traffic = GATE_UP_TRAFFIC
+        if args.fused:
+            # the whole layer is the one kernel: all of its algorithmic bytes
+            # over its mean launch duration
+            ly_ms = replay_ms(eng, ev0, ev1, n_prof, lambda t: eng.moe_forward(t % L, xd[t], od[t]))
+            eng.status()
+            prof["moe_layer"] = ly_ms
+            roof_bytes = TOKEN_BYTES
+            roof_ms = ly_ms
+            roof_kernel = "k_moe_fused (router+top-4+gate_up+SwiGLU+down+combine, one launch per layer)"
+            traffic = None
         extra = {"down_gbps": round(down_bytes(K) / (dn_ms * 1e-3) / 1e9, 1),
                  "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
                  "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9

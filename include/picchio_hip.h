@@ -247,6 +247,25 @@ int pk_moe_seq_reserve(pk_engine *e, int T);
  * row blocks. NULL turns tracing off. */
 int pk_moe_seq_trace(pk_engine *e, uint64_t *trace_dev);
 
+/* moe_forward (picchio.c:1309-1466) in one launch: with on != 0, every
+ * batch-1 MoE layer (pk_moe_forward, the MoE of pk_forward_token /
+ * pk_generate) runs router, top-k, gate_up + SwiGLU, down and the combine as
+ * one grid whose workgroups exchange the logits, activations and expert rows
+ * through device-coherent memory, instead of three launches. Results are
+ * bit-identical to the three-launch path. No counterpart in the reference:
+ * it selects between two implementations of the same call.
+ * PK_ERR_UNSUPPORTED when the shape or the device's occupancy cannot hold
+ * the whole grid at once (the three launches stay in use). */
+int pk_set_moe_fused(pk_engine *e, int on);
+/* Tracing of the single-launch layer: six 100 MHz timestamps per workgroup
+ * (start, routed, gate_up stored, activations ready, down stored, end) into
+ * trace_dev[workgroup][6]; NULL turns it off. */
+int pk_moe_fused_trace(pk_engine *e, uint64_t *trace_dev);
+/* Errors raised inside kernels since the last call (a bounded dependency
+ * wait of the single-launch MoE layer that timed out: that layer's output is
+ * invalid). Synchronises the stream, re-arms the flag and counters. */
+int pk_engine_status(pk_engine *e);
+
 /* gqa_attention (picchio.c:504-623) for one token at `pos`; writes K/V. */
 int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
                      float *out_dev);
@@ -283,6 +302,7 @@ int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out_h
 #define PK_PROF_MOE_SEQ        4   /* persistent MoE sequence kernel (whole launch)  */
 #define PK_PROF_LM_HEAD        5   /* lm_head GEMV + greedy argmax                   */
 #define PK_PROF_ATTENTION      6   /* QKV .. O-projection of one layer (5 launches)  */
+#define PK_PROF_MOE_LAYER      7   /* single-launch MoE layer (router .. combine)    */
 #define PK_PROF_N              8
 int pk_engine_profile(pk_engine *e, int enable);
 int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);

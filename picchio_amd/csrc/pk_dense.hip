@@ -407,6 +407,9 @@ __global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E,
             const int oi = __shfl_xor(bi, o, 64);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
+        // no logit above -1e30 (NaN inputs): the reference leaves -1;
+        // here the index stays inside the store
+        if (bi >= E) bi = 0;
         chosen[k] = bi;
         val[k] = bv;
         if (bi == lane) t0 = true;
@@ -518,6 +521,9 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
             const int oi = __shfl_xor(bi, o, 64);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
+        // no logit above -1e30 (NaN inputs): the reference leaves -1;
+        // here the index stays inside the store
+        if (bi >= E) bi = 0;
         if (lane == 0) { ci[k] = bi; cv[k] = bv; }
         if (bi == lane) t0 = true;
         if (bi == lane + 64) t1 = true;

@@ -21,6 +21,7 @@ struct pk_dstate {
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
+constexpr int PK_CTR_FUSED = 2048;        // single-launch MoE layer (pk_moe_fused.hip)
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
 constexpr int PK_CTR_N = PK_CTR_ATTN + PK_CTR_ATTN_N;
@@ -85,6 +86,12 @@ struct pk_engine {
 
     int n_cu = 256;                          // compute units of the device
 
+    // single-launch MoE layer (pk_moe_fused.hip)
+    bool moe_fused = false;                  // pk_moe_layer runs it instead of three launches
+    int fused_fit = -1;                      // shape + occupancy check (-1: not yet made)
+    int fused_occ = 0;                       // its workgroups per CU
+    uint64_t *fused_trace = nullptr;         // optional per-workgroup timeline
+
     // persistent MoE sequence (pk_moe_forward_seq): per-step exchange buffers
     int seq_cap = 0;
     bool seq_ready = false;
@@ -135,6 +142,10 @@ int pk_prof_end(pk_engine *e, int slot);
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out, const float *norm_w = nullptr);
 int pk_check_layer_experts(pk_engine *e, int layer);
+// single-launch MoE layer (router .. combine); fits: shape and occupancy allow it
+bool pk_moe_fused_fits(pk_engine *e);
+int pk_moe_fused_launch(pk_engine *e, int layer, const float *x, float *out, const float *residual,
+                        const float *norm_w);
 pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
 
 // ── expert-grouped MFMA GEMM (pk_mfma.hip) ──

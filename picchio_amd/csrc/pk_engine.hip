@@ -736,6 +736,11 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out, const float *norm_w) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[layer];
+    if (e->moe_fused && pk_moe_fused_fits(e)) {
+        const int pf = pk_prof_begin(e, PK_PROF_MOE_LAYER);
+        PK_TRY(pk_moe_fused_launch(e, layer, x_dev, residual ? res_out : out_dev, residual, norm_w));
+        return pk_prof_end(e, pf);
+    }
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,

@@ -131,6 +131,9 @@ __device__ void topk_publish(const seq_args &a, int t, float *sv_lds, int *si_ld
             const int oi = __shfl_xor(bi, o, 64);
             if (ov > bv || (ov == bv && oi < bi)) { bv = ov; bi = oi; }
         }
+        // no logit above -1e30 (NaN inputs): the reference leaves -1;
+        // here the index stays inside the store
+        if (bi >= E) bi = 0;
         if (lane == 0) { si_lds[k] = bi; sv_lds[k] = bv; }
         if (bi == lane) t0 = true;
         if (bi == lane + 64) t1 = true;
