@@ -199,31 +199,51 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
     }
 }
 
-// Attention partials: block (h, c, r) scores positions start+128c .. +127 of
-// row r's window for head h against its KV head (h / group). Scores are the
-// reference's in-order dot (uncontracted products added one by one,
-// picchio.c:573-577 as gcc builds it) times 1/sqrt(hd). Writes the chunk max,
-// the sum of exp(s - max) and the exp-weighted V sum (flash-decoding
-// partials). The V sum runs as hd/4 float4 columns x (128*4/hd) position
-// groups, each group's loads issued together, then the groups are added in
-// a fixed order.
+// Attention partials: block (b, c, r) covers positions start+128c .. +127 of
+// row r's window for gs of the G = H/KVH query heads that share one KV head
+// (block b: KV head b / (G/gs), heads (b % (G/gs)) * gs ..), so each K and V
+// row is read once per gs heads: gs = G at long contexts and large batches
+// (one read per group), smaller when there would be too few blocks. Per head the arithmetic
+// is fixed: scores are the reference's in-order dot (uncontracted products
+// added one by one, picchio.c:573-577 as gcc builds it) times 1/sqrt(hd); the
+// chunk max; p = exp(s - max) and its sum (lanes over t, t+64, then the wave
+// tree); the exp-weighted V sum as hd/4 float4 columns x (128*4/hd) position
+// groups summed in position order, the groups then added in order
+// (flash-decoding partials).
+//
+// Threads (128 per half, one or two halves): half = tid / 128 takes heads
+// [half*GH, half*GH + GH), GH = ceil(gs / halves); t = tid % 128 is the
+// position for the scores and (column, group) for V.
 //
 // The partials are stored device-coherently; the last of the row's chunk
-// blocks to arrive at its (row, head) counter combines them with the learned
-// sink (picchio.c:586-604: the sink joins the max and the denominator, not the
-// value sum), writes att [row][h*hd..] and re-arms the counter.
-__global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
-                                                         const float *qkv, int64_t qkv_stride, const float *Kl,
-                                                         const float *Vl, int64_t kv_row, int H, int KVH,
-                                                         int hd, int ctx, int sliding, int window, float *part,
-                                                         int max_chunks, const float *sinks, float *att,
-                                                         uint32_t *ctr) {
-    __shared__ __attribute__((aligned(16))) float q[128];
-    __shared__ float p[ATT_CHUNK];
-    __shared__ float red[2];
-    __shared__ __attribute__((aligned(16))) float vred[ATT_CHUNK * 4];
+// blocks to arrive at its (row, b) counter combines them for the gs heads
+// with the learned sinks (picchio.c:586-604: the sink joins the max and the
+// denominator, not the value sum), writes att [row][h*hd..] and re-arms the
+// counter.
+constexpr int ATT_THREADS = 256;
+constexpr int ATT_GH = 8;              // query heads per half-block (G <= 16)
+
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
+                                                           const float *qkv, int64_t qkv_stride, const float *Kl,
+                                                           const float *Vl, int64_t kv_row, int H, int KVH,
+                                                           int hd, int ctx, int sliding, int window, float *part,
+                                                           int max_chunks, const float *sinks, float *att,
+                                                           uint32_t *ctr, int gs) {
+    extern __shared__ __attribute__((aligned(16))) float att_lds[];
+    const int G = gs;                         // heads of this block
+    float *q = att_lds;                       // [G][hd]
+    float *p = q + G * hd;                    // [G][128]
+    float *vred = p + G * ATT_CHUNK;          // [G][PG][hd]
+    __shared__ float red[4][ATT_GH];
+    __shared__ float mh[2 * ATT_GH];
     __shared__ int last;
-    const int h = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
+    const int b = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
+    const int kvh = b / ((H / KVH) / gs);
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int half = tid >> 7, tt = tid & 127;
+    const int halves = blockDim.x >> 7, waves = blockDim.x >> 6;
+    const int GH = (G + halves - 1) / halves;
+    const int ja = half * GH, jn = min(G, ja + GH) - ja;    // this half's heads
     qkv += (int64_t)r * qkv_stride;
     part += (int64_t)r * H * max_chunks * (hd + 2);
     Kl += (int64_t)r * kv_row;
@@ -233,14 +253,20 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
     const int t0 = start + c * ATT_CHUNK;
     const int n = min(ATT_CHUNK, end - t0 + 1);
     if (n <= 0) return;
-    const int kv_dim = KVH * hd, kvh = h / (H / KVH);
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) q[i] = qkv[h * hd + i];
+    const int kv_dim = KVH * hd, h0 = b * gs;
+    for (int i = tid; i < G * hd; i += blockDim.x) q[i] = qkv[h0 * hd + i];
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)hd);
-    float s = -INFINITY;
-    if ((int)threadIdx.x < n) {
-        const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + threadIdx.x) * kv_dim + kvh * hd);
-        float dot = 0.0f;
+
+    // scores of position tt for this half's heads (K row loaded once)
+    float sc[ATT_GH];
+#pragma unroll
+    for (int jj = 0; jj < ATT_GH; ++jj) sc[jj] = -INFINITY;
+    if (tt < n) {
+        const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + tt) * kv_dim + kvh * hd);
+        float dot[ATT_GH];
+#pragma unroll
+        for (int jj = 0; jj < ATT_GH; ++jj) dot[jj] = 0.0f;
         for (int i0 = 0; i0 < hd; i0 += 32) {         // 32 columns: loads first, then the in-order adds
             float4 kv[8];
 #pragma unroll
@@ -248,88 +274,115 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
 #pragma unroll
             for (int u = 0; u < 8; ++u) {
                 if (i0 + 4 * u >= hd) break;
-                const float *qq = q + i0 + 4 * u;
-                float pr;
-                pr = qq[0] * kv[u].x; dot = dot + pr;
-                pr = qq[1] * kv[u].y; dot = dot + pr;
-                pr = qq[2] * kv[u].z; dot = dot + pr;
-                pr = qq[3] * kv[u].w; dot = dot + pr;
+#pragma unroll
+                for (int jj = 0; jj < ATT_GH; ++jj) {
+                    if (jj >= jn) break;
+                    const float *qq = q + (ja + jj) * hd + i0 + 4 * u;
+                    float pr;
+                    pr = qq[0] * kv[u].x; dot[jj] = dot[jj] + pr;
+                    pr = qq[1] * kv[u].y; dot[jj] = dot[jj] + pr;
+                    pr = qq[2] * kv[u].z; dot[jj] = dot[jj] + pr;
+                    pr = qq[3] * kv[u].w; dot[jj] = dot[jj] + pr;
+                }
             }
         }
-        s = dot * scale;
-    }
-    // chunk max (wave 0 / wave 1 halves), then p = exp(s - m)
-    float m = s;
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
-    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+        for (int jj = 0; jj < ATT_GH; ++jj) sc[jj] = dot[jj] * scale;
+    }
+    // per-head chunk max over the half's two waves, then p = exp(s - m)
+#pragma unroll
+    for (int jj = 0; jj < ATT_GH; ++jj) {
+        if (jj >= jn) break;
+        float m = sc[jj];
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        if (lane == 0) red[wave][jj] = m;
+    }
     __syncthreads();
-    m = fmaxf(red[0], red[1]);
-    const float e = (int)threadIdx.x < n ? expf(s - m) : 0.0f;
-    p[threadIdx.x] = e;
+#pragma unroll
+    for (int jj = 0; jj < ATT_GH; ++jj) {
+        if (jj >= jn) break;
+        const float m = fmaxf(red[2 * half][jj], red[2 * half + 1][jj]);
+        p[(ja + jj) * ATT_CHUNK + tt] = tt < n ? expf(sc[jj] - m) : 0.0f;
+        if (tt == 0) mh[ja + jj] = m;
+    }
     __syncthreads();
-    float* out = part + ((int64_t)h * max_chunks + c) * (hd + 2);
-    if (threadIdx.x < 64) {
+    // per-head sums: wave w takes heads w, w + waves, ...
+    for (int j = wave; j < G; j += waves) {
+        const float *pj = p + j * ATT_CHUNK;
         float sum = 0.0f;
-        for (int t = threadIdx.x; t < n; t += 64) sum += p[t];
+        for (int t = lane; t < n; t += 64) sum += pj[t];
         sum = wave_sum(sum);
-        if (threadIdx.x == 0) {
-            __hip_atomic_store(out, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (lane == 0) {
+            float *out = part + ((int64_t)(h0 + j) * max_chunks + c) * (hd + 2);
+            __hip_atomic_store(out, mh[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __hip_atomic_store(out + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     }
-    // V sum: thread = (column group c4 of hd/4, position group g of PG)
+    // V sums: thread = (column group c4 of hd/4, position group g of PG) of its half
     const int D4 = hd >> 2, PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
-    const int c4 = threadIdx.x % D4, g = threadIdx.x / D4;
+    const int c4 = tt % D4, g = tt / D4;
     const float4 *v4 = reinterpret_cast<const float4 *>(Vl + (int64_t)t0 * kv_dim + kvh * hd) + c4;
     const int kv4 = kv_dim >> 2;
-    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j0 = 0; j0 < PER; j0 += 16) {
-        float4 vv[16];
-        float pw[16];
+    float4 acc[ATT_GH];
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
+    for (int jj = 0; jj < ATT_GH; ++jj) acc[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j0 = 0; j0 < PER; j0 += 8) {
+        float4 vv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int t = g * PER + j0 + u;
+            vv[u] = j0 + u < PER && t < n ? v4[(int64_t)t * kv4] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
             const int t = g * PER + j0 + u;
             const bool ok = j0 + u < PER && t < n;
-            vv[u] = ok ? v4[(int64_t)t * kv4] : make_float4(0.f, 0.f, 0.f, 0.f);
-            pw[u] = ok ? p[t] : 0.0f;
-        }
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            acc.x = __builtin_fmaf(pw[u], vv[u].x, acc.x);
-            acc.y = __builtin_fmaf(pw[u], vv[u].y, acc.y);
-            acc.z = __builtin_fmaf(pw[u], vv[u].z, acc.z);
-            acc.w = __builtin_fmaf(pw[u], vv[u].w, acc.w);
+            for (int jj = 0; jj < ATT_GH; ++jj) {
+                if (jj >= jn) break;
+                const float pw = ok ? p[(ja + jj) * ATT_CHUNK + t] : 0.0f;
+                acc[jj].x = __builtin_fmaf(pw, vv[u].x, acc[jj].x);
+                acc[jj].y = __builtin_fmaf(pw, vv[u].y, acc[jj].y);
+                acc[jj].z = __builtin_fmaf(pw, vv[u].z, acc[jj].z);
+                acc[jj].w = __builtin_fmaf(pw, vv[u].w, acc[jj].w);
+            }
         }
     }
-    *reinterpret_cast<float4 *>(&vred[g * hd + 4 * c4]) = acc;
+#pragma unroll
+    for (int jj = 0; jj < ATT_GH; ++jj) {
+        if (jj >= jn) break;
+        *reinterpret_cast<float4 *>(&vred[((ja + jj) * PG + g) * hd + 4 * c4]) = acc[jj];
+    }
     __syncthreads();
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+    for (int idx = tid; idx < G * hd; idx += blockDim.x) {
+        const int j = idx / hd, i = idx - j * hd;
         float o = 0.0f;
-        for (int gg = 0; gg < PG; ++gg) o += vred[gg * hd + i];
+        for (int gg = 0; gg < PG; ++gg) o += vred[(j * PG + gg) * hd + i];
+        float *out = part + ((int64_t)(h0 + j) * max_chunks + c) * (hd + 2);
         __hip_atomic_store(out + 2 + i, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
-    // arrival: the last of the nc chunk blocks combines
+    // arrival: the last of the nc chunk blocks of (row, b) combines
     const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    uint32_t *cnt = ctr + (int64_t)r * H + h;
-    if (threadIdx.x == 0)
+    uint32_t *cnt = ctr + (int64_t)r * gridDim.x + b;
+    if (tid == 0)
         last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nc - 1);
     __syncthreads();
     if (!last) return;
-    const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
-    float M = sinks[h];
-    for (int cc = 0; cc < nc; ++cc)
-        M = fmaxf(M, __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
-    float S = expf(sinks[h] - M);
-    for (int cc = 0; cc < nc; ++cc) {
-        const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        S += __hip_atomic_load(ph + cc * (hd + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
-             expf(mc - M);
-    }
-    float *ar = att + (int64_t)r * H * hd + h * hd;
-    for (int i = threadIdx.x; i < hd; i += blockDim.x) {
+    for (int idx = tid; idx < G * hd; idx += blockDim.x) {
+        const int j = idx / hd, i = idx - j * hd, h = h0 + j;
+        const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
+        float M = sinks[h];
+        for (int cc = 0; cc < nc; ++cc)
+            M = fmaxf(M, __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        float S = expf(sinks[h] - M);
+        for (int cc = 0; cc < nc; ++cc) {
+            const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            S += __hip_atomic_load(ph + cc * (hd + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
+                 expf(mc - M);
+        }
         float o = 0.0f;
         for (int cc = 0; cc < nc; ++cc) {
             const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -337,9 +390,9 @@ __global__ __launch_bounds__(ATT_CHUNK) void k_attn_part(const pk_dstate *st, in
                                                  __HIP_MEMORY_SCOPE_AGENT),
                                expf(mc - M), o);
         }
-        ar[i] = o / S;
+        att[(int64_t)r * H * hd + h * hd + i] = o / S;
     }
-    if (threadIdx.x == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // y[o] += (W[o] . x + b[o])  — attention output projection + residual
@@ -562,10 +615,23 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     int chunks = st ? max_chunks : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
     if (sliding) chunks = std::min(chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK);
     chunks = std::min(chunks, max_chunks);
-    PK_CHECK((int64_t)n * H <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d heads", n, H);
-    hipLaunchKernelGGL(k_attn_part, dim3(H, chunks, n), dim3(ATT_CHUNK), 0, e->stream, st, pos_base, pos_step,
+    const int G = H / KVH;
+    PK_CHECK(H % KVH == 0 && G <= 2 * ATT_GH, PK_ERR_UNSUPPORTED, "attention: %d query heads per KV head", G);
+    // heads per block: the most that still gives >= 1024 blocks (K/V read once
+    // per gs heads), one head per 128-thread block when the grid is small
+    int gs = 1;
+    while (gs * 2 <= G && G % (gs * 2) == 0 && (int64_t)KVH * (G / (gs * 2)) * chunks * n >= 1024) gs *= 2;
+    if (const char *v = getenv("PK_ATT_GS")) {
+        const int f = atoi(v);
+        if (f >= 1 && f <= G && G % f == 0) gs = f;
+    }
+    PK_CHECK((int64_t)n * (H / gs) <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d blocks", n,
+             H / gs);
+    const size_t att_lds = (size_t)gs * (hd + ATT_CHUNK + ATT_CHUNK * 4) * sizeof(float);
+    hipLaunchKernelGGL(k_attn_part, dim3(H / gs, chunks, n), dim3(gs > 1 ? ATT_THREADS : ATT_CHUNK), att_lds,
+                       e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,
-                       part, max_chunks, d.sinks, att, e->counters + PK_CTR_ATTN);
+                       part, max_chunks, d.sinks, att, e->counters + PK_CTR_ATTN, gs);
     PK_HIP(hipGetLastError());
     if (n >= 4) {
         // several rows: one read of wo per 32 rows
