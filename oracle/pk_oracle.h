@@ -29,6 +29,13 @@
  *   po_model_build / po_fill_normal     the synthetic-input generator (not a
  *                          reference function); the GPU generator is checked
  *                          against it bit-for-bit in the GPU tests.
+ *   po_act_limbs           (the library's own int8 prefill arithmetic) the
+ *                          exponent's frexp definition, limb ranges incl. the
+ *                          +-64 boundaries, nearest-grid bound, exactness on
+ *                          grid points, ties to even
+ *   po_mfma_matvec         float64 brute force with exact int64 group sums,
+ *                          inside the fp32 fold's error bound (a planted wrong
+ *                          limb weight fails it)
  * Nothing here is "parity unpinned". Transcendentals (expf, cosf, sinf, powf,
  * logf) are glibc's, as in the reference build, so the oracle matches the
  * reference bit-for-bit on this image; the GPU path's own transcendentals are

@@ -483,3 +483,105 @@ def test_sink_minus_inf_is_plain_softmax(oracle):
             assert rel_l2(out, ref(1, x, pos)) < 1e-5
     finally:
         oracle.model_free(model)
+
+
+# ── the grouped MFMA path's arithmetic (not a reference function) ──
+# po_act_limbs / po_mfma_matvec restate what the library's int8 matrix-core
+# prefill computes. They are pinned here by what the mathematics fixes: the
+# exponent's definition, limb ranges, the rounding bound and ties-to-even of
+# the scaled grid, exactness on grid points, and a float64 brute force with
+# exact int64 group sums for the GEMV. A wrong shift, sign, nibble order or
+# limb weight fails one of these.
+
+def _limb_rows():
+    rng = np.random.default_rng(71)
+    cols = 192
+    x = rng.standard_normal((10, cols)).astype(np.float32)
+    x[1] = 0.0                                          # all zero: k = 0, limbs 0
+    x[2] *= np.float32(1e-30)                           # tiny magnitudes
+    x[3] *= np.float32(1e30)                            # huge magnitudes
+    x[4] = np.float32(0.25)
+    x[4, 5] = np.float32(1.0)                           # max an exact power of two: k = 1
+    k5 = 3                                              # a row on the grid of exponent 3
+    j = rng.integers(-(1 << 20), 1 << 20, cols)
+    j[0] = 1 << 20 - 1
+    x[5] = (j * 2.0 ** (k5 - 20)).astype(np.float32)
+    x[5, 0] = np.float32(7.5)                           # max in [4, 8): k = 3
+    half = rng.integers(-(1 << 18), 1 << 18, cols) + 0.5  # ties on the grid of x[6]
+    x[6] = (half * 2.0 ** (2 - 20)).astype(np.float32)
+    x[6, 0] = np.float32(3.0)                           # max in [2, 4): k = 2
+    x[7, :] = np.float32(-5.0)                          # negative extreme, constant row
+    # limb boundaries (k = 0, step 2^-20): A = 2^20 gives a0 = 64, A = 8191
+    # gives a1 = 64, A = +-8192 gives a1 = -64
+    x[8, 1::4] = np.float32(8191 * 2.0 ** -20)
+    x[8, 2::4] = np.float32(8192 * 2.0 ** -20)
+    x[8, 3::4] = np.float32(-8192 * 2.0 ** -20)
+    x[8, 4::4] = np.float32(-8191 * 2.0 ** -20)
+    x[8, 0] = np.nextafter(np.float32(1.0), np.float32(0.0))
+    return x
+
+
+def test_act_limbs_definition_and_bounds(oracle):
+    x = _limb_rows()
+    rows, cols = x.shape
+    limbs = np.empty((3, rows, cols), np.int8)
+    exps = np.empty(rows, np.int32)
+    oracle.act_limbs(x, rows, cols, limbs, exps)
+    L = limbs.astype(np.int64)
+    A = L[0] * 16384 + L[1] * 128 + L[2]
+    assert L[0].min() >= -64 and L[0].max() <= 64
+    assert L[1].min() >= -64 and L[1].max() <= 64
+    assert L[2].min() >= -64 and L[2].max() <= 63
+    for r in range(rows):
+        m = float(np.abs(x[r].astype(np.float64)).max())
+        if m == 0.0:
+            assert exps[r] == 0 and not A[r].any()
+            continue
+        k = int(exps[r])
+        assert 2.0 ** (k - 1) <= m < 2.0 ** k, (r, k, m)          # frexp exponent of max|x|
+        step = 2.0 ** (k - 20)
+        err = np.abs(A[r] * step - x[r].astype(np.float64))
+        assert err.max() <= step / 2, r                          # nearest grid point
+        assert np.abs(A[r]).max() <= 1 << 20
+    assert exps[4] == 1 and exps[5] == 3 and exps[6] == 2 and exps[8] == 0
+    assert A[8, 0] == 1 << 20 and L[0, 8, 0] == 64
+    assert L[1, 8].max() == 64 and L[1, 8].min() == -64
+    # on the grid: exact
+    assert np.array_equal(A[5] * 2.0 ** (3 - 20), x[5].astype(np.float64)[:])
+    # ties round to the even neighbour
+    t = x[6].astype(np.float64) * 2.0 ** (20 - 2)
+    tie = (t - np.floor(t)) == 0.5
+    assert tie.sum() > 100 and np.all(A[6][tie] % 2 == 0)
+
+
+@pytest.mark.parametrize("O,I,scale", [(96, 256, 1.0), (64, 192, 1e-6), (130, 320, 3e4)])
+def test_mfma_matvec_against_float64(oracle, O, I, scale):
+    rng = np.random.default_rng(O + I)
+    w = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    w[3, :64] = 0.0                                       # a zero group
+    q4, s = oracle.quant_gs(w, 64)
+    bias = (rng.standard_normal(O) * 0.02).astype(np.float32)
+    x = (rng.standard_normal((3, I)) * scale).astype(np.float32)
+    x[1, 10] = np.float32(-40.0 * scale)                  # one dominant element
+    x[2] = np.float32(0.0)                                 # zero row: y = bias
+    limbs = np.empty((3, 3, I), np.int8)
+    exps = np.empty(3, np.int32)
+    oracle.act_limbs(x, 3, I, limbs, exps)
+    A = limbs.astype(np.int64)
+    A = A[0] * 16384 + A[1] * 128 + A[2]                   # [3][I]
+    nib = np.empty((O, I), np.int64)
+    nib[:, 0::2] = q4 & 15
+    nib[:, 1::2] = q4 >> 4
+    q = nib - 8                                            # int4 values
+    ng = I // 64
+    for r in range(3):
+        y = np.empty(O, np.float32)
+        oracle.mfma_matvec(q4, s, bias, O, I, limbs[0, r], limbs[1, r], limbs[2, r], int(exps[r]), y)
+        # exact group sums C_g = sum A q (int64), then float64 terms
+        C = (q.reshape(O, ng, 64) * A[r].reshape(1, ng, 64)).sum(axis=2)
+        term = 16.0 * s.astype(np.float64) * C * 2.0 ** (int(exps[r]) - 24)
+        y64 = term.sum(axis=1) + bias
+        bound = (ng + 2) * 2.0 ** -24 * (np.abs(term).sum(axis=1) + np.abs(bias)) + 1e-45
+        assert np.all(np.abs(y.astype(np.float64) - y64) <= bound), r
+        if r == 2:
+            assert bits_equal(y, bias)
