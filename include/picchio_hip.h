@@ -257,9 +257,10 @@ int pk_moe_seq_trace(pk_engine *e, uint64_t *trace_dev);
  * PK_ERR_UNSUPPORTED when the shape or the device's occupancy cannot hold
  * the whole grid at once (the three launches stay in use). */
 int pk_set_moe_fused(pk_engine *e, int on);
-/* Tracing of the single-launch layer: six 100 MHz timestamps per workgroup
- * (start, routed, gate_up stored, activations ready, down stored, end) into
- * trace_dev[workgroup][6]; NULL turns it off. */
+/* Tracing of the single-launch layer, per workgroup into trace_dev[wg][6]:
+ * five 100 MHz timestamps (start, routed, first block done, last dependency
+ * wait done, last block published) and where it ran (XCC_ID << 32 | HW_ID);
+ * NULL turns it off. */
 int pk_moe_fused_trace(pk_engine *e, uint64_t *trace_dev);
 /* Errors raised inside kernels since the last call (a bounded dependency
  * wait of the single-launch MoE layer that timed out: that layer's output is

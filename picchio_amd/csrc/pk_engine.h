@@ -21,7 +21,12 @@ struct pk_dstate {
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
-constexpr int PK_CTR_FUSED = 2048;        // single-launch MoE layer (pk_moe_fused.hip)
+constexpr int PK_FUSED_CTL_BYTES = 131072;   // control block of the single-launch MoE layer
+// floats per private input row of the single-launch MoE layer (128-byte multiple)
+inline int pk_fused_row(const pk_cfg *c) {
+    const int n = c->hidden > c->moe_inter / 2 ? c->hidden : c->moe_inter / 2;
+    return (n + 31) & ~31;
+}
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
 constexpr int PK_CTR_N = PK_CTR_ATTN + PK_CTR_ATTN_N;
@@ -91,6 +96,8 @@ struct pk_engine {
     int fused_fit = -1;                      // shape + occupancy check (-1: not yet made)
     int fused_occ = 0;                       // its workgroups per CU
     uint64_t *fused_trace = nullptr;         // optional per-workgroup timeline
+    uint8_t *fused_ctl = nullptr;            // slots and counters (PK_FUSED_CTL_BYTES)
+    float *fused_xn = nullptr;               // [n_cu][2][pk_fused_row] rows private to each workgroup
 
     // persistent MoE sequence (pk_moe_forward_seq): per-step exchange buffers
     int seq_cap = 0;

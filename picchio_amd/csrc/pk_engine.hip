@@ -149,7 +149,8 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
-                    e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out};
+                    e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out,
+                    e->fused_ctl, e->fused_xn};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -207,7 +208,10 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->eo, (int64_t)K * D * 4);
     ALLOC(e->argmax_out, 64);
     ALLOC(e->counters, PK_CTR_N * 4);
+    ALLOC(e->fused_ctl, PK_FUSED_CTL_BYTES);
+    ALLOC(e->fused_xn, (int64_t)e->n_cu * 2 * pk_fused_row(c) * 4);   // two private rows per workgroup
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
+    PK_HIP(hipMemsetAsync(e->fused_ctl, 0, PK_FUSED_CTL_BYTES, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
 }
