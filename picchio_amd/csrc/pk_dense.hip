@@ -136,95 +136,102 @@ __global__ __launch_bounds__(256) void k_gemv_f32_rows(float *__restrict__ y, co
     if (threadIdx.x == 0) y[(int64_t)s * O + o] = bias ? v + bias[o] : v;
 }
 
-// ───────────────── skinny fp32 GEMM: several inputs per weight read ─────────────────
-// Y[s][o] = (residual ? Y[s][o] : 0) + (X[s] . W[o] + bias[o]) for s < S <= SB.
-// A wave owns 4 rows of W and all SB inputs: per 256-column chunk each lane
-// takes one float4 of each row (read once from HBM) against the chunk's SB
-// inputs staged in LDS (4 x SB accumulators per lane). The 64 lanes' partial
-// sums are then reduce-scattered in 6 exchange steps, leaving each lane two
-// finished (row, input) sums. grid = ceil(O / 16) workgroups of 4 waves.
-constexpr int SK_KC = 256;                 // columns per staged chunk
+// ───────────────── skinny fp32 GEMM on the matrix cores ─────────────────
+// Y[s][o] = (residual ? Y[s][o] : 0) + (X[s] . W[o] + bias[o]) for s < S <= 32.
+// A workgroup of 8 waves owns 16 output rows; wave w takes the w-th eighth
+// of the K range. Per 32 columns a lane loads two float4 of its W row
+// (o = o0 + lane % 16, columns k0 + 8 (lane / 16) .. +7: the four lane groups
+// read 128 contiguous bytes of each row) and the same columns of its two X
+// rows (s = lane % 16 and 16 + lane % 16), then issues 16
+// v_mfma_f32_16x16x4_f32 (8 steps x 2 halves of the inputs); step i takes
+// element i of every lane's 8 columns, so the four k slots of one MFMA are
+// columns k0 + i, k0 + 8 + i, k0 + 16 + i, k0 + 24 + i. W runs three steps
+// ahead in a register ring, X (L2-resident) one step ahead. The eight
+// partial tiles meet in LDS and are added in wave order. fp32 products and
+// sums throughout (not the reference's 8-lane order: within 1e-6 relative,
+// checked in tests).
+typedef float pk_f32x4v __attribute__((ext_vector_type(4)));
+constexpr int MF_WAVES = 8;
 
-template <int SB>
-__global__ __launch_bounds__(256) void k_gemm_skinny(float *__restrict__ Y, const float *__restrict__ X,
-                                                     const float *__restrict__ W,
-                                                     const float *__restrict__ bias, int S, int I, int O,
-                                                     int residual) {
-    __shared__ __attribute__((aligned(16))) float xs[SB][SK_KC];
+__global__ __launch_bounds__(64 * MF_WAVES) void k_gemm_mfma32(float *__restrict__ Y, const float *__restrict__ X,
+                                                               const float *__restrict__ W,
+                                                               const float *__restrict__ bias, int S, int I,
+                                                               int O, int residual) {
+    __shared__ __attribute__((aligned(16))) float red[MF_WAVES][2][4][64];   // [wave][half][v][lane]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = blockIdx.x * 16 + wave * 4;
-    float acc[4 * SB];
-#pragma unroll
-    for (int i = 0; i < 4 * SB; ++i) acc[i] = 0.0f;
-    const float4 *w4[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        const int row = min(row0 + r, O - 1);
-        w4[r] = reinterpret_cast<const float4 *>(W + (int64_t)row * I);
+    const int o0 = blockIdx.x * 16;
+    const int r16 = lane & 15, kq = lane >> 4;
+    const float *wrow = W + (int64_t)min(o0 + r16, O - 1) * I;
+    const float *x0 = X + (int64_t)min(r16, S - 1) * I;
+    const float *x1 = X + (int64_t)min(16 + r16, S - 1) * I;
+    const int slice = ((I + 32 * MF_WAVES - 1) / (32 * MF_WAVES)) * 32;   // columns per wave
+    const int kb = min(I, wave * slice), ke = min(I, kb + slice);
+
+    pk_f32x4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
+    float4 w0[2], w1[2], w2[2], a[2], b[2], an[2], bn[2];
+    // this lane's 8 columns of the step at K0 (zero past ke)
+#define PK_MF_W(K0, WV)                                                                           \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                              \
+        const int k = (K0) + 8 * kq + 4 * j;                                                      \
+        if (k < ke) {                                                                             \
+            const pk_f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4v *>(wrow + k)); \
+            WV[j] = make_float4(t.x, t.y, t.z, t.w);                                              \
+        } else {                                                                                  \
+            WV[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                              \
+        }                                                                                         \
     }
-    // this lane's float4 of each row for the chunk at k0 (zero past I)
-    auto wload = [](const float4 *const *w4p, int k0, int lane, int I, float4 *out) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-            pk_f32x4 t = {0.f, 0.f, 0.f, 0.f};
-            if (k0 + 4 * lane < I)
-                t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4 *>(w4p[r] + (k0 >> 2) + lane));
-            out[r] = make_float4(t.x, t.y, t.z, t.w);
-        }
-    };
-    float4 wv[4], wn[4];
-    wload(w4, 0, lane, I, wv);
-    for (int k0 = 0; k0 < I; k0 += SK_KC) {
-        const int kc = min(SK_KC, I - k0);
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < SB * (SK_KC / 4); idx += 256) {
-            const int s = idx / (SK_KC / 4), c4 = idx - s * (SK_KC / 4);
-            float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (s < S && 4 * c4 < kc) v = *reinterpret_cast<const float4 *>(X + (int64_t)s * I + k0 + 4 * c4);
-            *reinterpret_cast<float4 *>(&xs[s][4 * c4]) = v;
-        }
-        __syncthreads();
-        if (k0 + SK_KC < I) wload(w4, k0 + SK_KC, lane, I, wn);      // next chunk's weights in flight
-#pragma unroll
-        for (int s = 0; s < SB; ++s) {
-            const float4 xv = *reinterpret_cast<const float4 *>(&xs[s][4 * lane]);
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                float a = acc[r * SB + s];
-                a = __builtin_fmaf(wv[r].x, xv.x, a);
-                a = __builtin_fmaf(wv[r].y, xv.y, a);
-                a = __builtin_fmaf(wv[r].z, xv.z, a);
-                a = __builtin_fmaf(wv[r].w, xv.w, a);
-                acc[r * SB + s] = a;
-            }
-        }
-#pragma unroll
-        for (int r = 0; r < 4; ++r) wv[r] = wn[r];
+#define PK_MF_X(K0, AV, BV)                                                                       \
+    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                              \
+        const int k = (K0) + 8 * kq + 4 * j;                                                      \
+        const bool ok = k < ke;                                                                   \
+        AV[j] = ok ? *reinterpret_cast<const float4 *>(x0 + k) : make_float4(0.f, 0.f, 0.f, 0.f); \
+        BV[j] = ok ? *reinterpret_cast<const float4 *>(x1 + k) : make_float4(0.f, 0.f, 0.f, 0.f); \
     }
-    // reduce-scatter over the 64 lanes: at the step exchanging with lane ^ m
-    // the lane keeps the upper half of its c values if (lane & m), else the
-    // lower half, adding the partner's copy; after the six steps it holds the
-    // full sums of values 2*lane and 2*lane + 1 (value index = r * SB + s).
-    static_assert(SB == 32, "the exchange leaves 2 of 4 x 32 values per lane");
-#pragma unroll
-    for (int m = 32, c = 4 * SB; m >= 1; m >>= 1, c >>= 1) {
-        const bool upper = (lane & m) != 0;
-#pragma unroll
-        for (int i = 0; i < c / 2; ++i) {
-            const float lo = acc[i], hi = acc[i + c / 2];
-            acc[i] = (upper ? hi : lo) + __shfl_xor(upper ? lo : hi, m, 64);
-        }
+#define PK_MF_STEP(K0, WV)                                                                        \
+    if ((K0) < ke) {                                                                              \
+        PK_MF_X((K0) + 32, an, bn)                                                                \
+        _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
+            const float wv_[4] = {WV[j].x, WV[j].y, WV[j].z, WV[j].w};                            \
+            const float av_[4] = {a[j].x, a[j].y, a[j].z, a[j].w};                                \
+            const float bv_[4] = {b[j].x, b[j].y, b[j].z, b[j].w};                                \
+            _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av_[i], wv_[i], acc0, 0, 0, 0);      \
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv_[i], wv_[i], acc1, 0, 0, 0);      \
+            }                                                                                     \
+        }                                                                                         \
+        PK_MF_W((K0) + 96, WV)                                                                    \
+        _Pragma("unroll") for (int j = 0; j < 2; ++j) { a[j] = an[j]; b[j] = bn[j]; }            \
     }
+    PK_MF_W(kb, w0)
+    PK_MF_W(kb + 32, w1)
+    PK_MF_W(kb + 64, w2)
+    PK_MF_X(kb, a, b)
+    for (int k0 = kb; k0 < ke; k0 += 96) {
+        PK_MF_STEP(k0, w0)
+        PK_MF_STEP(k0 + 32, w1)
+        PK_MF_STEP(k0 + 64, w2)
+    }
+#undef PK_MF_STEP
+#undef PK_MF_X
+#undef PK_MF_W
+    // D layout of a 16x16 MFMA: lane l, element v -> input 4 (l / 16) + v, row l % 16
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const int idx = 2 * lane + j;
-        const int r = idx / SB, s = idx - r * SB;
-        const int row = row0 + r;
-        if (s < S && row < O) {
-            float v = acc[j];
-            if (bias) v = v + bias[row];
-            float *yp = Y + (int64_t)s * O + row;
-            *yp = residual ? *yp + v : v;
+    for (int v = 0; v < 4; ++v) {
+        red[wave][0][v][lane] = acc0[v];
+        red[wave][1][v][lane] = acc1[v];
+    }
+    __syncthreads();
+    {
+        const int idx = threadIdx.x;                    // (half, v, lane)
+        const int h = idx >> 8, v = (idx >> 6) & 3, l = idx & 63;
+        const int srow = 16 * h + 4 * (l >> 4) + v, orow = o0 + (l & 15);
+        if (srow < S && orow < O) {
+            float sum = red[0][h][v][l];
+#pragma unroll
+            for (int q = 1; q < MF_WAVES; ++q) sum = sum + red[q][h][v][l];
+            if (bias) sum = sum + bias[orow];
+            float *yp = Y + (int64_t)srow * O + orow;
+            *yp = residual ? *yp + sum : sum;
         }
     }
 }
@@ -234,7 +241,7 @@ int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float 
     PK_CHECK(S > 0 && S <= 32 && I > 0 && O > 0, PK_ERR_ARG, "skinny gemm: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0, PK_ERR_UNSUPPORTED,
              "skinny gemm: needs 16-byte aligned rows (I=%d)", I);
-    hipLaunchKernelGGL(k_gemm_skinny<32>, dim3((O + 15) / 16), dim3(256), 0, st, y, x, W, bias, S, I, O,
+    hipLaunchKernelGGL(k_gemm_mfma32, dim3((O + 15) / 16), dim3(64 * MF_WAVES), 0, st, y, x, W, bias, S, I, O,
                        residual);
     PK_HIP(hipGetLastError());
     return PK_OK;
