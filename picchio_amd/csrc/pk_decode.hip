@@ -215,8 +215,10 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 // [half*GH, half*GH + GH), GH = ceil(gs / halves); t = tid % 128 is the
 // position for the scores and (column, group) for V.
 //
-// The partials are stored device-coherently; the last of the row's chunk
-// blocks to arrive at its (row, b) counter combines them for the gs heads
+// A window of one chunk is finished by its block (the combine's operations
+// for one chunk). Otherwise the partials are stored device-coherently; the
+// last of the row's chunk blocks to arrive at its (row, b) counter combines
+// them (16 chunks' partials per load round) for the gs heads
 // with the learned sinks (picchio.c:586-604: the sink joins the max and the
 // denominator, not the value sum), writes att [row][h*hd..] and re-arms the
 // counter.
@@ -236,6 +238,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
     float *vred = p + G * ATT_CHUNK;          // [G][PG][hd]
     __shared__ float red[4][ATT_GH];
     __shared__ float mh[2 * ATT_GH];
+    __shared__ float ssum[2 * ATT_GH];
     __shared__ int last;
     const int b = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
     const int kvh = b / ((H / KVH) / gs);
@@ -307,6 +310,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         if (tt == 0) mh[ja + jj] = m;
     }
     __syncthreads();
+    // chunks of this row's window; with one, this block finishes the softmax
+    const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
     // per-head sums: wave w takes heads w, w + waves, ...
     for (int j = wave; j < G; j += waves) {
         const float *pj = p + j * ATT_CHUNK;
@@ -314,9 +319,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         for (int t = lane; t < n; t += 64) sum += pj[t];
         sum = wave_sum(sum);
         if (lane == 0) {
-            float *out = part + ((int64_t)(h0 + j) * max_chunks + c) * (hd + 2);
-            __hip_atomic_store(out, mh[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(out + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if (nc == 1) {
+                ssum[j] = sum;
+            } else {
+                float *out = part + ((int64_t)(h0 + j) * max_chunks + c) * (hd + 2);
+                __hip_atomic_store(out, mh[j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                __hip_atomic_store(out + 1, sum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
         }
     }
     // V sums: thread = (column group c4 of hd/4, position group g of PG) of its half
@@ -355,6 +364,20 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         *reinterpret_cast<float4 *>(&vred[((ja + jj) * PG + g) * hd + 4 * c4]) = acc[jj];
     }
     __syncthreads();
+    if (nc == 1) {
+        // the combine below with a single chunk, in its operations
+        for (int idx = tid; idx < G * hd; idx += blockDim.x) {
+            const int j = idx / hd, i = idx - j * hd, h = h0 + j;
+            float o = 0.0f;
+            for (int gg = 0; gg < PG; ++gg) o += vred[(j * PG + gg) * hd + i];
+            const float M = fmaxf(sinks[h], mh[j]);
+            const float e = expf(mh[j] - M);
+            float S = expf(sinks[h] - M);
+            S += ssum[j] * e;
+            att[(int64_t)r * H * hd + h * hd + i] = __builtin_fmaf(o, e, 0.0f) / S;
+        }
+        return;
+    }
     for (int idx = tid; idx < G * hd; idx += blockDim.x) {
         const int j = idx / hd, i = idx - j * hd;
         float o = 0.0f;
@@ -363,7 +386,6 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         __hip_atomic_store(out + 2 + i, o, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     // arrival: the last of the nc chunk blocks of (row, b) combines
-    const int nc = (end - start + 1 + ATT_CHUNK - 1) / ATT_CHUNK;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     uint32_t *cnt = ctr + (int64_t)r * gridDim.x + b;
@@ -371,24 +393,44 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nc - 1);
     __syncthreads();
     if (!last) return;
+    // chunk partials are read 16 chunks at a time (independent loads, one
+    // round trip), then used in chunk order
+    constexpr int CB = 16;
+    auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
     for (int idx = tid; idx < G * hd; idx += blockDim.x) {
         const int j = idx / hd, i = idx - j * hd, h = h0 + j;
         const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
         float M = sinks[h];
-        for (int cc = 0; cc < nc; ++cc)
-            M = fmaxf(M, __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+        for (int c0 = 0; c0 < nc; c0 += CB) {
+            float mv[CB];
+#pragma unroll
+            for (int u = 0; u < CB; ++u) mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : -INFINITY;
+#pragma unroll
+            for (int u = 0; u < CB; ++u) M = fmaxf(M, mv[u]);
+        }
         float S = expf(sinks[h] - M);
-        for (int cc = 0; cc < nc; ++cc) {
-            const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            S += __hip_atomic_load(ph + cc * (hd + 2) + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) *
-                 expf(mc - M);
+        for (int c0 = 0; c0 < nc; c0 += CB) {
+            float mv[CB], sv[CB];
+#pragma unroll
+            for (int u = 0; u < CB; ++u) {
+                mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
+                sv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 1) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < CB; ++u)
+                if (c0 + u < nc) S += sv[u] * expf(mv[u] - M);
         }
         float o = 0.0f;
-        for (int cc = 0; cc < nc; ++cc) {
-            const float mc = __hip_atomic_load(ph + cc * (hd + 2), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            o = __builtin_fmaf(__hip_atomic_load(ph + cc * (hd + 2) + 2 + i, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT),
-                               expf(mc - M), o);
+        for (int c0 = 0; c0 < nc; c0 += CB) {
+            float mv[CB], ov[CB];
+#pragma unroll
+            for (int u = 0; u < CB; ++u) {
+                mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
+                ov[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 2 + i) : 0.0f;
+            }
+#pragma unroll
+            for (int u = 0; u < CB; ++u)
+                if (c0 + u < nc) o = __builtin_fmaf(ov[u], expf(mv[u] - M), o);
         }
         att[(int64_t)r * H * hd + h * hd + i] = o / S;
     }
