@@ -240,8 +240,20 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
     __shared__ float mh[2 * ATT_GH];
     __shared__ float ssum[2 * ATT_GH];
     __shared__ int last;
-    const int b = blockIdx.x, c = blockIdx.y, r = blockIdx.z;
-    const int kvh = b / ((H / KVH) / gs);
+    // Workgroups go to the 8 XCDs round-robin by linear id, each XCD with its
+    // own L2: the SUB blocks that read the same (KV head, chunk) tile get ids
+    // equal mod 8, so the tile comes from HBM once.
+    const int SUB = (H / KVH) / gs;
+    int b = blockIdx.x, c = blockIdx.y;
+    if (SUB > 1 && (KVH * (int)gridDim.y) % 8 == 0) {
+        const int L = blockIdx.x + gridDim.x * blockIdx.y;
+        const int q8 = L >> 3, p8 = L & 7;
+        const int pp = (q8 / SUB) * 8 + p8;            // (KV head, chunk) pair
+        c = pp / KVH;
+        b = (pp - c * KVH) * SUB + q8 % SUB;
+    }
+    const int r = blockIdx.z;
+    const int kvh = b / SUB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = tid >> 7, tt = tid & 127;
     const int halves = blockDim.x >> 7, waves = blockDim.x >> 6;
@@ -393,46 +405,100 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
         last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nc - 1);
     __syncthreads();
     if (!last) return;
-    // chunk partials are read 16 chunks at a time (independent loads, one
-    // round trip), then used in chunk order
-    constexpr int CB = 16;
+    // every chunk's max and sum in one load round (LDS: the p region holds
+    // G x 128 values); then per head the max M, the chunk factors
+    // e_c = expf(m_c - M) and the denominator, in chunk order; the value
+    // partials are read 16 chunks per round
     auto ld = [](const float *q) { return __hip_atomic_load(q, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    for (int idx = tid; idx < G * hd; idx += blockDim.x) {
-        const int j = idx / hd, i = idx - j * hd, h = h0 + j;
-        const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
-        float M = sinks[h];
-        for (int c0 = 0; c0 < nc; c0 += CB) {
-            float mv[CB];
+    constexpr int CB = 16;
+    float *cm = p;                            // [G][nc] chunk maxima, then factors e_c
+    float *cs = vred;                         // [G][nc] chunk sums
+    __shared__ float hS[2 * ATT_GH];
+    if (nc <= ATT_CHUNK) {
+        for (int q0 = tid; q0 < G * nc; q0 += blockDim.x * 4) {
+            float mv[4], sv[4];
 #pragma unroll
-            for (int u = 0; u < CB; ++u) mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : -INFINITY;
-#pragma unroll
-            for (int u = 0; u < CB; ++u) M = fmaxf(M, mv[u]);
-        }
-        float S = expf(sinks[h] - M);
-        for (int c0 = 0; c0 < nc; c0 += CB) {
-            float mv[CB], sv[CB];
-#pragma unroll
-            for (int u = 0; u < CB; ++u) {
-                mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
-                sv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 1) : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + u * blockDim.x;
+                const int j = q / nc, cc = q - j * nc;
+                const float *pc = part + ((int64_t)(h0 + j) * max_chunks + cc) * (hd + 2);
+                mv[u] = q < G * nc ? ld(pc) : 0.0f;
+                sv[u] = q < G * nc ? ld(pc + 1) : 0.0f;
             }
 #pragma unroll
-            for (int u = 0; u < CB; ++u)
-                if (c0 + u < nc) S += sv[u] * expf(mv[u] - M);
-        }
-        float o = 0.0f;
-        for (int c0 = 0; c0 < nc; c0 += CB) {
-            float mv[CB], ov[CB];
-#pragma unroll
-            for (int u = 0; u < CB; ++u) {
-                mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
-                ov[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 2 + i) : 0.0f;
+            for (int u = 0; u < 4; ++u) {
+                const int q = q0 + u * blockDim.x;
+                if (q < G * nc) { cm[q] = mv[u]; cs[q] = sv[u]; }
             }
-#pragma unroll
-            for (int u = 0; u < CB; ++u)
-                if (c0 + u < nc) o = __builtin_fmaf(ov[u], expf(mv[u] - M), o);
         }
-        att[(int64_t)r * H * hd + h * hd + i] = o / S;
+        __syncthreads();
+        if (tid < G) {
+            const int j = tid, h = h0 + j;
+            float M = sinks[h];
+            for (int cc = 0; cc < nc; ++cc) M = fmaxf(M, cm[j * nc + cc]);
+            float S = expf(sinks[h] - M);
+            for (int cc = 0; cc < nc; ++cc) {
+                const float ec = expf(cm[j * nc + cc] - M);
+                S += cs[j * nc + cc] * ec;
+                cm[j * nc + cc] = ec;
+            }
+            hS[j] = S;
+        }
+        __syncthreads();
+        for (int idx = tid; idx < G * hd; idx += blockDim.x) {
+            const int j = idx / hd, i = idx - j * hd, h = h0 + j;
+            const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
+            float o = 0.0f;
+            for (int c0 = 0; c0 < nc; c0 += CB) {
+                float ov[CB];
+#pragma unroll
+                for (int u = 0; u < CB; ++u) ov[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 2 + i) : 0.0f;
+#pragma unroll
+                for (int u = 0; u < CB; ++u)
+                    if (c0 + u < nc) o = __builtin_fmaf(ov[u], cm[j * nc + c0 + u], o);
+            }
+            att[(int64_t)r * H * hd + h * hd + i] = o / hS[j];
+        }
+    } else {
+        // windows longer than 128 chunks: the same arithmetic, reading the
+        // partials 16 chunks per round in each pass
+        for (int idx = tid; idx < G * hd; idx += blockDim.x) {
+            const int j = idx / hd, i = idx - j * hd, h = h0 + j;
+            const float *ph = part + (int64_t)h * max_chunks * (hd + 2);
+            float M = sinks[h];
+            for (int c0 = 0; c0 < nc; c0 += CB) {
+                float mv[CB];
+#pragma unroll
+                for (int u = 0; u < CB; ++u) mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : -INFINITY;
+#pragma unroll
+                for (int u = 0; u < CB; ++u) M = fmaxf(M, mv[u]);
+            }
+            float S = expf(sinks[h] - M);
+            for (int c0 = 0; c0 < nc; c0 += CB) {
+                float mv[CB], sv[CB];
+#pragma unroll
+                for (int u = 0; u < CB; ++u) {
+                    mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
+                    sv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 1) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < CB; ++u)
+                    if (c0 + u < nc) S += sv[u] * expf(mv[u] - M);
+            }
+            float o = 0.0f;
+            for (int c0 = 0; c0 < nc; c0 += CB) {
+                float mv[CB], ov[CB];
+#pragma unroll
+                for (int u = 0; u < CB; ++u) {
+                    mv[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2)) : 0.0f;
+                    ov[u] = c0 + u < nc ? ld(ph + (c0 + u) * (hd + 2) + 2 + i) : 0.0f;
+                }
+#pragma unroll
+                for (int u = 0; u < CB; ++u)
+                    if (c0 + u < nc) o = __builtin_fmaf(ov[u], expf(mv[u] - M), o);
+            }
+            att[(int64_t)r * H * hd + h * hd + i] = o / S;
+        }
     }
     if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
