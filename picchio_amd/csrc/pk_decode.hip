@@ -35,23 +35,29 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
                                                        float *h, float *hn, const float *w, int D,
                                                        float eps) {
     __shared__ double part[4];
-    __shared__ float rs;
     const int tok = st->tok;
     const bool ok = tok >= 0 && tok < vocab;
     const float *row = embed + (int64_t)(ok ? tok : 0) * D;
-    double acc = 0.0;
-    for (int i = threadIdx.x; i < D; i += 256) {
-        const float v = ok ? row[i] : 0.0f;
-        h[i] = v;
-        acc += (double)v * (double)v;
+    // every load goes out before the reduction (clamped, unconditional)
+    float v[12], wv[12];
+    pk_rms_load(row, D, v);
+    pk_rms_load(w, D, wv);
+#pragma unroll
+    for (int k = 0; k < 12; ++k) v[k] = ok ? v[k] : 0.0f;
+    const float r = pk_rms_finish(v, row, D, eps, part, !ok);
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < D) {
+            h[i] = v[k];
+            hn[i] = v[k] * r * wv[k];
+        }
     }
-    acc = wave_sum_d(acc);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) rs = 1.0f / sqrtf((float)(((part[0] + part[1]) + (part[2] + part[3])) / D) + eps);
-    __syncthreads();
-    const float r = rs;
-    for (int i = threadIdx.x; i < D; i += 256) hn[i] = (ok ? row[i] : 0.0f) * r * w[i];
+    for (int i = threadIdx.x + 256 * 12; i < D; i += 256) {
+        const float x = ok ? row[i] : 0.0f;
+        h[i] = x;
+        hn[i] = x * r * w[i];
+    }
 }
 
 // Decode QKV projection with the in_ln rmsnorm, the biases, RoPE
@@ -61,6 +67,8 @@ __global__ __launch_bounds__(256) void k_embed_rmsnorm(const pk_dstate *st, cons
 // rows, and meet in LDS, where the first of the pair rotates them with the
 // host-built table at the decode position and writes q / K / V. The first
 // weight loads are issued before the norm reduction so that they overlap it.
+constexpr int QKV_U = 12;              // float4 per lane loaded up front (2880 columns = 11.25)
+
 __device__ __forceinline__ void qkv_fma4(float &a, float4 x, pk_f32x4 w) {
     a = __builtin_fmaf(x.x, w.x, a);
     a = __builtin_fmaf(x.y, w.y, a);
@@ -75,6 +83,7 @@ __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, cons
                                                        float *qkv, float *Kl, float *Vl) {
     __shared__ double npart[4];
     __shared__ float pv[4];
+    __shared__ __attribute__((aligned(16))) float xn[4 * 64 * QKV_U];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int half = hd / 2;
     const int n_rot = (H + KVH) * half, n_pairs = n_rot + KVH * half;
@@ -93,23 +102,41 @@ __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, cons
     const int r1 = pi < n_rot ? r0 + half : r0 + 1;
     const int row = live ? ((wave & 1) ? r1 : r0) : 0;
     const pk_f32x4 *w4 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)row * D);
-    const float4 *h4 = reinterpret_cast<const float4 *>(h);
-    const float4 *n4w = reinterpret_cast<const float4 *>(nw);
     const int n4 = D >> 2;
-    pk_f32x4 wf[4];
+    // Every load goes out at the start, unconditionally (range-checked buffer
+    // loads; a guarded load is waited for on its own): the norm's inputs and weights
+    // first, so that the reduction runs while the row's first QKV_U float4
+    // per lane are in flight, then this row's weights. The block writes the
+    // normalised input (x * r) * w once into LDS for its four rows; the sum
+    // runs over i = lane + 64 u, u ascending. A wave past the last pair
+    // reads row 0 and writes nothing.
+    float hv[12], nv[12];
+    pk_rms_load(h, D, hv);
+    pk_rms_load(nw, D, nv);
+    const pk_buf_t wr = pk_buf(w4, (uint32_t)n4 * 16u);
+    pk_f32x4 wf[QKV_U];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = lane + u * 64;
-        wf[u] = live && i < n4 ? __builtin_nontemporal_load(w4 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int u = 0; u < QKV_U; ++u) wf[u] = pk_buf_load4_nt(wr, (uint32_t)(lane + u * 64) * 16u);
+    const int pos = st->pos, kv_dim = KVH * hd;
+    const float b0 = b[r0], b1 = b[r1];
+    float cs = 0.0f, sn = 0.0f;
+    if (pi < n_rot) {
+        cs = rope[((int64_t)pos * half + j) * 2 + 0];
+        sn = rope[((int64_t)pos * half + j) * 2 + 1];
     }
-    const float rn = pk_block_rms_scale(h, D, eps, npart);
+    const float rn = pk_rms_finish(hv, h, D, eps, npart);
+    // (entries past the row are zeros on both sides: x = 0 * r * 0 in LDS,
+    // w = 0 from the range check, so their products add nothing)
+#pragma unroll
+    for (int k = 0; k < 12; ++k) xn[threadIdx.x + 256 * k] = hv[k] * rn * nv[k];
+    __syncthreads();
+    const float4 *xn4 = reinterpret_cast<const float4 *>(xn);
     float a = 0.0f;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-        const int i = lane + u * 64;
-        if (i < n4) qkv_fma4(a, pk_norm4(h4[i], rn, n4w[i]), wf[u]);
-    }
-    for (int i0 = lane + 256; live && i0 < n4; i0 += 256) {
+    for (int u = 0; u < QKV_U; ++u) qkv_fma4(a, xn4[lane + u * 64], wf[u]);
+    const float4 *h4 = reinterpret_cast<const float4 *>(h);
+    const float4 *n4w = reinterpret_cast<const float4 *>(nw);
+    for (int i0 = lane + 64 * QKV_U; live && i0 < n4; i0 += 256) {
         pk_f32x4 wv[4];
         float4 xv[4];
 #pragma unroll
@@ -125,11 +152,8 @@ __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, cons
     if (lane == 0) pv[wave] = a;
     __syncthreads();
     if (!live || (wave & 1) || lane != 0) return;
-    const float v0 = pv[wave] + b[r0], v1 = pv[wave + 1] + b[r1];
-    const int pos = st->pos, kv_dim = KVH * hd;
+    const float v0 = pv[wave] + b0, v1 = pv[wave + 1] + b1;
     if (pi < n_rot) {
-        const float cs = rope[((int64_t)pos * half + j) * 2 + 0];
-        const float sn = rope[((int64_t)pos * half + j) * 2 + 1];
         const float q0 = __builtin_fmaf(v0, cs, -(v1 * sn));     // a*cs - b*sn (contracted)
         const float q1 = __builtin_fmaf(v0, sn, v1 * cs);        // a*sn + b*cs (contracted)
         qkv[r0] = q0;
@@ -225,6 +249,7 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_GH = 8;              // query heads per half-block (G <= 16)
 
+template <int KD4>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
                                                            const float *qkv, int64_t qkv_stride, const float *Kl,
                                                            const float *Vl, int64_t kv_row, int H, int KVH,
@@ -269,41 +294,63 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
     const int n = min(ATT_CHUNK, end - t0 + 1);
     if (n <= 0) return;
     const int kv_dim = KVH * hd, h0 = b * gs;
-    for (int i = tid; i < G * hd; i += blockDim.x) q[i] = qkv[h0 * hd + i];
+    // The query rows and this thread's K row (position tt; KD4 >= hd / 4
+    // float4) go out before any wait, with the query rows' LDS copy behind
+    // them; the V rows go out right after the scores, so that they arrive
+    // during the softmax. Loads are unconditional: positions past the
+    // chunk's last are clamped to it and their values are not used.
+    float qv[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) qv[k] = qkv[h0 * hd + min(tid + k * (int)blockDim.x, G * hd - 1)];
+    const int D4 = hd >> 2;
+    const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + min(tt, n - 1)) * kv_dim + kvh * hd);
+    float4 kv[KD4];
+#pragma unroll
+    for (int u = 0; u < KD4; ++u) kv[u] = kt4[min(u, D4 - 1)];
+    // (clamped like the loads: threads past G * hd write the last value
+    // again; a guarded store would let its load sink behind the K loads)
+#pragma unroll
+    for (int k = 0; k < 4; ++k) q[min(tid + k * (int)blockDim.x, G * hd - 1)] = qv[k];
+    for (int i = tid + 4 * blockDim.x; i < G * hd; i += blockDim.x) q[i] = qkv[h0 * hd + i];
     __syncthreads();
     const float scale = 1.0f / sqrtf((float)hd);
 
-    // scores of position tt for this half's heads (K row loaded once)
+    // scores of position tt for this half's heads (columns in order)
     float sc[ATT_GH];
 #pragma unroll
     for (int jj = 0; jj < ATT_GH; ++jj) sc[jj] = -INFINITY;
     if (tt < n) {
-        const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + tt) * kv_dim + kvh * hd);
         float dot[ATT_GH];
 #pragma unroll
         for (int jj = 0; jj < ATT_GH; ++jj) dot[jj] = 0.0f;
-        for (int i0 = 0; i0 < hd; i0 += 32) {         // 32 columns: loads first, then the in-order adds
-            float4 kv[8];
+        // (guards, not early exits, so that kv[] stays in registers)
 #pragma unroll
-            for (int u = 0; u < 8; ++u) kv[u] = i0 + 4 * u < hd ? kt4[(i0 >> 2) + u] : make_float4(0.f, 0.f, 0.f, 0.f);
+        for (int u = 0; u < KD4; ++u) {
+            if (u < D4) {
 #pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                if (i0 + 4 * u >= hd) break;
-#pragma unroll
-                for (int jj = 0; jj < ATT_GH; ++jj) {
-                    if (jj >= jn) break;
-                    const float *qq = q + (ja + jj) * hd + i0 + 4 * u;
-                    float pr;
-                    pr = qq[0] * kv[u].x; dot[jj] = dot[jj] + pr;
-                    pr = qq[1] * kv[u].y; dot[jj] = dot[jj] + pr;
-                    pr = qq[2] * kv[u].z; dot[jj] = dot[jj] + pr;
-                    pr = qq[3] * kv[u].w; dot[jj] = dot[jj] + pr;
-                }
+            for (int jj = 0; jj < ATT_GH; ++jj) {
+                if (jj >= jn) break;
+                const float *qq = q + (ja + jj) * hd + 4 * u;
+                float pr;
+                pr = qq[0] * kv[u].x; dot[jj] = dot[jj] + pr;
+                pr = qq[1] * kv[u].y; dot[jj] = dot[jj] + pr;
+                pr = qq[2] * kv[u].z; dot[jj] = dot[jj] + pr;
+                pr = qq[3] * kv[u].w; dot[jj] = dot[jj] + pr;
+            }
             }
         }
 #pragma unroll
         for (int jj = 0; jj < ATT_GH; ++jj) sc[jj] = dot[jj] * scale;
     }
+    // V rows: thread = (column group c4 of hd/4, position group g of PG) of
+    // its half, positions g * PER + j, j < PER (PER = hd / 4 <= KD4)
+    const int PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
+    const int c4 = tt % D4, g = tt / D4;
+    const float4 *v4 = reinterpret_cast<const float4 *>(Vl + (int64_t)t0 * kv_dim + kvh * hd) + c4;
+    const int kv4 = kv_dim >> 2;
+    float4 vv[KD4];
+#pragma unroll
+    for (int j = 0; j < KD4; ++j) vv[j] = v4[(int64_t)min(g * PER + min(j, PER - 1), n - 1) * kv4];
     // per-head chunk max over the half's two waves, then p = exp(s - m)
 #pragma unroll
     for (int jj = 0; jj < ATT_GH; ++jj) {
@@ -340,34 +387,22 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
             }
         }
     }
-    // V sums: thread = (column group c4 of hd/4, position group g of PG) of its half
-    const int D4 = hd >> 2, PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
-    const int c4 = tt % D4, g = tt / D4;
-    const float4 *v4 = reinterpret_cast<const float4 *>(Vl + (int64_t)t0 * kv_dim + kvh * hd) + c4;
-    const int kv4 = kv_dim >> 2;
+    // V sums over this thread's positions, in position order
     float4 acc[ATT_GH];
 #pragma unroll
     for (int jj = 0; jj < ATT_GH; ++jj) acc[jj] = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int j0 = 0; j0 < PER; j0 += 8) {
-        float4 vv[8];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int t = g * PER + j0 + u;
-            vv[u] = j0 + u < PER && t < n ? v4[(int64_t)t * kv4] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    for (int j = 0; j < KD4; ++j) {
+        const int t = g * PER + j;
+        const bool ok = j < PER && t < n;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int t = g * PER + j0 + u;
-            const bool ok = j0 + u < PER && t < n;
-#pragma unroll
-            for (int jj = 0; jj < ATT_GH; ++jj) {
-                if (jj >= jn) break;
-                const float pw = ok ? p[(ja + jj) * ATT_CHUNK + t] : 0.0f;
-                acc[jj].x = __builtin_fmaf(pw, vv[u].x, acc[jj].x);
-                acc[jj].y = __builtin_fmaf(pw, vv[u].y, acc[jj].y);
-                acc[jj].z = __builtin_fmaf(pw, vv[u].z, acc[jj].z);
-                acc[jj].w = __builtin_fmaf(pw, vv[u].w, acc[jj].w);
-            }
+        for (int jj = 0; jj < ATT_GH; ++jj) {
+            if (jj >= jn) break;
+            const float pw = ok ? p[(ja + jj) * ATT_CHUNK + t] : 0.0f;
+            acc[jj].x = __builtin_fmaf(pw, vv[j].x, acc[jj].x);
+            acc[jj].y = __builtin_fmaf(pw, vv[j].y, acc[jj].y);
+            acc[jj].z = __builtin_fmaf(pw, vv[j].z, acc[jj].z);
+            acc[jj].w = __builtin_fmaf(pw, vv[j].w, acc[jj].w);
         }
     }
 #pragma unroll
@@ -506,6 +541,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
 // y[o] += (W[o] . x + b[o])  — attention output projection + residual
 // (picchio.c:615-616, :1690). One workgroup per 4 outputs (one per wave);
 // grid.y = row of a batch (x [rows][I], y [rows][O]).
+constexpr int RES_U = 16;              // float4 per lane loaded up front (4096 columns)
+
 __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restrict__ x,
                                                   const float *__restrict__ W,
                                                   const float *__restrict__ b, int I, int O) {
@@ -515,24 +552,37 @@ __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restr
     const int o = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (o >= O) return;
     const float4 *x4 = reinterpret_cast<const float4 *>(x);
-    const float4 *w4 = reinterpret_cast<const float4 *>(W + (int64_t)o * I);
+    const pk_f32x4 *w4 = reinterpret_cast<const pk_f32x4 *>(W + (int64_t)o * I);
     const int n4 = I >> 2;
+    // the row's first RES_U float4 per lane in one round trip; the sum runs
+    // over i = lane + 64 u, u ascending, as in the chunked loop after it
+    // (range-checked buffer loads, all issued before the first use; entries
+    // past the row read as zero and are not used)
+    const pk_buf_t wr = pk_buf(w4, (uint32_t)n4 * 16u), xr = pk_buf(x4, (uint32_t)n4 * 16u);
+    pk_f32x4 wv[RES_U];
+    float4 xv[RES_U];
+#pragma unroll
+    for (int u = 0; u < RES_U; ++u) {
+        xv[u] = pk_buf_load4(xr, (uint32_t)(lane + u * 64) * 16u);
+        wv[u] = pk_buf_load4_nt(wr, (uint32_t)(lane + u * 64) * 16u);
+    }
     float acc = 0.0f;
-    for (int i0 = lane; i0 < n4; i0 += 64 * 4) {
-        float4 xv[4], wv[4];
+#pragma unroll
+    for (int u = 0; u < RES_U; ++u) {
+        const int i = lane + u * 64;
+        if (i < n4) qkv_fma4(acc, xv[u], wv[u]);
+    }
+    for (int i0 = lane + 64 * RES_U; i0 < n4; i0 += 64 * 4) {
+        float4 xv[4];
+        pk_f32x4 wc[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
             const int i = i0 + u * 64;
             xv[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-            wv[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            wc[u] = i < n4 ? __builtin_nontemporal_load(w4 + i) : pk_f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            acc = __builtin_fmaf(xv[u].x, wv[u].x, acc);
-            acc = __builtin_fmaf(xv[u].y, wv[u].y, acc);
-            acc = __builtin_fmaf(xv[u].z, wv[u].z, acc);
-            acc = __builtin_fmaf(xv[u].w, wv[u].w, acc);
-        }
+        for (int u = 0; u < 4; ++u) qkv_fma4(acc, xv[u], wc[u]);
     }
     for (int i = (n4 << 2) + lane; i < I; i += 64) acc = __builtin_fmaf(x[i], W[(int64_t)o * I + i], acc);
     acc = wave_sum(acc);
@@ -736,7 +786,10 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     PK_CHECK((int64_t)n * (H / gs) <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d blocks", n,
              H / gs);
     const size_t att_lds = (size_t)gs * (hd + ATT_CHUNK + ATT_CHUNK * 4) * sizeof(float);
-    hipLaunchKernelGGL(k_attn_part, dim3(H / gs, chunks, n), dim3(gs > 1 ? ATT_THREADS : ATT_CHUNK), att_lds,
+    // K / V rows held in registers: 16 float4 up to head_dim 64, else 32
+    auto kern = hd <= 64 ? k_attn_part<16> : k_attn_part<32>;
+    PK_CHECK(hd % 4 == 0 && hd <= 128, PK_ERR_UNSUPPORTED, "attention: head_dim %d", hd);
+    hipLaunchKernelGGL(kern, dim3(H / gs, chunks, n), dim3(gs > 1 ? ATT_THREADS : ATT_CHUNK), att_lds,
                        e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,
                        part, max_chunks, d.sinks, att, e->counters + PK_CTR_ATTN, gs);

@@ -359,22 +359,20 @@ int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, cons
 __global__ __launch_bounds__(256) void k_rmsnorm(float *out, const float *x, const float *w, int D,
                                                  float eps) {
     __shared__ double part[4];
-    __shared__ float rs;
     const int t = blockIdx.x;
     const float *xr = x + (int64_t)t * D;
-    double acc = 0.0;
-    for (int i = threadIdx.x; i < D; i += 256) acc += (double)xr[i] * (double)xr[i];
-    acc = pk_wave_sum_d(acc);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = acc;
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const double ms = ((part[0] + part[1]) + (part[2] + part[3]));
-        rs = 1.0f / sqrtf((float)(ms / D) + eps);
-    }
-    __syncthreads();
-    const float r = rs;
+    // every load goes out before the reduction (clamped, unconditional)
+    float v[12], wv[12];
+    pk_rms_load(xr, D, v);
+    pk_rms_load(w, D, wv);
+    const float r = pk_rms_finish(v, xr, D, eps, part);
     float *o = out + (int64_t)t * D;
-    for (int i = threadIdx.x; i < D; i += 256) o[i] = xr[i] * r * w[i];
+#pragma unroll
+    for (int k = 0; k < 12; ++k) {
+        const int i = threadIdx.x + 256 * k;
+        if (i < D) o[i] = v[k] * r * wv[k];
+    }
+    for (int i = threadIdx.x + 256 * 12; i < D; i += 256) o[i] = xr[i] * r * w[i];
 }
 
 int pk_launch_rmsnorm(float *out, const float *x, const float *w, int D, float eps, int T,
@@ -461,32 +459,46 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
     const int e = blockIdx.x;
     float v;
     if (nw) {
-        // the router row's loads go out before the norm reduction
         const float4 *w4 = reinterpret_cast<const float4 *>(R + (int64_t)e * D);
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
         const float4 *n4w = reinterpret_cast<const float4 *>(nw);
         const int n4 = D >> 2;
-        float4 wf[GEMV_U];
+        // the norm's inputs go out before the router row, so that the
+        // reduction runs while the row is in flight
+        float hv[12];
+        pk_rms_load(x, D, hv);
+        // (range-checked buffer loads, unconditional: a guarded load would
+        // make the compiler wait for the row before the norm; entries past
+        // it read as zero and are not used), then the first chunk's inputs
+        const pk_buf_t wr = pk_buf(w4, (uint32_t)n4 * 16u), xr = pk_buf(x4, (uint32_t)n4 * 16u),
+                       nr = pk_buf(n4w, (uint32_t)n4 * 16u);
+        float4 wf[GEMV_U], xh[GEMV_U], xw[GEMV_U];
 #pragma unroll
         for (int u = 0; u < GEMV_U; ++u) {
-            const int i = threadIdx.x + u * 256;
-            wf[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            const uint32_t off = ((uint32_t)threadIdx.x + u * 256u) * 16u;
+            wf[u] = pk_buf_load4(wr, off);
+            xh[u] = pk_buf_load4(xr, off);
+            xw[u] = pk_buf_load4(nr, off);
         }
-        const float rn = pk_block_rms_scale(x, D, eps, npart);
+        const float rn = pk_rms_finish(hv, x, D, eps, npart);
         const int span = (D + E - 1) / E;
         for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
         float acc = 0.0f;
         for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
+            if (i0 != (int)threadIdx.x) {
 #pragma unroll
-            for (int u = 0; u < GEMV_U; ++u) {
-                const int i = i0 + u * 256;
-                if (i0 != (int)threadIdx.x) wf[u] = i < n4 ? w4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+                for (int u = 0; u < GEMV_U; ++u) {
+                    const uint32_t off = ((uint32_t)i0 + u * 256u) * 16u;
+                    wf[u] = pk_buf_load4(wr, off);
+                    xh[u] = pk_buf_load4(xr, off);
+                    xw[u] = pk_buf_load4(nr, off);
+                }
             }
 #pragma unroll
             for (int u = 0; u < GEMV_U; ++u) {
                 const int i = i0 + u * 256;
                 if (i < n4) {
-                    const float4 xv = pk_norm4(x4[i], rn, n4w[i]);
+                    const float4 xv = pk_norm4(xh[u], rn, xw[u]);
                     acc = __builtin_fmaf(xv.x, wf[u].x, acc);
                     acc = __builtin_fmaf(xv.y, wf[u].y, acc);
                     acc = __builtin_fmaf(xv.z, wf[u].z, acc);
