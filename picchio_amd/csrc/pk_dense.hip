@@ -515,6 +515,12 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
     } else {
         v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
     }
+    // without a counter the block only publishes its logit: the expert
+    // kernels that follow run the top-k themselves (pk_route_args)
+    if (!counter) {
+        if (threadIdx.x == 0) logits[e] = v + b[e];
+        return;
+    }
     if (threadIdx.x == 0) {
         pk_st_dev(logits + e, v + b[e]);
         __builtin_amdgcn_s_waitcnt(0);

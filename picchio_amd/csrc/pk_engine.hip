@@ -710,17 +710,20 @@ int pk_check_layer_experts(pk_engine *e, int layer) {
 // FFN of the experts listed in sel (device, n entries): act <- SwiGLU(gate_up x + b),
 // eo <- down act + b; with comb, the down launch also combines the n outputs
 // (weights comb->w) into comb->out (+ residual).
+// With route, the gate_up launch selects the experts from the router logits
+// and writes sel_dev (and the routing weights) for the down launch.
 static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, const float *x,
-                       int64_t x_stride, float *act, float *eo, const pk_combine_args *comb) {
+                       int64_t x_stride, float *act, float *eo, const pk_combine_args *comb,
+                       const pk_route_args *route = nullptr) {
     const pk_cfg *c = &e->c;
     pk_i4_items gu = pk_expert_items(e, layer, false);
-    gu.slots = sel_dev;
+    gu.slots = route ? nullptr : sel_dev;
     gu.x = x; gu.x_stride = x_stride;
     gu.y = act; gu.y_stride = c->moe_inter / 2;
     gu.n_items = n;
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
     PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
-                             nullptr, e->stream));
+                             nullptr, e->stream, route));
     PK_TRY(pk_prof_end(e, ps));
     pk_i4_items dn = pk_expert_items(e, layer, true);
     dn.slots = sel_dev;
@@ -745,19 +748,28 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
         PK_TRY(pk_moe_fused_launch(e, layer, x_dev, residual ? res_out : out_dev, residual, norm_w));
         return pk_prof_end(e, pf);
     }
+    // the router launch writes the logits only; the gate_up launch selects
+    // the experts from them and publishes the routing (sel, weights)
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
-                                 e->counters + PK_CTR_ROUTER, e->stream, norm_w, c->eps,
-                                 norm_w ? e->hn : nullptr));
+                                 nullptr, e->stream, norm_w, c->eps, norm_w ? e->hn : nullptr));
     PK_TRY(pk_prof_end(e, ps));
+    pk_route_args rt{};
+    rt.logits = e->r_logits;
+    rt.E = c->n_experts;
+    rt.K = c->topk;
+    rt.routed_scale = c->routed_scale;
+    rt.sel = e->sel;
+    rt.w_scaled = e->w_scaled;
+    rt.w_soft = e->w_soft;
     // the down launch combines the top-k outputs (routing order) + residual
     pk_combine_args cb{};
     cb.w = e->w_scaled;
     cb.out = residual ? res_out : out_dev;
     cb.residual = residual;
     cb.counters = e->counters + PK_CTR_COMBINE;
-    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb));
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb, &rt));
     return PK_OK;
 }
 

@@ -23,7 +23,8 @@
 // scales meet in LDS; wave 0 folds the groups of its 64 rows in order.
 template <int NW, int GPW, int EPI>
 __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int NG,
-                                                     float lim, float alpha, pk_combine_args cb) {
+                                                     float lim, float alpha, pk_combine_args cb,
+                                                     pk_route_args rt) {
     extern __shared__ float lds[];            // part[NG][64], scl[NG][64]
     float *part = lds;
     float *scl = lds + NG * 64;
@@ -32,7 +33,15 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     const int rb = blockIdx.x;
     const int item = blockIdx.y;
 
-    int slot = it.slot_base + (it.slots ? it.slots[item] : 0);
+    // the item's expert: given (slots), or selected here from the router
+    // logits (round `item` of the top-k, computed by every wave)
+    int slot;
+    if (rt.logits) {
+        float bv;
+        slot = it.slot_base + pk_wave_topk_nth(rt.logits, rt.E, item, &bv);
+    } else {
+        slot = it.slot_base + (it.slots ? it.slots[item] : 0);
+    }
     slot = __builtin_amdgcn_readfirstlane(slot);
     const uint8_t *base = it.base + (int64_t)slot * it.slot_stride;
     const uint4 *tiles = reinterpret_cast<const uint4 *>(base + it.off_tiles) +
@@ -102,11 +111,22 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     } else {
         if (row < O) y[row] = acc;
     }
+    // one wave of the launch publishes the routing for the launches after it
+    if constexpr (EPI != PK_EPI_COMBINE)
+        if (rt.logits && rb == 0 && item == 0) pk_wave_route_publish(rt);
 }
 
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
-                      float lim, float alpha, const pk_combine_args *comb, hipStream_t st) {
+                      float lim, float alpha, const pk_combine_args *comb, hipStream_t st,
+                      const pk_route_args *route) {
     pk_combine_args cb{};
+    pk_route_args rt{};
+    if (route) {
+        PK_CHECK(route->logits && route->sel && route->w_scaled && route->E > 0 && route->E <= 128 &&
+                     route->K > 0 && route->K <= 16 && it.n_items <= route->K && epilogue != PK_EPI_COMBINE,
+                 PK_ERR_ARG, "i4 gemv: routing of %d items over E=%d K=%d", it.n_items, route->E, route->K);
+        rt = *route;
+    }
     if (epilogue == PK_EPI_COMBINE) {
         PK_CHECK(comb && comb->w && comb->out && comb->counters, PK_ERR_ARG, "combine: missing buffers");
         PK_CHECK(sh.RB <= 1024, PK_ERR_UNSUPPORTED, "combine: %d row blocks", sh.RB);
@@ -120,13 +140,13 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
     constexpr int NW = 15, GPW = 3;
     if (epilogue == PK_EPI_SWIGLU)
         hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_SWIGLU>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb);
+                           it, sh.O, sh.NG, lim, alpha, cb, rt);
     else if (epilogue == PK_EPI_COMBINE)
         hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_COMBINE>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb);
+                           it, sh.O, sh.NG, lim, alpha, cb, rt);
     else
         hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_PLAIN>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb);
+                           it, sh.O, sh.NG, lim, alpha, cb, rt);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

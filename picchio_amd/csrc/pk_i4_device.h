@@ -73,3 +73,91 @@ __device__ __forceinline__ float pk_swiglu(float gate, float up, float lim, floa
     return (up + 1.0f) * gate * pk_sigmoid(alpha * gate);
 }
 
+
+// ───────────────────── router top-k of one token ─────────────────────
+// Maximum of a 32-bit key over the wave with DPP (row shifts 1, 2, 4, 8,
+// then the row broadcasts 15 and 31), read from lane 63: a handful of VALU
+// steps instead of a chain of LDS permutes. 0 is the identity.
+__device__ __forceinline__ uint32_t pk_wave_max_u32(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x111, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x112, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x114, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x118, 0xf, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x142, 0xa, 0xf, false));
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x143, 0xc, 0xf, false));
+    return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+// Order-preserving key of a float (NaN and -0.0 handled by the caller):
+// larger floats get larger unsigned keys, -inf the smallest above 0.
+__device__ __forceinline__ uint32_t pk_fkey(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Selection round by round on one wave, the rule of moe_forward's top-k
+// (picchio.c:1327-1339): repeated argmax with strict '>', so that the lowest
+// index wins a tie (a wave maximum, then the lowest lane holding it by
+// ballot; -0.0 counts as +0.0, NaN is never taken); when no logit is above
+// -1e30 the reference leaves -1, here the index becomes 0 (inside the store)
+// with the value -1e30. Lane l holds experts l and l + 64 (E <= 128).
+// Returns round n's (index, logit), the same on every lane; rounds 0..n-1
+// are taken out first.
+__device__ __forceinline__ int pk_wave_topk_nth(const float *logits, int E, int n, float *val) {
+    const int lane = threadIdx.x & 63;
+    // clamped, unconditional loads (entries past E are masked below)
+    const float v0 = logits[min(lane, E - 1)], v1 = logits[min(lane + 64, E - 1)];
+    const uint32_t k0 = (lane < E && v0 == v0) ? pk_fkey(v0 + 0.0f) : 0u;
+    const uint32_t k1 = (lane + 64 < E && v1 == v1) ? pk_fkey(v1 + 0.0f) : 0u;
+    const uint32_t floor_key = pk_fkey(-1e30f);
+    bool t0 = false, t1 = false;
+    int bi = 0;
+    float bv = -1e30f;
+    for (int k = 0; k <= n; ++k) {
+        const uint32_t a0 = t0 ? 0u : k0, a1 = t1 ? 0u : k1;
+        const uint32_t M = pk_wave_max_u32(max(a0, a1));
+        if (M <= floor_key) {
+            bi = 0;
+            bv = -1e30f;
+        } else {
+            const uint64_t m0 = __ballot(a0 == M);
+            bi = m0 ? __builtin_ctzll(m0) : 64 + __builtin_ctzll(__ballot(a1 == M));
+            bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bi < 64 ? v0 : v1), bi & 63));
+        }
+        if (bi == lane) t0 = true;
+        if (bi == lane + 64) t1 = true;
+    }
+    *val = bv;
+    return bi;
+}
+
+// Routing of one token from its logits, in the consumer of the router
+// logits: where the expert kernels select their own experts, one wave also
+// publishes the selection and the softmax weights (picchio.c:1353,
+// quant.h:406-412: max, expf, sum and division in routing order), with the
+// arithmetic of k_router_topk's last block.
+__device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
+    const int lane = threadIdx.x & 63;
+    float m = -1e30f, cv[16];
+    int ci[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+        if (k < rt.K) {
+            ci[k] = pk_wave_topk_nth(rt.logits, rt.E, k, &cv[k]);
+            if (cv[k] > m) m = cv[k];
+        }
+    }
+    if (lane != 0) return;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (k < rt.K) { cv[k] = expf(cv[k] - m); s += cv[k]; }
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+        if (k < rt.K) {
+            const float p = cv[k] / s;
+            rt.sel[k] = ci[k];
+            if (rt.w_soft) rt.w_soft[k] = p;
+            rt.w_scaled[k] = p * rt.routed_scale;
+        }
+}

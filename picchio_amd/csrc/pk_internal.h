@@ -123,9 +123,23 @@ struct pk_combine_args {
     uint32_t *counters;       // [RB] zero-initialised arrival counters (re-armed after use)
 };
 
+// Routing of one token selected inside an expert launch (see
+// pk_launch_i4_gemv's route argument).
+struct pk_route_args {
+    const float *logits;      // [E] router logits (+ bias) of the token
+    int E, K;
+    float routed_scale;
+    int32_t *sel;             // [K] outputs, written by one workgroup
+    float *w_scaled, *w_soft; // [K] (w_soft optional)
+};
+
+// route (optional): the items are rounds 0..n_items-1 of the top-k of the
+// router logits in route->logits, selected in the kernel; one workgroup
+// writes route->sel / w_scaled / w_soft for the launches that follow.
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
                       float swiglu_limit, float swiglu_alpha,
-                      const pk_combine_args *comb, hipStream_t st);
+                      const pk_combine_args *comb, hipStream_t st,
+                      const pk_route_args *route = nullptr);
 
 // Reference-layout INT4 gs GEMV, any I / group size (exact quant.h order).
 int pk_launch_i4_gemv_ref(float *y, const float *x, const uint8_t *q4, const float *s,

@@ -223,6 +223,32 @@ def test_moe_forward_parity(moe_setup, oracle):
     assert worst < 1e-5
 
 
+def test_router_ties_take_lowest_index(moe_setup, oracle):
+    """Equal router logits: the lowest expert index is taken first
+    (picchio.c:1327-1339, strict '>' over experts in order), and equal
+    logits get equal weights. Rows 2 and 5 of the router are the same, and
+    rows 1 and 6, so their logits have the same bits; the top-4 is then
+    2, 5, 1, 6 by construction."""
+    import torch
+    cfg, model, eng = moe_setup
+    D, E = cfg.hidden, cfg.n_experts
+    router = oracle.tensor(model, 6, 0, E * D)
+    rbias = oracle.tensor(model, 7, 0, E)
+    x = _token_x(oracle, cfg, 4242)
+    R = (router.reshape(E, D) * 0.01).astype(np.float32)
+    R[2] = R[5] = x * 0.05
+    R[1] = R[6] = x * 0.03
+    try:
+        eng.store_router(0, np.ascontiguousarray(R).ravel(), np.zeros(E, np.float32))
+        xd = eng.to_dev(x)
+        od = eng.empty(D, torch.float32)
+        sel, w = eng.moe_forward(0, xd, od, want_routing=True)
+        assert list(sel) == [2, 5, 1, 6], sel
+        assert w[0] == w[1] and w[2] == w[3] and w[0] > w[2], w
+    finally:
+        eng.store_router(0, router, rbias)
+
+
 def test_moe_forward_batch_prefill_order(moe_setup, oracle):
     """Batched MoE = forward_prefill's MoE (picchio.c:1829-1916): same routing
     as decode per token; each token sums its experts in the order the batch
