@@ -18,16 +18,8 @@ namespace {
 
 constexpr int ATT_CHUNK = 128;         // positions per attention partial
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return pk_wave_sum_f(v); }
+__device__ __forceinline__ double wave_sum_d(double v) { return pk_wave_sum_d(v); }
 
 // Token row -> h (zeros for an out-of-range id, picchio.c:1476-1480), and
 // hn = rmsnorm(h) (quant.h:396-402: double sum of squares).
@@ -355,9 +347,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
 #pragma unroll
     for (int jj = 0; jj < ATT_GH; ++jj) {
         if (jj >= jn) break;
-        float m = sc[jj];
-#pragma unroll
-        for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+        const float m = pk_wave_max_f(sc[jj]);
         if (lane == 0) red[wave][jj] = m;
     }
     __syncthreads();

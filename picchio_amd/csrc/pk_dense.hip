@@ -5,16 +5,7 @@
 #include "pk_synth.h"
 
 // ───────────────────────── wave reductions ─────────────────────────
-__device__ __forceinline__ float pk_wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-__device__ __forceinline__ double pk_wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float pk_wave_sum(float v) { return pk_wave_sum_f(v); }
 
 // ───────────────────────── fp32 GEMV ─────────────────────────
 // y[s][o] = x[s] . W[o] (+ bias[o]), matmul_f32 (quant.h:117-148). fp32 sum

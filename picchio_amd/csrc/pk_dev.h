@@ -2,10 +2,74 @@
 #pragma once
 #include "pk_internal.h"
 
-__device__ __forceinline__ double pk_dev_wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+// ───────────────────────── wave sums ─────────────────────────
+// Sum over the 64 lanes of a wave (all active), every lane getting it. The
+// tree is fixed: lane ^ 1, ^ 2, ^ 4, ^ 8 within each row of 16 lanes (own +
+// partner at each step), then the four row sums r0..r3 as (r0 + r1) +
+// (r2 + r3). The in-row steps are DPP moves (quad permutes and row
+// rotations) and the row sums are lane reads: a few VALU cycles each
+// instead of one LDS permute per step. Every kernel reduces with these, so
+// the kernels that restate another's arithmetic keep its bits.
+template <int CTRL>
+__device__ __forceinline__ int pk_dpp_i(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, 0xf, 0xf, false);
+}
+template <int CTRL>
+__device__ __forceinline__ float pk_dpp_f(float v) {
+    return __int_as_float(pk_dpp_i<CTRL>(__float_as_int(v)));
+}
+template <int CTRL>
+__device__ __forceinline__ double pk_dpp_d(double v) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)pk_dpp_i<CTRL>((int)(uint32_t)b);
+    const uint32_t hi = (uint32_t)pk_dpp_i<CTRL>((int)(uint32_t)(b >> 32));
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+__device__ __forceinline__ double pk_readlane_d(double v, int l) {
+    const uint64_t b = (uint64_t)__double_as_longlong(v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)b, l);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(b >> 32), l);
+    return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
+
+// DPP controls: quad_perm [1,0,3,2] (lane ^ 1), [2,3,0,1] (lane ^ 2); row
+// rotations by 4 and 12 (lane ^ 4 is +4 or -4 in the row), by 8 (lane ^ 8)
+__device__ __forceinline__ float pk_wave_sum_f(float v) {
+    v = v + pk_dpp_f<0xB1>(v);
+    v = v + pk_dpp_f<0x4E>(v);
+    const float p4 = pk_dpp_f<0x124>(v), m4 = pk_dpp_f<0x12C>(v);
+    v = v + ((threadIdx.x & 4) ? m4 : p4);
+    v = v + pk_dpp_f<0x128>(v);
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (r0 + r1) + (r2 + r3);
+}
+
+__device__ __forceinline__ double pk_wave_sum_d(double v) {
+    v = v + pk_dpp_d<0xB1>(v);
+    v = v + pk_dpp_d<0x4E>(v);
+    const double p4 = pk_dpp_d<0x124>(v), m4 = pk_dpp_d<0x12C>(v);
+    v = v + ((threadIdx.x & 4) ? m4 : p4);
+    v = v + pk_dpp_d<0x128>(v);
+    return (pk_readlane_d(v, 0) + pk_readlane_d(v, 16)) + (pk_readlane_d(v, 32) + pk_readlane_d(v, 48));
+}
+
+__device__ __forceinline__ double pk_dev_wave_sum_d(double v) { return pk_wave_sum_d(v); }
+
+// Maximum over the wave (fmaxf: a NaN lane is ignored), every lane getting
+// it; any tree gives the same value.
+__device__ __forceinline__ float pk_wave_max_f(float v) {
+    v = fmaxf(v, pk_dpp_f<0xB1>(v));
+    v = fmaxf(v, pk_dpp_f<0x4E>(v));
+    v = fmaxf(v, pk_dpp_f<0x124>(v));
+    v = fmaxf(v, pk_dpp_f<0x128>(v));
+    const float r0 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float r1 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float r2 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float r3 = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return fmaxf(fmaxf(r0, r1), fmaxf(r2, r3));
 }
 
 // ───────────── range-checked loads through a buffer resource ─────────────

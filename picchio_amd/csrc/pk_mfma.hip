@@ -20,6 +20,7 @@
 // is reproduced bit-for-bit by the oracle's restatement (po_moe_mfma_gemm).
 #include "pk_engine.h"
 #include "pk_i4_device.h"
+#include "pk_dev.h"
 
 namespace {
 
@@ -47,8 +48,7 @@ __global__ __launch_bounds__(256) void k_act_limbs(const float *__restrict__ x, 
     const float *xr = x + (int64_t)r * x_stride;
     float m = 0.0f;
     for (int i = threadIdx.x; i < cols; i += 256) m = fmaxf(m, fabsf(xr[i]));
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, 64));
+    m = pk_wave_max_f(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
     __syncthreads();
     m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));

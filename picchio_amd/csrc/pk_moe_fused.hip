@@ -134,11 +134,7 @@ __device__ __forceinline__ uint32_t *gu_ctr(const fused_args &a, int k) {
     return ctl_u(a, CTL_GU + k * CTL_GU_STRIDE);
 }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
+__device__ __forceinline__ float wave_sum(float v) { return pk_wave_sum_f(v); }
 
 __device__ __forceinline__ void mark(const fused_args &a, int i) {
     if (a.trace && threadIdx.x == STEER) a.trace[(int64_t)blockIdx.x * 6 + i] = wall_clock64();

@@ -21,6 +21,7 @@
 // the dependency of consecutive layers in decode.
 #include "pk_engine.h"
 #include "pk_i4_device.h"
+#include "pk_dev.h"
 
 #include <algorithm>
 #include <vector>
@@ -175,8 +176,7 @@ __device__ void router_task(const seq_args &a, int t, int e, float *red, float *
 #pragma unroll
         for (int u = 0; u < PER_LANE; ++u) acc = __builtin_fmaf(xv[u], wv[u], acc);
     }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o, 64);
+    acc = pk_wave_sum_f(acc);
     if (lane == 0) red[wave] = acc;
     __syncthreads();
     if (threadIdx.x == 0) {
