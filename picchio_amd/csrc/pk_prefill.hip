@@ -174,7 +174,7 @@ static int grouped_reserve(pk_engine *e, int T) {
 // batch's expert order. sel_in / w_in: routing supplied by the caller
 // (device [T][K], combine weights already x routed_scale), else the router's.
 static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
-                         const int32_t *sel_in, const float *w_in) {
+                         const int32_t *sel_in, const float *w_in, bool decode_order = false) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
     const int P = T * K;
@@ -189,8 +189,10 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
         PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr,
                                     e->stream));
     }
-    hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
-    PK_HIP(hipGetLastError());
+    if (!decode_order) {
+        hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+        PK_HIP(hipGetLastError());
+    }
     const int max_tiles = (P + 31) / 32 + E;
     int32_t *tile_exp = e->g_tiles, *tile_beg = tile_exp + max_tiles, *tile_cnt = tile_beg + max_tiles;
     int32_t *n_tiles = tile_cnt + max_tiles;
@@ -224,7 +226,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
     PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_PLAIN, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
-                       e->b_eo, e->b_w, e->b_perm, K, D);
+                       e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }
@@ -464,6 +466,17 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
         e->bd_cap = n_seq;
         e->bd_steps = n_steps + 1;
     }
+    // With PK_BATCH_MFMA_MIN=n (n > 0) and at least n sequences the MoE runs
+    // on the int8 matrix cores (pairs grouped by expert, three exact
+    // activation limbs; sums in another order than the per-pair GEMV, within
+    // 1e-6 relative). Off by default: at 32 sequences over 128 experts most
+    // experts get one or two pairs, and a 32-pair tile per expert costs more
+    // (25.5 against 22.3 ms per 120B-shaped step); without it every sequence
+    // gets forward_token's exact bits.
+    int mfma_min = 0;
+    if (const char *v = getenv("PK_BATCH_MFMA_MIN")) mfma_min = atoi(v);
+    const bool moe_mfma = mfma_min > 0 && n_seq >= mfma_min;
+    if (moe_mfma) PK_TRY(grouped_reserve(e, n_seq));
     PK_HIP(hipMemcpyAsync(e->bd_toks, toks_host, (size_t)n_seq * 4, hipMemcpyHostToDevice, e->stream));
     for (int step = 0; step < n_steps; ++step) {
         const int32_t *tk = e->bd_toks + (int64_t)step * n_seq;
@@ -474,7 +487,10 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
             PK_TRY(pk_attention_rows(e, l, nullptr, pos + step, 0, 0, 1, n_seq, e->p_XN, e->p_qkv, e->p_part,
                                      e->p_att, e->p_H));
             PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n_seq, e->stream));
-            PK_TRY(moe_rows(e, l, e->p_XN, n_seq, e->p_H, e->p_H, true));
+            if (moe_mfma)
+                PK_TRY(moe_rows_mfma(e, l, e->p_XN, n_seq, e->p_H, e->p_H, nullptr, nullptr, true));
+            else
+                PK_TRY(moe_rows(e, l, e->p_XN, n_seq, e->p_H, e->p_H, true));
         }
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->final_norm, D, c->eps, n_seq, e->stream));
         const int ps = pk_prof_begin(e, PK_PROF_LM_HEAD);

@@ -222,3 +222,43 @@ def test_batched_sequences_match_separate_streams(gpu, oracle, monkeypatch):
     finally:
         eng.close()
         oracle.model_free(model)
+
+
+def test_batched_decode_on_matrix_cores(gpu, oracle, monkeypatch):
+    """With PK_BATCH_MFMA_MIN=16, decode_batch of 16 sequences runs the MoE
+    as the expert-grouped int8 MFMA GEMM (exact activation limbs, sums in
+    another order than the per-pair GEMV): each stream follows the oracle's
+    forward_token while the oracle's top-2 logit margin is clear of the
+    last-bit differences; a stream is compared up to its first step with a
+    margin below 1e-3."""
+    import picchio_amd as pa
+    monkeypatch.setenv("PK_BATCH_MFMA_MIN", "16")
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=8, ctx_len=128, vocab=1000)
+    model = oracle.model_build(cfg, 4321, 0)
+    eng = pa.Engine(cfg)
+    n_seq, n_prompt, steps = 16, 24, 8
+    try:
+        upload_model(eng, oracle, model, cfg)
+        eng.batch_reserve(n_seq)
+        rng = np.random.default_rng(99)
+        prompts = [rng.integers(0, cfg.vocab, n_prompt).astype(np.int32) for _ in range(n_seq)]
+        first = [eng.prefill_seq(s, prompts[s]) for s in range(n_seq)]
+        got = eng.decode_batch(first, n_prompt, steps)
+        compared = 0
+        logits = np.empty(cfg.vocab, np.float32)
+        for s in range(n_seq):
+            oracle.model_reset_kv(model)
+            tok = oracle.prefill_tokens(model, prompts[s], n_prompt, 0, 64)
+            assert tok == first[s], s
+            for i in range(steps):
+                ref = oracle.forward_token(model, tok, n_prompt + i, logits.ctypes.data)
+                top2 = np.sort(logits)[-2:]
+                if top2[1] - top2[0] < 1e-3:
+                    break
+                assert got[i, s] == ref, (s, i, got[i, s], ref)
+                compared += 1
+                tok = ref
+        assert compared >= n_seq * steps // 2, compared
+    finally:
+        eng.close()
+        oracle.model_free(model)
