@@ -189,7 +189,7 @@ __device__ __forceinline__ int chunk_dst(int c) {              // byte offset in
     } while (0)
 
 template <int EPI>
-__global__ __launch_bounds__(NTHR) void k_moe_mfma(pk_mfma_args a) {
+__global__ __launch_bounds__(NTHR, 4) void k_moe_mfma(pk_mfma_args a) {
     __shared__ __attribute__((aligned(16))) int8_t bsh[2][3][TT][BROW];
     __shared__ __attribute__((aligned(16))) float ssh[2][G][WG_ROWS];
     __shared__ int tok_row[TT];
@@ -215,6 +215,9 @@ __global__ __launch_bounds__(NTHR) void k_moe_mfma(pk_mfma_args a) {
                                                       h * 1024 + 16 * (r64 + n));
     const float *scw = reinterpret_cast<const float *>(base + a.off_scales);
     const int n_stage = a.NG / G;
+    // the epilogue's output row goes out now
+    const float *bias = a.off_bias >= 0 ? reinterpret_cast<const float *>(base + a.off_bias) : nullptr;
+    const int p_out = a.pairs[beg + min(n, cnt - 1)];
     __syncthreads();
 
     const uint4 z4 = make_uint4(0, 0, 0, 0);
@@ -235,15 +238,26 @@ __global__ __launch_bounds__(NTHR) void k_moe_mfma(pk_mfma_args a) {
         for (int gi = 0; gi < G; ++gi) {
             pk_v4i A0, A1;
             expand_w(gi == 0 ? wc0 : gi == 1 ? wc1 : wc2, A0, A1);
-            pk_v16i P[3];
+            // limb products low to high, each folded into the exact sum as it
+            // arrives: C = (P0 << 10) + (P1 << 3) + (P2 >> 4) (two limb
+            // results live at a time, not three)
+            pk_v16i Cg;
 #pragma unroll
-            for (int l = 0; l < 3; ++l) {
+            for (int l = 2; l >= 0; --l) {
                 const int8_t *bp = &bsh[buf][l][n][gi * 64 + 32 * h];
                 const pk_v4i B0 = *reinterpret_cast<const pk_v4i *>(bp);
                 const pk_v4i B1 = *reinterpret_cast<const pk_v4i *>(bp + 16);
                 pk_v16i z = {};
                 z = __builtin_amdgcn_mfma_i32_32x32x32_i8(A0, B0, z, 0, 0, 0);
-                P[l] = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, z, 0, 0, 0);
+                z = __builtin_amdgcn_mfma_i32_32x32x32_i8(A1, B1, z, 0, 0, 0);
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    // (z << s) + C is one v_lshl_add_u32; two's complement
+                    // arithmetic, so it is z 2^s + C for negative z too
+                    if (l == 2) Cg[v] = z[v] >> 4;
+                    else if (l == 1) Cg[v] = (int)(((uint32_t)z[v] << 3) + (uint32_t)Cg[v]);
+                    else Cg[v] = (int)(((uint32_t)z[v] << 10) + (uint32_t)Cg[v]);
+                }
             }
             const float *sp = &ssh[buf][gi][wave * 32 + 4 * h];
 #pragma unroll
@@ -253,24 +267,25 @@ __global__ __launch_bounds__(NTHR) void k_moe_mfma(pk_mfma_args a) {
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int v = 4 * b4 + i;
-                    const int C = (P[0][v] << 10) + (P[1][v] << 3) + (P[2][v] >> 4);
-                    acc[v] = __builtin_fmaf(sv4[i], (float)C, acc[v]);
+                    acc[v] = __builtin_fmaf(sv4[i], (float)Cg[v], acc[v]);
                 }
             }
         }
     }
     if (!active || n >= cnt) return;
-    const int p = a.pairs[beg + n];
+    float bv[16];
+    if (bias) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) bv[v] = bias[row0 + 8 * (v >> 2) + 4 * h + (v & 3)];
+    }
     const int k = tok_exp[n];
-    const float *bias = a.off_bias >= 0 ? reinterpret_cast<const float *>(base + a.off_bias) : nullptr;
     float y[16];
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-        const int row = row0 + 8 * (v >> 2) + 4 * h + (v & 3);
         y[v] = ldexpf(acc[v], k - 24);
-        if (bias) y[v] = y[v] + bias[row];
+        if (bias) y[v] = y[v] + bv[v];
     }
-    float *yr = a.y + (int64_t)p * a.y_stride;
+    float *yr = a.y + (int64_t)p_out * a.y_stride;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
         const int row = row0 + 8 * b + 4 * h;
