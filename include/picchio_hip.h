@@ -129,6 +129,29 @@ int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l);
 int pk_store_globals(pk_engine *e, const pk_qt_host *embed,
                      const pk_qt_host *lm_head, const float *final_norm_host);
 
+/* ── converted checkpoints (convert.py output: config.json + safetensors
+ *    shards). Replaces cfg_load (picchio.c:349-420), the shard discovery of
+ *    main (picchio.c:2848-2915), load_dense_weights (picchio.c:2534-2650) and
+ *    expert_load / load_expert_bias (picchio.c:634-888) for every expert:
+ *    the whole model is made resident. ── */
+
+/* <dir>/config.json into cfg with cfg_load's keys and defaults, plus what
+ * picchio reads from the shards: the experts' group size (picchio.c:781-784)
+ * and the lm_head format (INT8 rows or F32). ctx_len > 0 replaces
+ * max_position_embeddings as the KV capacity. Reads host files only. */
+int pk_cfg_from_container(const char *dir, int ctx_len, pk_cfg *cfg);
+
+/* Every tensor of the container into the engine (created with that cfg):
+ * embedding (F32/BF16/F16, or INT8/INT4 rows dequantized as embed_token
+ * does), lm_head (F32 or INT8 rows), norms (1.0 when absent), F32 attention
+ * and biases (0 when absent), sinks, router (either name) and its bias, and
+ * the INT4 experts (the three name spellings, ".qs" group scales) with their
+ * biases (per expert, aggregated [E][n], or the legacy INT4 bias). Formats
+ * the GPU path does not hold (F32/BF16 experts, BF16 attention, INT4
+ * lm_head) return PK_ERR_UNSUPPORTED; a missing expert PK_ERR_MISSING.
+ * n_threads shard readers (<= 0: 8). */
+int pk_load_container(pk_engine *e, const char *dir, int n_threads);
+
 /* Builds every tensor of the engine's cfg from `seed` with the generator of
  * pk_synth.h (N(0,0.02) weights, norms 1.0), quantizing the experts on the GPU
  * with pk_quantize_int4_gs. `what`: bit 0 experts+routers, bit 1 attention,

@@ -81,6 +81,13 @@ def gptoss_cfg(**kw):
     return c
 
 
+def cfg_from_container(path, ctx_len=0):
+    """pk_cfg of a converted checkpoint directory (config.json + shards)."""
+    c = PkCfg()
+    check(lib().pk_cfg_from_container(os.fsencode(path), ctx_len, C.byref(c)))
+    return c
+
+
 _lib = None
 
 
@@ -107,6 +114,8 @@ def lib():
         "pk_store_layer": (C.c_int, [vp, C.c_int, C.POINTER(PkLayerHost)]),
         "pk_store_globals": (C.c_int, [vp, C.POINTER(PkQtHost), C.POINTER(PkQtHost), vp]),
         "pk_engine_build_synthetic": (C.c_int, [vp, C.c_uint64, C.c_int, C.c_int]),
+        "pk_cfg_from_container": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(PkCfg)]),
+        "pk_load_container": (C.c_int, [vp, C.c_char_p, C.c_int]),
         "pk_quantize_int4_gs": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
         "pk_qt_upload": (C.c_int, [vp, C.POINTER(PkQtHost), C.POINTER(vp)]),
         "pk_qt_free": (C.c_int, [vp, vp]),
@@ -243,6 +252,10 @@ class Engine:
     # library calls
     def build_synthetic(self, seed, what=7, threads=0):
         check(self.L.pk_engine_build_synthetic(self.h, seed, what, threads))
+
+    def load_container(self, path, threads=8):
+        """Every tensor of a converted checkpoint directory (pk_load_container)."""
+        check(self.L.pk_load_container(self.h, os.fsencode(path), threads))
 
     def store_expert(self, layer, eid, gu_q4, gu_s, d_q4, d_s, gu_b, d_b):
         c = self.cfg

@@ -12,7 +12,7 @@ CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libpicchio_hip.so")
 OBJ = os.path.join(HERE, "_build")
 SOURCES = ["pk_i4.hip", "pk_dense.hip", "pk_engine.hip", "pk_moe_seq.hip", "pk_decode.hip",
-           "pk_prefill.hip", "pk_mfma.hip", "pk_moe_fused.hip"]
+           "pk_prefill.hip", "pk_mfma.hip", "pk_moe_fused.hip", "pk_container.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 # -ffp-contract=off: every fused multiply-add in the kernels is an explicit
@@ -24,7 +24,7 @@ FLAGS = ["--offload-arch=gfx950", "-O3", "-std=c++17", "-fPIC", "-ffp-contract=o
 
 
 def _compile(src):
-    obj = os.path.join(OBJ, src.replace(".hip", ".o"))
+    obj = os.path.join(OBJ, os.path.splitext(src)[0] + ".o")
     cmd = [HIPCC, *FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     msgs = "\n".join(l for l in (r.stdout + r.stderr).splitlines()
