@@ -720,6 +720,112 @@ int po_argmax(const float *logits, int n) {                /* picchio.c:1555-156
     return best;
 }
 
+/* ───────────────────────── sampling (picchio.c:1509-1649) ───────────────────────── */
+void po_sampler_init(po_sampler *s, float temperature, float top_p, int top_k, float rep_penalty,
+                     uint64_t seed) {
+    s->temperature = temperature;
+    s->top_p = top_p;
+    s->top_k = top_k;
+    s->rep_penalty = rep_penalty;
+    s->rng = seed;
+    s->history_len = 0;
+}
+
+/* xorshift64 (picchio.c:1520-1526): shifts 13, 7, 17; the top 31 bits of the
+ * state over 2^31 */
+float po_rng_float(uint64_t *state) {
+    uint64_t x = *state;
+    x ^= x << 13;
+    x ^= x >> 7;
+    x ^= x << 17;
+    *state = x;
+    return (float)(x >> 33) / (float)(1ULL << 31);
+}
+
+typedef struct { float val; int idx; } po_iv;
+/* descending; equal values compare equal (the reference's comparators) */
+static int po_desc_iv(const void *a, const void *b) {
+    const float fa = ((const po_iv *)a)->val, fb = ((const po_iv *)b)->val;
+    return (fa < fb) - (fa > fb);
+}
+static int po_desc_f(const void *a, const void *b) {
+    const float fa = *(const float *)a, fb = *(const float *)b;
+    return (fa < fb) - (fa > fb);
+}
+
+static int po_sample_record(po_sampler *s, int tok) {
+    if (s->history_len < 4096) s->history[s->history_len++] = tok;
+    return tok;
+}
+
+int po_sample_logits(po_sampler *s, float *logits, int vocab) {
+    /* 1. repetition penalty, once per history entry (picchio.c:1541-1551) */
+    if (s->rep_penalty > 1.0f)
+        for (int i = 0; i < s->history_len; i++) {
+            const int t = s->history[i];
+            if (t >= 0 && t < vocab) {
+                if (logits[t] > 0) logits[t] /= s->rep_penalty;
+                else logits[t] *= s->rep_penalty;
+            }
+        }
+    /* 2. greedy below 1e-6 (first maximum), else temperature */
+    if (s->temperature < 1e-6f) return po_sample_record(s, po_argmax(logits, vocab));
+    const float inv_temp = 1.0f / s->temperature;
+    for (int i = 0; i < vocab; i++) logits[i] *= inv_temp;
+    /* 3. top-k: the K-th largest of a sorted copy; below it -> -1e30 */
+    if (s->top_k > 0 && s->top_k < vocab) {
+        float *cp = (float *)malloc((size_t)vocab * sizeof(float));
+        memcpy(cp, logits, (size_t)vocab * sizeof(float));
+        qsort(cp, (size_t)vocab, sizeof(float), po_desc_f);
+        const float thr = cp[s->top_k - 1];
+        free(cp);
+        for (int i = 0; i < vocab; i++)
+            if (logits[i] < thr) logits[i] = -1e30f;
+    }
+    /* 4. softmax in vocabulary order */
+    float mx = -1e30f;
+    for (int i = 0; i < vocab; i++) if (logits[i] > mx) mx = logits[i];
+    float sum = 0.0f;
+    for (int i = 0; i < vocab; i++) {
+        logits[i] = expf(logits[i] - mx);
+        sum += logits[i];
+    }
+    for (int i = 0; i < vocab; i++) logits[i] /= sum;
+    /* 5. top-p over the probabilities > 1e-10, sorted descending */
+    if (s->top_p < 1.0f && s->top_p > 0.0f) {
+        int n = 0;
+        for (int i = 0; i < vocab; i++) if (logits[i] > 1e-10f) n++;
+        if (n > 1) {
+            po_iv *v = (po_iv *)malloc((size_t)n * sizeof(po_iv));
+            int k = 0;
+            for (int i = 0; i < vocab; i++)
+                if (logits[i] > 1e-10f) { v[k].val = logits[i]; v[k].idx = i; k++; }
+            qsort(v, (size_t)n, sizeof(po_iv), po_desc_iv);
+            float cum = 0.0f;
+            int cut = n;
+            for (int i = 0; i < n; i++) {
+                cum += v[i].val;
+                if (cum >= s->top_p) { cut = i + 1; break; }
+            }
+            for (int i = cut; i < n; i++) logits[v[i].idx] = 0.0f;
+            sum = 0.0f;
+            for (int i = 0; i < vocab; i++) sum += logits[i];
+            if (sum > 0) for (int i = 0; i < vocab; i++) logits[i] /= sum;
+            free(v);
+        }
+    }
+    /* 6. the draw, cumulative in vocabulary order; else the last p > 0 */
+    const float r = po_rng_float(&s->rng);
+    float cum = 0.0f;
+    for (int i = 0; i < vocab; i++) {
+        cum += logits[i];
+        if (cum >= r) return po_sample_record(s, i);
+    }
+    for (int i = vocab - 1; i >= 0; i--)
+        if (logits[i] > 0) return po_sample_record(s, i);
+    return 0;
+}
+
 static void po_lm_head(po_model *m, const float *hn, float *logits) {
     const pk_cfg *c = &m->c;
     if (c->lm_head_fmt == PK_FMT_INT8)

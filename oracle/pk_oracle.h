@@ -115,6 +115,25 @@ int po_prefill_tokens(po_model *m, const int *ids, int n, int pos_base, int batc
 /* greedy branch of sample_logits (picchio.c:1555-1560). */
 int po_argmax(const float *logits, int n);
 
+/* sample_logits (picchio.c:1509-1649) with its globals as explicit state:
+ * repetition penalty over the sampled history, greedy below temperature
+ * 1e-6, temperature, top-k by the K-th largest value (ties kept), softmax,
+ * top-p over the probabilities > 1e-10 sorted descending, then the
+ * xorshift64 draw and the cumulative pick in vocabulary order. Modifies
+ * logits in place as the reference does. */
+typedef struct po_sampler {
+    float temperature, top_p;
+    int top_k;
+    float rep_penalty;
+    uint64_t rng;
+    int history_len;
+    int history[4096];
+} po_sampler;
+void po_sampler_init(po_sampler *s, float temperature, float top_p, int top_k, float rep_penalty,
+                     uint64_t seed);
+float po_rng_float(uint64_t *state);
+int po_sample_logits(po_sampler *s, float *logits, int vocab);
+
 /* ── the GPU's expert-grouped (int8 matrix core) path, restated ──
  * Not a reference function: the exact arithmetic the library's grouped
  * prefill uses, so its integer parts and fold order can be checked bit for

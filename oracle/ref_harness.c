@@ -44,6 +44,23 @@ void ref_rmsnorm(float *o, const float *x, const float *w, int D, float eps) {
 }
 void ref_softmax(float *x, int n) { softmax(x, n); }
 
+/* sample_logits (picchio.c:1509-1649) with its globals set from the
+ * arguments: the token, the logits as it leaves them, and in *rng the state
+ * after the draw. */
+int ref_sample_logits(float *logits, int vocab, float temperature, float top_p, int top_k,
+                      float rep_penalty, uint64_t *rng, const int *history, int history_len) {
+    g_temperature = temperature;
+    g_top_p = top_p;
+    g_top_k = top_k;
+    g_rep_penalty = rep_penalty;
+    g_rng = *rng;
+    g_history_len = history_len < 4096 ? history_len : 4096;
+    memcpy(g_history, history, (size_t)g_history_len * sizeof(int));
+    const int t = sample_logits(logits, vocab);
+    *rng = g_rng;
+    return t;
+}
+
 /* ── model attached to an oracle po_model ── */
 
 static void ref_cfg_from(Cfg *c, const pk_cfg *p) {

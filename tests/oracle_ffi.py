@@ -82,6 +82,10 @@ class Oracle:
         self.forward_prefill = _bind(L, "po_forward_prefill", C.c_int, vp, i32p, C.c_int, C.c_int)
         self.prefill_tokens = _bind(L, "po_prefill_tokens", C.c_int, vp, i32p, C.c_int, C.c_int, C.c_int)
         self.argmax = _bind(L, "po_argmax", C.c_int, f32p, C.c_int)
+        self._sampler_init = _bind(L, "po_sampler_init", None, C.c_void_p, C.c_float, C.c_float, C.c_int,
+                                   C.c_float, C.c_uint64)
+        self._sample_logits = _bind(L, "po_sample_logits", C.c_int, C.c_void_p, f32p, C.c_int)
+        self.rng_float = _bind(L, "po_rng_float", C.c_float, C.POINTER(C.c_uint64))
         self.act_limbs = _bind(L, "po_act_limbs", None, f32p, C.c_int, C.c_int, i8p, i32p)
         self.mfma_matvec = _bind(L, "po_mfma_matvec", None, u8p, f32p, _nd(np.float32), C.c_int, C.c_int,
                                  i8p, i8p, i8p, C.c_int, f32p)
@@ -124,6 +128,15 @@ class Oracle:
         d_b = arr(ptrs[5], C.c_float, D, np.float32)
         return gu_q4, gu_s, d_q4, d_s, gu_b, d_b
 
+    def sampler(self, temperature, top_p, top_k, rep_penalty, seed):
+        """po_sampler state (sample_logits' globals), as a ctypes buffer."""
+        st = (C.c_byte * (4 * 4 + 8 + 4 + 4 * 4096 + 4))()
+        self._sampler_init(C.cast(st, C.c_void_p), temperature, top_p, top_k, rep_penalty, seed)
+        return st
+
+    def sample_logits(self, st, logits):
+        return self._sample_logits(C.cast(st, C.c_void_p), logits, logits.size)
+
     def tensor(self, model, kind, layer, n):
         p = self.model_tensor(model, kind, layer, None)
         return np.ctypeslib.as_array(C.cast(p, C.POINTER(C.c_float)), shape=(n,)).copy()
@@ -152,6 +165,8 @@ class Reference:
         self.yarn_inv_freq = _bind(L, "ref_yarn_inv_freq", C.c_float, C.POINTER(PkCfg), C.c_int)
         self.forward_token = _bind(L, "ref_forward_token", C.c_int, C.c_int, C.c_int)
         self.prefill_tokens = _bind(L, "ref_prefill_tokens", C.c_int, i32p, C.c_int, C.c_int, C.c_int)
+        self.sample_logits = _bind(L, "ref_sample_logits", C.c_int, f32p, C.c_int, C.c_float, C.c_float,
+                                   C.c_int, C.c_float, C.POINTER(C.c_uint64), i32p, C.c_int)
 
 
 def reference_available():
