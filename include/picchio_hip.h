@@ -294,8 +294,10 @@ int pk_engine_status(pk_engine *e);
 int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
                      float *out_dev);
 
-/* forward_token (picchio.c:1655-1756), greedy (TEMPERATURE=0, REP=1):
- * returns the next token id in *next_host; logits_dev optional [vocab]. */
+/* forward_token (picchio.c:1655-1756): returns the next token id in
+ * *next_host, drawn by the engine's sampler (greedy until pk_set_sampling
+ * asks otherwise); logits_dev optional [vocab]: the logits, or with sampling
+ * on the array sample_logits leaves (probabilities, 0 where dropped). */
 int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host,
                      float *logits_dev);
 
@@ -304,16 +306,62 @@ int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_host,
 int pk_prefill_tokens(pk_engine *e, const int32_t *ids_host, int n, int pos_base,
                       int32_t *next_host);
 
-/* Greedy decode of n_steps after a prompt: out_host[n_steps] token ids.
- * The prompt runs position by position (prefill_tokens with PREFILL_BATCH=1,
- * picchio.c:1946-1954), then one captured decode step is replayed n_steps
- * times with the token and position carried on the device. */
+/* A turn's generation (picchio.c:2771-2790 without the protocol): the
+ * prompt through prefill_tokens (PREFILL_BATCH positions per chunk, default
+ * 64; 1 = position by position), then n_steps - 1 replays of one captured
+ * decode step with token and position carried on the device;
+ * out_host[n_steps] token ids, out_host[0] the prompt's next token. Tokens
+ * are drawn by the engine's sampler. */
 int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
                 int n_steps, int32_t *out_host);
 
 /* n_steps greedy decode steps from (tok, pos) over the existing KV cache,
  * replaying the captured step (for timing); out_host[n_steps] token ids. */
 int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out_host);
+
+/* ── sampling (sample_logits, picchio.c:1509-1649) on the device ──
+ * One sampler state per engine, in device memory: temperature, top-p,
+ * top-k, repetition penalty, the xorshift64 state and the penalty history
+ * (4096 ids). Every token the decode path produces (forward_token, each
+ * prefill chunk, each generate step) is drawn from it as the reference
+ * draws: penalty over the history, greedy below temperature 1e-6, top-k
+ * threshold with ties kept, softmax, top-p over probabilities > 1e-10,
+ * cumulative pick, and the pick appended to the history. Results equal the
+ * reference's up to the device expf's last ulp (a draw within an ulp of a
+ * boundary may differ). Until configured the engine is greedy. Batched
+ * decode (pk_decode_batch) stays greedy and refuses to run with sampling on. */
+
+/* The start-up settings TEMPERATURE, TOPP, TOPK, REP and SEED
+ * (picchio.c:3033-3037, defaults 1.0 / 0.95 / 50 / 1.1 at :1510-1513):
+ * replaces every parameter, seeds the rng and empties the history.
+ * Temperature < 1e-6 with rep_penalty <= 1 is the plain argmax. */
+int pk_set_sampling(pk_engine *e, float temperature, float top_p, int top_k,
+                    float rep_penalty, uint64_t seed);
+/* A TURN's per-request temperature, top-p and top-k (picchio.c:2737-2743,
+ * with its clamp: temperature to [0, 5], top-p outside (0, 1] -> 1, negative
+ * top-k -> 0); penalty, rng and history carry on. */
+int pk_set_turn_sampling(pk_engine *e, float temperature, float top_p, int top_k);
+/* RESET's history clear (picchio.c:2711-2716). */
+int pk_reset_history(pk_engine *e);
+/* sample_logits(logits, vocab) (picchio.c:1540) on a device vector, which is
+ * modified in place as the reference modifies its array; the id into
+ * *tok_host. Advances the rng and the history like any draw. */
+int pk_sample_logits(pk_engine *e, float *logits_dev, int vocab, int32_t *tok_host);
+/* No reference counterpart (a speed option): with on != 0, draws that keep
+ * more than 4096 entries (no top-k over a large vocabulary) add their floats
+ * exactly, as 64-bit integers of the values times a power of two, rounded to
+ * float once, instead of one at a time in the reference's order; the top-p
+ * cut is the shortest descending prefix whose exact sum reaches top_p and the
+ * pick the first index whose exact running sum reaches the draw. About ten
+ * times faster there; the probabilities differ from the reference's by its
+ * own float rounding (about 1e-5 relative at 200k entries), which over a
+ * flat distribution moves a top-p cut or a pick now and then. Draws keeping
+ * up to 4096 entries are unaffected. Default off. */
+int pk_set_sampling_fast_sums(pk_engine *e, int on);
+/* The sampler's rng state and history (up to cap ids into history_host,
+ * which may be NULL); *history_len the full length. */
+int pk_sampler_state(pk_engine *e, uint64_t *rng, int32_t *history_host, int cap,
+                     int *history_len);
 
 /* ── measurement (no reference counterpart: benchmark plumbing) ──
  * With profiling on, the engine brackets each launch of the listed kernels

@@ -826,6 +826,109 @@ int po_sample_logits(po_sampler *s, float *logits, int vocab) {
     return 0;
 }
 
+/* ── the library's arithmetic beyond 4096 kept entries (not a reference
+ * function) ── Sums exact: each value times 2^S truncated to a 64-bit
+ * integer (exact above 2^(23-S)), added as integers, the total rounded to
+ * float once. Top-p: the shortest prefix of the candidates (> 1e-10), sorted
+ * by value descending then index, whose exact sum reaches top_p; the pick:
+ * the first index whose exact cumulative sum reaches the draw. Everything
+ * else as po_sample_logits, which it is outright up to 4096 kept entries. */
+static uint64_t po_fx(float v, int S) {
+    uint32_t b;
+    memcpy(&b, &v, 4);
+    const int e = (int)(b >> 23) & 255;
+    if (e == 0 || (b >> 31)) return 0;
+    const uint64_t m = (b & 0x7fffffu) | 0x800000u;
+    const int sh = e - 150 + S;
+    if (sh >= 0) return m << sh;
+    return sh <= -24 ? 0 : m >> (-sh);
+}
+static float po_unfx(uint64_t q, int S) { return ldexpf((float)q, -S); }
+static int po_desc_iv_idx(const void *a, const void *b) {
+    const po_iv *x = (const po_iv *)a, *y = (const po_iv *)b;
+    if (x->val != y->val) return x->val > y->val ? -1 : 1;
+    return (x->idx > y->idx) - (x->idx < y->idx);
+}
+
+int po_sample_logits_fx(po_sampler *s, float *logits, int vocab) {
+    if (s->temperature < 1e-6f) return po_sample_logits(s, logits, vocab);
+    const float inv_temp = 1.0f / s->temperature;
+    float *cp = (float *)malloc((size_t)vocab * sizeof(float));
+    memcpy(cp, logits, (size_t)vocab * sizeof(float));
+    if (s->rep_penalty > 1.0f)
+        for (int i = 0; i < s->history_len; i++) {
+            const int t = s->history[i];
+            if (t >= 0 && t < vocab) cp[t] = cp[t] > 0 ? cp[t] / s->rep_penalty : cp[t] * s->rep_penalty;
+        }
+    for (int i = 0; i < vocab; i++) cp[i] *= inv_temp;
+    int n = vocab;
+    float thr = -INFINITY;
+    if (s->top_k > 0 && s->top_k < vocab) {
+        float *sc = (float *)malloc((size_t)vocab * sizeof(float));
+        memcpy(sc, cp, (size_t)vocab * sizeof(float));
+        qsort(sc, (size_t)vocab, sizeof(float), po_desc_f);
+        thr = sc[s->top_k - 1];
+        free(sc);
+        n = 0;
+        for (int i = 0; i < vocab; i++) n += !(cp[i] < thr);
+    }
+    if (n <= 4096) {
+        free(cp);
+        return po_sample_logits(s, logits, vocab);
+    }
+    /* cp holds the penalised, scaled logits; -1e30 below the threshold -> 0 */
+    float mx = -1e30f;
+    for (int i = 0; i < vocab; i++)
+        if (!(cp[i] < thr) && cp[i] > mx) mx = cp[i];
+    int bits = 0;
+    while ((n >> bits) != 0) bits++;
+    const int se = 63 - bits;
+    uint64_t q = 0;
+    for (int i = 0; i < vocab; i++) {
+        logits[i] = (cp[i] < thr) ? 0.0f : expf(cp[i] - mx);
+        q += po_fx(logits[i], se);
+    }
+    free(cp);
+    const float sum = po_unfx(q, se);
+    for (int i = 0; i < vocab; i++) logits[i] /= sum;
+    if (s->top_p < 1.0f && s->top_p > 0.0f) {
+        int na = 0;
+        for (int i = 0; i < vocab; i++) if (logits[i] > 1e-10f) na++;
+        if (na > 1) {
+            po_iv *v = (po_iv *)malloc((size_t)na * sizeof(po_iv));
+            int k = 0;
+            for (int i = 0; i < vocab; i++)
+                if (logits[i] > 1e-10f) { v[k].val = logits[i]; v[k].idx = i; k++; }
+            qsort(v, (size_t)na, sizeof(po_iv), po_desc_iv_idx);
+            uint64_t target = po_fx(s->top_p, 62);
+            if (target == 0) target = 1;
+            uint64_t acc = 0;
+            int cut = na;
+            for (int i = 0; i < na; i++) {
+                acc += po_fx(v[i].val, 62);
+                if (acc >= target) { cut = i + 1; break; }
+            }
+            for (int i = cut; i < na; i++) logits[v[i].idx] = 0.0f;
+            uint64_t q2 = 0;
+            for (int i = 0; i < vocab; i++) q2 += po_fx(logits[i], 62);
+            const float s2 = po_unfx(q2, 62);
+            if (s2 > 0) for (int i = 0; i < vocab; i++) logits[i] /= s2;
+            free(v);
+        }
+    }
+    const float r = po_rng_float(&s->rng);
+    if (r <= 0.0f) return po_sample_record(s, 0);
+    const uint64_t R = po_fx(r, 62);
+    uint64_t acc = 0;
+    for (int i = 0; i < vocab; i++) {
+        acc += po_fx(logits[i], 62);
+        if (acc >= R) return po_sample_record(s, i);
+    }
+    for (int i = vocab - 1; i >= 0; i--)
+        if (logits[i] > 0) return po_sample_record(s, i);
+    return 0;
+}
+
 static void po_lm_head(po_model *m, const float *hn, float *logits) {
     const pk_cfg *c = &m->c;
     if (c->lm_head_fmt == PK_FMT_INT8)

@@ -133,6 +133,11 @@ void po_sampler_init(po_sampler *s, float temperature, float top_p, int top_k, f
                      uint64_t seed);
 float po_rng_float(uint64_t *state);
 int po_sample_logits(po_sampler *s, float *logits, int vocab);
+/* Not a reference function: the library's sampler arithmetic, which beyond
+ * 4096 kept entries makes every sum exact (64-bit integers of the values
+ * times a power of two, rounded once) where the reference adds floats one at
+ * a time; up to 4096 kept entries it is po_sample_logits. */
+int po_sample_logits_fx(po_sampler *s, float *logits, int vocab);
 
 /* ── the GPU's expert-grouped (int8 matrix core) path, restated ──
  * Not a reference function: the exact arithmetic the library's grouped

@@ -116,6 +116,12 @@ def lib():
         "pk_engine_build_synthetic": (C.c_int, [vp, C.c_uint64, C.c_int, C.c_int]),
         "pk_cfg_from_container": (C.c_int, [C.c_char_p, C.c_int, C.POINTER(PkCfg)]),
         "pk_load_container": (C.c_int, [vp, C.c_char_p, C.c_int]),
+        "pk_set_sampling": (C.c_int, [vp, f32, f32, C.c_int, f32, C.c_uint64]),
+        "pk_set_turn_sampling": (C.c_int, [vp, f32, f32, C.c_int]),
+        "pk_reset_history": (C.c_int, [vp]),
+        "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
+        "pk_sample_logits": (C.c_int, [vp, vp, C.c_int, C.POINTER(i32)]),
+        "pk_sampler_state": (C.c_int, [vp, C.POINTER(C.c_uint64), vp, C.c_int, C.POINTER(C.c_int)]),
         "pk_quantize_int4_gs": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
         "pk_qt_upload": (C.c_int, [vp, C.POINTER(PkQtHost), C.POINTER(vp)]),
         "pk_qt_free": (C.c_int, [vp, vp]),
@@ -256,6 +262,42 @@ class Engine:
     def load_container(self, path, threads=8):
         """Every tensor of a converted checkpoint directory (pk_load_container)."""
         check(self.L.pk_load_container(self.h, os.fsencode(path), threads))
+
+    def set_sampling(self, temperature, top_p, top_k, rep_penalty, seed):
+        """Sampling parameters, seed and an empty history (the TEMPERATURE /
+        TOPP / TOPK / REP / SEED start-up settings, picchio.c:3033-3037)."""
+        check(self.L.pk_set_sampling(self.h, temperature, top_p, top_k, rep_penalty, seed))
+
+    def set_turn_sampling(self, temperature, top_p, top_k):
+        """A TURN's per-request temperature / top-p / top-k with the
+        reference's clamp; rng and history carry on (picchio.c:2737-2743)."""
+        check(self.L.pk_set_turn_sampling(self.h, temperature, top_p, top_k))
+
+    def set_sampling_fast_sums(self, on):
+        """Exact integer sums instead of the reference's float order for
+        draws keeping more than 4096 entries (pk_set_sampling_fast_sums)."""
+        check(self.L.pk_set_sampling_fast_sums(self.h, 1 if on else 0))
+
+    def reset_history(self):
+        """RESET's history clear (picchio.c:2711-2716)."""
+        check(self.L.pk_reset_history(self.h))
+
+    def sample_logits(self, logits_dev, vocab=None):
+        """sample_logits on a device fp32 vector, modified in place as the
+        reference modifies its array; returns the token id."""
+        tok = C.c_int32()
+        n = logits_dev.numel() if vocab is None else vocab
+        check(self.L.pk_sample_logits(self.h, ptr(logits_dev), n, C.byref(tok)))
+        return tok.value
+
+    def sampler_state(self):
+        """(rng state, repetition-penalty history) of the device sampler."""
+        import numpy as np
+        rng = C.c_uint64()
+        n = C.c_int()
+        hist = np.zeros(4096, np.int32)
+        check(self.L.pk_sampler_state(self.h, C.byref(rng), ptr(hist), len(hist), C.byref(n)))
+        return rng.value, hist[:n.value].copy()
 
     def store_expert(self, layer, eid, gu_q4, gu_s, d_q4, d_s, gu_b, d_b):
         c = self.cfg

@@ -18,6 +18,20 @@ struct pk_dstate {
     int32_t tok, pos, n_out, next;
 };
 
+// Sampler state in device memory (picchio.c:1509-1520): parameters, the
+// xorshift64 state and the repetition-penalty history. The sampling kernel
+// reads and advances it, so a captured decode step samples on replay.
+constexpr int PK_HISTORY_CAP = 4096;
+struct pk_sampler_dev {
+    float temperature, top_p, rep_penalty;
+    int top_k;
+    uint64_t rng;
+    int32_t history_len, last;
+    int32_t fast_sums;                        // exact integer sums beyond 4096 kept entries (opt-in)
+    int32_t pad;
+    int32_t history[PK_HISTORY_CAP];
+};
+
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
@@ -126,6 +140,14 @@ struct pk_engine {
     int64_t g_cap = 0;
     int8_t *g_limbs = nullptr;
     int32_t *g_exps = nullptr, *g_pairs = nullptr, *g_tiles = nullptr;
+    // sampler (pk_sample.hip): device state, host mirror of its parameters,
+    // kept entries (value, index) for vocabularies up to samp_cap entries
+    pk_sampler_dev *samp = nullptr;
+    pk_sampler_dev samp_params{};             // temperature .. rng as last set from the host
+    bool samp_on = false;                     // the decode step samples instead of argmax
+    int samp_cap = 0;
+    float *samp_av = nullptr;
+    int32_t *samp_ai = nullptr;
 };
 
 int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes);
@@ -189,6 +211,12 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                       int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
                       const float *norm_w = nullptr);
 int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap);
+// sampler (pk_sample.hip): draw from logits[0..vocab) with the engine's
+// sampler state; st != nullptr also updates the decode state like the argmax
+int pk_sample_reserve(pk_engine *e, int vocab);
+int pk_launch_sample(pk_engine *e, float *logits, int vocab, pk_dstate *st, int32_t *out_toks, int out_cap);
+// prompt tokens into the repetition-penalty history (prefill_tokens, picchio.c:1960-1967)
+int pk_sample_seed_history(pk_engine *e, const int32_t *ids_dev, int n);
 // one forward_token step for (tok, pos), greedy id appended to out_toks
 int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap);
 // prefill_tokens (pk_prefill.hip): the prompt, next id into the decode state / out_toks

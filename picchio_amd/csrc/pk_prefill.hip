@@ -328,6 +328,8 @@ int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_bas
     PK_TRY(prefill_reserve(e, B));
     PK_TRY(batch_reserve(e, B));
     PK_HIP(hipMemcpyAsync(e->p_ids, ids, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
+    // a repetition penalty counts the prompt itself (picchio.c:1960-1967)
+    PK_TRY(pk_sample_seed_history(e, e->p_ids, n));
     for (int off = 0; off < n; off += B) {
         const int len = n - off < B ? n - off : B;
         PK_TRY(prefill_chunk(e, seq, e->p_ids + off, ids[off + len - 1], len, pos_base + off, out_toks, out_cap,
@@ -448,6 +450,8 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
     PK_CHECK(n_seq <= e->n_seq, PK_ERR_ARG, "%d sequences, %d reserved (pk_batch_reserve)", n_seq, e->n_seq);
     PK_CHECK(pos >= 0 && pos + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL, "positions exceed context");
     PK_CHECK(!e->capturing, PK_ERR_ARG, "decode_batch: not available while capturing");
+    PK_CHECK(!e->samp_on, PK_ERR_UNSUPPORTED,
+             "decode_batch: greedy only (one sampler state is one sequence's history and rng)");
     PK_TRY(pk_check_model(e));
     PK_TRY(pk_decode_reserve(e));
     const pk_cfg *c = &e->c;

@@ -85,6 +85,7 @@ class Oracle:
         self._sampler_init = _bind(L, "po_sampler_init", None, C.c_void_p, C.c_float, C.c_float, C.c_int,
                                    C.c_float, C.c_uint64)
         self._sample_logits = _bind(L, "po_sample_logits", C.c_int, C.c_void_p, f32p, C.c_int)
+        self._sample_logits_fx = _bind(L, "po_sample_logits_fx", C.c_int, C.c_void_p, f32p, C.c_int)
         self.rng_float = _bind(L, "po_rng_float", C.c_float, C.POINTER(C.c_uint64))
         self.act_limbs = _bind(L, "po_act_limbs", None, f32p, C.c_int, C.c_int, i8p, i32p)
         self.mfma_matvec = _bind(L, "po_mfma_matvec", None, u8p, f32p, _nd(np.float32), C.c_int, C.c_int,
@@ -136,6 +137,30 @@ class Oracle:
 
     def sample_logits(self, st, logits):
         return self._sample_logits(C.cast(st, C.c_void_p), logits, logits.size)
+
+    def sample_logits_fx(self, st, logits):
+        return self._sample_logits_fx(C.cast(st, C.c_void_p), logits, logits.size)
+
+    @staticmethod
+    def sampler_state(st):
+        """(rng, history) of a po_sampler buffer (rng at byte 16, history_len
+        at 24, history from 28)."""
+        raw = bytes(st)
+        rng = int.from_bytes(raw[16:24], "little")
+        n = int.from_bytes(raw[24:28], "little", signed=True)
+        return rng, np.frombuffer(raw[28:28 + 4 * n], np.int32).copy()
+
+    @staticmethod
+    def sampler_push_history(st, ids, vocab):
+        """Append ids to a po_sampler's history as prefill_tokens seeds it
+        (picchio.c:1960-1967): valid ids only, up to 4096 entries."""
+        n = int.from_bytes(bytes(st)[24:28], "little", signed=True)
+        hist = (C.c_int32 * 4096).from_buffer(st, 28)
+        for t in ids:
+            if n < 4096 and 0 <= int(t) < vocab:
+                hist[n] = int(t)
+                n += 1
+        C.c_int32.from_buffer(st, 24).value = n
 
     def tensor(self, model, kind, layer, n):
         p = self.model_tensor(model, kind, layer, None)
