@@ -167,6 +167,14 @@ def cpu_decode_baseline(cfg, seed, budget_s, prompt):
                       f"threads; model build {build_s:.0f} s"}
 
 
+def parse_sampling(spec):
+    """--sample T,top_p,top_k,rep (picchio's defaults: 1.0,0.95,50,1.1) or None."""
+    if not spec:
+        return None
+    t, p, k, r = spec.split(",")
+    return float(t), float(p), int(k), float(r)
+
+
 def run_decode(args):
     """GPT-OSS-20B-shaped model, 512-token prompt through
     prefill_tokens, then `steps` greedy decode steps replayed from the
@@ -182,11 +190,19 @@ def run_decode(args):
     print(f"[bench] 20B model built on the GPU: {eng.device_bytes() / 1e9:.2f} GB in "
           f"{time.perf_counter() - t0:.1f} s", file=sys.stderr, flush=True)
     prompt = np.random.default_rng(args.seed + 100).integers(0, cfg.vocab, n_prompt).astype(np.int32)
+    sampling = parse_sampling(args.sample)
+    if sampling:
+        eng.set_sampling(*sampling, args.seed)
     t0 = time.perf_counter()
     nxt = eng.prefill_tokens(prompt)
     prefill_s = time.perf_counter() - t0
     # warm-up: captures the step graph and runs `warmup` steps from the same state
+    # (the sampler restarts from the same seed before each run)
+    if sampling:
+        eng.set_sampling(*sampling, args.seed)
     warm = eng.decode_replay(nxt, n_prompt, max(args.warmup, 1))
+    if sampling:
+        eng.set_sampling(*sampling, args.seed)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(eng.stream)
@@ -214,8 +230,11 @@ def run_decode(args):
         "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic",
-        "config": {"workload": "config2: GPT-OSS-20B-shaped greedy decode, batch 1, 512-token "
-                               "random-id prompt then 256 steps, all experts HBM-resident",
+        "config": {"workload": "config2: GPT-OSS-20B-shaped " + ("sampled" if sampling else "greedy") +
+                               " decode, batch 1, 512-token random-id prompt then 256 steps, all "
+                               "experts HBM-resident",
+                   "sampling": ({"temperature": sampling[0], "top_p": sampling[1], "top_k": sampling[2],
+                                 "rep_penalty": sampling[3], "seed": args.seed} if sampling else "greedy"),
                    "layers": cfg.n_layers, "experts": cfg.n_experts, "vocab": cfg.vocab,
                    "lm_head": "fp32", "bytes_per_token": int(bpt),
                    "hbm_gbps": round(bpt * tok_s / 1e9, 1),
@@ -465,6 +484,9 @@ def main():
     ap.add_argument("--fused", type=int, default=0,
                     help="kernels mode: 1 = each MoE layer as one launch (router .. combine), "
                          "0 = three launches")
+    ap.add_argument("--sample", default="",
+                    help="decode mode: draw tokens on the device with T,top_p,top_k,rep "
+                         "(e.g. 1.0,0.95,50,1.1, picchio's defaults) instead of greedy")
     ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill", "decode120b"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
                          "down+combine) replayed from a HIP graph; seq: one block-ordered "

@@ -837,7 +837,8 @@ int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *o
     PK_HIP(hipGetLastError());
     if (e->samp_on) {
         // sample_logits on the logits (picchio.c:1750): the draw updates the decode state
-        PK_TRY(pk_launch_sample(e, lg, c->vocab, e->dstate, out_toks, out_cap));
+        PK_TRY(pk_launch_sample(e, lg, c->vocab, e->dstate, out_toks, out_cap, e->lm_bval, lm_blocks,
+                                logits_dev != nullptr));
     } else {
         hipLaunchKernelGGL(k_argmax_blocks, dim3(1), dim3(1024), 0, e->stream, e->lm_bval, e->lm_bidx, lm_blocks,
                            e->dstate, out_toks, out_cap);

@@ -214,7 +214,10 @@ int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *o
 // sampler (pk_sample.hip): draw from logits[0..vocab) with the engine's
 // sampler state; st != nullptr also updates the decode state like the argmax
 int pk_sample_reserve(pk_engine *e, int vocab);
-int pk_launch_sample(pk_engine *e, float *logits, int vocab, pk_dstate *st, int32_t *out_toks, int out_cap);
+// block_max[0..n_blocks): optional maxima of blocks of the logits before the
+// penalty; write_back = false when nobody reads the logits afterwards
+int pk_launch_sample(pk_engine *e, float *logits, int vocab, pk_dstate *st, int32_t *out_toks, int out_cap,
+                     const float *block_max, int n_blocks, bool write_back);
 // prompt tokens into the repetition-penalty history (prefill_tokens, picchio.c:1960-1967)
 int pk_sample_seed_history(pk_engine *e, const int32_t *ids_dev, int n);
 // one forward_token step for (tok, pos), greedy id appended to out_toks

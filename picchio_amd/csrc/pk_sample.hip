@@ -638,8 +638,13 @@ __device__ __forceinline__ int pick_exact_sums(const float *pv, int n, float r, 
     return *s_pick;
 }
 
+// bmax[0..nb): optional maxima of disjoint blocks of lg as the GEMV wrote it
+// (before the penalty, which only lowers values: an upper bound of the
+// maximum, which is all the top-k window needs). write_back = 0: nobody
+// reads lg afterwards, so a top-k draw leaves it as it is.
 __global__ __launch_bounds__(SNT) void k_sample(float *lg, int V, pk_sampler_dev *sp, float *av, int *ai,
-                                                pk_dstate *st, int32_t *out_toks, int out_cap) {
+                                                pk_dstate *st, int32_t *out_toks, int out_cap,
+                                                const float *bmax, int nb, int write_back) {
     // radix histograms (counts, exact sums) and the small path's sort share one block
     __shared__ __align__(16) uint64_t lds_raw[sizeof(lds_hist) / 8];
     // the small path's kept entries double as the staging buffer of the serial sums
@@ -659,7 +664,8 @@ __global__ __launch_bounds__(SNT) void k_sample(float *lg, int V, pk_sampler_dev
     int *ki = reinterpret_cast<int *>(stage + SMALL);
     __shared__ float cv[CAND];                          // top-k candidates (value, index)
     __shared__ int ci[CAND];
-    __shared__ int s_nc, s_cnt;
+    __shared__ int s_nc, s_cnt, s_win;
+    __shared__ uint64_t s_q2[NW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const float T = sp->temperature, top_p = sp->top_p, rep = sp->rep_penalty;
     const int K = sp->top_k;
@@ -741,44 +747,105 @@ __global__ __launch_bounds__(SNT) void k_sample(float *lg, int V, pk_sampler_dev
                 }
                 __syncthreads();
                 if (tid == 0) {
-                    uint32_t k = s_k, above = 0;
+                    uint32_t k = s_k;
                     int d = 255;
                     for (; d > 0; --d) {
                         if (k <= H.c[0][d]) break;
                         k -= H.c[0][d];
-                        above += H.c[0][d];
                     }
                     s_k = k;
                     s_prefix = s_prefix | ((uint32_t)d << shift);
                     s_mask = s_mask | (255u << shift);
-                    s_nc = (int)(above + H.c[0][d]);          // entries at or above the digit
+                    // entries at or above the new bucket: K - k above it, and the bucket
+                    s_nc = (int)((uint32_t)K - k + H.c[0][d]);
                     s_cnt = 0;
                 }
                 __syncthreads();
             };
-            for (int b = tid; b < NW * 256; b += SNT) (&H.c[0][0])[b] = 0;
-            __syncthreads();
-            seg_for(lg, V, [&](int, float v, bool ok) {
-                if (ok) atomicAdd(&H.c[wave][key_of(v * inv_t) >> 24], 1u);
-            });
-            radix_walk(24);
-            const int nc = s_nc;
-            const bool in_lds = nc <= CAND;
-            if (in_lds) {
-                const uint32_t top = s_prefix;
-                seg_for(lg, V, [&](int j, float v, bool ok) {
-                    const float x = v * inv_t;
-                    if (ok && key_of(x) >= top) {
-                        const int o = atomicAdd(&s_cnt, 1);   // below nc: counted in the first pass
-                        if (o < CAND) {
-                            cv[o] = x;
-                            ci[o] = j;
-                        }
-                    }
+            // First 8 bits. The K-th largest nearly always lies within a few
+            // binades of the maximum: the maximum key, then the counts of the 8
+            // sign/exponent buckets at and below it in 16-bit fields of two
+            // registers per lane (no atomics: a whole wave would hit the same
+            // few LDS counters). Otherwise a full histogram pass.
+            uint32_t mk = 0;
+            if (bmax) {
+                for (int b = tid; b < nb; b += SNT) mk = max(mk, key_of(bmax[b] * inv_t));
+            } else {
+                seg_for(lg, V, [&](int, float v, bool ok) {
+                    if (ok) mk = max(mk, key_of(v * inv_t));
                 });
-                __syncthreads();
             }
-            for (int shift = 16; shift >= 0; shift -= 8) {
+            for (int o = 32; o > 0; o >>= 1) mk = max(mk, (uint32_t)__shfl_xor((int)mk, o, 64));
+            if (lane == 0) s_w[wave] = (int)mk;
+            __syncthreads();
+            mk = 0;
+            for (int w = 0; w < NW; ++w) mk = max(mk, (uint32_t)s_w[w]);
+            const uint32_t tb = mk >> 24;
+            uint64_t lo = 0, hi = 0;
+            seg_for(lg, V, [&](int, float v, bool ok) {
+                const uint32_t d = tb - (key_of(v * inv_t) >> 24);
+                const uint64_t inc = (ok && d < 8u) ? (1ull << (16u * (d & 3u))) : 0ull;
+                lo += d < 4u ? inc : 0ull;
+                hi += d < 4u ? 0ull : inc;
+            });
+            lo = wave_sum_u64(lo);                        // per wave at most V/16 per field
+            hi = wave_sum_u64(hi);
+            if (lane == 0) { s_q[wave] = lo; s_q2[wave] = hi; }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t cum = 0, rank = 0;
+                int i = 0;
+                for (; i < 8; ++i) {
+                    uint32_t c = 0;
+                    for (int w = 0; w < NW; ++w)
+                        c += (uint32_t)(((i < 4 ? s_q[w] : s_q2[w]) >> (16 * (i & 3))) & 0xffffu);
+                    if (cum + c >= (uint32_t)K) {
+                        rank = (uint32_t)K - cum;         // the K-th largest's rank inside bucket i
+                        cum += c;
+                        break;
+                    }
+                    cum += c;
+                }
+                s_win = i < 8 && (int)tb - i >= 0;
+                if (s_win) {
+                    s_k = rank;
+                    s_prefix = (tb - (uint32_t)i) << 24;
+                    s_mask = 0xff000000u;
+                    s_nc = (int)cum;
+                    s_cnt = 0;
+                }
+            }
+            __syncthreads();
+            if (!s_win) {
+                for (int b = tid; b < NW * 256; b += SNT) (&H.c[0][0])[b] = 0;
+                __syncthreads();
+                seg_for(lg, V, [&](int, float v, bool ok) {
+                    if (ok) atomicAdd(&H.c[wave][key_of(v * inv_t) >> 24], 1u);
+                });
+                radix_walk(24);
+            }
+            // the remaining 24 bits; as soon as the entries at or above the
+            // current bucket fit in LDS they are gathered there and the rest runs on them
+            bool in_lds = false;
+            int nc = 0;
+            for (int shift = 16; shift >= -8; shift -= 8) {
+                if (!in_lds && s_nc <= CAND) {
+                    nc = s_nc;
+                    const uint32_t top = s_prefix;
+                    seg_for(lg, V, [&](int j, float v, bool ok) {
+                        const float x = v * inv_t;
+                        if (ok && key_of(x) >= top) {
+                            const int o = atomicAdd(&s_cnt, 1);   // below nc: counted by the passes
+                            if (o < CAND) {
+                                cv[o] = x;
+                                ci[o] = j;
+                            }
+                        }
+                    });
+                    in_lds = true;
+                    __syncthreads();
+                }
+                if (shift < 0) break;
                 for (int b = tid; b < NW * 256; b += SNT) (&H.c[0][0])[b] = 0;
                 __syncthreads();
                 const uint32_t prefix = s_prefix, mask = s_mask;
@@ -836,11 +903,12 @@ __global__ __launch_bounds__(SNT) void k_sample(float *lg, int V, pk_sampler_dev
             }
             __syncthreads();
             // the array as the reference leaves it: probabilities, 0 elsewhere
-            if (use_k) {
+            if (use_k && write_back) {
                 for (int i = tid; i < V; i += SNT) lg[i] = 0.0f;
                 __syncthreads();
             }
-            for (int j = tid; j < n; j += SNT) lg[ki[j]] = kv[j];
+            if (!use_k || write_back)
+                for (int j = tid; j < n; j += SNT) lg[ki[j]] = kv[j];
         } else {
             // 5b. over pv[0..n) in global memory (av after top-k, else lg in place)
             float *pv = use_k ? av : lg;
@@ -914,7 +982,7 @@ __global__ __launch_bounds__(SNT) void k_sample(float *lg, int V, pk_sampler_dev
             // a draw of 0 takes the first vocabulary entry even when it was dropped
             if (tid == 0) s_tok = r <= 0.0f ? 0 : (pick >= 0 ? (use_k ? ai[pick] : pick) : -1);
             __syncthreads();
-            if (use_k) {
+            if (use_k && write_back) {
                 for (int i = tid; i < V; i += SNT) lg[i] = 0.0f;
                 __syncthreads();
                 for (int j = tid; j < n; j += SNT) lg[ai[j]] = av[j];
@@ -977,11 +1045,12 @@ int pk_sample_reserve(pk_engine *e, int vocab) {
     return PK_OK;
 }
 
-int pk_launch_sample(pk_engine *e, float *logits, int vocab, pk_dstate *st, int32_t *out_toks, int out_cap) {
+int pk_launch_sample(pk_engine *e, float *logits, int vocab, pk_dstate *st, int32_t *out_toks, int out_cap,
+                     const float *block_max, int n_blocks, bool write_back) {
     PK_CHECK(e->samp && vocab >= 1 && vocab <= e->samp_cap, PK_ERR_ARG,
              "sampling: vocabulary %d, scratch for %d", vocab, e->samp_cap);
     hipLaunchKernelGGL(k_sample, dim3(1), dim3(SNT), 0, e->stream, logits, vocab, e->samp, e->samp_av,
-                       e->samp_ai, st, out_toks, out_cap);
+                       e->samp_ai, st, out_toks, out_cap, block_max, n_blocks, write_back ? 1 : 0);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }
@@ -1069,7 +1138,7 @@ extern "C" int pk_sample_logits(pk_engine *e, float *logits_dev, int vocab, int3
     PK_CHECK(vocab >= 1, PK_ERR_ARG, "vocab %d", vocab);
     PK_CHECK(!e->capturing, PK_ERR_ARG, "sample_logits: host result; not available while capturing");
     PK_TRY(pk_sample_reserve(e, vocab));
-    PK_TRY(pk_launch_sample(e, logits_dev, vocab, nullptr, nullptr, 0));
+    PK_TRY(pk_launch_sample(e, logits_dev, vocab, nullptr, nullptr, 0, nullptr, 0, true));
     int32_t last = 0;
     PK_HIP(hipMemcpyAsync(&last, (char *)e->samp + offsetof(pk_sampler_dev, last), 4, hipMemcpyDeviceToHost,
                           e->stream));
