@@ -191,6 +191,30 @@ int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_dev, int n,
 int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
                    const float *act_dev, float *eo_dev);
 
+/* ── integer-dot expert arithmetic (opt-in; no reference counterpart) ──
+ * The expert GEMVs on v_dot8 instead of picchio's fp32 FMA chains: each
+ * 32-value half-group of an input row becomes A = rint(x 2^(18-k)) (k the
+ * frexp exponent of its largest magnitude) in five balanced base-16 digits,
+ * a record of 24 ints; a group's sum over the stored nibbles is then exact
+ * in int32 and folded in fp32 as (16 s) 2^(k-22) C. Results are within
+ * ~5e-6 relative of picchio's (the north star's bar is 1e-4) instead of
+ * bit-identical; measured ~3.5 % faster per MoE token. */
+/* With on != 0 the three-launch MoE layer (pk_moe_forward, forward_token,
+ * generate) runs on it: the router writes the input's records, the gate_up
+ * launch its SwiGLU outputs' records for the down launch. Default off
+ * (also PK_I4_DOT=1 in the environment at engine creation). */
+int pk_set_i4_dot(pk_engine *e, int on);
+/* Records of x_dev[0..n) (n a multiple of 32) into rec_dev[n/32][24]. */
+int pk_act_records(pk_engine *e, const float *x_dev, int n, int32_t *rec_dev);
+/* pk_expert_gate_up / pk_expert_down on records: rec_dev = the input row's
+ * records (shared by the n experts); act_rec_dev (optional) receives the
+ * records of each expert's SwiGLU outputs, [n][moe_inter/64][24], which are
+ * pk_expert_down_dot's input. */
+int pk_expert_gate_up_dot(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                          const int32_t *rec_dev, float *act_dev, int32_t *act_rec_dev);
+int pk_expert_down_dot(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                       const int32_t *act_rec_dev, float *eo_dev);
+
 /* moe_forward (picchio.c:1309-1466): out_dev = Σ_k (w_k·routed_scale)·expert_k(x).
  * Optional host outputs: sel_host[topk], w_host[topk] (softmaxed weights) —
  * passing either forces a stream sync. */

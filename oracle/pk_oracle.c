@@ -1039,6 +1039,60 @@ int po_prefill_tokens(po_model *m, const int *ids, int n, int pos_base, int batc
 
 /* ═══════════════ the grouped int8 path's arithmetic (not a reference function) ═══════════════ */
 
+/* ── the library's opt-in integer-dot expert arithmetic, restated ──
+ * Not a reference function (pk_i4_device.h pk_write_digits / pk_dot_group). */
+void po_act_records(const float *x, int n, int32_t *rec) {
+    for (int h = 0; h < n / 32; h++) {
+        const float *v = x + 32 * h;
+        float m = 0.0f;
+        for (int c = 0; c < 32; c++) m = fmaxf(m, fabsf(v[c]));
+        int k = 0;
+        if (m > 0.0f) (void)frexpf(m, &k);
+        int32_t *r = rec + (int64_t)h * 24;
+        memset(r, 0, 24 * sizeof(int32_t));
+        for (int c = 0; c < 32; c++) {
+            int A = (int)rintf(ldexpf(v[c], 18 - k));
+            for (int i = 0; i < 5; i++) {
+                const int d = ((A + 8) & 15) - 8;
+                r[4 * i + c / 8] |= (int32_t)((uint32_t)(d & 15) << (4 * (c % 8)));
+                A = (A - d) >> 4;
+            }
+        }
+        r[20] = k;
+    }
+}
+
+void po_i4_dot_matvec(const uint8_t *q4, const float *s, const float *bias, int O, int I,
+                      const int32_t *rec, float *y) {
+    const int NG = I / 64;
+    for (int o = 0; o < O; o++) {
+        const uint8_t *qr = q4 + (int64_t)o * (I / 2);
+        float acc = 0.0f;
+        for (int g = 0; g < NG; g++) {
+            const float s16 = 16.0f * s[(int64_t)o * NG + g];
+            float t = 0.0f;
+            for (int h = 0; h < 2; h++) {
+                const int32_t *r = rec + (int64_t)(2 * g + h) * 24;
+                int P[5] = {0, 0, 0, 0, 0};
+                for (int c = 0; c < 32; c++) {
+                    const int col = 64 * g + 32 * h + c;
+                    const int q = (col & 1) ? (qr[col / 2] >> 4) : (qr[col / 2] & 15);
+                    for (int i = 0; i < 5; i++) {
+                        int d = (int)(((uint32_t)r[4 * i + c / 8] >> (4 * (c % 8))) & 15u);
+                        if (d >= 8) d -= 16;
+                        P[i] += (q - 8) * d;
+                    }
+                }
+                const int C = P[0] + 16 * (P[1] + 16 * (P[2] + 16 * (P[3] + 16 * P[4])));
+                const float S = ldexpf(s16, r[20] - 22);
+                t = h ? fmaf(S, (float)C, t) : S * (float)C;
+            }
+            acc = acc + t;
+        }
+        y[o] = bias ? acc + bias[o] : acc;
+    }
+}
+
 void po_act_limbs(const float *x, int rows, int cols, int8_t *limbs, int32_t *exps) {
     const int64_t plane = (int64_t)rows * cols;
     for (int r = 0; r < rows; r++) {

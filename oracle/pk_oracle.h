@@ -139,6 +139,19 @@ int po_sample_logits(po_sampler *s, float *logits, int vocab);
  * a time; up to 4096 kept entries it is po_sample_logits. */
 int po_sample_logits_fx(po_sampler *s, float *logits, int vocab);
 
+/* ── the opt-in integer-dot expert arithmetic, restated ──
+ * Not a reference function: the arithmetic of the library's v_dot8 GEMV.
+ * po_act_records: per 32 values (n % 32 == 0) a record of 24 ints: k = frexp
+ * exponent of the largest magnitude (0 if none), A = rint(x 2^(18-k)) as five
+ * balanced base-16 digits d_i in [-8, 7] (A = sum d_i 16^i), int 4i + w =
+ * digit i of columns 8w..8w+7 (nibble n = column 8w+n), int 20 = k.
+ * po_i4_dot_matvec: y[o] = sum over groups (in order) of
+ * t_g = S_g0 C_g0 then fma(S_g1, C_g1, t_g), acc = acc + t_g, + bias, with
+ * C = sum (q-8) A exact and S = (16 s) 2^(k-22). */
+void po_act_records(const float *x, int n, int32_t *rec);
+void po_i4_dot_matvec(const uint8_t *q4, const float *s, const float *bias, int O, int I,
+                      const int32_t *rec, float *y);
+
 /* ── the GPU's expert-grouped (int8 matrix core) path, restated ──
  * Not a reference function: the exact arithmetic the library's grouped
  * prefill uses, so its integer parts and fold order can be checked bit for

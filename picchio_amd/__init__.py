@@ -120,6 +120,10 @@ def lib():
         "pk_set_turn_sampling": (C.c_int, [vp, f32, f32, C.c_int]),
         "pk_reset_history": (C.c_int, [vp]),
         "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
+        "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
+        "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
+        "pk_expert_gate_up_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
+        "pk_expert_down_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
         "pk_sample_logits": (C.c_int, [vp, vp, C.c_int, C.POINTER(i32)]),
         "pk_sampler_state": (C.c_int, [vp, C.POINTER(C.c_uint64), vp, C.c_int, C.POINTER(C.c_int)]),
         "pk_quantize_int4_gs": (C.c_int, [vp, vp, C.c_int, C.c_int, C.c_int, vp, vp]),
@@ -272,6 +276,23 @@ class Engine:
         """A TURN's per-request temperature / top-p / top-k with the
         reference's clamp; rng and history carry on (picchio.c:2737-2743)."""
         check(self.L.pk_set_turn_sampling(self.h, temperature, top_p, top_k))
+
+    def set_i4_dot(self, on):
+        """The three-launch MoE layer on the integer-dot expert arithmetic
+        (default) or on picchio's fp32 chains, bit-identical (pk_set_i4_dot)."""
+        check(self.L.pk_set_i4_dot(self.h, 1 if on else 0))
+
+    def act_records(self, x_dev, rec_dev):
+        """Half-group records of the integer-dot arithmetic for a device row."""
+        check(self.L.pk_act_records(self.h, ptr(x_dev), x_dev.numel(), ptr(rec_dev)))
+
+    def expert_gate_up_dot(self, layer, eids_dev, rec_dev, act_dev, act_rec_dev=None):
+        check(self.L.pk_expert_gate_up_dot(self.h, layer, ptr(eids_dev), eids_dev.numel(), ptr(rec_dev),
+                                           ptr(act_dev), ptr(act_rec_dev) if act_rec_dev is not None else None))
+
+    def expert_down_dot(self, layer, eids_dev, act_rec_dev, eo_dev):
+        check(self.L.pk_expert_down_dot(self.h, layer, ptr(eids_dev), eids_dev.numel(), ptr(act_rec_dev),
+                                        ptr(eo_dev)))
 
     def set_sampling_fast_sums(self, on):
         """Exact integer sums instead of the reference's float order for

@@ -2,6 +2,7 @@
 // on-device synthetic weight generator.
 #include "pk_internal.h"
 #include "pk_dev.h"
+#include "pk_i4_device.h"
 #include "pk_synth.h"
 
 // ───────────────────────── wave reductions ─────────────────────────
@@ -443,12 +444,14 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
                                                      const float *__restrict__ b, int E, int D, int K,
                                                      float routed_scale, float *logits, int32_t *sel,
                                                      float *w_scaled, float *w_soft, uint32_t *counter,
-                                                     const float *__restrict__ nw, float eps, float *hn) {
+                                                     const float *__restrict__ nw, float eps, float *hn,
+                                                     int32_t *hq) {
     __shared__ float red[4];
     __shared__ double npart[4];
     __shared__ int last;
     const int e = blockIdx.x;
     float v;
+    float rn = 1.0f;
     if (nw) {
         const float4 *w4 = reinterpret_cast<const float4 *>(R + (int64_t)e * D);
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
@@ -471,9 +474,11 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
             xh[u] = pk_buf_load4(xr, off);
             xw[u] = pk_buf_load4(nr, off);
         }
-        const float rn = pk_rms_finish(hv, x, D, eps, npart);
-        const int span = (D + E - 1) / E;
-        for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
+        rn = pk_rms_finish(hv, x, D, eps, npart);
+        if (!hq) {
+            const int span = (D + E - 1) / E;
+            for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
+        }
         float acc = 0.0f;
         for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
             if (i0 != (int)threadIdx.x) {
@@ -505,6 +510,21 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
         v = (red[0] + red[1]) + (red[2] + red[3]);
     } else {
         v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
+    }
+    if (hq) {
+        // the experts' input (the normalised row, or x) as half-group records
+        // of the integer-dot arithmetic: one wave per 32 values, whole
+        // half-groups per workgroup (with the norm, hn is written here too)
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int nhg = (D + 31) >> 5, per = (nhg + E - 1) / E;
+        for (int hg = e * per + wv; hg < min(nhg, (e + 1) * per); hg += 4) {
+            const int i = hg * 32 + lane;
+            const bool has = lane < 32 && i < D;
+            const int ic = has ? i : 0;
+            const float xv = nw ? x[ic] * rn * nw[ic] : x[ic];
+            if (has && nw) hn[i] = xv;
+            pk_write_digits<1>(xv, has, hq + (int64_t)hg * PK_XQ_INTS);
+        }
     }
     // without a counter the block only publishes its logit: the expert
     // kernels that follow run the top-k themselves (pk_route_args)
@@ -562,14 +582,14 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D, int K,
                           float routed_scale, float *logits, int32_t *sel, float *w_scaled,
                           float *w_soft, uint32_t *counter, hipStream_t st, const float *nw, float eps,
-                          float *hn) {
+                          float *hn, int32_t *hq) {
     PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
              "router: E=%d K=%d outside 1..128 / 1..16", E, K);
     PK_CHECK(((uintptr_t)R & 15) == 0 && ((uintptr_t)x & 15) == 0 && (D & 3) == 0, PK_ERR_UNSUPPORTED,
              "router: needs 16-byte aligned rows");
     PK_CHECK(!nw || (hn && ((uintptr_t)nw & 15) == 0), PK_ERR_ARG, "router: fused norm needs hn");
     hipLaunchKernelGGL(k_router_topk, dim3(E), dim3(256), 0, st, x, R, b, E, D, K, routed_scale, logits,
-                       sel, w_scaled, w_soft, counter, nw, eps, hn);
+                       sel, w_scaled, w_soft, counter, nw, eps, hn, hq);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

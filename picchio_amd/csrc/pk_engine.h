@@ -82,6 +82,11 @@ struct pk_engine {
     float *attn_part = nullptr;               // split-K attention partials
     int32_t *argmax_out = nullptr;
     uint32_t *counters = nullptr;
+    // integer-dot expert arithmetic of the three-launch MoE layer (opt-in:
+    // PK_I4_DOT=1 or pk_set_i4_dot; default picchio's fp32 chains, bit-identical)
+    bool i4_dot = false;
+    int32_t *hn_q = nullptr;                  // the layer input's half-group records
+    int32_t *act_q = nullptr;                 // [topk] SwiGLU outputs' records
 
     bool capturing = false;                  // inside pk_capture_begin/end
 

@@ -150,7 +150,7 @@ static void engine_free(pk_engine *e) {
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out,
-                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai};
+                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -208,6 +208,9 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->eo, (int64_t)K * D * 4);
     ALLOC(e->argmax_out, 64);
     ALLOC(e->counters, PK_CTR_N * 4);
+    ALLOC(e->hn_q, (int64_t)((D + 31) / 32) * PK_XQ_INTS * 4);
+    ALLOC(e->act_q, (int64_t)K * e->ex.gu.RB * PK_XQ_INTS * 4);
+    if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     ALLOC(e->fused_ctl, PK_FUSED_CTL_BYTES);
     ALLOC(e->fused_xn, (int64_t)e->n_cu * 2 * pk_fused_row(c) * 4);   // two private rows per workgroup
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
@@ -712,15 +715,23 @@ int pk_check_layer_experts(pk_engine *e, int layer) {
 // (weights comb->w) into comb->out (+ residual).
 // With route, the gate_up launch selects the experts from the router logits
 // and writes sel_dev (and the routing weights) for the down launch.
+// dot: the integer-dot arithmetic, inputs from e->hn_q (one row shared by
+// the items), the SwiGLU outputs' records through e->act_q.
 static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, const float *x,
                        int64_t x_stride, float *act, float *eo, const pk_combine_args *comb,
-                       const pk_route_args *route = nullptr) {
+                       const pk_route_args *route = nullptr, bool dot = false) {
     const pk_cfg *c = &e->c;
     pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = route ? nullptr : sel_dev;
     gu.x = x; gu.x_stride = x_stride;
     gu.y = act; gu.y_stride = c->moe_inter / 2;
     gu.n_items = n;
+    if (dot) {
+        gu.xq = e->hn_q;
+        gu.xq_stride = 0;
+        gu.yq = e->act_q;
+        gu.yq_stride = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    }
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
     PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
                              nullptr, e->stream, route));
@@ -730,6 +741,10 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     dn.x = act; dn.x_stride = c->moe_inter / 2;
     dn.y = eo; dn.y_stride = c->hidden;
     dn.n_items = n;
+    if (dot) {
+        dn.xq = e->act_q;
+        dn.xq_stride = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    }
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
     PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, comb ? PK_EPI_COMBINE : PK_EPI_PLAIN, 0.f, 0.f, comb,
                              e->stream));
@@ -751,9 +766,13 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     // the router launch writes the logits only; the gate_up launch selects
     // the experts from them and publishes the routing (sel, weights)
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
+    // integer-dot arithmetic: the router also writes the input's records, the
+    // gate_up epilogue those of its SwiGLU outputs for the down launch
+    const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
-                                 nullptr, e->stream, norm_w, c->eps, norm_w ? e->hn : nullptr));
+                                 nullptr, e->stream, norm_w, c->eps, norm_w ? e->hn : nullptr,
+                                 dot ? e->hn_q : nullptr));
     PK_TRY(pk_prof_end(e, ps));
     pk_route_args rt{};
     rt.logits = e->r_logits;
@@ -769,7 +788,19 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     cb.out = residual ? res_out : out_dev;
     cb.residual = residual;
     cb.counters = e->counters + PK_CTR_COMBINE;
-    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb, &rt));
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb, &rt,
+                       dot));
+    return PK_OK;
+}
+
+extern "C" int pk_set_i4_dot(pk_engine *e, int on) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_i4_dot: not available while capturing");
+    if (e->i4_dot != (on != 0) && e->step_exec) {      // the captured step holds the other kernels
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+    }
+    e->i4_dot = on != 0;
     return PK_OK;
 }
 
@@ -830,6 +861,44 @@ extern "C" int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_de
     PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha,
                              nullptr, e->stream));
     return pk_prof_end(e, ps);
+}
+
+extern "C" int pk_act_records(pk_engine *e, const float *x_dev, int n, int32_t *rec_dev) {
+    PK_CHECK(e && x_dev && rec_dev, PK_ERR_ARG, "null argument");
+    return pk_launch_act_records(x_dev, n, rec_dev, e->stream);
+}
+
+extern "C" int pk_expert_gate_up_dot(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                                     const int32_t *rec_dev, float *act_dev, int32_t *act_rec_dev) {
+    PK_CHECK(e && rec_dev, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(c->hidden % 64 == 0 && c->moe_inter % 128 == 0, PK_ERR_UNSUPPORTED,
+             "integer-dot experts need hidden %% 64 == 0 and moe_inter %% 128 == 0");
+    PK_TRY(check_expert_batch(e, layer, eids_dev, n, rec_dev, act_dev));
+    pk_i4_items gu = pk_expert_items(e, layer, false);
+    gu.slots = eids_dev;
+    gu.x = nullptr; gu.x_stride = 0;
+    gu.xq = rec_dev; gu.xq_stride = 0;
+    gu.y = act_dev; gu.y_stride = c->moe_inter / 2;
+    gu.yq = act_rec_dev; gu.yq_stride = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    gu.n_items = n;
+    return pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, nullptr, e->stream);
+}
+
+extern "C" int pk_expert_down_dot(pk_engine *e, int layer, const int32_t *eids_dev, int n,
+                                  const int32_t *act_rec_dev, float *eo_dev) {
+    PK_CHECK(e && act_rec_dev, PK_ERR_ARG, "null argument");
+    const pk_cfg *c = &e->c;
+    PK_CHECK(c->hidden % 64 == 0 && c->moe_inter % 128 == 0, PK_ERR_UNSUPPORTED,
+             "integer-dot experts need hidden %% 64 == 0 and moe_inter %% 128 == 0");
+    PK_TRY(check_expert_batch(e, layer, eids_dev, n, act_rec_dev, eo_dev));
+    pk_i4_items dn = pk_expert_items(e, layer, true);
+    dn.slots = eids_dev;
+    dn.x = nullptr; dn.x_stride = 0;
+    dn.xq = act_rec_dev; dn.xq_stride = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    dn.y = eo_dev; dn.y_stride = c->hidden;
+    dn.n_items = n;
+    return pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream);
 }
 
 extern "C" int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,

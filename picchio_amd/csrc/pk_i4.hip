@@ -21,7 +21,9 @@
 // grid = (RB, n_items); block = NW waves. Wave w handles groups w, w+NW, ...
 // (GPW groups per pass, loads issued before the math); partial sums and
 // scales meet in LDS; wave 0 folds the groups of its 64 rows in order.
-template <int NW, int GPW, int EPI>
+// DOT: the integer-dot arithmetic (pk_dot_group) on the input records it.xq;
+// each (row, group) value then goes to LDS and wave 0 adds them in group order.
+template <int NW, int GPW, int EPI, bool DOT>
 __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int NG,
                                                      float lim, float alpha, pk_combine_args cb,
                                                      pk_route_args rt) {
@@ -48,6 +50,7 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
                          (int64_t)rb * NG * (PK_TILE_BYTES / 16);
     const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
     const float *__restrict__ x = it.x + (int64_t)(item / it.x_div) * it.x_stride;
+    const int32_t *__restrict__ xq = DOT ? it.xq + (int64_t)(item / it.x_div) * it.xq_stride : nullptr;
 
     for (int g0 = wave; g0 < NG; g0 += NW * GPW) {
         uint4 wa[GPW], wb[GPW];
@@ -65,8 +68,13 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
         for (int u = 0; u < GPW; ++u) {
             const int g = g0 + u * NW;
             if (g < NG) {
-                part[g * 64 + lane] = pk_group_dot(wa[u], wb[u], x + g * 64);
-                scl[g * 64 + lane] = s[u];
+                if constexpr (DOT) {
+                    part[g * 64 + lane] = pk_dot_group(wa[u], wb[u], xq + 2 * g * PK_XQ_INTS,
+                                                       xq + (2 * g + 1) * PK_XQ_INTS, s[u]);
+                } else {
+                    part[g * 64 + lane] = pk_group_dot(wa[u], wb[u], x + g * 64);
+                    scl[g * 64 + lane] = s[u];
+                }
             }
         }
     }
@@ -74,14 +82,22 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     if (wave != 0) return;
 
     float acc = 0.0f;
-    for (int g = 0; g < NG; ++g) acc = __builtin_fmaf(part[g * 64 + lane], scl[g * 64 + lane], acc);
+    if constexpr (DOT) {
+        for (int g = 0; g < NG; ++g) acc = acc + part[g * 64 + lane];
+    } else {
+        for (int g = 0; g < NG; ++g) acc = __builtin_fmaf(part[g * 64 + lane], scl[g * 64 + lane], acc);
+    }
     const int row = rb * 64 + lane;
     if (it.off_bias >= 0 && row < O)
         acc = acc + reinterpret_cast<const float *>(base + it.off_bias)[row];
     float *y = it.y + (int64_t)item * it.y_stride;
     if constexpr (EPI == PK_EPI_SWIGLU) {
         const float up = __shfl_down(acc, 1, 64);
-        if ((lane & 1) == 0 && row + 1 < O) y[row >> 1] = pk_swiglu(acc, up, lim, alpha);
+        const bool has = (lane & 1) == 0 && row + 1 < O;
+        const float a = pk_swiglu(acc, up, lim, alpha);
+        if (has) y[row >> 1] = a;
+        // the 32 outputs of this row block are one half-group of the next input
+        if (it.yq) pk_write_digits<2>(a, has, it.yq + (int64_t)item * it.yq_stride + rb * PK_XQ_INTS);
     } else if constexpr (EPI == PK_EPI_COMBINE) {
         // moe_forward's accumulation (picchio.c:1387, :1445-1454) fused: each
         // item's rows go out device-coherently; the last item to finish this
@@ -116,6 +132,21 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
         if (rt.logits && rb == 0 && item == 0) pk_wave_route_publish(rt);
 }
 
+// Half-group records of x[0..n) (n a multiple of 32): one wave per record.
+__global__ __launch_bounds__(64) void k_act_records(const float *x, int n, int32_t *rec) {
+    const int lane = threadIdx.x;
+    const int i = blockIdx.x * 32 + lane;
+    const bool has = lane < 32 && i < n;
+    pk_write_digits<1>(x[has ? i : 0], has, rec + (int64_t)blockIdx.x * PK_XQ_INTS);
+}
+
+int pk_launch_act_records(const float *x, int n, int32_t *rec, hipStream_t st) {
+    PK_CHECK(n > 0 && n % 32 == 0, PK_ERR_ARG, "act records: n=%d is not a multiple of 32", n);
+    hipLaunchKernelGGL(k_act_records, dim3(n / 32), dim3(64), 0, st, x, n, rec);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
                       float lim, float alpha, const pk_combine_args *comb, hipStream_t st,
                       const pk_route_args *route) {
@@ -134,19 +165,23 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
     }
     PK_CHECK(sh.NG > 0 && sh.RB > 0 && it.n_items > 0, PK_ERR_ARG, "i4 gemv: empty shape");
     PK_CHECK(sh.NG <= 128, PK_ERR_UNSUPPORTED, "i4 gemv: I=%d above 8192", sh.I);
+    PK_CHECK(!it.yq || epilogue == PK_EPI_SWIGLU, PK_ERR_ARG, "i4 gemv: output records need the SwiGLU epilogue");
     const dim3 grid(sh.RB, it.n_items);
     const size_t lds = (size_t)sh.NG * 64 * 2 * sizeof(float);
     // 15 waves x 3 groups covers the 45 groups of a 2880-wide row in one pass.
     constexpr int NW = 15, GPW = 3;
-    if (epilogue == PK_EPI_SWIGLU)
-        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_SWIGLU>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb, rt);
-    else if (epilogue == PK_EPI_COMBINE)
-        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_COMBINE>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb, rt);
-    else
-        hipLaunchKernelGGL((k_i4_gemv<NW, GPW, PK_EPI_PLAIN>), grid, dim3(NW * 64), lds, st,
-                           it, sh.O, sh.NG, lim, alpha, cb, rt);
+#define PK_I4_LAUNCH(E, D)                                                                      \
+    hipLaunchKernelGGL((k_i4_gemv<NW, GPW, E, D>), grid, dim3(NW * 64), lds, st, it, sh.O, sh.NG, \
+                       lim, alpha, cb, rt)
+    const bool dot = it.xq != nullptr;
+    if (epilogue == PK_EPI_SWIGLU) {
+        if (dot) PK_I4_LAUNCH(PK_EPI_SWIGLU, true); else PK_I4_LAUNCH(PK_EPI_SWIGLU, false);
+    } else if (epilogue == PK_EPI_COMBINE) {
+        if (dot) PK_I4_LAUNCH(PK_EPI_COMBINE, true); else PK_I4_LAUNCH(PK_EPI_COMBINE, false);
+    } else {
+        if (dot) PK_I4_LAUNCH(PK_EPI_PLAIN, true); else PK_I4_LAUNCH(PK_EPI_PLAIN, false);
+    }
+#undef PK_I4_LAUNCH
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

@@ -161,3 +161,75 @@ __device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
             rt.w_scaled[k] = p * rt.routed_scale;
         }
 }
+
+// ─────────────── integer-dot arithmetic (opt-in to bit-exactness) ───────────────
+// Not picchio's arithmetic: the expert GEMV on v_dot8c_i32_i4. An input row
+// is cut into half-groups of 32 values; each has an exponent k (frexp of its
+// largest magnitude, 0 if all are zero) and the integers A = rint(x 2^(18-k))
+// (|A| <= 2^18) written as five balanced base-16 digits, A = sum_i d_i 16^i,
+// d_i in [-8, 7] (which reach -559240 .. 489335: 2^19 would not fit). Record of a half-group (PK_XQ_INTS ints): dword 4i + w
+// holds digit i of columns 8w .. 8w+7 (nibble n = column 8w+n), int 20 = k
+// (PK_XQ_INTS ints with padding).
+// The store holds each weight nibble as q ^ 8, the signed 4-bit q - 8
+// (k_i4_repack), so per half-group and digit four v_dot8 give
+// sum (q-8) d_i exactly, and
+// C = sum_i 16^i P_i = sum (q-8) A exactly (|C| <= 2^26). The row's value is
+// then sum over groups g and halves h of (16 s_g) 2^(k_h - 22) C_gh, folded
+// in fp32 in a fixed order (pk_dot_group).
+// 32 values of a half-group: lane src(c) holds column c's value v (has: the
+// lane holds one). Writes the record to dst (lanes 0..20 store).
+template <int LS>
+__device__ __forceinline__ void pk_write_digits(float v, bool has, int32_t *dst) {
+    const int lane = threadIdx.x & 63;
+    // the largest magnitude (non-negative floats order as their bits)
+    const float m = __uint_as_float(pk_wave_max_u32(__float_as_uint(has ? fabsf(v) : 0.0f)));
+    int k = 0;
+    if (m > 0.0f) (void)frexpf(m, &k);
+    int A = has ? (int)rintf(ldexpf(v, 18 - k)) : 0;
+    // five balanced digits of A, packed one per nibble
+    uint32_t dig = 0;
+#pragma unroll
+    for (int i = 0; i < 5; ++i) {
+        const int d = ((A + 8) & 15) - 8;
+        dig |= (uint32_t)(d & 15) << (4 * i);
+        A = (A - d) >> 4;
+    }
+    // lane 4i + w gathers digit i of columns 8w .. 8w+7
+    const int i = lane >> 2, w = lane & 3;
+    uint32_t word = 0;
+#pragma unroll
+    for (int n = 0; n < 8; ++n) {
+        const uint32_t src = (uint32_t)__shfl((int)dig, (8 * w + n) * LS, 64);
+        word |= ((src >> (4 * (i < 5 ? i : 0))) & 15u) << (4 * n);
+    }
+    if (lane < 20) dst[lane] = (int32_t)word;
+    if (lane == 20) dst[20] = k;
+    if (lane > 20 && lane < PK_XQ_INTS) dst[lane] = 0;   // padding
+}
+
+// One 64-column group of one row on the integer dot: wa / wb = the stored
+// nibbles (q ^ 8) of columns 0..31 / 32..63, x0 / x1 = the two half-group records
+// (wave-uniform), s16 = the stored scale (16 s). Returns the group's value.
+__device__ __forceinline__ float pk_dot_group(uint4 wa, uint4 wb, const int32_t *x0, const int32_t *x1,
+                                              float s16) {
+    float t = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const uint4 w = h ? wb : wa;
+        const int32_t *xq = h ? x1 : x0;
+        const int w0 = (int)w.x, w1 = (int)w.y, w2 = (int)w.z, w3 = (int)w.w;
+        int P[5];
+#pragma unroll
+        for (int i = 0; i < 5; ++i) {
+            int p = __builtin_amdgcn_sdot8(w0, xq[4 * i + 0], 0, false);
+            p = __builtin_amdgcn_sdot8(w1, xq[4 * i + 1], p, false);
+            p = __builtin_amdgcn_sdot8(w2, xq[4 * i + 2], p, false);
+            p = __builtin_amdgcn_sdot8(w3, xq[4 * i + 3], p, false);
+            P[i] = p;
+        }
+        const int C = P[0] + 16 * (P[1] + 16 * (P[2] + 16 * (P[3] + 16 * P[4])));
+        const float S = ldexpf(s16, xq[20] - 22);
+        t = h ? __builtin_fmaf(S, (float)C, t) : S * (float)C;
+    }
+    return t;
+}

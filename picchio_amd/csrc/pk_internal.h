@@ -112,7 +112,19 @@ struct pk_i4_items {
     float *y;                  // output of item i at y + i * y_stride
     int64_t y_stride;
     int n_items;
+    // integer-dot arithmetic (pk_dot_group): input half-group records of item i
+    // at xq + (i / x_div) * xq_stride (ints); with xq set the launch runs on them
+    const int32_t *xq = nullptr;
+    int64_t xq_stride = 0;
+    // SwiGLU epilogue: also the output's records, item i at yq + i * yq_stride
+    // (one per 64-row block)
+    int32_t *yq = nullptr;
+    int64_t yq_stride = 0;
 };
+
+// ints per half-group record of the integer-dot expert arithmetic
+// (pk_i4_device.h: five digit planes of 4 dwords, the exponent, padding)
+constexpr int PK_XQ_INTS = 24;
 
 enum pk_i4_epilogue { PK_EPI_PLAIN = 0, PK_EPI_SWIGLU = 1, PK_EPI_COMBINE = 2 };
 
@@ -141,6 +153,9 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
                       const pk_combine_args *comb, hipStream_t st,
                       const pk_route_args *route = nullptr);
 
+// Half-group records (integer-dot arithmetic) of x[0..n), n % 32 == 0.
+int pk_launch_act_records(const float *x, int n, int32_t *rec, hipStream_t st);
+
 // Reference-layout INT4 gs GEMV, any I / group size (exact quant.h order).
 int pk_launch_i4_gemv_ref(float *y, const float *x, const uint8_t *q4, const float *s,
                           int S, int I, int O, int gs, hipStream_t st);
@@ -168,7 +183,7 @@ int pk_launch_router_topk(const float *x, const float *R, const float *b, int E,
                           int K, float routed_scale, float *logits, int32_t *sel,
                           float *w_scaled, float *w_soft, uint32_t *counter,
                           hipStream_t st, const float *nw = nullptr, float eps = 0.f,
-                          float *hn = nullptr);
+                          float *hn = nullptr, int32_t *hq = nullptr);
 // y = W . rmsnorm(h; nw, eps) + bias for one row (rmsnorm fused into the GEMV).
 int pk_launch_gemv_f32_norm(float *y, const float *h, const float *nw, float eps, const float *W,
                             const float *bias, int I, int O, hipStream_t st);

@@ -86,6 +86,9 @@ class Oracle:
                                    C.c_float, C.c_uint64)
         self._sample_logits = _bind(L, "po_sample_logits", C.c_int, C.c_void_p, f32p, C.c_int)
         self._sample_logits_fx = _bind(L, "po_sample_logits_fx", C.c_int, C.c_void_p, f32p, C.c_int)
+        self.act_records = _bind(L, "po_act_records", None, f32p, C.c_int, i32p)
+        self.i4_dot_matvec = _bind(L, "po_i4_dot_matvec", None, u8p, f32p, C.c_void_p, C.c_int, C.c_int,
+                                   i32p, f32p)
         self.rng_float = _bind(L, "po_rng_float", C.c_float, C.POINTER(C.c_uint64))
         self.act_limbs = _bind(L, "po_act_limbs", None, f32p, C.c_int, C.c_int, i8p, i32p)
         self.mfma_matvec = _bind(L, "po_mfma_matvec", None, u8p, f32p, _nd(np.float32), C.c_int, C.c_int,
