@@ -133,6 +133,7 @@ struct pk_engine {
     int64_t batch_cap = 0;
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
     int32_t *b_sel = nullptr, *b_perm = nullptr;
+    int32_t *b_xq = nullptr, *b_actq = nullptr;   // integer-dot records (rows, pairs' SwiGLU outputs)
     // prompt-chunk scratch for up to p_cap positions (pk_prefill.hip)
     int p_cap = 0;
     float *p_H = nullptr, *p_XN = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_part = nullptr;

@@ -150,7 +150,7 @@ static void engine_free(pk_engine *e) {
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out,
-                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q};
+                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {

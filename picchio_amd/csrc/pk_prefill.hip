@@ -91,10 +91,10 @@ static int batch_reserve(pk_engine *e, int T) {
     PK_CHECK((int64_t)T * c->topk <= 65535, PK_ERR_UNSUPPORTED, "batched MoE: %d tokens x top-%d", T,
              c->topk);
     PK_HIP(hipStreamSynchronize(e->stream));
-    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm};
+    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm, e->b_xq, e->b_actq};
     for (void *p : ptrs) pk_dev_free(e, p);
     e->b_logits = e->b_w = e->b_act = e->b_eo = nullptr;
-    e->b_sel = e->b_perm = nullptr;
+    e->b_sel = e->b_perm = e->b_xq = e->b_actq = nullptr;
     e->batch_cap = 0;
     const int64_t TK = (int64_t)T * c->topk;
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_logits, (int64_t)T * c->n_experts * 4));
@@ -103,6 +103,9 @@ static int batch_reserve(pk_engine *e, int T) {
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_perm, TK * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_act, TK * (c->moe_inter / 2) * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_eo, TK * c->hidden * 4));
+    // integer-dot records: the token rows', each pair's SwiGLU outputs'
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_xq, (int64_t)T * ((c->hidden + 31) / 32) * PK_XQ_INTS * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_actq, TK * e->ex.gu.RB * PK_XQ_INTS * 4));
     e->batch_cap = T;
     return PK_OK;
 }
@@ -124,11 +127,19 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
         PK_HIP(hipGetLastError());
     }
+    // the integer-dot option: records of the token rows, then of each pair's SwiGLU outputs
+    const bool dot = e->i4_dot && D % 64 == 0 && c->moe_inter % 128 == 0;
+    const int64_t xq_row = (int64_t)(D / 32) * PK_XQ_INTS, aq_row = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    if (dot) PK_TRY(pk_launch_act_records(x, T * D, e->b_xq, e->stream));
     pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = e->b_sel;
     gu.x = x; gu.x_stride = D; gu.x_div = K;
     gu.y = e->b_act; gu.y_stride = half;
     gu.n_items = T * K;
+    if (dot) {
+        gu.xq = e->b_xq; gu.xq_stride = xq_row;
+        gu.yq = e->b_actq; gu.yq_stride = aq_row;
+    }
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
     PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, nullptr,
                              e->stream));
@@ -138,6 +149,9 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     dn.x = e->b_act; dn.x_stride = half;
     dn.y = e->b_eo; dn.y_stride = D;
     dn.n_items = T * K;
+    if (dot) {
+        dn.xq = e->b_actq; dn.xq_stride = aq_row;
+    }
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
     PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));

@@ -109,3 +109,32 @@ def test_moe_layer_and_decode_within_bars(dot_setup, oracle):
     got = [int(v) for v in eng.generate(prompt, n)]
     eng.set_i4_dot(False)
     assert got == stream
+
+
+def test_batched_decode_on_integer_dot(gpu, oracle, monkeypatch):
+    """decode_batch (the per-pair expert GEMV of several sequences, with the
+    prompts' prefill chunks) on the integer-dot arithmetic: each sequence's
+    stream is the oracle's prefill_tokens + forward_token stream."""
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=8, ctx_len=128, vocab=1000)
+    model = oracle.model_build(cfg, 1235, 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg)
+        eng.set_i4_dot(True)
+        monkeypatch.setenv("PREFILL_BATCH", "64")
+        eng.batch_reserve(3)
+        rng = np.random.default_rng(78)
+        prompts = [rng.integers(0, cfg.vocab, 40).astype(np.int32) for _ in range(3)]
+        first = [eng.prefill_seq(s, prompts[s]) for s in range(3)]
+        got = eng.decode_batch(first, 40, 10)
+        for s in range(3):
+            oracle.model_reset_kv(model)
+            ref = [oracle.prefill_tokens(model, prompts[s], 40, 0, 64)]
+            for i in range(10):
+                ref.append(oracle.forward_token(model, ref[-1], 40 + i, None))
+            assert ref[0] == first[s]
+            assert list(got[:, s]) == ref[1:], s
+    finally:
+        eng.close()
+        oracle.model_free(model)
