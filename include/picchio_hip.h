@@ -191,7 +191,8 @@ int pk_expert_gate_up(pk_engine *e, int layer, const int32_t *eids_dev, int n,
 int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
                    const float *act_dev, float *eo_dev);
 
-/* ── integer-dot expert arithmetic (opt-in; no reference counterpart) ──
+/* ── integer-dot expert arithmetic (no reference counterpart; opt-in for one
+ *    sequence, the default of pk_decode_batch) ──
  * The expert GEMVs on v_dot8 instead of picchio's fp32 FMA chains: each
  * 32-value half-group of an input row becomes A = rint(x 2^(18-k)) (k the
  * frexp exponent of its largest magnitude) in five balanced base-16 digits,
@@ -226,7 +227,11 @@ int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,
  * n_seq sequences in lockstep (BASELINE config 4's batch-32 decode), each
  * sequence with its own KV cache, every weight read once per step for all
  * of them. Per sequence the result is forward_token's within the fp32 bar
- * (fp32 dot products in a different order; MoE GEMVs bit-identical). */
+ * (fp32 dot products in a different order; the MoE on the integer-dot
+ * arithmetic above, the (token, expert) pairs grouped by expert so that each
+ * expert block is read once per 4 pairs: within ~5e-6 of picchio's
+ * arithmetic. PK_I4_DOT_BATCH=0 at engine creation: picchio's fp32 chains,
+ * one launch item per pair, bit-identical GEMVs). */
 
 /* KV caches for n_seq sequences (sequence 0 is the one pk_forward_token,
  * pk_prefill_tokens and pk_generate use). Growing the count clears every

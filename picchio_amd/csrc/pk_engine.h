@@ -85,6 +85,7 @@ struct pk_engine {
     // integer-dot expert arithmetic of the three-launch MoE layer (opt-in:
     // PK_I4_DOT=1 or pk_set_i4_dot; default picchio's fp32 chains, bit-identical)
     bool i4_dot = false;
+    bool i4_dot_batch = true;                 // pk_decode_batch's MoE on it (PK_I4_DOT_BATCH=0: not)
     int32_t *hn_q = nullptr;                  // the layer input's half-group records
     int32_t *act_q = nullptr;                 // [topk] SwiGLU outputs' records
 
@@ -134,6 +135,8 @@ struct pk_engine {
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
     int32_t *b_sel = nullptr, *b_perm = nullptr;
     int32_t *b_xq = nullptr, *b_actq = nullptr;   // integer-dot records (rows, pairs' SwiGLU outputs)
+    int32_t *b_pairs = nullptr, *b_tiles = nullptr;  // pairs grouped by expert (tiles of 4)
+    bool dot_tiles_off = false;                   // PK_DOT_TILES=0: one launch item per pair
     // prompt-chunk scratch for up to p_cap positions (pk_prefill.hip)
     int p_cap = 0;
     float *p_H = nullptr, *p_XN = nullptr, *p_qkv = nullptr, *p_att = nullptr, *p_part = nullptr;
@@ -202,8 +205,10 @@ struct pk_mfma_args {
 };
 int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, int8_t *limbs, int64_t plane,
                         int32_t *exps, int permuted, hipStream_t st);
+// tile_pairs: pairs per tile (0: the MFMA GEMM's 32)
 int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int32_t *tile_exp,
-                          int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st);
+                          int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
+                          int tile_pairs = 0);
 int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
 
 // decode driver pieces (pk_decode.hip) reused by the prompt driver

@@ -150,7 +150,7 @@ static void engine_free(pk_engine *e) {
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
                     e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out,
-                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq};
+                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -211,6 +211,8 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->hn_q, (int64_t)((D + 31) / 32) * PK_XQ_INTS * 4);
     ALLOC(e->act_q, (int64_t)K * e->ex.gu.RB * PK_XQ_INTS * 4);
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
+    if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
+    if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
     ALLOC(e->fused_ctl, PK_FUSED_CTL_BYTES);
     ALLOC(e->fused_xn, (int64_t)e->n_cu * 2 * pk_fused_row(c) * 4);   // two private rows per workgroup
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));

@@ -132,6 +132,97 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
         if (rt.logits && rb == 0 && item == 0) pk_wave_route_publish(rt);
 }
 
+// ─────────────── integer-dot GEMV over expert-grouped pairs ───────────────
+// grid = (RB, max_tiles); workgroup (rb, t) covers tile t's pairs (one expert,
+// at most DT_M pairs): each wave loads its 3 groups of the expert's 64-row
+// block once and runs the integer dot for every pair of the tile (inputs:
+// the pair's records, it.xq + (pair / x_div) * xq_stride); wave j then adds
+// pair j's groups in order and writes its rows (pair-indexed outputs, as the
+// per-pair launch writes them: the same values).
+constexpr int DT_M = 4;
+
+template <int EPI>
+__global__ __launch_bounds__(15 * 64) void k_i4_dot_tiles(pk_i4_items it, pk_i4_tiles tl, int O, int NG,
+                                                          float lim, float alpha) {
+    extern __shared__ float lds[];            // part[DT_M][NG][64]
+    constexpr int NW = 15, GPW = 3;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int rb = blockIdx.x, t = blockIdx.y;
+    if (t >= *tl.n_tiles) return;
+    const int beg = tl.tile_beg[t], cnt = tl.tile_cnt[t];
+    const int slot = it.slot_base + tl.tile_exp[t];
+    const uint8_t *base = it.base + (int64_t)slot * it.slot_stride;
+    const uint4 *tiles = reinterpret_cast<const uint4 *>(base + it.off_tiles) +
+                         (int64_t)rb * NG * (PK_TILE_BYTES / 16);
+    const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
+    const int32_t *xr[DT_M];
+#pragma unroll
+    for (int j = 0; j < DT_M; ++j)
+        xr[j] = it.xq + (int64_t)(tl.pairs[beg + min(j, cnt - 1)] / it.x_div) * it.xq_stride;
+
+    for (int g0 = wave; g0 < NG; g0 += NW * GPW) {
+        uint4 wa[GPW], wb[GPW];
+        float s[GPW];
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = g0 + u * NW;
+            if (g < NG) {
+                wa[u] = pk_load_nt(&tiles[g * 128 + lane]);
+                wb[u] = pk_load_nt(&tiles[g * 128 + 64 + lane]);
+                s[u] = sc[g * 64 + lane];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = g0 + u * NW;
+            if (g < NG) {
+#pragma unroll
+                for (int j = 0; j < DT_M; ++j)
+                    if (j < cnt)
+                        lds[((int64_t)j * NG + g) * 64 + lane] =
+                            pk_dot_group(wa[u], wb[u], xr[j] + 2 * g * PK_XQ_INTS,
+                                         xr[j] + (2 * g + 1) * PK_XQ_INTS, s[u]);
+            }
+        }
+    }
+    __syncthreads();
+    if (wave >= cnt) return;
+    const int pair = tl.pairs[beg + wave];
+    float acc = 0.0f;
+    for (int g = 0; g < NG; ++g) acc = acc + lds[((int64_t)wave * NG + g) * 64 + lane];
+    const int row = rb * 64 + lane;
+    if (it.off_bias >= 0 && row < O) acc = acc + reinterpret_cast<const float *>(base + it.off_bias)[row];
+    float *y = it.y + (int64_t)pair * it.y_stride;
+    if constexpr (EPI == PK_EPI_SWIGLU) {
+        const float up = __shfl_down(acc, 1, 64);
+        const bool has = (lane & 1) == 0 && row + 1 < O;
+        const float a = pk_swiglu(acc, up, lim, alpha);
+        if (has) y[row >> 1] = a;
+        if (it.yq) pk_write_digits<2>(a, has, it.yq + (int64_t)pair * it.yq_stride + rb * PK_XQ_INTS);
+    } else {
+        if (row < O) y[row] = acc;
+    }
+}
+
+int pk_launch_i4_dot_tiles(const pk_i4_items &it, const pk_i4_tiles &tl, const pk_i4_shape &sh, int epilogue,
+                           float lim, float alpha, int max_tiles, hipStream_t st) {
+    PK_CHECK(it.xq && tl.pairs && tl.tile_exp && tl.tile_beg && tl.tile_cnt && tl.n_tiles, PK_ERR_ARG,
+             "dot tiles: missing buffers");
+    PK_CHECK(epilogue != PK_EPI_COMBINE && max_tiles > 0 && sh.NG * DT_M * 64 * 4 <= 65536, PK_ERR_UNSUPPORTED,
+             "dot tiles: epilogue %d, %d tiles, %d groups", epilogue, max_tiles, sh.NG);
+    const dim3 grid(sh.RB, max_tiles);
+    const size_t lds = (size_t)DT_M * sh.NG * 64 * sizeof(float);
+    if (epilogue == PK_EPI_SWIGLU)
+        hipLaunchKernelGGL(k_i4_dot_tiles<PK_EPI_SWIGLU>, grid, dim3(15 * 64), lds, st, it, tl, sh.O, sh.NG,
+                           lim, alpha);
+    else
+        hipLaunchKernelGGL(k_i4_dot_tiles<PK_EPI_PLAIN>, grid, dim3(15 * 64), lds, st, it, tl, sh.O, sh.NG,
+                           lim, alpha);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 // Half-group records of x[0..n) (n a multiple of 32): one wave per record.
 __global__ __launch_bounds__(64) void k_act_records(const float *x, int n, int32_t *rec) {
     const int lane = threadIdx.x;

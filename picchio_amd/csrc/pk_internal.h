@@ -153,6 +153,16 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
                       const pk_combine_args *comb, hipStream_t st,
                       const pk_route_args *route = nullptr);
 
+// Pairs grouped by expert into tiles (k_group_pairs): tile t = expert
+// tile_exp[t], pairs[tile_beg[t] .. + tile_cnt[t]]; *n_tiles tiles (device).
+struct pk_i4_tiles {
+    const int32_t *pairs, *tile_exp, *tile_beg, *tile_cnt, *n_tiles;
+};
+// Integer-dot GEMV of every pair of every tile (at most 4 pairs per tile),
+// each expert block loaded once per tile; outputs pair-indexed.
+int pk_launch_i4_dot_tiles(const pk_i4_items &it, const pk_i4_tiles &tl, const pk_i4_shape &sh, int epilogue,
+                           float lim, float alpha, int max_tiles, hipStream_t st);
+
 // Half-group records (integer-dot arithmetic) of x[0..n), n % 32 == 0.
 int pk_launch_act_records(const float *x, int n, int32_t *rec, hipStream_t st);
 

@@ -77,7 +77,7 @@ constexpr int GP_LDS = 16384;
 __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict__ sel, int P, int E,
                                                       int32_t *__restrict__ pairs, int32_t *__restrict__ tile_exp,
                                                       int32_t *__restrict__ tile_beg,
-                                                      int32_t *__restrict__ tile_cnt, int32_t *n_tiles) {
+                                                      int32_t *__restrict__ tile_cnt, int32_t *n_tiles, int tt) {
     __shared__ int cnt[128], off[129];
     __shared__ int s_sel[GP_LDS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -96,10 +96,10 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
         for (int e = 0; e < E; ++e) off[e + 1] = off[e] + cnt[e];
         int j = 0;
         for (int e = 0; e < E; ++e)
-            for (int b = 0; b < cnt[e]; b += TT) {
+            for (int b = 0; b < cnt[e]; b += tt) {
                 tile_exp[j] = e;
                 tile_beg[j] = off[e] + b;
-                tile_cnt[j] = min(TT, cnt[e] - b);
+                tile_cnt[j] = min(tt, cnt[e] - b);
                 ++j;
             }
         *n_tiles = j;
@@ -310,10 +310,11 @@ int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, in
 }
 
 int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int32_t *tile_exp,
-                          int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st) {
+                          int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
+                          int tile_pairs) {
     PK_CHECK(P > 0 && E > 0 && E <= 128, PK_ERR_ARG, "group pairs: P=%d E=%d", P, E);
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, st, sel, P, E, pairs, tile_exp, tile_beg,
-                       tile_cnt, n_tiles);
+                       tile_cnt, n_tiles, tile_pairs > 0 ? tile_pairs : TT);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

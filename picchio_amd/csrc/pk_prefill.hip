@@ -91,10 +91,11 @@ static int batch_reserve(pk_engine *e, int T) {
     PK_CHECK((int64_t)T * c->topk <= 65535, PK_ERR_UNSUPPORTED, "batched MoE: %d tokens x top-%d", T,
              c->topk);
     PK_HIP(hipStreamSynchronize(e->stream));
-    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm, e->b_xq, e->b_actq};
+    void *ptrs[] = {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm, e->b_xq, e->b_actq,
+                    e->b_pairs, e->b_tiles};
     for (void *p : ptrs) pk_dev_free(e, p);
     e->b_logits = e->b_w = e->b_act = e->b_eo = nullptr;
-    e->b_sel = e->b_perm = e->b_xq = e->b_actq = nullptr;
+    e->b_sel = e->b_perm = e->b_xq = e->b_actq = e->b_pairs = e->b_tiles = nullptr;
     e->batch_cap = 0;
     const int64_t TK = (int64_t)T * c->topk;
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_logits, (int64_t)T * c->n_experts * 4));
@@ -106,6 +107,9 @@ static int batch_reserve(pk_engine *e, int T) {
     // integer-dot records: the token rows', each pair's SwiGLU outputs'
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_xq, (int64_t)T * ((c->hidden + 31) / 32) * PK_XQ_INTS * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_actq, TK * e->ex.gu.RB * PK_XQ_INTS * 4));
+    // pairs grouped by expert for the tiled integer-dot launches (tiles of 4)
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_pairs, TK * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->b_tiles, (3 * (TK / 4 + 1 + c->n_experts) + 1) * 4));
     e->batch_cap = T;
     return PK_OK;
 }
@@ -128,7 +132,8 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
         PK_HIP(hipGetLastError());
     }
     // the integer-dot option: records of the token rows, then of each pair's SwiGLU outputs
-    const bool dot = e->i4_dot && D % 64 == 0 && c->moe_inter % 128 == 0;
+    // (the lockstep decode of several sequences, decode_order, uses it by default)
+    const bool dot = (e->i4_dot || (decode_order && e->i4_dot_batch)) && D % 64 == 0 && c->moe_inter % 128 == 0;
     const int64_t xq_row = (int64_t)(D / 32) * PK_XQ_INTS, aq_row = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
     if (dot) PK_TRY(pk_launch_act_records(x, T * D, e->b_xq, e->stream));
     pk_i4_items gu = pk_expert_items(e, layer, false);
@@ -140,9 +145,21 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
         gu.xq = e->b_xq; gu.xq_stride = xq_row;
         gu.yq = e->b_actq; gu.yq_stride = aq_row;
     }
+    // with the integer dot, pairs of one expert share each weight load (tiles of 4)
+    const int P = T * K;
+    const int mt = P / 4 + 1 + E;
+    pk_i4_tiles tl{e->b_pairs, e->b_tiles, e->b_tiles + mt, e->b_tiles + 2 * mt, e->b_tiles + 3 * mt};
+    const bool tiled = dot && !e->dot_tiles_off;
+    if (tiled)
+        PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->b_pairs, e->b_tiles, e->b_tiles + mt,
+                                     e->b_tiles + 2 * mt, e->b_tiles + 3 * mt, e->stream, 4));
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
-    PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, nullptr,
-                             e->stream));
+    if (tiled)
+        PK_TRY(pk_launch_i4_dot_tiles(gu, tl, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, mt,
+                                      e->stream));
+    else
+        PK_TRY(pk_launch_i4_gemv(gu, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, nullptr,
+                                 e->stream));
     PK_TRY(pk_prof_end(e, ps));
     pk_i4_items dn = pk_expert_items(e, layer, true);
     dn.slots = e->b_sel;
@@ -153,7 +170,10 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
         dn.xq = e->b_actq; dn.xq_stride = aq_row;
     }
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
-    PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
+    if (tiled)
+        PK_TRY(pk_launch_i4_dot_tiles(dn, tl, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, mt, e->stream));
+    else
+        PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
                        e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);

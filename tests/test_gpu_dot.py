@@ -138,3 +138,32 @@ def test_batched_decode_on_integer_dot(gpu, oracle, monkeypatch):
     finally:
         eng.close()
         oracle.model_free(model)
+
+
+def test_expert_tiles_match_per_pair_launches(gpu, oracle, monkeypatch):
+    """The batched MoE on the integer dot with pairs grouped by expert (each
+    expert block loaded once per tile of up to 4 pairs) gives the per-pair
+    launches' values bit for bit: 48 tokens over 8 experts, so most experts
+    carry several tiles."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=8, ctx_len=16, vocab=64)
+    model = oracle.model_build(cfg, 99, 0)
+    outs = []
+    try:
+        for tiles in ("1", "0"):
+            monkeypatch.setenv("PK_DOT_TILES", tiles)
+            eng = pa.Engine(cfg)
+            try:
+                upload_model(eng, oracle, model, cfg, globals_=False)
+                eng.set_i4_dot(True)
+                T = 48
+                x = np.random.default_rng(5).standard_normal((T, cfg.hidden)).astype(np.float32)
+                out = eng.empty((T, cfg.hidden), torch.float32)
+                eng.moe_forward_batch(0, eng.to_dev(x), out)
+                outs.append(eng.to_host(out))
+            finally:
+                eng.close()
+    finally:
+        oracle.model_free(model)
+    assert bits_equal(outs[0], outs[1]), first_mismatch(outs[0].ravel(), outs[1].ravel())
