@@ -91,20 +91,29 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        off[0] = 0;
-        for (int e = 0; e < E; ++e) off[e + 1] = off[e] + cnt[e];
-        int j = 0;
-        for (int e = 0; e < E; ++e)
-            for (int b = 0; b < cnt[e]; b += tt) {
-                tile_exp[j] = e;
-                tile_beg[j] = off[e] + b;
-                tile_cnt[j] = min(tt, cnt[e] - b);
-                ++j;
-            }
-        *n_tiles = j;
+    // offsets of the experts' pairs and of their tiles: one wave scans the
+    // counts (lane l holds experts l and l + 64), then every expert writes its tiles
+    __shared__ int toff[128];
+    if (wave == 0) {
+        const int c0 = lane < E ? cnt[lane] : 0, c1 = lane + 64 < E ? cnt[lane + 64] : 0;
+        int p0 = c0, p1 = c1, q0 = (c0 + tt - 1) / tt, q1 = (c1 + tt - 1) / tt;
+        for (int d = 1; d < 64; d <<= 1) {
+            const int a = __shfl_up(p0, d, 64), b = __shfl_up(p1, d, 64);
+            const int u = __shfl_up(q0, d, 64), v = __shfl_up(q1, d, 64);
+            if (lane >= d) { p0 += a; p1 += b; q0 += u; q1 += v; }
+        }
+        const int pt = __shfl(p0, 63, 64), qt = __shfl(q0, 63, 64);   // first half's totals
+        if (lane < E) { off[lane] = p0 - c0; toff[lane] = q0 - (c0 + tt - 1) / tt; }
+        if (lane + 64 < E) { off[lane + 64] = pt + p1 - c1; toff[lane + 64] = qt + q1 - (c1 + tt - 1) / tt; }
+        if (lane == 63) { off[E] = pt + p1; *n_tiles = qt + q1; }
     }
     __syncthreads();
+    for (int e = threadIdx.x; e < E; e += blockDim.x)
+        for (int b = 0, j = toff[e]; b < cnt[e]; b += tt, ++j) {
+            tile_exp[j] = e;
+            tile_beg[j] = off[e] + b;
+            tile_cnt[j] = min(tt, cnt[e] - b);
+        }
     for (int e = wave; e < E; e += nw) {
         int run = off[e];
         for (int b = 0; b < P; b += 64) {
