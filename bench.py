@@ -35,10 +35,10 @@ ROUTER_BYTES = E * D * 4 + E * 4
 TOKEN_BYTES = K * EXPERT_BYTES + ROUTER_BYTES + 2 * D * 4      # 56,517,248
 
 # HBM bytes per 4-expert gate_up launch measured by rocprofv3 --pmc (profiles/
-# k_i4_gemv_gate_up_moe_config1.txt): FETCH_SIZE 18419.82 KiB x 2.000 +
+# k_i4_gemv_gate_up_moe_config1.txt): FETCH_SIZE 18425.54 KiB x 2.000 +
 # WRITE_SIZE 45.04 KiB x 1.000, the factors being what the two counters read
 # for a plain copy kernel over 1 GiB.
-GATE_UP_TRAFFIC = 37768853
+GATE_UP_TRAFFIC = 37780589
 
 
 def gate_up_bytes(n):
