@@ -149,7 +149,8 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     const int P = T * K;
     const int mt = P / 4 + 1 + E;
     pk_i4_tiles tl{e->b_pairs, e->b_tiles, e->b_tiles + mt, e->b_tiles + 2 * mt, e->b_tiles + 3 * mt};
-    const bool tiled = dot && !e->dot_tiles_off;
+    // (the tile kernel keeps 4 pairs' group sums in LDS: rows of at most 64 groups)
+    const bool tiled = dot && !e->dot_tiles_off && e->ex.gu.NG <= 64 && e->ex.dn.NG <= 64 && E <= 128;
     if (tiled)
         PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->b_pairs, e->b_tiles, e->b_tiles + mt,
                                      e->b_tiles + 2 * mt, e->b_tiles + 3 * mt, e->stream, 4));
