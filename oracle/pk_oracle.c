@@ -477,6 +477,13 @@ void po_model_reset_kv(po_model *m) {
     }
 }
 
+void po_model_fill_kv(po_model *m, int layer, int n_pos, uint64_t sk, uint64_t sv) {
+    if (layer < 0 || layer >= m->c.n_layers || n_pos < 0 || n_pos > m->c.ctx_len) return;
+    int64_t n = (int64_t)n_pos * m->c.n_kv_heads * m->c.head_dim;
+    pk_fill_normal(m->L[layer].K, n, sk, 1.0f, 0);
+    pk_fill_normal(m->L[layer].V, n, sv, 1.0f, 0);
+}
+
 int po_model_expert(po_model *m, int layer, int eid,
                     const uint8_t **gu_q4, const float **gu_s,
                     const uint8_t **d_q4, const float **d_s,

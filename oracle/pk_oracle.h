@@ -79,6 +79,9 @@ typedef struct po_model po_model;
 po_model *po_model_build(const pk_cfg *cfg, uint64_t seed, int n_threads);
 void po_model_free(po_model *m);
 void po_model_reset_kv(po_model *m);
+/* Positions 0..n_pos-1 of layer's K and V caches drawn N(0,1) from the raw
+ * stream seeds sk and sv (a synthetic prefilled context; test support). */
+void po_model_fill_kv(po_model *m, int layer, int n_pos, uint64_t sk, uint64_t sv);
 
 /* Raw views of one expert (reference layout) for tests. */
 int po_model_expert(po_model *m, int layer, int eid,

@@ -68,6 +68,7 @@ class Oracle:
         self.model_build = _bind(L, "po_model_build", vp, C.POINTER(PkCfg), C.c_uint64, C.c_int)
         self.model_free = _bind(L, "po_model_free", None, vp)
         self.model_reset_kv = _bind(L, "po_model_reset_kv", None, vp)
+        self.model_fill_kv = _bind(L, "po_model_fill_kv", None, vp, C.c_int, C.c_int, C.c_uint64, C.c_uint64)
         self.model_tensor = _bind(L, "po_model_tensor", vp, vp, C.c_int, C.c_int, C.POINTER(vp))
         self._model_expert = _bind(L, "po_model_expert", C.c_int, vp, C.c_int, C.c_int,
                                    *([C.POINTER(vp)] * 6))

@@ -54,6 +54,39 @@ def test_gqa_attention_parity(dec_setup, oracle):
     assert worst < 1e-5, worst
 
 
+def test_gqa_attention_long_context(gpu, oracle):
+    """Windows of 16, 17, 32 and 33 chunks of 128 positions (the full layer)
+    and 1-2 chunks (the sliding layer) over a 4100-position synthetic
+    context that the engine (pk_kv_fill_synthetic) and the oracle fill from
+    the same generator streams: the chunk partials and their combine by the
+    last-arriving block against gqa_attention's single pass."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=4, ctx_len=4224, vocab=2000)
+    model = oracle.model_build(cfg, 556, 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg)
+        n_ctx, seed, M = 4100, 17, (1 << 64) - 1
+        eng.kv_fill_synthetic(0, n_ctx, seed)
+        for layer in (0, 1):
+            s = (seed * 0x9E3779B97F4A7C15 + layer * 2) & M
+            oracle.model_fill_kv(model, layer, n_ctx, s, (s + 1) & M)
+        D = cfg.hidden
+        od = eng.empty(D, torch.float32)
+        for i, pos in enumerate((2047, 2048, 4095, 4099)):
+            for layer in (0, 1):
+                x = _x(oracle, cfg, 700 + 2 * i + layer)
+                ref = np.empty(D, np.float32)
+                oracle.gqa_attention(model, layer, x, pos, ref)
+                eng.gqa_attention(layer, eng.to_dev(x), pos, od)
+                err = rel_l2(eng.to_host(od), ref)
+                assert err < 1e-5, (pos, layer, err)
+    finally:
+        eng.close()
+        oracle.model_free(model)
+
+
 def test_forward_token_parity(dec_setup, oracle):
     import torch
     cfg, model, eng = dec_setup
