@@ -345,7 +345,10 @@ int pk_generate(pk_engine *e, const int32_t *prompt_host, int n_prompt,
                 int n_steps, int32_t *out_host);
 
 /* n_steps greedy decode steps from (tok, pos) over the existing KV cache,
- * replaying the captured step (for timing); out_host[n_steps] token ids. */
+ * replaying the captured step (for timing); out_host[n_steps] token ids.
+ * The captured step's attention covers positions below a power of two of at
+ * least 1024; a call that goes past it captures the step again (once per
+ * doubling). */
 int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int32_t *out_host);
 
 /* ── sampling (sample_logits, picchio.c:1509-1649) on the device ──

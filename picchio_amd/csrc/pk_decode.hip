@@ -760,7 +760,8 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     }
     const int sliding = c->layer_type[l] == 0;
     const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
-    int chunks = st ? max_chunks : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
+    int chunks = st ? (e->att_pos_cap >= 0 ? e->att_pos_cap / ATT_CHUNK + 1 : max_chunks)
+                    : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
     if (sliding) chunks = std::min(chunks, (c->sliding_window + ATT_CHUNK - 1) / ATT_CHUNK);
     chunks = std::min(chunks, max_chunks);
     const int G = H / KVH;
@@ -796,6 +797,14 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     }
     return pk_prof_end(e, ps);
 }
+
+// Sets the decode attention's position bound for one scope.
+struct att_cap_scope {
+    pk_engine *e;
+    int old;
+    att_cap_scope(pk_engine *eng, int cap) : e(eng), old(eng->att_pos_cap) { e->att_pos_cap = cap; }
+    ~att_cap_scope() { e->att_pos_cap = old; }
+};
 
 // Decode attention of layer l on the residual row h (in_ln rmsnorm fused
 // into the QKV GEMV); adds the output projection into h.
@@ -870,6 +879,7 @@ extern "C" int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int
     PK_TRY(pk_set_state(e, 0, pos));
     PK_HIP(hipMemcpyAsync(e->hn, x_dev, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
     PK_HIP(hipMemsetAsync(e->h, 0, (size_t)c->hidden * 4, e->stream));
+    att_cap_scope cap(e, pos);
     PK_TRY(pk_attention_rows(e, layer, e->dstate, 0, 0, 0, 0, 1, e->hn, e->qkv, e->attn_part, e->att,
                              e->h));                // h = 0 + attn(x)
     PK_HIP(hipMemcpyAsync(out_dev, e->h, (size_t)c->hidden * 4, hipMemcpyDeviceToDevice, e->stream));
@@ -885,6 +895,7 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
     PK_TRY(pk_check_model(e));
     PK_TRY(pk_decode_reserve(e));
     PK_TRY(pk_set_state(e, tok, pos));
+    att_cap_scope cap(e, pos);
     PK_TRY(decode_step(e, logits_dev, nullptr, 0));
     if (next_host) {
         pk_dstate s{};
@@ -897,6 +908,7 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
 
 int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_cap) {
     PK_TRY(pk_set_state(e, tok, pos));
+    att_cap_scope cap(e, e->capturing ? e->att_pos_cap : pos);
     return decode_step(e, nullptr, out_toks, out_cap);
 }
 
@@ -923,7 +935,11 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
                 rc = PK_ERR_HIP; break;
             }
             e->capturing = true;
-            rc = decode_step(e, nullptr, out_dev, n_steps);
+            {
+                // the replays reach positions n_prompt .. n_prompt + n_steps - 2
+                att_cap_scope cap(e, n_prompt + n_steps - 1);
+                rc = decode_step(e, nullptr, out_dev, n_steps);
+            }
             e->capturing = false;
             hipError_t hr = hipStreamEndCapture(e->stream, &graph);
             if (rc != PK_OK) break;
@@ -953,20 +969,38 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
     PK_CHECK(pos + n_steps <= e->c.ctx_len, PK_ERR_CONTEXT_FULL, "positions exceed context");
     PK_TRY(pk_check_model(e));
     PK_TRY(pk_decode_reserve(e));
+    // The graph's attention grids cover positions 0..step_cap: captured
+    // again, with the bound doubled, when a call goes past it
+    const int need = pos + n_steps - 1;
+    if (e->step_exec && need > e->step_cap) {
+        PK_HIP(hipStreamSynchronize(e->stream));
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+    }
     if (!e->step_exec) {
-        int32_t *od = nullptr;
-        PK_TRY(pk_dev_alloc(e, (void **)&od, (int64_t)e->c.ctx_len * 4));
-        e->step_out = od;
+        if (!e->step_out) {
+            int32_t *od = nullptr;
+            PK_TRY(pk_dev_alloc(e, (void **)&od, (int64_t)e->c.ctx_len * 4));
+            e->step_out = od;
+        }
+        int64_t bound = 1024;
+        while (bound <= need) bound *= 2;
+        const int cap = (int)std::min<int64_t>(bound, e->c.ctx_len) - 1;
         hipGraph_t g = nullptr;
         PK_HIP(hipStreamBeginCapture(e->stream, hipStreamCaptureModeThreadLocal));
         e->capturing = true;
-        int rc = decode_step(e, nullptr, e->step_out, e->c.ctx_len);
+        int rc;
+        {
+            att_cap_scope scope(e, cap);
+            rc = decode_step(e, nullptr, e->step_out, e->c.ctx_len);
+        }
         e->capturing = false;
         hipError_t hr = hipStreamEndCapture(e->stream, &g);
         PK_TRY(rc);
         PK_HIP(hr);
         PK_HIP(hipGraphInstantiate(&e->step_exec, g, nullptr, nullptr, 0));
         (void)hipGraphDestroy(g);
+        e->step_cap = cap;
     }
     PK_TRY(pk_set_state(e, tok, pos));
     for (int i = 0; i < n_steps; ++i) PK_HIP(hipGraphLaunch(e->step_exec, e->stream));

@@ -98,6 +98,11 @@ struct pk_engine {
     float *lm_bval = nullptr;                 // lm_head block maxima
     int32_t *lm_bidx = nullptr;
     hipGraphExec_t step_exec = nullptr;       // captured decode step (pk_decode_replay)
+    int step_cap = -1;                        // att_pos_cap the step graph was captured with
+    // Decode attention from the device state: the grid covers positions
+    // 0..att_pos_cap (-1: the whole context), set by the callers that know
+    // the highest position a launch or a replayed graph will reach
+    int att_pos_cap = -1;
     int32_t *step_out = nullptr;
 
     // opt-in per-kernel timing (pk_engine_profile)

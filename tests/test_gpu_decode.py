@@ -87,6 +87,30 @@ def test_gqa_attention_long_context(gpu, oracle):
         oracle.model_free(model)
 
 
+def test_replay_graph_recaptured_past_its_position_bound(gpu):
+    """The replayed step graph's attention grids cover positions up to a
+    bound (1024 positions, doubled as needed); a replay that goes past it
+    captures the step again. Tokens across the 1024 boundary equal the
+    eager forward_token chain's over the same synthetic context."""
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=4, ctx_len=2100, vocab=2000)
+    eng = pa.Engine(cfg)
+    try:
+        eng.build_synthetic(5, what=7)
+        eng.kv_fill_synthetic(0, 1000, 9)
+        a = eng.decode_replay(7, 990, 8)                 # positions 990..997: bound 1023
+        b = eng.decode_replay(int(a[-1]), 998, 40)       # to 1037: captured again (2047)
+        c = eng.decode_replay(int(b[-1]), 1038, 10)      # within the bound
+        eng.kv_fill_synthetic(0, 1000, 9)
+        ref, tok = [], 7
+        for pos in range(990, 1048):
+            tok = eng.forward_token(tok, pos)
+            ref.append(tok)
+        assert list(a) + list(b) + list(c) == ref
+    finally:
+        eng.close()
+
+
 def test_forward_token_parity(dec_setup, oracle):
     import torch
     cfg, model, eng = dec_setup
