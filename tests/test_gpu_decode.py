@@ -281,6 +281,39 @@ def test_batched_sequences_match_separate_streams(gpu, oracle, monkeypatch):
         oracle.model_free(model)
 
 
+def test_batched_sequences_over_long_contexts(gpu, oracle):
+    """Three sequences, each with its own 1100-position synthetic context
+    (pk_kv_fill_synthetic; the oracle's caches filled from the same
+    generator streams), decoded in lockstep: every row's attention spans 9
+    chunks of 128 positions on the full layer. Each stream equals the
+    oracle's forward_token stream over that sequence's context."""
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=2, n_experts=8, ctx_len=1200, vocab=1000)
+    model = oracle.model_build(cfg, 4321, 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg)
+        n_ctx, steps, seed, M = 1100, 8, 23, (1 << 64) - 1
+        eng.batch_reserve(3)
+        for s in range(3):
+            eng.kv_fill_synthetic(s, n_ctx, seed)
+        first = [5, 17, 99]
+        got = eng.decode_batch(first, n_ctx, steps)
+        for s in range(3):
+            oracle.model_reset_kv(model)
+            for layer in range(cfg.n_layers):
+                sk = (seed * 0x9E3779B97F4A7C15 + (s * 1024 + layer) * 2) & M
+                oracle.model_fill_kv(model, layer, n_ctx, sk, (sk + 1) & M)
+            ref, tok = [], first[s]
+            for i in range(steps):
+                tok = oracle.forward_token(model, tok, n_ctx + i, None)
+                ref.append(tok)
+            assert list(got[:, s]) == ref, s
+    finally:
+        eng.close()
+        oracle.model_free(model)
+
+
 def test_batched_decode_on_matrix_cores(gpu, oracle, monkeypatch):
     """With PK_BATCH_MFMA_MIN=16, decode_batch of 16 sequences runs the MoE
     as the expert-grouped int8 MFMA GEMM (exact activation limbs, sums in
