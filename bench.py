@@ -481,16 +481,12 @@ def main():
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="after the timed region, run a plain read+write kernel over this many "
                          "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--fused", type=int, default=0,
-                    help="kernels mode: 1 = each MoE layer as one launch (router .. combine), "
-                         "0 = three launches")
     ap.add_argument("--sample", default="",
                     help="decode mode: draw tokens on the device with T,top_p,top_k,rep "
                          "(e.g. 1.0,0.95,50,1.1, picchio's defaults) instead of greedy")
-    ap.add_argument("--mode", choices=["seq", "kernels", "decode", "prefill", "decode120b"], default="kernels",
+    ap.add_argument("--mode", choices=["kernels", "decode", "prefill", "decode120b"], default="kernels",
                     help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
-                         "down+combine) replayed from a HIP graph; seq: one block-ordered "
-                         "kernel per sequence of steps; decode: config 2, the whole 20B-shaped "
+                         "down+combine) replayed from a HIP graph; decode: config 2, the whole 20B-shaped "
                          "model (use --steps 256); prefill: config 3, grouped MFMA MoE (--steps 20); "
                          "decode120b: config 4, 120B shape at batch 1 and 32 (--steps 128)")
     args = ap.parse_args()
@@ -530,43 +526,7 @@ def main():
     ev1 = torch.cuda.Event(enable_timing=True)
     W, S = args.warmup, args.steps
 
-    if args.mode == "seq":
-        # one persistent launch per sequence; chained steps = batch-1 decode
-        eng.moe_seq_reserve(max(W, S))
-        eng.moe_forward_seq(ld[:W], xd[:W], od[:W], W, chain=True)
-        eng.moe_seq_status()
-        torch.cuda.synchronize()
-        ev0.record(eng.stream)
-        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=True)
-        ev1.record(eng.stream)
-        ev1.synchronize()
-        eng.moe_seq_status()
-        ms = ev0.elapsed_time(ev1)
-        # the same launch bracketed by the engine's per-kernel events
-        eng.profile(True)
-        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=True)
-        eng.moe_seq_status()
-        tot, cnt = eng.profile_read(pa.PROF_MOE_SEQ)
-        eng.profile(False)
-        kern_ms = tot / max(cnt, 1)
-        # independent steps (no chain): the throughput bound of the same kernel
-        ev0.record(eng.stream)
-        eng.moe_forward_seq(ld[W:], xd[W:], od[W:], S, chain=False)
-        ev1.record(eng.stream)
-        ev1.synchronize()
-        eng.moe_seq_status()
-        ms_nochain = ev0.elapsed_time(ev1)
-        prof = {"moe_seq_launch": kern_ms}
-        roof_bytes = S * TOKEN_BYTES
-        roof_ms = kern_ms
-        roof_kernel = "k_moe_seq (persistent: router+top-4+gate_up+SwiGLU+down+combine, chained steps)"
-        traffic = None
-        extra = {"unchained_us_per_token": round(ms_nochain / S * 1e3, 3),
-                 "unchained_gbps": round(S * TOKEN_BYTES / (ms_nochain * 1e-3) / 1e9, 1)}
-    else:
-        if args.fused:
-            eng.set_moe_fused(True)
-
+    if True:
         def enqueue(t):
             eng.moe_forward(t % L, xd[t], od[t])
         eng.capture_begin()
@@ -587,7 +547,6 @@ def main():
         ms = ev0.elapsed_time(ev1)
         eng.graph_destroy(g_warm)
         eng.graph_destroy(g_run)
-        eng.status()
         # The dominant kernel alone: each token's gate_up launch (4 experts of
         # its layer copy, the same k_i4_gemv<SWIGLU> the MoE step runs)
         # replayed back to back from a graph; HIP events on the engine stream
@@ -610,16 +569,6 @@ def main():
         roof_ms = gu_ms
         roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up + bias + SwiGLU, 4 experts/launch)"
         traffic = GATE_UP_TRAFFIC
-        if args.fused:
-            # the whole layer is the one kernel: all of its algorithmic bytes
-            # over its mean launch duration
-            ly_ms = replay_ms(eng, ev0, ev1, n_prof, lambda t: eng.moe_forward(t % L, xd[t], od[t]))
-            eng.status()
-            prof["moe_layer"] = ly_ms
-            roof_bytes = TOKEN_BYTES
-            roof_ms = ly_ms
-            roof_kernel = "k_moe_fused (router+top-4+gate_up+SwiGLU+down+combine, one launch per layer)"
-            traffic = None
         extra = {"down_gbps": round(down_bytes(K) / (dn_ms * 1e-3) / 1e9, 1),
                  "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
                  "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9

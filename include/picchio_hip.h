@@ -279,46 +279,6 @@ int pk_quantize_act_i8x3(pk_engine *e, const float *x_dev, int rows, int cols,
 int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
                          float *out_dev, int32_t *sel_dev, float *w_dev);
 
-/* A sequence of T batch-1 MoE steps in one persistent kernel: step t runs
- * moe_forward on layer layers_dev[t] with input x_dev[t][hidden] into
- * out_dev[t][hidden]. chain != 0 makes step t+1 wait for step t (the layer
- * dependency of decode); chain == 0 lets independent steps overlap.
- * Results equal pk_moe_forward step by step. Errors raised inside the kernel
- * (a bounded dependency wait that timed out) are reported by
- * pk_moe_seq_status, which synchronises the stream. */
-int pk_moe_forward_seq(pk_engine *e, const int32_t *layers_dev, const float *x_dev, int T,
-                       float *out_dev, int chain);
-int pk_moe_seq_status(pk_engine *e);
-/* Sizes the per-step buffers for sequences of up to T steps (allocates;
- * call before capturing or timing). */
-int pk_moe_seq_reserve(pk_engine *e, int T);
-/* Tracing: with trace_dev != NULL, later sequence launches record four
- * 100 MHz timestamps per task (start, dependencies ready, math done, end)
- * into trace_dev[task][4]; tasks are numbered step-major: per step
- * n_experts router rows, then topk x gate_up row blocks, then topk x down
- * row blocks. NULL turns tracing off. */
-int pk_moe_seq_trace(pk_engine *e, uint64_t *trace_dev);
-
-/* moe_forward (picchio.c:1309-1466) in one launch: with on != 0, every
- * batch-1 MoE layer (pk_moe_forward, the MoE of pk_forward_token /
- * pk_generate) runs router, top-k, gate_up + SwiGLU, down and the combine as
- * one grid whose workgroups exchange the logits, activations and expert rows
- * through device-coherent memory, instead of three launches. Results are
- * bit-identical to the three-launch path. No counterpart in the reference:
- * it selects between two implementations of the same call.
- * PK_ERR_UNSUPPORTED when the shape or the device's occupancy cannot hold
- * the whole grid at once (the three launches stay in use). */
-int pk_set_moe_fused(pk_engine *e, int on);
-/* Tracing of the single-launch layer, per workgroup into trace_dev[wg][6]:
- * five 100 MHz timestamps (start, routed, first block done, last dependency
- * wait done, last block published) and where it ran (XCC_ID << 32 | HW_ID);
- * NULL turns it off. */
-int pk_moe_fused_trace(pk_engine *e, uint64_t *trace_dev);
-/* Errors raised inside kernels since the last call (a bounded dependency
- * wait of the single-launch MoE layer that timed out: that layer's output is
- * invalid). Synchronises the stream, re-arms the flag and counters. */
-int pk_engine_status(pk_engine *e);
-
 /* gqa_attention (picchio.c:504-623) for one token at `pos`; writes K/V. */
 int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
                      float *out_dev);
@@ -403,10 +363,8 @@ int pk_sampler_state(pk_engine *e, uint64_t *rng, int32_t *history_host, int cap
 #define PK_PROF_EXPERT_DOWN    1   /* INT4 down GEMV                                 */
 #define PK_PROF_ROUTER         2   /* router GEMV + top-k                            */
 #define PK_PROF_COMBINE        3   /* weighted combine                               */
-#define PK_PROF_MOE_SEQ        4   /* persistent MoE sequence kernel (whole launch)  */
 #define PK_PROF_LM_HEAD        5   /* lm_head GEMV + greedy argmax                   */
 #define PK_PROF_ATTENTION      6   /* QKV .. O-projection of one layer (5 launches)  */
-#define PK_PROF_MOE_LAYER      7   /* single-launch MoE layer (router .. combine)    */
 #define PK_PROF_N              8
 int pk_engine_profile(pk_engine *e, int enable);
 int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);

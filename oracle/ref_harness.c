@@ -205,3 +205,9 @@ int ref_prefill_tokens(const int *ids, int n, int pos_base, int batch) {
     setenv("PREFILL_BATCH", b, 1);
     return prefill_tokens(&g_ref, ids, n, pos_base);
 }
+
+/* Per-stage .npy dumps of picchio's ORACLE_DIR mode (picchio.c:204-249) into
+ * `dir` (NULL: off). With dumps on, forward_token writes its logits to
+ * <dir>/logits.npy (picchio.c:1746) and prefill_tokens runs position by
+ * position (picchio.c:1947-1948), so switch them on after a batched prefill. */
+void ref_set_dump_dir(const char *dir) { g_oracle_dir = dir; }

@@ -16,8 +16,8 @@ PK_OK = 0
 ERRORS = {-1: "PK_ERR_ARG", -2: "PK_ERR_HIP", -3: "PK_ERR_OOM", -4: "PK_ERR_UNSUPPORTED",
           -5: "PK_ERR_MISSING", -6: "PK_ERR_CONTEXT_FULL"}
 FMT_F32, FMT_INT8, FMT_INT4 = 0, 1, 2
-PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE, PROF_MOE_SEQ = 0, 1, 2, 3, 4
-PROF_LM_HEAD, PROF_ATTENTION, PROF_MOE_LAYER = 5, 6, 7
+PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE = 0, 1, 2, 3
+PROF_LM_HEAD, PROF_ATTENTION = 5, 6
 
 
 class PkError(RuntimeError):
@@ -144,13 +144,6 @@ def lib():
         "pk_engine_profile": (C.c_int, [vp, C.c_int]),
         "pk_engine_profile_read": (C.c_int, [vp, C.c_int, C.POINTER(C.c_double), C.POINTER(i64)]),
         "pk_engine_stall": (C.c_int, [vp, C.c_int]),
-        "pk_moe_forward_seq": (C.c_int, [vp, vp, vp, C.c_int, vp, C.c_int]),
-        "pk_moe_seq_status": (C.c_int, [vp]),
-        "pk_moe_seq_reserve": (C.c_int, [vp, C.c_int]),
-        "pk_moe_seq_trace": (C.c_int, [vp, vp]),
-        "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
-        "pk_moe_fused_trace": (C.c_int, [vp, vp]),
-        "pk_engine_status": (C.c_int, [vp]),
         "pk_decode_replay": (C.c_int, [vp, C.c_int, C.c_int, C.c_int, vp]),
         "pk_batch_reserve": (C.c_int, [vp, C.c_int]),
         "pk_kv_fill_synthetic": (C.c_int, [vp, C.c_int, C.c_int, C.c_uint64]),
@@ -419,28 +412,6 @@ class Engine:
         out = np.empty(n_steps, np.int32)
         check(self.L.pk_decode_replay(self.h, tok, pos, n_steps, ptr(out)))
         return out
-
-    def moe_forward_seq(self, layers_dev, x_dev, out_dev, T, chain=True):
-        check(self.L.pk_moe_forward_seq(self.h, ptr(layers_dev), ptr(x_dev), T, ptr(out_dev),
-                                        1 if chain else 0))
-
-    def moe_seq_reserve(self, T):
-        check(self.L.pk_moe_seq_reserve(self.h, T))
-
-    def moe_seq_status(self):
-        check(self.L.pk_moe_seq_status(self.h))
-
-    def set_moe_fused(self, on=True):
-        """Batch-1 MoE layers as one launch (True) or three (False)."""
-        check(self.L.pk_set_moe_fused(self.h, 1 if on else 0))
-
-    def moe_fused_trace(self, trace_dev):
-        """Per-workgroup timeline [grid][6] of the single-launch layer (None: off)."""
-        check(self.L.pk_moe_fused_trace(self.h, ptr(trace_dev) if trace_dev is not None else None))
-
-    def status(self):
-        """Raises if a kernel's bounded dependency wait timed out since the last call."""
-        check(self.L.pk_engine_status(self.h))
 
     def expert_apply(self, layer, eid, x_dev, dst_dev, w):
         check(self.L.pk_expert_apply(self.h, layer, eid, ptr(x_dev), ptr(dst_dev), w))

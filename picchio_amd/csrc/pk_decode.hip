@@ -604,6 +604,7 @@ __global__ __launch_bounds__(256) void k_lm_head(const float *__restrict__ x, co
     const int n4 = I >> 2;
     const int o0 = blockIdx.x * LM_ROWS_PER_BLOCK + wave * 2;
     float acc[2] = {0.0f, 0.0f};
+    bool nan0 = false;                        // logit 0 is NaN (block 0, wave 0)
     if (Q8) {
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
@@ -650,6 +651,7 @@ __global__ __launch_bounds__(256) void k_lm_head(const float *__restrict__ x, co
         if (o < O) {
             if (Q8) v = v * sc[o];
             if (lane == 0 && logits) logits[o] = v;
+            if (o == 0 && v != v) nan0 = true;
             better(bv, bi, v, o);
         }
     }
@@ -658,7 +660,7 @@ __global__ __launch_bounds__(256) void k_lm_head(const float *__restrict__ x, co
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w) better(bv, bi, rv[w], ri[w]);
         bval[blockIdx.x] = bv;
-        bidx[blockIdx.x] = bi;
+        bidx[blockIdx.x] = nan0 ? -1 : bi;     // -1: the argmax must keep index 0
     }
 }
 
@@ -680,7 +682,10 @@ __global__ __launch_bounds__(1024) void k_argmax_blocks(const float *bval, const
     __syncthreads();
     if (threadIdx.x == 0) {
         for (int w = 1; w < (int)(blockDim.x >> 6); ++w) better(bv, bi, rv[w], ri[w]);
-        const int tok = bi == 0x7fffffff ? 0 : bi;
+        // the reference's greedy scan (picchio.c:1555-1560) starts at index 0
+        // and moves on a strictly greater value only: with logit 0 NaN it
+        // keeps 0 (k_lm_head marks that case with index -1 in block 0)
+        const int tok = (bi == 0x7fffffff || bidx[0] < 0) ? 0 : bi;
         if (st->n_out < out_cap) out_toks[st->n_out] = tok;
         st->n_out = st->n_out + 1;
         st->next = tok;
@@ -733,7 +738,7 @@ int pk_check_model(pk_engine *e) {
 // and adds the output projection into h [n][D] (residual).
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
                       int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
-                      const float *norm_w) {
+                      const float *norm_w, bool exact) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[l];
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
@@ -752,13 +757,29 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                            c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl);
         PK_HIP(hipGetLastError());
     } else {
-        PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
+        if (exact)
+            PK_TRY(pk_launch_gemm_chain8(xn, D, d.wqkv, d.bqkv, qkv, qkv_dim, n, D, qkv_dim, false, e->stream));
+        else
+            PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream));
         const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
         hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base,
                            pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
         PK_HIP(hipGetLastError());
     }
     const int sliding = c->layer_type[l] == 0;
+    if (exact && !st && pos_step == 1 && seq_step == 0) {
+        // prompt rows: softmax with sink and value sums in position order,
+        // then the output projection's chains (when the window fits in LDS)
+        const int last = pos_base + n - 1;
+        int span = (last < c->ctx_len ? last : c->ctx_len - 1) + 1;
+        if (sliding && span > c->sliding_window) span = c->sliding_window;
+        if (span <= 16384) {
+            PK_TRY(pk_launch_attn_rows_exact(pos_base, n, qkv, qkv_dim, Kl, Vl, H, KVH, hd, c->ctx_len, sliding,
+                                             c->sliding_window, d.sinks, att, e->stream));
+            PK_TRY(pk_launch_gemm_chain8(att, (int64_t)H * hd, d.wo, d.bo, h, D, n, H * hd, D, true, e->stream));
+            return pk_prof_end(e, ps);
+        }
+    }
     const int max_chunks = (c->ctx_len + ATT_CHUNK - 1) / ATT_CHUNK;
     int chunks = st ? (e->att_pos_cap >= 0 ? e->att_pos_cap / ATT_CHUNK + 1 : max_chunks)
                     : (pos_base + (n - 1) * pos_step + ATT_CHUNK) / ATT_CHUNK;
@@ -976,6 +997,7 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
         PK_HIP(hipStreamSynchronize(e->stream));
         (void)hipGraphExecDestroy(e->step_exec);
         e->step_exec = nullptr;
+        e->step_cap = -1;
     }
     if (!e->step_exec) {
         if (!e->step_out) {
@@ -996,10 +1018,15 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
         }
         e->capturing = false;
         hipError_t hr = hipStreamEndCapture(e->stream, &g);
+        if (rc == PK_OK && hr == hipSuccess) hr = hipGraphInstantiate(&e->step_exec, g, nullptr, nullptr, 0);
+        if (g) (void)hipGraphDestroy(g);            // every exit path after the capture
         PK_TRY(rc);
-        PK_HIP(hr);
-        PK_HIP(hipGraphInstantiate(&e->step_exec, g, nullptr, nullptr, 0));
-        (void)hipGraphDestroy(g);
+        if (hr != hipSuccess) {
+            e->step_exec = nullptr;
+            e->step_cap = -1;
+            pk_set_error("decode step capture failed: %s", hipGetErrorString(hr));
+            return PK_ERR_HIP;
+        }
         e->step_cap = cap;
     }
     PK_TRY(pk_set_state(e, tok, pos));

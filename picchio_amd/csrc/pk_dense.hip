@@ -416,7 +416,7 @@ __global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E,
         float m = -1e30f;
         for (int k = 0; k < K; ++k) if (val[k] > m) m = val[k];
         float e[16], s = 0.0f;
-        for (int k = 0; k < K; ++k) { e[k] = expf(val[k] - m); s += e[k]; }
+        for (int k = 0; k < K; ++k) { e[k] = pk_expf_cr(val[k] - m); s += e[k]; }
         for (int k = 0; k < K; ++k) {
             const float p = e[k] / s;
             sel[(int64_t)t * K + k] = chosen[k];
@@ -568,7 +568,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
         float m = -1e30f;
         for (int k = 0; k < K; ++k) if (cv[k] > m) m = cv[k];
         float s = 0.0f;
-        for (int k = 0; k < K; ++k) { cv[k] = expf(cv[k] - m); s += cv[k]; }
+        for (int k = 0; k < K; ++k) { cv[k] = pk_expf_cr(cv[k] - m); s += cv[k]; }
         for (int k = 0; k < K; ++k) {
             const float p = cv[k] / s;
             sel[k] = ci[k];

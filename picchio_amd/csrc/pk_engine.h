@@ -35,12 +35,6 @@ struct pk_sampler_dev {
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
-constexpr int PK_FUSED_CTL_BYTES = 131072;   // control block of the single-launch MoE layer
-// floats per private input row of the single-launch MoE layer (128-byte multiple)
-inline int pk_fused_row(const pk_cfg *c) {
-    const int n = c->hidden > c->moe_inter / 2 ? c->hidden : c->moe_inter / 2;
-    return (n + 31) & ~31;
-}
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
 constexpr int PK_CTR_N = PK_CTR_ATTN + PK_CTR_ATTN_N;
@@ -116,25 +110,6 @@ struct pk_engine {
 
     int n_cu = 256;                          // compute units of the device
 
-    // single-launch MoE layer (pk_moe_fused.hip)
-    bool moe_fused = false;                  // pk_moe_layer runs it instead of three launches
-    int fused_fit = -1;                      // shape + occupancy check (-1: not yet made)
-    int fused_occ = 0;                       // its workgroups per CU
-    uint64_t *fused_trace = nullptr;         // optional per-workgroup timeline
-    uint8_t *fused_ctl = nullptr;            // slots and counters (PK_FUSED_CTL_BYTES)
-    float *fused_xn = nullptr;               // [n_cu][2][pk_fused_row] rows private to each workgroup
-
-    // persistent MoE sequence (pk_moe_forward_seq): per-step exchange buffers
-    int seq_cap = 0;
-    bool seq_ready = false;
-    float *s_logits = nullptr, *s_act = nullptr, *s_eo = nullptr, *s_w = nullptr;
-    int32_t *s_sel = nullptr;
-    uint32_t *s_ctr = nullptr;
-    int64_t s_ctr_n = 0, s_act_stride = 0, s_eo_stride = 0;
-    void *router_tab = nullptr;               // device [2L] router / bias pointers
-    uint64_t *seq_trace = nullptr;            // optional task timeline (pk_moe_seq_trace)
-    bool router_tab_dirty = true;
-
     // batched MoE scratch for up to batch_cap tokens (pk_prefill.hip)
     int64_t batch_cap = 0;
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
@@ -185,10 +160,6 @@ int pk_prof_end(pk_engine *e, int slot);
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out, const float *norm_w = nullptr);
 int pk_check_layer_experts(pk_engine *e, int layer);
-// single-launch MoE layer (router .. combine); fits: shape and occupancy allow it
-bool pk_moe_fused_fits(pk_engine *e);
-int pk_moe_fused_launch(pk_engine *e, int layer, const float *x, float *out, const float *residual,
-                        const float *norm_w);
 pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
 
 // ── expert-grouped MFMA GEMM (pk_mfma.hip) ──
@@ -223,9 +194,20 @@ int pk_set_state(pk_engine *e, int tok, int pos);
 // Rows r = 0..n-1 at position (st ? st->pos : pos_base + r * pos_step) of
 // sequence seq0 + r * seq_step.
 // norm_w (n == 1 only): xn is the raw residual row, normalised inside the QKV GEMV.
+// exact: the prompt rows in the reference's operation order (pk_exact.hip).
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
                       int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
-                      const float *norm_w = nullptr);
+                      const float *norm_w = nullptr, bool exact = false);
+// the prompt path's dense steps in the reference's order (pk_exact.hip)
+int pk_launch_gemm_chain8(const float *X, int64_t ldx, const float *W, const float *bias, float *out, int64_t ldo,
+                          int S, int I, int O, bool add_res, hipStream_t st);
+int pk_launch_gemm_chain8_q8(const float *X, const int8_t *W, const float *scale, float *out, int S, int I, int O,
+                             hipStream_t st);
+int pk_launch_attn_rows_exact(int pos_base, int n, const float *qkv, int64_t qkv_stride, const float *Kl,
+                              const float *Vl, int H, int KVH, int hd, int ctx, int sliding, int window,
+                              const float *sinks, float *att, hipStream_t st);
+int pk_launch_router_seq(const float *X, const float *R, const float *bias, int S, int D, int E, float *logits,
+                         hipStream_t st);
 int pk_lm_head_step(pk_engine *e, const float *hn, float *logits_dev, int32_t *out_toks, int out_cap);
 // sampler (pk_sample.hip): draw from logits[0..vocab) with the engine's
 // sampler state; st != nullptr also updates the decode state like the argmax

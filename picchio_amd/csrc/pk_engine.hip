@@ -148,9 +148,7 @@ static void engine_free(pk_engine *e) {
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
-                    e->s_logits, e->s_act, e->s_eo, e->s_ctr, e->router_tab,
-                    e->s_sel, e->s_w, e->lm_bval, e->lm_bidx, e->dstate, e->step_out,
-                    e->fused_ctl, e->fused_xn, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles};
+                    e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -213,10 +211,7 @@ static int engine_init(pk_engine *e) {
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
-    ALLOC(e->fused_ctl, PK_FUSED_CTL_BYTES);
-    ALLOC(e->fused_xn, (int64_t)e->n_cu * 2 * pk_fused_row(c) * 4);   // two private rows per workgroup
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
-    PK_HIP(hipMemsetAsync(e->fused_ctl, 0, PK_FUSED_CTL_BYTES, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
 }
@@ -443,7 +438,6 @@ extern "C" int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l) {
         PK_TRY(upload_f32(e, &d.router, l->router, (int64_t)E * D));
         PK_TRY(upload_f32(e, &d.router_b, l->router_bias, E));
         d.have_router = true;
-        e->router_tab_dirty = true;
     }
     if (l->wq.data) {
         const pk_qt_host *ws[3] = {&l->wq, &l->wk, &l->wv};
@@ -538,8 +532,7 @@ extern "C" int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, 
             PK_TRY(synth_fill(e, d.router, (int64_t)E * D, seed, PK_T_ROUTER, l, 0, 0.02f));
             PK_TRY(synth_fill(e, d.router_b, E, seed, PK_T_ROUTER_B, l, 0, 0.02f));
             d.have_router = true;
-            e->router_tab_dirty = true;
-            for (int x = 0; x < E; ++x) {
+                for (int x = 0; x < E; ++x) {
                 uint8_t *s = slot_ptr(e, l, x);
                 PK_TRY(synth_expert_matrix(e, inter, D, seed, PK_T_GU, l, x, s + e->ex.off_gu_tiles,
                                            (float *)(s + e->ex.off_gu_scales)));
@@ -663,10 +656,11 @@ extern "C" int pk_matmul_qt(pk_engine *e, float *y, const float *x, const pk_qt 
     PK_CHECK(e && y && x && w, PK_ERR_ARG, "null argument");
     PK_CHECK(S > 0, PK_ERR_ARG, "S=%d", S);
     switch (w->fmt) {
-    case PK_FMT_F32:
-        return pk_launch_gemv_f32(y, x, (const float *)w->data, nullptr, S, w->I, w->O, e->stream);
-    case PK_FMT_INT8:
-        return pk_launch_gemv_q8(y, x, (const int8_t *)w->data, w->s, S, w->I, w->O, e->stream);
+    case PK_FMT_F32:    // quant.h:117-148's chains and tree: the reference's bits
+        return pk_launch_gemm_chain8(x, w->I, (const float *)w->data, nullptr, y, w->O, S, w->I, w->O, false,
+                                     e->stream);
+    case PK_FMT_INT8:   // quant.h:152-186, likewise
+        return pk_launch_gemm_chain8_q8(x, (const int8_t *)w->data, w->s, y, S, w->I, w->O, e->stream);
     case PK_FMT_INT4:
         if (w->gs <= 0)
             return pk_launch_i4_rowscale_gemv(y, x, (const uint8_t *)w->data, w->s, S, w->I, w->O, e->stream);
@@ -760,11 +754,6 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out, const float *norm_w) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[layer];
-    if (e->moe_fused && pk_moe_fused_fits(e)) {
-        const int pf = pk_prof_begin(e, PK_PROF_MOE_LAYER);
-        PK_TRY(pk_moe_fused_launch(e, layer, x_dev, residual ? res_out : out_dev, residual, norm_w));
-        return pk_prof_end(e, pf);
-    }
     // the router launch writes the logits only; the gate_up launch selects
     // the experts from them and publishes the routing (sel, weights)
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
@@ -801,6 +790,7 @@ extern "C" int pk_set_i4_dot(pk_engine *e, int on) {
     if (e->i4_dot != (on != 0) && e->step_exec) {      // the captured step holds the other kernels
         (void)hipGraphExecDestroy(e->step_exec);
         e->step_exec = nullptr;
+        e->step_cap = -1;
     }
     e->i4_dot = on != 0;
     return PK_OK;

@@ -63,7 +63,12 @@ __device__ __forceinline__ float pk_group_dot(uint4 a, uint4 b, XP xg) {
     return (b0 + b2) + (b1 + b3);
 }
 
-__device__ __forceinline__ float pk_sigmoid(float v) { return 1.0f / (1.0f + expf(-v)); }
+// expf as the double exp rounded once to float: the correctly rounded value
+// (but for double rounding in about 2^-29 of inputs), which is glibc's expf
+// except where glibc's own result is not correctly rounded (~8e-5 of inputs).
+__device__ __forceinline__ float pk_expf_cr(float x) { return (float)exp((double)x); }
+
+__device__ __forceinline__ float pk_sigmoid(float v) { return 1.0f / (1.0f + pk_expf_cr(-v)); }
 
 // GPT-OSS clamped SwiGLU of one (gate, up) pair (picchio.c:1416-1424).
 __device__ __forceinline__ float pk_swiglu(float gate, float up, float lim, float alpha) {
@@ -151,7 +156,7 @@ __device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
     float s = 0.0f;
 #pragma unroll
     for (int k = 0; k < 16; ++k)
-        if (k < rt.K) { cv[k] = expf(cv[k] - m); s += cv[k]; }
+        if (k < rt.K) { cv[k] = pk_expf_cr(cv[k] - m); s += cv[k]; }
 #pragma unroll
     for (int k = 0; k < 16; ++k)
         if (k < rt.K) {

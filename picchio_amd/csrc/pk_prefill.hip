@@ -114,6 +114,22 @@ static int batch_reserve(pk_engine *e, int T) {
     return PK_OK;
 }
 
+// Router logits, top-k and softmax of T rows into b_sel / b_w. The prompt's
+// router (picchio.c:1840-1844) starts each dot at the bias and adds the
+// products in order; the lockstep decode of several sequences sums them in a
+// fixed tree and adds the bias last (within the fp32 bar of moe_forward's
+// order, picchio.c:1316-1324).
+static int route_rows(pk_engine *e, int layer, const float *x, int T, bool prompt_order) {
+    const pk_cfg *c = &e->c;
+    const pk_layer_dev &d = e->L[layer];
+    if (prompt_order)
+        PK_TRY(pk_launch_router_seq(x, d.router, d.router_b, T, c->hidden, c->n_experts, e->b_logits, e->stream));
+    else
+        PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, c->hidden, c->n_experts, e->stream));
+    return pk_launch_topk_batch(e->b_logits, T, c->n_experts, c->topk, c->routed_scale, e->b_sel, e->b_w, nullptr,
+                                e->stream);
+}
+
 // The MoE of forward_prefill (picchio.c:1829-1916) for T tokens x [T][D]:
 // out[t] = (residual ? residual[t] : 0) + sum over the token's experts, in the
 // batch's expert order, of (w_k * routed_scale) * expert_k(x[t]). With
@@ -124,9 +140,7 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
     const pk_cfg *c = &e->c;
     const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
     PK_TRY(batch_reserve(e, T));
-    const pk_layer_dev &d = e->L[layer];
-    PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
-    PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr, e->stream));
+    PK_TRY(route_rows(e, layer, x, T, !decode_order));
     if (!decode_order) {
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
         PK_HIP(hipGetLastError());
@@ -219,10 +233,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
         PK_HIP(hipMemcpyAsync(e->b_sel, sel_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
         PK_HIP(hipMemcpyAsync(e->b_w, w_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
     } else {
-        const pk_layer_dev &d = e->L[layer];
-        PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, D, E, e->stream));
-        PK_TRY(pk_launch_topk_batch(e->b_logits, T, E, K, c->routed_scale, e->b_sel, e->b_w, nullptr,
-                                    e->stream));
+        PK_TRY(route_rows(e, layer, x, T, !decode_order));
     }
     if (!decode_order) {
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
@@ -335,7 +346,7 @@ static int prefill_chunk(pk_engine *e, int seq, const int32_t *ids_dev, int last
     for (int l = 0; l < c->n_layers; ++l) {
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].in_ln, D, c->eps, n, e->stream));
         PK_TRY(pk_attention_rows(e, l, nullptr, pos_base, 1, seq, 0, n, e->p_XN, e->p_qkv, e->p_part, e->p_att,
-                                 e->p_H));
+                                 e->p_H, nullptr, true));
         PK_TRY(pk_launch_rmsnorm(e->p_XN, e->p_H, e->L[l].post_ln, D, c->eps, n, e->stream));
         if (mfma)
             PK_TRY(moe_rows_mfma(e, l, e->p_XN, n, e->p_H, e->p_H, nullptr, nullptr));
@@ -415,7 +426,9 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int V,
     if (threadIdx.x == 0) {
         for (int w = 1; w < 4; ++w)
             if (bv[w] > v || (bv[w] == v && bi[w] < i)) { v = bv[w]; i = bi[w]; }
-        out[blockIdx.x] = i == 0x7fffffff ? 0 : i;
+        // the reference's scan starts at index 0 and moves on a strictly
+        // greater value only: a NaN (or the maximum) at index 0 keeps 0
+        out[blockIdx.x] = (i == 0x7fffffff || !(v > lg[0])) ? 0 : i;
     }
 }
 
@@ -434,6 +447,7 @@ extern "C" int pk_batch_reserve(pk_engine *e, int n_seq) {
     if (e->step_exec) {                       // the captured step addresses the old cache
         (void)hipGraphExecDestroy(e->step_exec);
         e->step_exec = nullptr;
+        e->step_cap = -1;
     }
     e->n_seq = 0;
     PK_TRY(pk_dev_alloc(e, (void **)&e->K, bytes));

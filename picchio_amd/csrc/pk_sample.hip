@@ -1075,6 +1075,7 @@ static int put_params(pk_engine *e, const pk_sampler_dev &p, bool reset) {
     if (on != e->samp_on && e->step_exec) {   // the captured step ends in the other kernel
         (void)hipGraphExecDestroy(e->step_exec);
         e->step_exec = nullptr;
+        e->step_cap = -1;
     }
     e->samp_on = on;
     return PK_OK;

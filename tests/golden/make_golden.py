@@ -8,10 +8,13 @@ inputs and the outputs picchio's functions produced for them, as .npz
 seed; the tests rebuild the same weights with the oracle's generator
 (po_model_build), which is also what the reference ran on here.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py            # kernel and tiny-model vectors
+    python tests/golden/make_golden.py config2    # config-2 stream (~18 GB RAM)
 """
 import os
+import shutil
 import sys
+import tempfile
 
 import numpy as np
 
@@ -165,8 +168,58 @@ def model_level(oracle, ref):
     oracle.model_free(model)
 
 
+# GPT-OSS-20B shape, 512-token prompt, 256 greedy tokens.
+C2_PROMPT, C2_STEPS, C2_SEED = 512, 256, 2025
+C2_LOGIT_STEPS = (1, 255)       # decode steps whose full logits are kept
+
+
+def config2_stream(oracle, ref, small=None, out="config2_stream.npz"):
+    """picchio's own greedy stream on the full-size config-2 model: the
+    prompt through prefill_tokens (chunks of 64), then forward_token; the
+    logits of every decode step come from picchio's ORACLE_DIR dump
+    (picchio.c:1746). Keeps the ids, each step's top-1 minus top-2 logit and
+    the whole logit vector of the steps in C2_LOGIT_STEPS. About 18 GB of
+    host memory and a few minutes of CPU."""
+    cfg = make_cfg(**dict(small or {}, ctx_len=C2_PROMPT + C2_STEPS + 1))
+    model = oracle.model_build(cfg, C2_SEED, 0)
+    assert ref.attach(model, cfg) == 0
+    ref.reset_kv()
+    prompt = np.random.default_rng(C2_SEED).integers(0, cfg.vocab, C2_PROMPT).astype(np.int32)
+    ids = [ref.prefill_tokens(prompt, C2_PROMPT, 0, 64)]
+    margins = [np.nan]
+    kept = {}
+    dump = tempfile.mkdtemp(prefix="pk_c2_")
+    dump_c = dump.encode()          # picchio keeps the pointer: keep the bytes alive
+    try:
+        ref.set_dump_dir(dump_c)
+        for i in range(C2_STEPS - 1):
+            ids.append(ref.forward_token(ids[-1], C2_PROMPT + i))
+            lg = np.load(os.path.join(dump, "logits.npy"), allow_pickle=False).reshape(-1)
+            assert lg.size == cfg.vocab and int(np.argmax(lg)) == ids[-1]
+            top = np.sort(lg)[-2:]
+            margins.append(float(top[1]) - float(top[0]))
+            if len(ids) - 1 in C2_LOGIT_STEPS:
+                kept[f"logits_step{len(ids) - 1}"] = lg.astype(np.float32)
+            if i % 32 == 0:
+                print(f"config2: step {len(ids) - 1} id {ids[-1]} margin {margins[-1]:.3g}", flush=True)
+    finally:
+        ref.set_dump_dir(None)
+        shutil.rmtree(dump, ignore_errors=True)
+    save(out, seed=np.array(C2_SEED), prompt=prompt, stream=np.array(ids, np.int32),
+         margins=np.array(margins, np.float32), logit_steps=np.array(C2_LOGIT_STEPS, np.int32),
+         **kept, **cfg_array(cfg))
+    oracle.model_free(model)
+
+
 def main():
     oracle, ref = Oracle(), Reference()
+    if sys.argv[1:] == ["config2"]:
+        config2_stream(oracle, ref)
+        return
+    if sys.argv[1:] == ["config2-dry"]:     # the same recipe on a small model, not kept
+        config2_stream(oracle, ref, small=TINY, out="_dry.npz")
+        os.remove(os.path.join(HERE, "_dry.npz"))
+        return
     rng = np.random.default_rng(20261201)
     kernels(ref, rng)
     rope(ref)

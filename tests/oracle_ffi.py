@@ -194,6 +194,7 @@ class Reference:
         self.yarn_inv_freq = _bind(L, "ref_yarn_inv_freq", C.c_float, C.POINTER(PkCfg), C.c_int)
         self.forward_token = _bind(L, "ref_forward_token", C.c_int, C.c_int, C.c_int)
         self.prefill_tokens = _bind(L, "ref_prefill_tokens", C.c_int, i32p, C.c_int, C.c_int, C.c_int)
+        self.set_dump_dir = _bind(L, "ref_set_dump_dir", None, C.c_char_p)
         self.sample_logits = _bind(L, "ref_sample_logits", C.c_int, f32p, C.c_int, C.c_float, C.c_float,
                                    C.c_int, C.c_float, C.POINTER(C.c_uint64), i32p, C.c_int)
 

@@ -1,51 +1,81 @@
 """BASELINE config 2 at full size: the GPT-OSS-20B-shaped model (24 layers,
-32 experts, vocab 201088), a 512-token prompt of uniform random ids through
-prefill_tokens (chunks of 64, picchio's default), then 256 greedy steps —
-the GPU stream must equal the oracle's (itself bit-exact with picchio).
+32 experts, vocab 201088) from seed 2025, a 512-token prompt of uniform
+random ids through prefill_tokens (chunks of 64, picchio's default), then
+256 greedy steps. The expected stream and the logits of two decode steps
+come from picchio's own prefill_tokens / forward_token (oracle/_ref, built
+from the reference sources) on the same weights, committed as
+tests/golden/config2_stream.npz by tests/golden/make_golden.py config2.
 
-The CPU side builds the 18 GB model and runs 768 positions (about three
-minutes on 16 host cores), so this test runs only with PK_FULL_STREAM=1;
-the same path is covered at reduced depth by test_gpu_decode.py on every run.
+Bars: an identical greedy token stream over 256 steps;
+fp32 logits of the full 201,088-row lm_head within relative L2 1e-4.
 """
 import os
-import time
 
 import numpy as np
 import pytest
 
-from helpers import upload_model
+from helpers import REL_L2_TOL, rel_l2
 
 pytestmark = pytest.mark.gpu
 
-N_PROMPT, N_STEPS, SEED = 512, 256, 2025
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "config2_stream.npz")
 
 
-@pytest.mark.skipif(os.environ.get("PK_FULL_STREAM") != "1",
-                    reason="full-size 20B stream check: set PK_FULL_STREAM=1 (about 3 min of CPU)")
-def test_config2_greedy_stream_256(gpu, oracle):
+def _fixture():
+    return np.load(FIXTURE, allow_pickle=False)
+
+
+def _cfg(z):
     import picchio_amd as pa
-    cfg = pa.gptoss_cfg(ctx_len=N_PROMPT + N_STEPS + 1)
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
-    t0 = time.time()
-    model = oracle.model_build(cfg, SEED, threads)
-    print(f"oracle model built in {time.time() - t0:.0f} s", flush=True)
-    eng = pa.Engine(cfg)
+    cfg = pa.gptoss_cfg(ctx_len=int(z["cfg_ctx_len"]))
+    for name, _ in cfg._fields_:
+        if name == "layer_type":
+            assert list(cfg.layer_type) == list(z["cfg_layer_type"])
+        else:
+            assert np.isclose(getattr(cfg, name), z[f"cfg_{name}"]), name
+    return cfg
+
+
+@pytest.fixture(scope="module")
+def c2_engine(gpu):
+    import picchio_amd as pa
+    z = _fixture()
+    eng = pa.Engine(_cfg(z))
+    eng.build_synthetic(int(z["seed"]), what=7)
+    yield z, eng
+    eng.close()
+
+
+@pytest.mark.parametrize("dot", [False, True], ids=["fp32-chains", "integer-dot"])
+def test_config2_greedy_stream_256(c2_engine, dot):
+    """pk_generate (prefill chunks + the replayed decode step): picchio's 256 ids."""
+    z, eng = c2_engine
+    eng.set_i4_dot(dot)
     try:
-        t0 = time.time()
-        upload_model(eng, oracle, model, cfg)
-        print(f"uploaded in {time.time() - t0:.0f} s", flush=True)
-        prompt = np.random.default_rng(SEED).integers(0, cfg.vocab, N_PROMPT).astype(np.int32)
-        t0 = time.time()
-        got = [int(v) for v in eng.generate(prompt, N_STEPS)]
-        print(f"GPU stream in {time.time() - t0:.1f} s: {got[:12]}", flush=True)
-        t0 = time.time()
-        oracle.model_reset_kv(model)
-        ref = [oracle.prefill_tokens(model, prompt, N_PROMPT, 0, 64)]
-        for i in range(N_STEPS - 1):
-            ref.append(oracle.forward_token(model, ref[-1], N_PROMPT + i, None))
-        print(f"oracle stream in {time.time() - t0:.0f} s: {ref[:12]}", flush=True)
-        first = next((i for i, (a, b) in enumerate(zip(got, ref)) if a != b), None)
-        assert first is None, f"streams diverge at step {first}: {got[first:first + 4]} vs {ref[first:first + 4]}"
+        got = [int(v) for v in eng.generate(z["prompt"], len(z["stream"]))]
     finally:
-        eng.close()
-        oracle.model_free(model)
+        eng.set_i4_dot(False)
+    ref = [int(v) for v in z["stream"]]
+    first = next((i for i, (a, b) in enumerate(zip(got, ref)) if a != b), None)
+    assert first is None, (f"stream diverges at step {first}: {got[first:first + 4]} vs {ref[first:first + 4]}"
+                           f" (picchio's top-2 margin there {float(z['margins'][first]):.3g})")
+
+
+def test_config2_eager_logits_full_vocab(c2_engine):
+    """prefill_tokens, then forward_token step by step (the eager lm_head +
+    argmax path): every id equals picchio's, and the full-vocabulary logits
+    of the kept steps are within relative L2 1e-4 of picchio's."""
+    import torch
+    z, eng = c2_engine
+    prompt, ref = z["prompt"], [int(v) for v in z["stream"]]
+    n_prompt = len(prompt)
+    assert eng.prefill_tokens(prompt) == ref[0]
+    keep = set(int(k) for k in z["logit_steps"])
+    lg_dev = eng.empty(int(z["cfg_vocab"]), torch.float32)
+    for k in range(1, len(ref)):
+        nxt = eng.forward_token(ref[k - 1], n_prompt + k - 1, lg_dev if k in keep else None)
+        assert nxt == ref[k], (k, nxt, ref[k])
+        if k in keep:
+            err = rel_l2(eng.to_host(lg_dev), z[f"logits_step{k}"])
+            print(f"step {k}: logits rel-L2 {err:.2e}", flush=True)
+            assert err < REL_L2_TOL, (k, err)

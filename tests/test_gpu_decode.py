@@ -352,3 +352,48 @@ def test_batched_decode_on_matrix_cores(gpu, oracle, monkeypatch):
     finally:
         eng.close()
         oracle.model_free(model)
+
+
+def _greedy_rule(lg):
+    """picchio's greedy pick (picchio.c:1555-1560): start at index 0, move on
+    a strictly greater value only (a NaN at index 0 keeps 0; later NaNs never win)."""
+    best = 0
+    for i in range(1, lg.size):
+        if lg[i] > lg[best]:
+            best = i
+    return best
+
+
+@pytest.mark.parametrize("nan_rows", [(0,), (7,), (0, 3)])
+def test_greedy_with_nan_logits(gpu, oracle, nan_rows):
+    """lm_head rows made NaN: forward_token's argmax (per-block maxima) and
+    decode_batch's per-row argmax both follow the reference's scan."""
+    import torch
+    import picchio_amd as pa
+    from helpers import T_EMBED, T_LM_HEAD
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=32, vocab=600)
+    model = oracle.model_build(cfg, 808, 0)
+    eng = pa.Engine(cfg)
+    try:
+        upload_model(eng, oracle, model, cfg, globals_=False)
+        D, V = cfg.hidden, cfg.vocab
+        lm = oracle.tensor(model, T_LM_HEAD, 0, V * D).reshape(V, D)
+        for r in nan_rows:
+            lm[r] = np.nan
+        eng.store_globals(oracle.tensor(model, T_EMBED, 0, V * D), lm.ravel(), oracle.tensor(model, 0, 0, D))
+        lg_dev = eng.empty(V, torch.float32)
+        for pos, tok in enumerate([3, 11, 5]):
+            nxt = eng.forward_token(tok, pos, lg_dev)
+            lg = eng.to_host(lg_dev)
+            assert all(np.isnan(lg[r]) for r in nan_rows)
+            assert nxt == _greedy_rule(lg), (pos, nxt, _greedy_rule(lg))
+        # the batched decode's per-row argmax on the same weights
+        eng.batch_reserve(2)
+        got = eng.decode_batch([3, 3], 0, 2)
+        if 0 in nan_rows:
+            assert (got == 0).all(), got
+        else:
+            assert (got != nan_rows[0]).all(), got
+    finally:
+        eng.close()
+        oracle.model_free(model)

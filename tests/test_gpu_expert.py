@@ -124,7 +124,33 @@ def test_matmul_qt_formats(gpu, oracle, fmt, S):
         eng.matmul_qt(yd, xd, qt, S)
         y = eng.to_host(yd)
         eng.qt_free(qt)
-    assert rel_l2(y, y_ref) < 1e-6
+    if fmt in ("f32", "q8"):                       # quant.h's chains and hsum tree: the same bits
+        assert bits_equal(y, y_ref), first_mismatch(y, y_ref)
+    else:
+        assert rel_l2(y, y_ref) < 1e-6
+
+
+def test_matmul_qt_dense_golden(gpu):
+    """matmul_qt F32 / INT8 on the vectors picchio's own matmul_f32 / matmul_q8
+    produced (tests/golden/matmul_dense.npz: ragged I = 13, 37, 4101, I < 8,
+    I = 1): bit for bit."""
+    import os
+    import torch
+    import picchio_amd as pa
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "matmul_dense.npz"), allow_pickle=False)
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
+    with _engine(cfg) as eng:
+        for i in range(int(z["n"])):
+            S, I, O = (int(v) for v in z[f"c{i}_shape"])
+            x = z[f"c{i}_x"]
+            for args, ref in [((pa.FMT_F32, z[f"c{i}_W"], None, O, I, 0), z[f"c{i}_yf"]),
+                              ((pa.FMT_INT8, z[f"c{i}_q8"], z[f"c{i}_s8"], O, I, 0), z[f"c{i}_y8"])]:
+                qt = eng.qt_upload(*args)
+                yd = eng.empty((S, O), torch.float32)
+                eng.matmul_qt(yd, eng.to_dev(x), qt, S)
+                y = eng.to_host(yd)
+                eng.qt_free(qt)
+                assert bits_equal(y, ref), (i, args[0], first_mismatch(y, ref))
 
 
 # ───────────────────────── expert FFN / MoE layer ─────────────────────────
@@ -292,59 +318,3 @@ def test_missing_expert_is_an_error(gpu, oracle):
 
 
 # ───────────────────────── persistent MoE sequence ─────────────────────────
-
-@pytest.fixture(scope="module")
-def seq_setup(gpu, oracle):
-    """Two GPT-OSS-20B-shaped MoE layers with 8 full-size experts each."""
-    import picchio_amd as pa
-    cfg = pa.gptoss_cfg(n_layers=2, n_experts=8, ctx_len=16, vocab=64)
-    model = oracle.model_build(cfg, 99, 0)
-    eng = pa.Engine(cfg)
-    D, E = cfg.hidden, cfg.n_experts
-    for l in range(cfg.n_layers):
-        for e in range(E):
-            eng.store_expert(l, e, *oracle.expert_arrays(model, l, e, cfg))
-        eng.store_router(l, oracle.tensor(model, 6, l, E * D), oracle.tensor(model, 7, l, E))
-    yield cfg, model, eng
-    eng.close()
-    oracle.model_free(model)
-
-
-@pytest.mark.parametrize("chain", [True, False])
-def test_moe_seq_parity(seq_setup, oracle, chain):
-    """One persistent launch over T steps == moe_forward step by step."""
-    import torch
-    cfg, model, eng = seq_setup
-    D, K, E, T = cfg.hidden, cfg.topk, cfg.n_experts, 9
-    layers = np.array([t % cfg.n_layers for t in range(T)], np.int32)
-    xs = np.stack([_token_x(oracle, cfg, 300 + t) for t in range(T)])
-    ld = eng.to_dev(layers)
-    xd = eng.to_dev(xs)
-    od = eng.empty((T, D), torch.float32)
-    eng.moe_forward_seq(ld, xd, od, T, chain=chain)
-    eng.moe_seq_status()
-    got = eng.to_host(od)
-    for t in range(T):
-        ref = np.empty(D, np.float32)
-        lg = np.empty(E, np.float32)
-        oracle.moe_forward(model, int(layers[t]), xs[t], ref, None, None, lg)
-        srt = np.sort(lg)[::-1]
-        if srt[K - 1] - srt[K] > 1e-5:
-            assert rel_l2(got[t], ref) < 1e-5, (t, rel_l2(got[t], ref))
-
-
-def test_moe_seq_repeatable(seq_setup, oracle):
-    """Two launches give identical bits (fixed reduction and combine order)."""
-    import torch
-    cfg, model, eng = seq_setup
-    D, T = cfg.hidden, 6
-    layers = np.array([1, 0, 1, 1, 0, 0], np.int32)
-    xs = np.stack([_token_x(oracle, cfg, 400 + t) for t in range(T)])
-    ld, xd = eng.to_dev(layers), eng.to_dev(xs)
-    outs = []
-    for _ in range(2):
-        od = eng.empty((T, D), torch.float32)
-        eng.moe_forward_seq(ld, xd, od, T, chain=False)
-        eng.moe_seq_status()
-        outs.append(eng.to_host(od))
-    assert bits_equal(outs[0], outs[1])
