@@ -279,6 +279,19 @@ int pk_quantize_act_i8x3(pk_engine *e, const float *x_dev, int rows, int cols,
 int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev, int T,
                          float *out_dev, int32_t *sel_dev, float *w_dev);
 
+/* No counterpart in the reference: pk_moe_forward_batch for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * that forbid it). Same arguments and results (the same kernels), but its
+ * scratch (router logits, routing, the pairs' activations and outputs) is a
+ * fixed 16 MiB device array, one per GPU, held until the process ends; the
+ * call allocates and frees nothing. Up to about 120 tokens of the
+ * GPT-OSS-20B shape fit (hidden 2880, top-4); a T that needs more scratch is
+ * refused with PK_ERR_UNSUPPORTED. Calls on one GPU share that array: calls
+ * that overlap on one GPU (other engines or streams) race, and each call
+ * leaves its contents behind. */
+int pk_moe_forward_batch_noalloc(pk_engine *e, int layer, const float *x_dev, int T,
+                                 float *out_dev, int32_t *sel_dev, float *w_dev);
+
 /* gqa_attention (picchio.c:504-623) for one token at `pos`; writes K/V. */
 int pk_gqa_attention(pk_engine *e, int layer, const float *x_dev, int pos,
                      float *out_dev);

@@ -135,6 +135,7 @@ def lib():
         "pk_expert_down": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
         "pk_moe_forward": (C.c_int, [vp, C.c_int, vp, vp, vp, vp]),
         "pk_moe_forward_batch": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
+        "pk_moe_forward_batch_noalloc": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
         "pk_moe_forward_grouped": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp, vp, vp]),
         "pk_quantize_act_i8x3": (C.c_int, [vp, vp, C.c_int, C.c_int, vp, vp]),
         "pk_gqa_attention": (C.c_int, [vp, C.c_int, vp, C.c_int, vp]),

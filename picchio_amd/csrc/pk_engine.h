@@ -109,6 +109,7 @@ struct pk_engine {
     int64_t prof_cnt[PK_PROF_N] = {0};
 
     int n_cu = 256;                          // compute units of the device
+    uint8_t *noalloc_scratch = nullptr;      // this device's fixed scratch array (pk_noalloc_scratch_init)
 
     // batched MoE scratch for up to batch_cap tokens (pk_prefill.hip)
     int64_t batch_cap = 0;
@@ -138,6 +139,12 @@ struct pk_engine {
     float *samp_av = nullptr;
     int32_t *samp_ai = nullptr;
 };
+
+// Fixed device array of pk_moe_forward_batch_noalloc (pk_prefill.hip): its
+// size, and its address on the engine's device into e->noalloc_scratch.
+constexpr int64_t PK_NOALLOC_SCRATCH_BYTES = 16ll << 20;
+constexpr int PK_NOALLOC_MAX_DEVICES = 64;
+int pk_noalloc_scratch_init(pk_engine *e);
 
 int pk_dev_alloc(pk_engine *e, void **p, int64_t bytes);
 void pk_dev_free(pk_engine *e, void *p);

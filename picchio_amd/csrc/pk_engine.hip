@@ -177,6 +177,7 @@ static int engine_init(pk_engine *e) {
     const int half = c->moe_inter / 2;
     e->ex = make_layout(c);
     PK_HIP(hipDeviceGetAttribute(&e->n_cu, hipDeviceAttributeMultiprocessorCount, e->device));
+    PK_TRY(pk_noalloc_scratch_init(e));
     ALLOC(e->store, e->ex.stride * (int64_t)L * E);
     e->expert_ready = (uint8_t *)calloc((size_t)L * E, 1);
     PK_CHECK(e->expert_ready, PK_ERR_OOM, "host allocation failed");

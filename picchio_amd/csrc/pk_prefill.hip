@@ -15,6 +15,7 @@
 #include <stdlib.h>
 
 #include <algorithm>
+#include <mutex>
 
 namespace {
 
@@ -114,19 +115,31 @@ static int batch_reserve(pk_engine *e, int T) {
     return PK_OK;
 }
 
-// Router logits, top-k and softmax of T rows into b_sel / b_w. The prompt's
+// Scratch of the batched MoE over T rows: router logits, routing, the
+// chunk's expert order, the pairs' activations and outputs, and the
+// integer-dot records and pair tiles.
+struct rows_scratch {
+    float *logits, *w, *act, *eo;
+    int32_t *sel, *perm, *xq, *actq, *pairs, *tiles;
+};
+
+static rows_scratch engine_rows_scratch(pk_engine *e) {
+    return {e->b_logits, e->b_w, e->b_act, e->b_eo, e->b_sel, e->b_perm, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles};
+}
+
+// Router logits, top-k and softmax of T rows into sc.sel / sc.w. The prompt's
 // router (picchio.c:1840-1844) starts each dot at the bias and adds the
 // products in order; the lockstep decode of several sequences sums them in a
 // fixed tree and adds the bias last (within the fp32 bar of moe_forward's
 // order, picchio.c:1316-1324).
-static int route_rows(pk_engine *e, int layer, const float *x, int T, bool prompt_order) {
+static int route_rows(pk_engine *e, const rows_scratch &sc, int layer, const float *x, int T, bool prompt_order) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[layer];
     if (prompt_order)
-        PK_TRY(pk_launch_router_seq(x, d.router, d.router_b, T, c->hidden, c->n_experts, e->b_logits, e->stream));
+        PK_TRY(pk_launch_router_seq(x, d.router, d.router_b, T, c->hidden, c->n_experts, sc.logits, e->stream));
     else
-        PK_TRY(pk_launch_gemv_f32(e->b_logits, x, d.router, d.router_b, T, c->hidden, c->n_experts, e->stream));
-    return pk_launch_topk_batch(e->b_logits, T, c->n_experts, c->topk, c->routed_scale, e->b_sel, e->b_w, nullptr,
+        PK_TRY(pk_launch_gemv_f32(sc.logits, x, d.router, d.router_b, T, c->hidden, c->n_experts, e->stream));
+    return pk_launch_topk_batch(sc.logits, T, c->n_experts, c->topk, c->routed_scale, sc.sel, sc.w, nullptr,
                                 e->stream);
 }
 
@@ -135,39 +148,38 @@ static int route_rows(pk_engine *e, int layer, const float *x, int T, bool promp
 // batch's expert order, of (w_k * routed_scale) * expert_k(x[t]). With
 // decode_order the sum runs in routing order instead, as moe_forward adds
 // (picchio.c:1445-1454): T independent decode tokens.
-static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
-                    bool decode_order = false) {
+static int moe_rows_on(pk_engine *e, const rows_scratch &sc, int layer, const float *x, int T, float *out,
+                       const float *residual, bool decode_order) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
-    PK_TRY(batch_reserve(e, T));
-    PK_TRY(route_rows(e, layer, x, T, !decode_order));
+    PK_TRY(route_rows(e, sc, layer, x, T, !decode_order));
     if (!decode_order) {
-        hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
+        hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, sc.sel, T, K, E, sc.perm);
         PK_HIP(hipGetLastError());
     }
     // the integer-dot option: records of the token rows, then of each pair's SwiGLU outputs
     // (the lockstep decode of several sequences, decode_order, uses it by default)
     const bool dot = (e->i4_dot || (decode_order && e->i4_dot_batch)) && D % 64 == 0 && c->moe_inter % 128 == 0;
     const int64_t xq_row = (int64_t)(D / 32) * PK_XQ_INTS, aq_row = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
-    if (dot) PK_TRY(pk_launch_act_records(x, T * D, e->b_xq, e->stream));
+    if (dot) PK_TRY(pk_launch_act_records(x, T * D, sc.xq, e->stream));
     pk_i4_items gu = pk_expert_items(e, layer, false);
-    gu.slots = e->b_sel;
+    gu.slots = sc.sel;
     gu.x = x; gu.x_stride = D; gu.x_div = K;
-    gu.y = e->b_act; gu.y_stride = half;
+    gu.y = sc.act; gu.y_stride = half;
     gu.n_items = T * K;
     if (dot) {
-        gu.xq = e->b_xq; gu.xq_stride = xq_row;
-        gu.yq = e->b_actq; gu.yq_stride = aq_row;
+        gu.xq = sc.xq; gu.xq_stride = xq_row;
+        gu.yq = sc.actq; gu.yq_stride = aq_row;
     }
     // with the integer dot, pairs of one expert share each weight load (tiles of 4)
     const int P = T * K;
     const int mt = P / 4 + 1 + E;
-    pk_i4_tiles tl{e->b_pairs, e->b_tiles, e->b_tiles + mt, e->b_tiles + 2 * mt, e->b_tiles + 3 * mt};
+    pk_i4_tiles tl{sc.pairs, sc.tiles, sc.tiles + mt, sc.tiles + 2 * mt, sc.tiles + 3 * mt};
     // (the tile kernel keeps 4 pairs' group sums in LDS: rows of at most 64 groups)
     const bool tiled = dot && !e->dot_tiles_off && e->ex.gu.NG <= 64 && e->ex.dn.NG <= 64 && E <= 128;
     if (tiled)
-        PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->b_pairs, e->b_tiles, e->b_tiles + mt,
-                                     e->b_tiles + 2 * mt, e->b_tiles + 3 * mt, e->stream, 4));
+        PK_TRY(pk_launch_group_pairs(sc.sel, P, E, sc.pairs, sc.tiles, sc.tiles + mt,
+                                     sc.tiles + 2 * mt, sc.tiles + 3 * mt, e->stream, 4));
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
     if (tiled)
         PK_TRY(pk_launch_i4_dot_tiles(gu, tl, e->ex.gu, PK_EPI_SWIGLU, c->swiglu_limit, c->swiglu_alpha, mt,
@@ -177,12 +189,12 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
                                  e->stream));
     PK_TRY(pk_prof_end(e, ps));
     pk_i4_items dn = pk_expert_items(e, layer, true);
-    dn.slots = e->b_sel;
-    dn.x = e->b_act; dn.x_stride = half;
-    dn.y = e->b_eo; dn.y_stride = D;
+    dn.slots = sc.sel;
+    dn.x = sc.act; dn.x_stride = half;
+    dn.y = sc.eo; dn.y_stride = D;
     dn.n_items = T * K;
     if (dot) {
-        dn.xq = e->b_actq; dn.xq_stride = aq_row;
+        dn.xq = sc.actq; dn.xq_stride = aq_row;
     }
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
     if (tiled)
@@ -191,9 +203,15 @@ static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, 
         PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
-                       e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);
+                       sc.eo, sc.w, decode_order ? nullptr : sc.perm, K, D);
     PK_HIP(hipGetLastError());
     return PK_OK;
+}
+
+static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
+                    bool decode_order = false) {
+    PK_TRY(batch_reserve(e, T));
+    return moe_rows_on(e, engine_rows_scratch(e), layer, x, T, out, residual, decode_order);
 }
 
 static int grouped_reserve(pk_engine *e, int T) {
@@ -233,7 +251,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
         PK_HIP(hipMemcpyAsync(e->b_sel, sel_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
         PK_HIP(hipMemcpyAsync(e->b_w, w_in, (size_t)P * 4, hipMemcpyDeviceToDevice, e->stream));
     } else {
-        PK_TRY(route_rows(e, layer, x, T, !decode_order));
+        PK_TRY(route_rows(e, engine_rows_scratch(e), layer, x, T, !decode_order));
     }
     if (!decode_order) {
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
@@ -309,6 +327,77 @@ extern "C" int pk_moe_forward_batch(pk_engine *e, int layer, const float *x_dev,
         PK_HIP(hipMemcpyAsync(sel_dev, e->b_sel, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
     if (w_dev)
         PK_HIP(hipMemcpyAsync(w_dev, e->b_w, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    return PK_OK;
+}
+
+// ───────────── the batched MoE on a fixed device array ─────────────
+// For callers that cannot allocate (graph capture, serving loops): the
+// scratch of pk_moe_forward_batch_noalloc lives in this file-scope array,
+// one copy per GPU for the life of the process. Host code uses the address
+// hipGetSymbolAddress returns on each device (pk_noalloc_scratch_init, at
+// engine creation), never the array's name.
+static __device__ __align__(256) uint8_t scratch[PK_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static uint8_t *g_scratch_dev[PK_NOALLOC_MAX_DEVICES];
+
+int pk_noalloc_scratch_init(pk_engine *e) {
+    PK_CHECK(e->device >= 0 && e->device < PK_NOALLOC_MAX_DEVICES, PK_ERR_UNSUPPORTED,
+             "device %d: no fixed scratch beyond %d devices", e->device, PK_NOALLOC_MAX_DEVICES);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[e->device]) {
+        int cur = 0;
+        PK_HIP(hipGetDevice(&cur));
+        if (cur != e->device) PK_HIP(hipSetDevice(e->device));
+        void *p = nullptr;
+        const hipError_t rc = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (cur != e->device) PK_HIP(hipSetDevice(cur));
+        PK_CHECK(rc == hipSuccess && p, PK_ERR_HIP, "hipGetSymbolAddress(scratch) on device %d: %s", e->device,
+                 hipGetErrorString(rc));
+        g_scratch_dev[e->device] = (uint8_t *)p;
+    }
+    e->noalloc_scratch = g_scratch_dev[e->device];
+    return PK_OK;
+}
+
+// The pieces of rows_scratch for T rows carved from base (256-byte aligned,
+// the sizes batch_reserve allocates); returns the bytes used.
+static int64_t rows_scratch_carve(pk_engine *e, int T, uint8_t *base, rows_scratch *sc) {
+    const pk_cfg *c = &e->c;
+    const int64_t TK = (int64_t)T * c->topk;
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) { uint8_t *p = base ? base + off : nullptr; off = pk_align256(off + bytes); return p; };
+    sc->logits = (float *)take((int64_t)T * c->n_experts * 4);
+    sc->w = (float *)take(TK * 4);
+    sc->sel = (int32_t *)take(TK * 4);
+    sc->perm = (int32_t *)take(TK * 4);
+    sc->act = (float *)take(TK * (c->moe_inter / 2) * 4);
+    sc->eo = (float *)take(TK * c->hidden * 4);
+    sc->xq = (int32_t *)take((int64_t)T * ((c->hidden + 31) / 32) * PK_XQ_INTS * 4);
+    sc->actq = (int32_t *)take(TK * e->ex.gu.RB * PK_XQ_INTS * 4);
+    sc->pairs = (int32_t *)take(TK * 4);
+    sc->tiles = (int32_t *)take((3 * (TK / 4 + 1 + c->n_experts) + 1) * 4);
+    return off;
+}
+
+extern "C" int pk_moe_forward_batch_noalloc(pk_engine *e, int layer, const float *x_dev, int T, float *out_dev,
+                                            int32_t *sel_dev, float *w_dev) {
+    PK_CHECK(e && x_dev && out_dev && T > 0, PK_ERR_ARG, "bad argument");
+    PK_CHECK(e->noalloc_scratch, PK_ERR_HIP, "fixed scratch not set up on device %d", e->device);
+    PK_CHECK((int64_t)T * e->c.topk <= 65535, PK_ERR_UNSUPPORTED, "batched MoE: %d tokens x top-%d", T, e->c.topk);
+    PK_TRY(pk_check_layer_experts(e, layer));
+    rows_scratch sc{};
+    const int64_t need = rows_scratch_carve(e, T, nullptr, &sc);
+    PK_CHECK(need <= PK_NOALLOC_SCRATCH_BYTES, PK_ERR_UNSUPPORTED,
+             "moe_forward_batch_noalloc: %d tokens need %lld bytes of scratch, the fixed array holds %lld", T,
+             (long long)need, (long long)PK_NOALLOC_SCRATCH_BYTES);
+    rows_scratch_carve(e, T, e->noalloc_scratch, &sc);
+    PK_TRY(moe_rows_on(e, sc, layer, x_dev, T, out_dev, nullptr, false));
+    const int K = e->c.topk;
+    if (sel_dev)
+        PK_HIP(hipMemcpyAsync(sel_dev, sc.sel, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
+    if (w_dev)
+        PK_HIP(hipMemcpyAsync(w_dev, sc.w, (size_t)T * K * 4, hipMemcpyDeviceToDevice, e->stream));
     return PK_OK;
 }
 
