@@ -1,19 +1,25 @@
 #!/usr/bin/env python3
 """Benchmark of the INT4 expert path on one MI355X.
 
-Workload: one GPT-OSS-20B-shaped MoE layer at batch-1
-decode — RMSNorm'd fp32 x [2880], fp32 router [32x2880] + bias, top-4 of 32
-INT4 gs64 experts (gate_up 5760x2880, down 2880x2880, biases), clamped SwiGLU,
-softmax-weighted combine — over fresh seeded tokens. A "step" is one token
-through that layer. Token t uses layer copy t % L (L = 24 by default, the
-20B model's MoE layers, 10.8 GB of experts) so the expert bytes come from HBM,
-not from the 256 MB MALL; --layers 1 gives the single-layer figure.
+Default run (no --mode): BASELINE config 1 is the headline `value`; config 2
+(20B-shaped greedy decode) and config 4 (120B-shaped decode at batch 1 and
+32) are timed in the same process and reported under `config`.
+
+Config 1: one GPT-OSS-20B-shaped MoE layer at
+batch-1 decode -- RMSNorm'd fp32 x [2880], fp32 router [32x2880] + bias,
+top-4 of 32 INT4 gs64 experts (gate_up 5760x2880, down 2880x2880, biases),
+clamped SwiGLU, softmax-weighted combine -- over fresh seeded tokens. A
+"step" is one token through that layer, three launches (router, gate_up
+with the in-launch top-4, down with the combine) replayed from a HIP graph.
+Token t uses layer copy t % L (L = 24, the 20B model's MoE layers, 10.8 GB of
+experts) so the expert bytes come from HBM, not from the 256 MB MALL.
 
 value = algorithmic HBM bytes per token (experts + router + x/out) x tokens/s.
-roofline = the dominant kernel (INT4 gate_up GEMV + SwiGLU, four experts per
-launch), its algorithmic bytes per launch / its mean duration from HIP events
-on the engine stream. cpu_baseline = picchio's MoE layer on the host cores
-(oracle/_ref build of the reference when present, else the C restatement).
+roofline = the dominant kernel (gate_up + SwiGLU, four routed experts per
+launch): its algorithmic bytes per launch / its mean duration, from HIP
+events on the engine stream around each of its launches in eager layers.
+cpu_baseline = picchio's MoE layer on the host cores (oracle/_ref build of
+the reference when present, else the C restatement).
 """
 import argparse
 import json
@@ -39,6 +45,25 @@ TOKEN_BYTES = K * EXPERT_BYTES + ROUTER_BYTES + 2 * D * 4      # 56,517,248
 # WRITE_SIZE 45.04 KiB x 1.000, the factors being what the two counters read
 # for a plain copy kernel over 1 GiB.
 GATE_UP_TRAFFIC = 37780589
+
+
+def host_info():
+    """CPU model, threads available to this process, NUMA nodes of the host."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nodes = sorted(d for d in os.listdir("/sys/devices/system/node") if d.startswith("node"))
+    except OSError:
+        nodes = []
+    return {"cpu_model": model, "threads_available": len(os.sched_getaffinity(0)),
+            "numa_nodes": len(nodes), "nproc": os.cpu_count()}
 
 
 def gate_up_bytes(n):
@@ -175,13 +200,13 @@ def parse_sampling(spec):
     return float(t), float(p), int(k), float(r)
 
 
-def run_decode(args):
+def measure_decode20b(args, steps, warmup, cpu_on):
     """GPT-OSS-20B-shaped model, 512-token prompt through
     prefill_tokens, then `steps` greedy decode steps replayed from the
     captured step graph. value = decode tokens/s."""
     import torch
     import picchio_amd as pa
-    n_prompt, steps = 512, args.steps
+    n_prompt = 512
     cfg = pa.gptoss_cfg(ctx_len=n_prompt + steps + 1)
     eng = pa.Engine(cfg)
     t0 = time.perf_counter()
@@ -200,7 +225,7 @@ def run_decode(args):
     # (the sampler restarts from the same seed before each run)
     if sampling:
         eng.set_sampling(*sampling, args.seed)
-    warm = eng.decode_replay(nxt, n_prompt, max(args.warmup, 1))
+    warm = eng.decode_replay(nxt, n_prompt, max(warmup, 1))
     if sampling:
         eng.set_sampling(*sampling, args.seed)
     ev0 = torch.cuda.Event(enable_timing=True)
@@ -222,12 +247,14 @@ def run_decode(args):
     bpt = sum(decode_bytes_per_token(cfg, n_prompt + i) for i in range(steps)) / steps
     lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
     cpu = None
-    if not args.no_cpu:
+    if cpu_on:
         cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    print(f"[bench] config 2: {tok_s:.1f} tok/s ({ms / steps * 1e3:.1f} us/token), prefill "
+          f"{prefill_s:.3f} s", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
-        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms / steps, 5),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "config2: GPT-OSS-20B-shaped " + ("sampled" if sampling else "greedy") +
@@ -249,10 +276,10 @@ def run_decode(args):
                      "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line))
+    return line
 
 
-def run_decode120b(args):
+def measure_decode120b(args, steps, warmup, cpu_on):
     """GPT-OSS-120B-shaped model (36 layers, 128 INT4 experts
     per layer, ~65 GB of experts resident in HBM), a 4096-position KV context
     filled with synthetic rows, then `steps` greedy decode steps at batch 1
@@ -260,7 +287,7 @@ def run_decode120b(args):
     lockstep). value = batch-1 tokens/s."""
     import torch
     import picchio_amd as pa
-    ctx, steps, B = 4096, args.steps, 32
+    ctx, B = 4096, 32
     cfg = pa.gptoss_cfg(n_layers=36, n_experts=128, ctx_len=ctx + steps + 1)
     eng = pa.Engine(cfg)
     t0 = time.perf_counter()
@@ -274,7 +301,7 @@ def run_decode120b(args):
     # batch 1
     eng.kv_fill_synthetic(0, ctx, args.seed)
     tok = int(rng.integers(0, cfg.vocab))
-    warm = eng.decode_replay(tok, ctx, max(args.warmup, 1))
+    warm = eng.decode_replay(tok, ctx, max(warmup, 1))
     ev0.record(eng.stream)
     toks1 = eng.decode_replay(tok, ctx, steps)
     ev1.record(eng.stream)
@@ -290,7 +317,7 @@ def run_decode120b(args):
     for sq in range(B):
         eng.kv_fill_synthetic(sq, ctx, args.seed + sq)
     first = rng.integers(0, cfg.vocab, B).astype(np.int32)
-    eng.decode_batch(first, ctx, max(args.warmup, 1))
+    eng.decode_batch(first, ctx, max(warmup, 1))
     ev0.record(eng.stream)
     out32 = eng.decode_batch(first, ctx, steps)
     ev1.record(eng.stream)
@@ -311,12 +338,14 @@ def run_decode120b(args):
     bstep32 = dense + cfg.n_layers * uniq * expert + B * kv_bytes(ctx + steps // 2)
     lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
     cpu = None
-    if not args.no_cpu:
+    if cpu_on:
         cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, first)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+    print(f"[bench] config 4: batch 1 {tok1:.1f} tok/s, batch 32 {tok32:.1f} tok/s", file=sys.stderr,
+          flush=True)
     line = {
         "metric": METRIC, "value": round(tok1, 2), "unit": "tok/s", "n_gpus": 1,
-        "steps": steps, "warmup": args.warmup, "ms_per_step": round(ms1 / steps, 5),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms1 / steps, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "config4: GPT-OSS-120B-shaped greedy decode (36 layers, 128 INT4 experts, "
@@ -339,7 +368,7 @@ def run_decode120b(args):
                      "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line))
+    return line
 
 
 def zipf_routing(T, E, K, seed, s=1.1, lo=16, hi=512):
@@ -468,140 +497,91 @@ def run_prefill(args):
     print(json.dumps(line))
 
 
-def main():
-    ap = argparse.ArgumentParser()
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000, help="timed tokens")
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--layers", type=int, default=24, help="distinct MoE layer copies")
-    ap.add_argument("--seed", type=int, default=1)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--profile-tokens", type=int, default=400)
-    ap.add_argument("--calib-copy-mib", type=int, default=0,
-                    help="after the timed region, run a plain read+write kernel over this many "
-                         "MiB (the scale for rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
-    ap.add_argument("--sample", default="",
-                    help="decode mode: draw tokens on the device with T,top_p,top_k,rep "
-                         "(e.g. 1.0,0.95,50,1.1, picchio's defaults) instead of greedy")
-    ap.add_argument("--mode", choices=["kernels", "decode", "prefill", "decode120b"], default="kernels",
-                    help="kernels: three kernels per step (router+top-k, gate_up+SwiGLU, "
-                         "down+combine) replayed from a HIP graph; decode: config 2, the whole 20B-shaped "
-                         "model (use --steps 256); prefill: config 3, grouped MFMA MoE (--steps 20); "
-                         "decode120b: config 4, 120B shape at batch 1 and 32 (--steps 128)")
-    args = ap.parse_args()
-    if args.gpus != 1:
-        print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
-              "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
-        sys.exit(2)
-    if args.mode == "decode":
-        run_decode(args)
-        return
-    if args.mode == "prefill":
-        run_prefill(args)
-        return
-    if args.mode == "decode120b":
-        run_decode120b(args)
-        return
-
+def measure_moe_layer(args):
+    """the batch-1 MoE layer over fresh seeded tokens."""
     import torch
     import picchio_amd as pa
 
     L = args.layers
     cfg = pa.gptoss_cfg(n_layers=L, n_experts=E, ctx_len=16, vocab=64)
     eng = pa.Engine(cfg)
+    if args.dot >= 0:
+        eng.set_i4_dot(args.dot == 1)
     t0 = time.perf_counter()
     eng.build_synthetic(args.seed, what=1)
     build_s = time.perf_counter() - t0
     print(f"[bench] store built: {L} layers x {E} experts, {eng.device_bytes() / 1e9:.2f} GB in "
           f"{build_s:.1f} s", file=sys.stderr, flush=True)
 
-    n_tok = args.warmup + args.steps
+    W, S = args.warmup, args.steps
+    n_tok = W + S
     x = token_inputs(n_tok, 1000 + args.seed)
     xd = eng.to_dev(x)
     od = eng.empty((n_tok, D), torch.float32)
-    layers = np.array([t % L for t in range(n_tok)], np.int32)
-    ld = eng.to_dev(layers)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
-    W, S = args.warmup, args.steps
 
-    if True:
-        def enqueue(t):
-            eng.moe_forward(t % L, xd[t], od[t])
-        eng.capture_begin()
-        for t in range(W):
-            enqueue(t)
-        g_warm = eng.capture_end()
-        eng.capture_begin()
-        for t in range(W, n_tok):
-            enqueue(t)
-        g_run = eng.capture_end()
-        eng.graph_launch(g_warm)
-        eng.sync()
-        torch.cuda.synchronize()
-        ev0.record(eng.stream)
-        eng.graph_launch(g_run)
-        ev1.record(eng.stream)
-        ev1.synchronize()
-        ms = ev0.elapsed_time(ev1)
-        eng.graph_destroy(g_warm)
-        eng.graph_destroy(g_run)
-        # The dominant kernel alone: each token's gate_up launch (4 experts of
-        # its layer copy, the same k_i4_gemv<SWIGLU> the MoE step runs)
-        # replayed back to back from a graph; HIP events on the engine stream
-        # around the replay / launches = the mean launch duration.
-        n_prof = min(args.profile_tokens, S)
-        rng = np.random.default_rng(7)
-        eids = np.stack([rng.choice(E, K, replace=False) for _ in range(n_prof)]).astype(np.int32)
-        eids_d = eng.to_dev(eids)
-        act = eng.empty((E, HALF), torch.float32)
-        eo = eng.empty((E, D), torch.float32)
-        all_e = eng.to_dev(np.arange(E, dtype=np.int32))
-        gu_ms = replay_ms(eng, ev0, ev1, n_prof,
-                          lambda t: eng.expert_gate_up(t % L, eids_d[t], xd[t], act))
-        dn_ms = replay_ms(eng, ev0, ev1, n_prof,
-                          lambda t: eng.expert_down(t % L, eids_d[t], act, eo))
-        # streaming shape: all 32 experts of a layer copy in one gate_up launch
-        st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act))
-        prof = {"gate_up": gu_ms, "down": dn_ms, "gate_up_32_experts": st_ms}
-        roof_bytes = gate_up_bytes(K)
-        roof_ms = gu_ms
-        roof_kernel = "k_i4_gemv<15,3,SWIGLU> (gate_up + bias + SwiGLU, 4 experts/launch)"
-        traffic = GATE_UP_TRAFFIC
-        extra = {"down_gbps": round(down_bytes(K) / (dn_ms * 1e-3) / 1e9, 1),
-                 "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
-                 "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
-                                                      / HBM_PEAK_GBPS, 4)}
+    # timed region: S tokens, three launches each, replayed from one graph
+    def enqueue(t):
+        eng.moe_forward(t % L, xd[t], od[t])
+    eng.capture_begin()
+    for t in range(W):
+        enqueue(t)
+    g_warm = eng.capture_end()
+    eng.capture_begin()
+    for t in range(W, n_tok):
+        enqueue(t)
+    g_run = eng.capture_end()
+    eng.graph_launch(g_warm)
+    eng.sync()
+    torch.cuda.synchronize()
+    ev0.record(eng.stream)
+    eng.graph_launch(g_run)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms = ev0.elapsed_time(ev1)
+    eng.graph_destroy(g_warm)
+    eng.graph_destroy(g_run)
 
-    if args.calib_copy_mib:
-        n = args.calib_copy_mib << 18                       # fp32 elements
-        src = torch.ones(n, device="cuda")
-        dst = torch.empty_like(src)
-        for _ in range(3):
-            torch.neg(src, out=dst)                         # reads n*4 B, writes n*4 B
-        torch.cuda.synchronize()
-        del src, dst
+    # each kernel of the layer as the layer runs it: eager layers with HIP
+    # events on the engine stream around every router / gate_up / down launch
+    n_prof = min(args.profile_tokens, S)
+    eng.profile(True)
+    for t in range(W, W + n_prof):
+        enqueue(t)
+    kern = {}
+    for name, kind in (("router", pa.PROF_ROUTER), ("gate_up", pa.PROF_EXPERT_GATE_UP),
+                       ("down_combine", pa.PROF_EXPERT_DOWN)):
+        tot, cnt = eng.profile_read(kind)
+        kern[name] = tot / max(cnt, 1)
+    eng.profile(False)
+    # streaming shape: all 32 experts of a layer copy in one gate_up launch
+    act = eng.empty((E, HALF), torch.float32)
+    all_e = eng.to_dev(np.arange(E, dtype=np.int32))
+    st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act))
+    dot_on = args.dot == 1 or (args.dot < 0 and os.environ.get("PK_I4_DOT", "0") not in ("", "0"))
+    arith = "integer-dot" if dot_on else "fp32 chains (bit-exact with quant.h)"
+    eng.close()
 
     ms_tok = ms / S
     gbps = TOKEN_BYTES / (ms_tok * 1e-3) / 1e9
-    achieved = roof_bytes / (roof_ms * 1e-3) / 1e9
-    print(f"[bench] {S} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, {gbps:.1f} GB/s; "
-          f"kernel {achieved:.1f} GB/s; {extra}", file=sys.stderr, flush=True)
-    eng.close()
-
+    gu_bytes = gate_up_bytes(K)
+    achieved = gu_bytes / (kern["gate_up"] * 1e-3) / 1e9
+    print(f"[bench] config 1: {S} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, {gbps:.1f} GB/s; "
+          f"kernels (us) " + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in kern.items()) +
+          f"; gate_up {achieved:.1f} GB/s ({arith})", file=sys.stderr, flush=True)
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(x[:4000], args.seed, args.cpu_seconds)
+        cpu.update(host_info())
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
-
-    line = {
+    return {
         "metric": METRIC,
         "value": round(gbps, 2),
         "unit": "GB/s",
         "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": args.warmup,
+        "steps": S,
+        "warmup": W,
         "ms_per_step": round(ms_tok, 5),
         "higher_is_better": True,
         "scaling": "weak",
@@ -611,16 +591,78 @@ def main():
         "config": {"workload": "config1: GPT-OSS-20B MoE layer, batch-1 decode, top-4 of 32 "
                                "INT4 gs64 experts, fresh seeded tokens",
                    "layer_copies": L, "experts": E, "topk": K, "hidden": D, "weights": "int4-gs64",
+                   "expert_arithmetic": arith,
                    "bytes_per_token": TOKEN_BYTES, "tokens_per_s": round(1e3 / ms_tok, 1),
-                   "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
-                   "mode": args.mode, "chained": True,
-                   "kernel_us": {k: round(v * 1e3, 3) for k, v in prof.items()}, **extra},
+                   "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "chained": True,
+                   "kernel_us": {k: round(v * 1e3, 3) for k, v in kern.items()},
+                   "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
+                   "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
+                                                        / HBM_PEAK_GBPS, 4)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
-                     "kernel": roof_kernel, "bytes_per_launch": roof_bytes,
-                     "mean_us": round(roof_ms * 1e3, 3)},
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": GATE_UP_TRAFFIC,
+                     "kernel": "k_i4_gemv<SWIGLU> (gate_up + bias + SwiGLU, the layer's 4 routed experts "
+                               "per launch, top-4 selected in the launch)",
+                     "bytes_per_launch": gu_bytes, "mean_us": round(kern["gate_up"] * 1e3, 3)},
         "cpu_baseline": cpu,
     }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000, help="timed tokens (config 1) or decode steps")
+    ap.add_argument("--warmup", type=int, default=100)
+    ap.add_argument("--layers", type=int, default=24, help="distinct MoE layer copies (config 1)")
+    ap.add_argument("--seed", type=int, default=1)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--profile-tokens", type=int, default=400)
+    ap.add_argument("--dot", type=int, default=-1,
+                    help="config 1 expert arithmetic: 1 integer dot, 0 fp32 chains, -1 the engine's default")
+    ap.add_argument("--decode-steps", type=int, default=128,
+                    help="default run: decode steps of configs 2 and 4")
+    ap.add_argument("--sample", default="",
+                    help="decode mode: draw tokens on the device with T,top_p,top_k,rep "
+                         "(e.g. 1.0,0.95,50,1.1, picchio's defaults) instead of greedy")
+    ap.add_argument("--mode", choices=["all", "kernels", "decode", "prefill", "decode120b"], default="all",
+                    help="all (default): config 1 headline with configs 2 and 4 under config; "
+                         "kernels: config 1 only; decode: config 2 (use --steps 256); prefill: "
+                         "config 3, grouped MFMA MoE (--steps 20); decode120b: config 4 (--steps 128)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
+              "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
+        sys.exit(2)
+    if args.mode == "decode":
+        print(json.dumps(measure_decode20b(args, args.steps, args.warmup, not args.no_cpu)))
+        return
+    if args.mode == "prefill":
+        run_prefill(args)
+        return
+    if args.mode == "decode120b":
+        print(json.dumps(measure_decode120b(args, args.steps, args.warmup, not args.no_cpu)))
+        return
+    line = measure_moe_layer(args)
+    if args.mode == "all":
+        # configs 2 and 4 in the same run: decode tok/s of both model shapes
+        # (the 120B CPU baseline is left out: its model build on the host
+        # takes minutes; --mode decode120b measures it)
+        ds = args.decode_steps
+        d20 = measure_decode20b(args, ds, 8, not args.no_cpu)
+        d120 = measure_decode120b(args, ds, 4, False)
+        line["config"]["decode_20b"] = {"tok_s": d20["value"], "ms_per_token": d20["ms_per_step"],
+                                        "steps": ds, **{k: d20["config"][k] for k in
+                                                        ("workload", "bytes_per_token", "hbm_gbps", "hbm_frac",
+                                                         "prefill_tok_s", "attention_us_per_layer")},
+                                        "lm_head_roofline": d20["roofline"], "cpu_baseline": d20["cpu_baseline"]}
+        line["config"]["decode_120b"] = {"batch1_tok_s": d120["config"]["batch1_tok_s"],
+                                         "steps": ds, **{k: d120["config"][k] for k in
+                                                         ("workload", "batch1_bytes_per_token", "batch1_hbm_gbps",
+                                                          "batch32_tok_s", "batch32_ms_per_step",
+                                                          "batch32_hbm_gbps")},
+                                         "lm_head_roofline": d120["roofline"],
+                                         "cpu_baseline": "not run by default (host model build takes minutes): "
+                                                         "bench.py --mode decode120b"}
     print(json.dumps(line))
 
 

@@ -51,6 +51,18 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
     const float *__restrict__ x = it.x + (int64_t)(item / it.x_div) * it.x_stride;
     const int32_t *__restrict__ xq = DOT ? it.xq + (int64_t)(item / it.x_div) * it.xq_stride : nullptr;
+    const int row = rb * 64 + lane;
+    // the epilogue's operands go out with the weights, not after the fold
+    // (a load issued there would put a memory round trip on the critical path)
+    float bias = 0.0f, res = 0.0f, cw[16];
+    if (wave == 0) {
+        if (it.off_bias >= 0) bias = reinterpret_cast<const float *>(base + it.off_bias)[min(row, O - 1)];
+        if constexpr (EPI == PK_EPI_COMBINE) {
+            if (cb.residual) res = cb.residual[min(row, O - 1)];
+#pragma unroll
+            for (int k = 0; k < 16; ++k) cw[k] = k < it.n_items ? cb.w[k] : 0.0f;
+        }
+    }
 
     for (int g0 = wave; g0 < NG; g0 += NW * GPW) {
         uint4 wa[GPW], wb[GPW];
@@ -87,9 +99,7 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     } else {
         for (int g = 0; g < NG; ++g) acc = __builtin_fmaf(part[g * 64 + lane], scl[g * 64 + lane], acc);
     }
-    const int row = rb * 64 + lane;
-    if (it.off_bias >= 0 && row < O)
-        acc = acc + reinterpret_cast<const float *>(base + it.off_bias)[row];
+    if (it.off_bias >= 0 && row < O) acc = acc + bias;
     float *y = it.y + (int64_t)item * it.y_stride;
     if constexpr (EPI == PK_EPI_SWIGLU) {
         const float up = __shfl_down(acc, 1, 64);
@@ -104,23 +114,30 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
         // row block adds them up in routing order, out = fma(w_k, eo_k, out),
         // then the residual (forward_token, picchio.c:1716), and re-arms the
         // block's arrival counter.
+        // Ordering: every lane's row store is followed by a release fence at
+        // device scope before lane 0 counts the item in (the wave issues the
+        // fence of all lanes before the count); the last arriver's lanes
+        // take an acquire fence before reading the other items' rows.
         if (row < O)
             __hip_atomic_store(y + row, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        __builtin_amdgcn_s_waitcnt(0);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         uint32_t arrived = 0;
         if (lane == 0)
             arrived = __hip_atomic_fetch_add(cb.counters + rb, 1u, __ATOMIC_RELAXED,
                                              __HIP_MEMORY_SCOPE_AGENT);
         arrived = __shfl(arrived, 0, 64);
         if (arrived != (uint32_t)(it.n_items - 1)) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
         if (row < O) {
             float o = 0.0f;
-            for (int k = 0; k < it.n_items; ++k)
-                o = __builtin_fmaf(cb.w[k],
-                                   __hip_atomic_load(it.y + (int64_t)k * it.y_stride + row,
-                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
-                                   o);
-            cb.out[row] = cb.residual ? cb.residual[row] + o : o;
+#pragma unroll
+            for (int k = 0; k < 16; ++k)
+                if (k < it.n_items)
+                    o = __builtin_fmaf(cw[k],
+                                       __hip_atomic_load(it.y + (int64_t)k * it.y_stride + row,
+                                                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT),
+                                       o);
+            cb.out[row] = cb.residual ? res + o : o;
         }
         if (lane == 0)
             __hip_atomic_store(cb.counters + rb, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -251,6 +268,7 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
     }
     if (epilogue == PK_EPI_COMBINE) {
         PK_CHECK(comb && comb->w && comb->out && comb->counters, PK_ERR_ARG, "combine: missing buffers");
+        PK_CHECK(it.n_items <= 16, PK_ERR_UNSUPPORTED, "combine: %d items (at most 16)", it.n_items);
         PK_CHECK(sh.RB <= 1024, PK_ERR_UNSUPPORTED, "combine: %d row blocks", sh.RB);
         cb = *comb;
     }
