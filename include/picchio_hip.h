@@ -205,6 +205,12 @@ int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
  * launch its SwiGLU outputs' records for the down launch. Default off
  * (also PK_I4_DOT=1 in the environment at engine creation). */
 int pk_set_i4_dot(pk_engine *e, int on);
+/* Batch-1 MoE layers (pk_moe_forward, pk_forward_token, pk_generate) as one
+ * launch per layer (k_moe_ffn: gate_up + SwiGLU, then down + combine, the
+ * down workgroups waiting on device-side counters for their expert's
+ * activations) or as a gate_up launch and a down launch. Same results either
+ * way. Default on (PK_MOE_FUSED=0 in the environment at engine creation: off). */
+int pk_set_moe_fused(pk_engine *e, int on);
 /* Records of x_dev[0..n) (n a multiple of 32) into rec_dev[n/32][24]. */
 int pk_act_records(pk_engine *e, const float *x_dev, int n, int32_t *rec_dev);
 /* pk_expert_gate_up / pk_expert_down on records: rec_dev = the input row's
@@ -376,6 +382,7 @@ int pk_sampler_state(pk_engine *e, uint64_t *rng, int32_t *history_host, int cap
 #define PK_PROF_EXPERT_DOWN    1   /* INT4 down GEMV                                 */
 #define PK_PROF_ROUTER         2   /* router GEMV + top-k                            */
 #define PK_PROF_COMBINE        3   /* weighted combine                               */
+#define PK_PROF_MOE_FFN        4   /* batch-1 experts in one launch: gate_up .. combine */
 #define PK_PROF_LM_HEAD        5   /* lm_head GEMV + greedy argmax                   */
 #define PK_PROF_ATTENTION      6   /* QKV .. O-projection of one layer (5 launches)  */
 #define PK_PROF_N              8

@@ -17,7 +17,7 @@ ERRORS = {-1: "PK_ERR_ARG", -2: "PK_ERR_HIP", -3: "PK_ERR_OOM", -4: "PK_ERR_UNSU
           -5: "PK_ERR_MISSING", -6: "PK_ERR_CONTEXT_FULL"}
 FMT_F32, FMT_INT8, FMT_INT4 = 0, 1, 2
 PROF_EXPERT_GATE_UP, PROF_EXPERT_DOWN, PROF_ROUTER, PROF_COMBINE = 0, 1, 2, 3
-PROF_LM_HEAD, PROF_ATTENTION = 5, 6
+PROF_MOE_FFN, PROF_LM_HEAD, PROF_ATTENTION = 4, 5, 6
 
 
 class PkError(RuntimeError):
@@ -121,6 +121,7 @@ def lib():
         "pk_reset_history": (C.c_int, [vp]),
         "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
+        "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
         "pk_expert_gate_up_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
         "pk_expert_down_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
@@ -272,9 +273,14 @@ class Engine:
         check(self.L.pk_set_turn_sampling(self.h, temperature, top_p, top_k))
 
     def set_i4_dot(self, on):
-        """The three-launch MoE layer on the integer-dot expert arithmetic
-        (default) or on picchio's fp32 chains, bit-identical (pk_set_i4_dot)."""
+        """Batch-1 MoE experts on the integer-dot arithmetic, or on picchio's
+        fp32 chains, bit-identical (the default) (pk_set_i4_dot)."""
         check(self.L.pk_set_i4_dot(self.h, 1 if on else 0))
+
+    def set_moe_fused(self, on):
+        """Batch-1 MoE layer's experts as one launch (default) or as a
+        gate_up launch and a down launch; same results (pk_set_moe_fused)."""
+        check(self.L.pk_set_moe_fused(self.h, 1 if on else 0))
 
     def act_records(self, x_dev, rec_dev):
         """Half-group records of the integer-dot arithmetic for a device row."""

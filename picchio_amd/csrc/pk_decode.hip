@@ -922,6 +922,7 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
         pk_dstate s{};
         PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
+        PK_TRY(pk_check_waits(e));
         *next_host = s.next;
     }
     return PK_OK;
@@ -974,6 +975,7 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
         if (rc != PK_OK) break;
         if (hipMemcpyAsync(out, out_dev, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
             hipStreamSynchronize(e->stream) != hipSuccess) { rc = PK_ERR_HIP; break; }
+        rc = pk_check_waits(e);
     } while (0);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
@@ -1033,5 +1035,5 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
     for (int i = 0; i < n_steps; ++i) PK_HIP(hipGraphLaunch(e->step_exec, e->stream));
     PK_HIP(hipMemcpyAsync(out, e->step_out, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
-    return PK_OK;
+    return pk_check_waits(e);
 }

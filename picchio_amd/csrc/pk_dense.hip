@@ -445,8 +445,10 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
                                                      float routed_scale, float *logits, int32_t *sel,
                                                      float *w_scaled, float *w_soft, uint32_t *counter,
                                                      const float *__restrict__ nw, float eps, float *hn,
-                                                     int32_t *hq) {
+                                                     int32_t *hq, uint32_t *epoch) {
     __shared__ float red[4];
+    // a new epoch for the expert launch that follows (its hand-over tag)
+    if (epoch && blockIdx.x == 0 && threadIdx.x == 0) *epoch = *epoch + 1u;
     __shared__ double npart[4];
     __shared__ int last;
     const int e = blockIdx.x;
@@ -582,14 +584,14 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D, int K,
                           float routed_scale, float *logits, int32_t *sel, float *w_scaled,
                           float *w_soft, uint32_t *counter, hipStream_t st, const float *nw, float eps,
-                          float *hn, int32_t *hq) {
+                          float *hn, int32_t *hq, uint32_t *epoch) {
     PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
              "router: E=%d K=%d outside 1..128 / 1..16", E, K);
     PK_CHECK(((uintptr_t)R & 15) == 0 && ((uintptr_t)x & 15) == 0 && (D & 3) == 0, PK_ERR_UNSUPPORTED,
              "router: needs 16-byte aligned rows");
     PK_CHECK(!nw || (hn && ((uintptr_t)nw & 15) == 0), PK_ERR_ARG, "router: fused norm needs hn");
     hipLaunchKernelGGL(k_router_topk, dim3(E), dim3(256), 0, st, x, R, b, E, D, K, routed_scale, logits,
-                       sel, w_scaled, w_soft, counter, nw, eps, hn, hq);
+                       sel, w_scaled, w_soft, counter, nw, eps, hn, hq, epoch);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

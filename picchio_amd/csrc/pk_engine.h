@@ -34,6 +34,8 @@ struct pk_sampler_dev {
 
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
+constexpr int PK_CTR_MOE_EPOCH = 8;      // router launches so far: k_moe_ffn's hand-over tag
+constexpr int PK_CTR_MOE_STATUS = 40;    // k_moe_ffn: 1 once a wait gave up (checked by the host)
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
@@ -79,9 +81,12 @@ struct pk_engine {
     // integer-dot expert arithmetic of the three-launch MoE layer (opt-in:
     // PK_I4_DOT=1 or pk_set_i4_dot; default picchio's fp32 chains, bit-identical)
     bool i4_dot = false;
+    bool moe_fused = true;                    // batch-1 MoE as one k_moe_ffn launch (PK_MOE_FUSED=0: two launches)
     bool i4_dot_batch = true;                 // pk_decode_batch's MoE on it (PK_I4_DOT_BATCH=0: not)
     int32_t *hn_q = nullptr;                  // the layer input's half-group records
     int32_t *act_q = nullptr;                 // [topk] SwiGLU outputs' records
+    uint64_t *moe_act_t = nullptr;            // k_moe_ffn hand-over words: [topk][max(gu RB x 24, moe_inter/2)]
+    uint64_t *moe_eo_t = nullptr;             // k_moe_ffn hand-over words: [topk][hidden]
 
     bool capturing = false;                  // inside pk_capture_begin/end
 
@@ -230,3 +235,6 @@ int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_c
 // prefill_tokens (pk_prefill.hip): the prompt, next id into the decode state / out_toks
 int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base, int32_t *out_toks,
                    int out_cap);
+
+// Reads (and clears) the k_moe_ffn wait flag after a stream sync.
+int pk_check_waits(pk_engine *e);

@@ -148,7 +148,8 @@ static void engine_free(pk_engine *e) {
                     e->attn_part, e->argmax_out, e->counters, e->b_logits, e->b_w, e->b_act,
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
-                    e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles};
+                    e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
+                    e->moe_act_t, e->moe_eo_t};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -209,9 +210,15 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->counters, PK_CTR_N * 4);
     ALLOC(e->hn_q, (int64_t)((D + 31) / 32) * PK_XQ_INTS * 4);
     ALLOC(e->act_q, (int64_t)K * e->ex.gu.RB * PK_XQ_INTS * 4);
+    const int64_t act_words = std::max<int64_t>((int64_t)e->ex.gu.RB * PK_XQ_INTS, half);
+    ALLOC(e->moe_act_t, (int64_t)K * act_words * 8);
+    ALLOC(e->moe_eo_t, (int64_t)K * D * 8);
+    PK_HIP(hipMemsetAsync(e->moe_act_t, 0, (int64_t)K * act_words * 8, e->stream));
+    PK_HIP(hipMemsetAsync(e->moe_eo_t, 0, (int64_t)K * D * 8, e->stream));
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
+    if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v) != 0;
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -253,10 +260,24 @@ extern "C" int pk_engine_destroy(pk_engine *e) {
 
 extern "C" void *pk_engine_stream(pk_engine *e) { return e ? (void *)e->stream : nullptr; }
 
+// After a stream sync: an error if a device-side wait of k_moe_ffn gave up
+// (its results are then not to be trusted); the flag is cleared.
+int pk_check_waits(pk_engine *e) {
+    uint32_t st = 0;
+    PK_HIP(hipMemcpy(&st, e->counters + PK_CTR_MOE_STATUS, 4, hipMemcpyDeviceToHost));
+    if (st) {
+        PK_HIP(hipMemsetAsync(e->counters + PK_CTR_MOE_STATUS, 0, 4, e->stream));
+        PK_HIP(hipStreamSynchronize(e->stream));
+        pk_set_error("a device-side wait of the expert launch gave up: results are invalid");
+        return PK_ERR_HIP;
+    }
+    return PK_OK;
+}
+
 extern "C" int pk_engine_sync(pk_engine *e) {
     PK_CHECK(e, PK_ERR_ARG, "engine is null");
     PK_HIP(hipStreamSynchronize(e->stream));
-    return PK_OK;
+    return pk_check_waits(e);
 }
 
 extern "C" int64_t pk_engine_device_bytes(pk_engine *e) { return e ? e->device_bytes : -1; }
@@ -749,6 +770,14 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     return PK_OK;
 }
 
+// Shapes k_moe_ffn takes (pk_launch_moe_ffn checks the same).
+static bool moe_ffn_fits(const pk_engine *e) {
+    const pk_cfg *c = &e->c;
+    return e->ex.gu.NG <= 45 && e->ex.dn.NG <= 45 && e->ex.gu.O == e->ex.gu.RB * 64 &&
+           e->ex.dn.NG * 64 == e->ex.gu.O / 2 && c->topk <= 4 && e->ex.dn.RB * c->topk <= 240 &&
+           e->ex.dn.RB <= e->ex.gu.RB && e->ex.stride < ((int64_t)1 << 31);   // 32-bit offsets in a slot
+}
+
 // norm_w: x_dev is the raw residual row; the router normalises it (rmsnorm
 // fused) and writes the normalised row to e->hn, which the experts read.
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
@@ -764,7 +793,7 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
                                  c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
                                  nullptr, e->stream, norm_w, c->eps, norm_w ? e->hn : nullptr,
-                                 dot ? e->hn_q : nullptr));
+                                 dot ? e->hn_q : nullptr, e->counters + PK_CTR_MOE_EPOCH));
     PK_TRY(pk_prof_end(e, ps));
     pk_route_args rt{};
     rt.logits = e->r_logits;
@@ -780,8 +809,39 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     cb.out = residual ? res_out : out_dev;
     cb.residual = residual;
     cb.counters = e->counters + PK_CTR_COMBINE;
-    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, norm_w ? e->hn : x_dev, 0, e->act, e->eo, &cb, &rt,
-                       dot));
+    const float *xin = norm_w ? e->hn : x_dev;
+    if (e->moe_fused && moe_ffn_fits(e)) {
+        pk_moe_ffn_args a{};
+        a.store = e->store;
+        a.slot_stride = e->ex.stride;
+        a.slot_base = layer * c->n_experts;
+        a.gu_tiles = (uint32_t)e->ex.off_gu_tiles;
+        a.gu_scales = (uint32_t)e->ex.off_gu_scales;
+        a.dn_tiles = (uint32_t)e->ex.off_dn_tiles;
+        a.dn_scales = (uint32_t)e->ex.off_dn_scales;
+        a.gu_bias = (int32_t)e->ex.off_gu_bias;
+        a.dn_bias = (int32_t)e->ex.off_dn_bias;
+        a.gu_NG = e->ex.gu.NG; a.gu_O = e->ex.gu.O; a.gu_RB = e->ex.gu.RB;
+        a.dn_NG = e->ex.dn.NG; a.dn_O = e->ex.dn.O; a.dn_RB = e->ex.dn.RB;
+        a.K = c->topk;
+        a.n_cu = e->n_cu;
+        a.dot = dot;
+        a.lim = c->swiglu_limit;
+        a.alpha = c->swiglu_alpha;
+        a.x = xin;
+        a.xq = dot ? e->hn_q : nullptr;
+        a.out = cb.out;
+        a.residual = cb.residual;
+        a.rt = rt;
+        a.act_t = e->moe_act_t;
+        a.eo_t = e->moe_eo_t;
+        a.epoch = e->counters + PK_CTR_MOE_EPOCH;
+        a.status = e->counters + PK_CTR_MOE_STATUS;
+        ps = pk_prof_begin(e, PK_PROF_MOE_FFN);
+        PK_TRY(pk_launch_moe_ffn(a, e->stream));
+        return pk_prof_end(e, ps);
+    }
+    PK_TRY(experts_ffn(e, layer, e->sel, c->topk, xin, 0, e->act, e->eo, &cb, &rt, dot));
     return PK_OK;
 }
 
@@ -794,6 +854,18 @@ extern "C" int pk_set_i4_dot(pk_engine *e, int on) {
         e->step_cap = -1;
     }
     e->i4_dot = on != 0;
+    return PK_OK;
+}
+
+extern "C" int pk_set_moe_fused(pk_engine *e, int on) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_moe_fused: not available while capturing");
+    if (e->moe_fused != (on != 0) && e->step_exec) {   // the captured step holds the other kernels
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+        e->step_cap = -1;
+    }
+    e->moe_fused = on != 0;
     return PK_OK;
 }
 
@@ -810,6 +882,7 @@ extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float
         if (w_host)
             PK_HIP(hipMemcpyAsync(w_host, e->w_soft, e->c.topk * 4, hipMemcpyDeviceToHost, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
+        PK_TRY(pk_check_waits(e));
     }
     return PK_OK;
 }

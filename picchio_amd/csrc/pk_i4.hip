@@ -93,12 +93,7 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
     __syncthreads();
     if (wave != 0) return;
 
-    float acc = 0.0f;
-    if constexpr (DOT) {
-        for (int g = 0; g < NG; ++g) acc = acc + part[g * 64 + lane];
-    } else {
-        for (int g = 0; g < NG; ++g) acc = __builtin_fmaf(part[g * 64 + lane], scl[g * 64 + lane], acc);
-    }
+    float acc = pk_fold_groups<DOT>(part, scl, NG);
     if (it.off_bias >= 0 && row < O) acc = acc + bias;
     float *y = it.y + (int64_t)item * it.y_stride;
     if constexpr (EPI == PK_EPI_SWIGLU) {
@@ -206,8 +201,7 @@ __global__ __launch_bounds__(15 * 64) void k_i4_dot_tiles(pk_i4_items it, pk_i4_
     __syncthreads();
     if (wave >= cnt) return;
     const int pair = tl.pairs[beg + wave];
-    float acc = 0.0f;
-    for (int g = 0; g < NG; ++g) acc = acc + lds[((int64_t)wave * NG + g) * 64 + lane];
+    float acc = pk_fold_groups<true>(lds + (int64_t)wave * NG * 64, nullptr, NG);
     const int row = rb * 64 + lane;
     if (it.off_bias >= 0 && row < O) acc = acc + reinterpret_cast<const float *>(base + it.off_bias)[row];
     float *y = it.y + (int64_t)pair * it.y_stride;
@@ -291,6 +285,252 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
         if (dot) PK_I4_LAUNCH(PK_EPI_PLAIN, true); else PK_I4_LAUNCH(PK_EPI_PLAIN, false);
     }
 #undef PK_I4_LAUNCH
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// ───────────── a token's routed experts in one launch (batch-1 decode) ─────────────
+// grid = the gate_up tasks (gu RB x K, item-minor); the first dn RB x K
+// workgroups also take the down task of the same index (same item, so the
+// same expert) once their gate_up math is done. Every workgroup selects its
+// expert from the router logits (round `item` of the top-k).
+// Values that cross workgroups travel without fences, as 64-bit words
+// (tag << 32 | bits) written and read with device-scope atomics; the tag is
+// *epoch, a device word that the router launch before each expert launch
+// advances (never 0: the hand-over buffers start zeroed). A reader polls its
+// words until every tag matches: a word is single-copy atomic, so a
+// matching tag carries this launch's value.
+// The polls are bounded: past the bound a wave flags *status and goes on, so
+// that every wave ends (the host turns the flag into an error).
+//  * gate_up task: the k_i4_gemv SwiGLU body (fp32 chains, or the integer
+//    dot on the input records); wave 0 publishes the row block's 32
+//    activations (fp32) or their record (integer dot) as tagged words.
+//  * down task: its weight loads go out as soon as the gate_up math has
+//    freed the registers (before the gate_up epilogue); then, group by
+//    group, each wave waits for that group's tagged inputs (two gate_up row
+//    blocks) and runs the k_i4_gemv body; wave 0 publishes the row block's
+//    rows as tagged words, except for item K-1, whose task waits for the
+//    other items' rows and adds them in routing order,
+//    out = fma(w_k, eo_k, out) (moe_forward, picchio.c:1387, :1445-1454),
+//    then the residual (forward_token, picchio.c:1716).
+// Deadlock freedom: only workgroups in their down task wait, and only for
+// gate_up epilogues and other down tasks. The launcher keeps the down tasks
+// below the workgroups the device holds at once, so a workgroup that has not
+// started yet always finds a slot whatever the dispatch order.
+// Wave 0 runs each epilogue at the highest wave priority (s_setprio): the
+// epilogues are the launch's critical path.
+constexpr uint32_t PK_POLL_BOUND = 1u << 18;
+
+// Polls the tagged word at p (lanes with use) until its tag is `tag` on
+// every such lane of the wave; returns the low halves.
+__device__ __forceinline__ uint32_t pk_wait_tagged(const uint64_t *p, bool use, uint32_t tag, uint32_t *status) {
+    uint64_t w = use ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
+    uint32_t n = 0;
+    while (__any((uint32_t)(w >> 32) != tag)) {
+        __builtin_amdgcn_s_sleep(1);
+        if ((uint32_t)(w >> 32) != tag) w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++n == PK_POLL_BOUND) {
+            if ((threadIdx.x & 63) == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ void pk_put_tagged(uint64_t *p, uint32_t tag, uint32_t bits) {
+    __hip_atomic_store(p, (uint64_t)tag << 32 | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// KM: an upper bound of the routed experts K. NW waves of GPW groups each
+// cover a row block's groups in one pass; WPE: waves per SIMD the launch
+// needs for two workgroups per CU.
+template <bool DOT, int KM, int NW, int GPW, int WPE>
+__global__ __launch_bounds__(NW * 64, WPE) void k_moe_ffn(pk_moe_ffn_args a) {
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int task = blockIdx.x;
+    const int item = task % a.K;
+    // the down task this workgroup also takes: the first ones go to the
+    // workgroups that have a CU to themselves (workgroups n_cu.. share the CUs
+    // of workgroups 0.. with them), so that the bytes per CU even out
+    const int n2 = max((int)gridDim.x - a.n_cu, 0);
+    const int dtask = task >= n2 && task < a.n_cu ? task - n2 : task < n2 ? a.n_cu - n2 + task : task;
+    const bool has_down = dtask < a.dn_RB * a.K;
+    const int ditem = dtask % a.K;
+    const pk_wave_logits lg = pk_load_wave_logits(a.rt.logits, a.rt.E);
+    float bv;
+    const int e = __builtin_amdgcn_readfirstlane(pk_wave_topk_nth(lg, a.rt.E, item, &bv));
+    const uint8_t *eb = a.store + (int64_t)(a.slot_base + e) * a.slot_stride;   // the expert's slot
+    const uint8_t *ebd = nullptr;                                               // the down task's
+    const int64_t act_stride = DOT ? (int64_t)a.gu_RB * PK_XQ_INTS : a.gu_O / 2;
+    float *part = lds;                                   // [NG][64] partials
+    float *scl = lds + 64 * NW * GPW;                    // [NG][64] scales (fp32 chains)
+    float *cwl = lds + 2 * 64 * NW * GPW;                // [K] combine weights
+    uint4 wa[GPW], wb[GPW];
+    float s[GPW];
+    // one row block of one matrix of the expert: every group in one pass
+    auto issue = [&](const uint8_t *xb, uint32_t off_tiles, uint32_t off_scales, int NG, int rb) {
+        const uint4 *tiles = reinterpret_cast<const uint4 *>(xb + off_tiles) + (int64_t)rb * NG * (PK_TILE_BYTES / 16);
+        const float *sc = reinterpret_cast<const float *>(xb + off_scales) + (int64_t)rb * NG * 64;
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = wave + u * NW;
+            if (g < NG) {
+                wa[u] = pk_load_nt(&tiles[g * 128 + lane]);
+                wb[u] = pk_load_nt(&tiles[g * 128 + 64 + lane]);
+                s[u] = sc[g * 64 + lane];
+            }
+        }
+    };
+
+    // ── gate_up task ──
+    {
+        const int NG = a.gu_NG, O = a.gu_O, rb = task / a.K;
+        const int row = rb * 64 + lane;
+        issue(eb, a.gu_tiles, a.gu_scales, NG, rb);
+        // the down task's expert, while the gate_up weights stream in
+        if (has_down) {
+            const int ed = ditem == item ? e : __builtin_amdgcn_readfirstlane(pk_wave_topk_nth(lg, a.rt.E, ditem, &bv));
+            ebd = a.store + (int64_t)(a.slot_base + ed) * a.slot_stride;
+        }
+        // while the weights stream in, wave 0 takes what else needs the
+        // logits: the combine weights (the combining task: item K-1's) into
+        // LDS, and the routing published for the launches (and the host)
+        // after this one (the last workgroup)
+        if (wave == 0) {
+            if (has_down && ditem == a.K - 1) {
+                int ci[KM];
+                float cw[KM], wp[KM];
+                pk_wave_route<KM>(a.rt, lg, ci, cw, wp);
+#pragma unroll
+                for (int k = 0; k < KM; ++k)
+                    if (k < a.K && lane == 0) cwl[k] = cw[k];
+            }
+            if (task == (int)gridDim.x - 1) pk_wave_route_publish<KM>(a.rt, lg);
+        }
+        // (after the weight loads: a scalar load's wait would hold them back)
+        const float bias = (wave == 0 && a.gu_bias >= 0)
+                               ? reinterpret_cast<const float *>(eb + a.gu_bias)[min(row, O - 1)] : 0.0f;
+        // the inputs come from an earlier launch: scalar loads
+        const pk_cptr<float> x = pk_const(a.x);
+        const pk_cptr<int32_t> xq = pk_const(a.xq);
+#pragma unroll
+        for (int u = 0; u < GPW; ++u) {
+            const int g = wave + u * NW;
+            if (g < NG) {
+                if constexpr (DOT) {
+                    part[g * 64 + lane] = pk_dot_group(wa[u], wb[u], xq + 2 * g * PK_XQ_INTS,
+                                                       xq + (2 * g + 1) * PK_XQ_INTS, s[u]);
+                } else {
+                    part[g * 64 + lane] = pk_group_dot(wa[u], wb[u], x + g * 64);
+                    scl[g * 64 + lane] = s[u];
+                }
+            }
+        }
+        __syncthreads();
+        // the down task's weights go out before the gate_up epilogue (wave 0
+        // issues its share after it, so that the two do not meet in registers)
+        if (wave != 0) {
+            if (has_down) issue(ebd, a.dn_tiles, a.dn_scales, a.dn_NG, dtask / a.K);
+        } else {
+            __builtin_amdgcn_s_setprio(3);
+            const uint32_t tag = *pk_const(a.epoch);
+            float acc = pk_fold_groups<DOT>(part, scl, NG);
+            if (a.gu_bias >= 0 && row < O) acc = acc + bias;
+            const float up = __shfl_down(acc, 1, 64);
+            const bool has = (lane & 1) == 0 && row + 1 < O;
+            const float v = pk_swiglu(acc, up, a.lim, a.alpha);
+            uint64_t *dst = a.act_t + item * act_stride;
+            if constexpr (DOT) {
+                // the row block's 32 outputs are one half-group of the down input
+                const int32_t word = pk_record_word<2>(v, has);
+                if (lane < PK_XQ_INTS) pk_put_tagged(dst + rb * PK_XQ_INTS + lane, tag, (uint32_t)word);
+            } else {
+                if (has) pk_put_tagged(dst + (row >> 1), tag, __float_as_uint(v));
+            }
+            __builtin_amdgcn_s_setprio(0);
+            if (has_down) issue(ebd, a.dn_tiles, a.dn_scales, a.dn_NG, dtask / a.K);
+        }
+        if (!has_down) return;
+        __syncthreads();                                  // part / scl are free again
+    }
+
+    // ── down task: row block dtask / K of item ditem's down matrix ──
+    const int NG = a.dn_NG, O = a.dn_O, rb = dtask / a.K;
+    const int row = rb * 64 + lane;
+    const uint32_t tag = *pk_const(a.epoch);
+    float bias = 0.0f, res = 0.0f;
+    if (wave == 0) {
+        if (a.dn_bias >= 0) bias = reinterpret_cast<const float *>(ebd + a.dn_bias)[min(row, O - 1)];
+        if (ditem == a.K - 1 && a.residual) res = a.residual[min(row, O - 1)];
+    }
+    // group by group: wait for the tagged inputs (one per lane), read them
+    // with v_readlane: group g's two records (48 ints) / 64 activations
+    const uint64_t *src_item = a.act_t + ditem * act_stride;
+#pragma unroll
+    for (int u = 0; u < GPW; ++u) {
+        const int g = wave + u * NW;
+        if (g < NG) {
+            if constexpr (DOT) {
+                const bool use = lane < 2 * PK_XQ_INTS;
+                const int r = (int)pk_wait_tagged(src_item + 2 * g * PK_XQ_INTS + (use ? lane : 0), use, tag,
+                                                  a.status);
+                part[g * 64 + lane] = pk_dot_group(wa[u], wb[u], pk_lanes<int>{r, 0},
+                                                   pk_lanes<int>{r, PK_XQ_INTS}, s[u]);
+            } else {
+                const int r = (int)pk_wait_tagged(src_item + g * 64 + lane, true, tag, a.status);
+                part[g * 64 + lane] = pk_group_dot(wa[u], wb[u], pk_lanes<float>{r, 0});
+                scl[g * 64 + lane] = s[u];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    __builtin_amdgcn_s_setprio(3);
+    float acc = pk_fold_groups<DOT>(part, scl, NG);
+    if (a.dn_bias >= 0 && row < O) acc = acc + bias;
+    // the combine: the row block's rows out as tagged words; item K-1's task
+    // waits for the other items' rows and adds them in routing order
+    if (ditem != a.K - 1) {
+        if (row < O) pk_put_tagged(a.eo_t + (int64_t)ditem * O + row, tag, __float_as_uint(acc));
+        return;
+    }
+    float o = 0.0f;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (k < a.K) {
+            const float ek = k == ditem ? acc
+                                       : __uint_as_float(pk_wait_tagged(a.eo_t + (int64_t)k * O + min(row, O - 1),
+                                                                        row < O, tag, a.status));
+            o = __builtin_fmaf(cwl[k], ek, o);
+        }
+    if (row < O) a.out[row] = a.residual ? res + o : o;
+}
+
+int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st) {
+    constexpr int NW = 15, GPW = 3, WPE = 8;
+    PK_CHECK(a.rt.logits && a.rt.sel && a.rt.w_scaled && a.rt.E > 0 && a.rt.E <= 128 && a.K > 0 &&
+                 a.K <= a.rt.E && a.rt.K == a.K,
+             PK_ERR_ARG, "moe ffn: routing of K=%d over E=%d", a.K, a.rt.E);
+    // (the routing state of more experts would not fit the registers of two
+    // workgroups per CU: larger top-k runs as two launches)
+    PK_CHECK(a.K <= 4, PK_ERR_UNSUPPORTED, "moe ffn: top-%d (at most 4 in one launch)", a.K);
+    PK_CHECK(a.store && a.out && a.act_t && a.eo_t && a.epoch && a.status, PK_ERR_ARG, "moe ffn: missing buffers");
+    PK_CHECK(a.dot ? a.xq != nullptr : a.x != nullptr, PK_ERR_ARG, "moe ffn: missing input");
+    PK_CHECK(a.gu_NG > 0 && a.gu_NG <= NW * GPW && a.dn_NG > 0 && a.dn_NG <= NW * GPW && a.gu_O == a.gu_RB * 64 &&
+                 a.dn_NG * 64 == a.gu_O / 2 && a.dn_RB * 64 >= a.dn_O && a.dn_RB <= a.gu_RB,
+             PK_ERR_UNSUPPORTED, "moe ffn: shapes gate_up %d x %d groups, down %d x %d groups", a.gu_O, a.gu_NG,
+             a.dn_O, a.dn_NG);
+    // workgroups in their down task wait; they must leave room for the rest
+    // (at least one 15-wave workgroup per CU fits on any gfx950 part)
+    PK_CHECK(a.dn_RB * a.K <= 240, PK_ERR_UNSUPPORTED, "moe ffn: %d down tasks", a.dn_RB * a.K);
+    PK_CHECK(a.n_cu > 0, PK_ERR_ARG, "moe ffn: n_cu %d", a.n_cu);
+    const int grid = a.gu_RB * a.K;
+    // partials + scales of NW x GPW groups, then the combine weights
+    const size_t lds = (size_t)2 * NW * GPW * 64 * sizeof(float) + 16 * sizeof(float);
+    if (a.dot) hipLaunchKernelGGL((k_moe_ffn<true, 4, NW, GPW, WPE>), dim3(grid), dim3(NW * 64), lds, st, a);
+    else hipLaunchKernelGGL((k_moe_ffn<false, 4, NW, GPW, WPE>), dim3(grid), dim3(NW * 64), lds, st, a);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

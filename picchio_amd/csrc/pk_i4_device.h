@@ -63,6 +63,58 @@ __device__ __forceinline__ float pk_group_dot(uint4 a, uint4 b, XP xg) {
     return (b0 + b2) + (b1 + b3);
 }
 
+// A pointer into the constant address space: wave-uniform loads through it
+// are scalar loads (s_load, the scalar cache) whatever else the kernel
+// writes. Only for data that no wave of the launch writes.
+template <typename T>
+using pk_cptr = const __attribute__((address_space(4))) T *;
+template <typename T>
+__device__ __forceinline__ pk_cptr<T> pk_const(const T *p) {
+    return (pk_cptr<T>)(const __attribute__((address_space(1))) T *)p;
+}
+
+// 64 values held one per lane of a wave, read wave-uniformly: v[i] is
+// lane (off + i)'s value (v_readlane: the operand lands in a scalar
+// register). An input pointer for pk_group_dot / pk_dot_group when a wave
+// has loaded its inputs itself instead of taking them from constant memory.
+template <typename T>
+struct pk_lanes {
+    int v, off;
+    __device__ __forceinline__ pk_lanes operator+(int d) const { return {v, off + d}; }
+    __device__ __forceinline__ T operator[](int i) const {
+        const int r = __builtin_amdgcn_readlane(v, off + i);
+        if constexpr (sizeof(T) == 4 && T(0.5) != T(0)) return __int_as_float(r);
+        else return r;
+    }
+};
+
+// The row's value from its per-group partials in LDS (part[g][64], and the
+// scales scl[g][64] for the fp32 chains), folded in group order: a = a + p_g
+// (integer dot: the partials carry their scales) or a = fma(p_g, s_g, a)
+// (quant.h:313). The LDS reads go out C at a time ahead of the chain.
+template <bool DOT>
+__device__ __forceinline__ float pk_fold_groups(const float *part, const float *scl, int NG) {
+    const int lane = threadIdx.x & 63;
+    constexpr int C = DOT ? 15 : 8;
+    float acc = 0.0f;
+    for (int g0 = 0; g0 < NG; g0 += C) {
+        float p[C], q[C];
+#pragma unroll
+        for (int j = 0; j < C; ++j) {
+            const int g = min(g0 + j, NG - 1);
+            p[j] = part[g * 64 + lane];
+            if constexpr (!DOT) q[j] = scl[g * 64 + lane];
+        }
+#pragma unroll
+        for (int j = 0; j < C; ++j)
+            if (g0 + j < NG) {
+                if constexpr (DOT) acc = acc + p[j];
+                else acc = __builtin_fmaf(p[j], q[j], acc);
+            }
+    }
+    return acc;
+}
+
 // expf as the double exp rounded once to float: the correctly rounded value
 // (but for double rounding in about 2^-29 of inputs), which is glibc's expf
 // except where glibc's own result is not correctly rounded (~8e-5 of inputs).
@@ -108,10 +160,19 @@ __device__ __forceinline__ uint32_t pk_fkey(float f) {
 // with the value -1e30. Lane l holds experts l and l + 64 (E <= 128).
 // Returns round n's (index, logit), the same on every lane; rounds 0..n-1
 // are taken out first.
-__device__ __forceinline__ int pk_wave_topk_nth(const float *logits, int E, int n, float *val) {
+// The logits as one wave holds them: lane l has experts l and l + 64
+// (clamped, unconditional loads; entries past E are masked by the users).
+struct pk_wave_logits {
+    float v0, v1;
+};
+__device__ __forceinline__ pk_wave_logits pk_load_wave_logits(const float *logits, int E) {
     const int lane = threadIdx.x & 63;
-    // clamped, unconditional loads (entries past E are masked below)
-    const float v0 = logits[min(lane, E - 1)], v1 = logits[min(lane + 64, E - 1)];
+    return {logits[min(lane, E - 1)], logits[min(lane + 64, E - 1)]};
+}
+
+__device__ __forceinline__ int pk_wave_topk_nth(const pk_wave_logits &lg, int E, int n, float *val) {
+    const int lane = threadIdx.x & 63;
+    const float v0 = lg.v0, v1 = lg.v1;
     const uint32_t k0 = (lane < E && v0 == v0) ? pk_fkey(v0 + 0.0f) : 0u;
     const uint32_t k1 = (lane + 64 < E && v1 == v1) ? pk_fkey(v1 + 0.0f) : 0u;
     const uint32_t floor_key = pk_fkey(-1e30f);
@@ -136,35 +197,64 @@ __device__ __forceinline__ int pk_wave_topk_nth(const float *logits, int E, int 
     return bi;
 }
 
+__device__ __forceinline__ int pk_wave_topk_nth(const float *logits, int E, int n, float *val) {
+    return pk_wave_topk_nth(pk_load_wave_logits(logits, E), E, n, val);
+}
+
 // Routing of one token from its logits, in the consumer of the router
-// logits: where the expert kernels select their own experts, one wave also
-// publishes the selection and the softmax weights (picchio.c:1353,
-// quant.h:406-412: max, expf, sum and division in routing order), with the
-// arithmetic of k_router_topk's last block.
-__device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
-    const int lane = threadIdx.x & 63;
-    float m = -1e30f, cv[16];
-    int ci[16];
+// logits (picchio.c:1353, quant.h:406-412: max, expf, sum and division in
+// routing order), with the arithmetic of k_router_topk's last block: ci[k] /
+// ws[k] / wp[k] = round k's expert, its weight * routed_scale and its weight,
+// the same on every lane.
+// KM: an upper bound of rt.K (the arrays' length).
+template <int KM = 16>
+__device__ __forceinline__ void pk_wave_route(const pk_route_args &rt, const pk_wave_logits &lg, int *ci, float *ws,
+                                              float *wp) {
+    float m = -1e30f, cv[KM];
 #pragma unroll
-    for (int k = 0; k < 16; ++k) {
+    for (int k = 0; k < KM; ++k) {
         if (k < rt.K) {
-            ci[k] = pk_wave_topk_nth(rt.logits, rt.E, k, &cv[k]);
+            ci[k] = pk_wave_topk_nth(lg, rt.E, k, &cv[k]);
             if (cv[k] > m) m = cv[k];
         }
     }
-    if (lane != 0) return;
     float s = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
+    for (int k = 0; k < KM; ++k)
         if (k < rt.K) { cv[k] = pk_expf_cr(cv[k] - m); s += cv[k]; }
 #pragma unroll
-    for (int k = 0; k < 16; ++k)
+    for (int k = 0; k < KM; ++k)
         if (k < rt.K) {
-            const float p = cv[k] / s;
-            rt.sel[k] = ci[k];
-            if (rt.w_soft) rt.w_soft[k] = p;
-            rt.w_scaled[k] = p * rt.routed_scale;
+            wp[k] = cv[k] / s;
+            ws[k] = wp[k] * rt.routed_scale;
         }
+}
+
+// Where the expert kernels select their own experts, one wave also publishes
+// the selection and the weights for the launches (and the host) after them.
+template <int KM = 16>
+__device__ __forceinline__ void pk_wave_route(const pk_route_args &rt, int *ci, float *ws, float *wp) {
+    pk_wave_route<KM>(rt, pk_load_wave_logits(rt.logits, rt.E), ci, ws, wp);
+}
+
+template <int KM = 16>
+__device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt, const pk_wave_logits &lg) {
+    int ci[KM];
+    float ws[KM], wp[KM];
+    pk_wave_route<KM>(rt, lg, ci, ws, wp);
+    if ((threadIdx.x & 63) != 0) return;
+#pragma unroll
+    for (int k = 0; k < KM; ++k)
+        if (k < rt.K) {
+            rt.sel[k] = ci[k];
+            if (rt.w_soft) rt.w_soft[k] = wp[k];
+            rt.w_scaled[k] = ws[k];
+        }
+}
+
+template <int KM = 16>
+__device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
+    pk_wave_route_publish<KM>(rt, pk_load_wave_logits(rt.logits, rt.E));
 }
 
 // ─────────────── integer-dot arithmetic (opt-in to bit-exactness) ───────────────
@@ -181,10 +271,11 @@ __device__ __forceinline__ void pk_wave_route_publish(const pk_route_args &rt) {
 // C = sum_i 16^i P_i = sum (q-8) A exactly (|C| <= 2^26). The row's value is
 // then sum over groups g and halves h of (16 s_g) 2^(k_h - 22) C_gh, folded
 // in fp32 in a fixed order (pk_dot_group).
-// 32 values of a half-group: lane src(c) holds column c's value v (has: the
-// lane holds one). Writes the record to dst (lanes 0..20 store).
+// 32 values of a half-group: lane src(c) = c * LS holds column c's value v
+// (has: the lane holds one). Returns int `lane` of the record (lanes
+// 0..PK_XQ_INTS-1).
 template <int LS>
-__device__ __forceinline__ void pk_write_digits(float v, bool has, int32_t *dst) {
+__device__ __forceinline__ int32_t pk_record_word(float v, bool has) {
     const int lane = threadIdx.x & 63;
     // the largest magnitude (non-negative floats order as their bits)
     const float m = __uint_as_float(pk_wave_max_u32(__float_as_uint(has ? fabsf(v) : 0.0f)));
@@ -207,21 +298,28 @@ __device__ __forceinline__ void pk_write_digits(float v, bool has, int32_t *dst)
         const uint32_t src = (uint32_t)__shfl((int)dig, (8 * w + n) * LS, 64);
         word |= ((src >> (4 * (i < 5 ? i : 0))) & 15u) << (4 * n);
     }
-    if (lane < 20) dst[lane] = (int32_t)word;
-    if (lane == 20) dst[20] = k;
-    if (lane > 20 && lane < PK_XQ_INTS) dst[lane] = 0;   // padding
+    return lane < 20 ? (int32_t)word : lane == 20 ? k : 0;   // then padding
+}
+
+// The record of a half-group written to dst (lanes 0..PK_XQ_INTS-1 store):
+// lane src(c) holds column c's value v (has: the lane holds one).
+template <int LS>
+__device__ __forceinline__ void pk_write_digits(float v, bool has, int32_t *dst) {
+    const int32_t word = pk_record_word<LS>(v, has);
+    if ((threadIdx.x & 63) < PK_XQ_INTS) dst[threadIdx.x & 63] = word;
 }
 
 // One 64-column group of one row on the integer dot: wa / wb = the stored
 // nibbles (q ^ 8) of columns 0..31 / 32..63, x0 / x1 = the two half-group records
 // (wave-uniform), s16 = the stored scale (16 s). Returns the group's value.
-__device__ __forceinline__ float pk_dot_group(uint4 wa, uint4 wb, const int32_t *x0, const int32_t *x1,
-                                              float s16) {
+// XP: any pointer to the records (global, constant or LDS address space).
+template <typename XP>
+__device__ __forceinline__ float pk_dot_group(uint4 wa, uint4 wb, XP x0, XP x1, float s16) {
     float t = 0.0f;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
         const uint4 w = h ? wb : wa;
-        const int32_t *xq = h ? x1 : x0;
+        const XP xq = h ? x1 : x0;
         const int w0 = (int)w.x, w1 = (int)w.y, w2 = (int)w.z, w3 = (int)w.w;
         int P[5];
 #pragma unroll

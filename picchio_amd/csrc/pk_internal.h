@@ -153,6 +153,34 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
                       const pk_combine_args *comb, hipStream_t st,
                       const pk_route_args *route = nullptr);
 
+// A token's routed experts in one launch (k_moe_ffn): gate_up + SwiGLU,
+// down + combine, experts selected from rt.logits in the launch. Kept lean:
+// every field a kernel argument reads stays in scalar registers.
+struct pk_moe_ffn_args {
+    const uint8_t *store;          // expert slots: slot (slot_base + e) at store + slot * slot_stride
+    int64_t slot_stride;
+    int slot_base;
+    uint32_t gu_tiles, gu_scales, dn_tiles, dn_scales;   // byte offsets inside a slot
+    int32_t gu_bias, dn_bias;      // byte offsets inside a slot, -1: no bias
+    int gu_NG, gu_O, gu_RB;        // gate_up: O rows in RB row blocks of 64, NG groups of 64 columns
+    int dn_NG, dn_O, dn_RB;        // down: its input is the gu_O / 2 = gu_RB * 32 activations
+    int K;                         // routed experts (items)
+    int n_cu;                      // compute units (placement of the down tasks)
+    bool dot;                      // integer-dot arithmetic (xq) or picchio's fp32 chains (x)
+    float lim, alpha;
+    const float *x;                // input row (fp32 chains)
+    const int32_t *xq;             // its half-group records (integer dot)
+    float *out;                    // combined rows (+ residual)
+    const float *residual;         // optional
+    pk_route_args rt;
+    // hand-over words (tag << 32 | bits), zero-initialised:
+    uint64_t *act_t;               // [K][dot ? gu_RB * PK_XQ_INTS : gu_O / 2]
+    uint64_t *eo_t;                // [K][dn_O]
+    const uint32_t *epoch;         // the tag: advanced before each launch (router), never 0
+    uint32_t *status;              // set to 1 if a wait gave up
+};
+int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st);
+
 // Pairs grouped by expert into tiles (k_group_pairs): tile t = expert
 // tile_exp[t], pairs[tile_beg[t] .. + tile_cnt[t]]; *n_tiles tiles (device).
 struct pk_i4_tiles {
@@ -189,11 +217,12 @@ int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, cons
 // Router for one token: logits = R x + b, top-k by repeated argmax, softmax.
 // nw (optional): x is the raw residual row, normalised in the kernel
 // (rmsnorm fused); the normalised row is also written to hn.
+// epoch (optional): incremented by one thread (k_moe_ffn's hand-over tag).
 int pk_launch_router_topk(const float *x, const float *R, const float *b, int E, int D,
                           int K, float routed_scale, float *logits, int32_t *sel,
                           float *w_scaled, float *w_soft, uint32_t *counter,
                           hipStream_t st, const float *nw = nullptr, float eps = 0.f,
-                          float *hn = nullptr, int32_t *hq = nullptr);
+                          float *hn = nullptr, int32_t *hq = nullptr, uint32_t *epoch = nullptr);
 // y = W . rmsnorm(h; nw, eps) + bias for one row (rmsnorm fused into the GEMV).
 int pk_launch_gemv_f32_norm(float *y, const float *h, const float *nw, float eps, const float *W,
                             const float *bias, int I, int O, hipStream_t st);

@@ -249,6 +249,36 @@ def test_moe_forward_parity(moe_setup, oracle):
     assert worst < 1e-5
 
 
+@pytest.mark.parametrize("dot", [0, 1])
+def test_moe_one_launch_matches_two(moe_setup, oracle, dot):
+    """The batch-1 experts as one launch (down workgroups waiting on the
+    gate_up counters) give the same bits as the gate_up launch + down launch,
+    token after token (the counters re-arm themselves), on picchio's fp32
+    chains and on the integer dot; and no device-side wait gave up."""
+    import torch
+    cfg, model, eng = moe_setup
+    D = cfg.hidden
+    eng.set_i4_dot(dot)
+    try:
+        for t in range(6):
+            x = _token_x(oracle, cfg, 500 + t)
+            xd = eng.to_dev(x)
+            outs, sels = [], []
+            for fused in (1, 0, 1):
+                eng.set_moe_fused(fused)
+                od = eng.empty(D, torch.float32)
+                sel, w = eng.moe_forward(0, xd, od, want_routing=True)
+                outs.append(eng.to_host(od))
+                sels.append((list(sel), list(w)))
+            assert sels[0] == sels[1] == sels[2], (t, sels)
+            assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), t
+            assert np.array_equal(outs[2].view(np.uint32), outs[1].view(np.uint32)), t
+        eng.sync()
+    finally:
+        eng.set_moe_fused(1)
+        eng.set_i4_dot(0)
+
+
 def test_router_ties_take_lowest_index(moe_setup, oracle):
     """Equal router logits: the lowest expert index is taken first
     (picchio.c:1327-1339, strict '>' over experts in order), and equal
