@@ -48,7 +48,26 @@ def build(verbose=False):
     if r.returncode != 0:
         raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
     os.replace(tmp, OUT)
+    build_service()
     return OUT
+
+
+SERVICE_SRC = os.path.join(HERE, "host", "picchio_service.c")
+SERVICE_OUT = os.path.join(HERE, "picchio_service")
+INCLUDE = os.path.join(os.path.dirname(HERE), "include")
+
+
+def build_service():
+    """picchio's SERVICE=1 loop as a C program over the C-ABI (gcc, linked
+    against the library next to it)."""
+    tmp = SERVICE_OUT + ".tmp"
+    cmd = [os.environ.get("CC", "gcc"), "-O2", "-std=c11", "-Wall", "-Wextra", "-I", INCLUDE, SERVICE_SRC,
+           "-L", HERE, "-lpicchio_hip", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath-link,/opt/rocm/lib", "-o", tmp]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("service build failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp, SERVICE_OUT)
+    return SERVICE_OUT
 
 
 if __name__ == "__main__":
