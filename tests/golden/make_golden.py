@@ -10,6 +10,7 @@ seed; the tests rebuild the same weights with the oracle's generator
 
     python tests/golden/make_golden.py            # kernel and tiny-model vectors
     python tests/golden/make_golden.py config2    # config-2 stream (~18 GB RAM)
+    python tests/golden/make_golden.py sampling   # sample_logits sequences
 """
 import os
 import shutil
@@ -211,8 +212,45 @@ def config2_stream(oracle, ref, small=None, out="config2_stream.npz"):
     oracle.model_free(model)
 
 
+SAMPLE_CASES = [  # temperature, top_p, top_k, rep_penalty (the sampler tests' cases)
+    (1.0, 0.95, 50, 1.1), (0.7, 1.0, 0, 1.0), (1.3, 0.5, 0, 1.0), (0.8, 1.0, 5, 1.3),
+    (0.0, 0.95, 50, 1.2), (1.0, 0.9, 1, 1.0)]
+
+
+def sampling(ref):
+    """sample_logits (picchio.c:1509-1649) sequences per case: the logits in,
+    the arrays as the function leaves them, the ids, the rng state after
+    each draw; the history is the ids drawn so far (as the caller keeps it)."""
+    import ctypes as C
+    rng = np.random.default_rng(20261202)
+    out = {}
+    for ci, (t, p, k, rep) in enumerate(SAMPLE_CASES):
+        for V, steps in ((64, 25), (700, 10)):
+            state = C.c_uint64(777)
+            hist, ins, outs, ids, states = [], [], [], [], []
+            for _ in range(steps):
+                lg = (rng.standard_normal(V) * 2.5).astype(np.float32)
+                b = lg.copy()
+                h = np.array(hist + [0], np.int32)
+                tok = ref.sample_logits(b, V, t, p, k, rep, C.byref(state), h, len(hist))
+                ins.append(lg)
+                outs.append(b)
+                ids.append(tok)
+                states.append(state.value)
+                hist.append(tok)
+            key = f"c{ci}_v{V}"
+            out.update({f"{key}_in": np.stack(ins), f"{key}_out": np.stack(outs),
+                        f"{key}_ids": np.array(ids, np.int32), f"{key}_rng": np.array(states, np.uint64)})
+    out["cases"] = np.array(SAMPLE_CASES, np.float64)
+    out["seed"] = np.array(777, np.uint64)
+    save("sample_logits.npz", **out)
+
+
 def main():
     oracle, ref = Oracle(), Reference()
+    if sys.argv[1:] == ["sampling"]:
+        sampling(ref)
+        return
     if sys.argv[1:] == ["config2"]:
         config2_stream(oracle, ref)
         return

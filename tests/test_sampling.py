@@ -75,6 +75,26 @@ def test_sampler_matches_reference(oracle, case):
             hist.append(tb)
 
 
+def test_sampler_matches_reference_fixtures(oracle):
+    """The oracle against sample_logits sequences recorded from the
+    reference's own function (tests/golden/sample_logits.npz, written by
+    make_golden.py sampling from oracle/_ref): ids, the arrays as the
+    function leaves them, the rng after each draw, for every case at V = 64
+    and 700; the history is the ids drawn so far."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "sample_logits.npz"))
+    seed = int(z["seed"])
+    for ci, (t, p, k, rep) in enumerate(z["cases"]):
+        for V in (64, 700):
+            key = f"c{ci}_v{V}"
+            st = oracle.sampler(float(t), float(p), int(k), float(rep), seed)
+            for i, lg in enumerate(z[f"{key}_in"]):
+                a = lg.copy()
+                assert oracle.sample_logits(st, a) == z[f"{key}_ids"][i], (key, i)
+                assert np.array_equal(a.view(np.uint32), z[f"{key}_out"][i].view(np.uint32)), (key, i)
+                assert oracle.sampler_state(st)[0] == int(z[f"{key}_rng"][i]), (key, i)
+
+
 def _draw_r(state):
     return _xorshift(state)[1]
 
