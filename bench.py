@@ -543,20 +543,42 @@ def measure_moe_layer(args):
     eng.graph_destroy(g_warm)
     eng.graph_destroy(g_run)
 
-    # each kernel of the layer as the layer runs it: eager layers with HIP
-    # events on the engine stream around every router / gate_up / down launch
-    n_prof = min(args.profile_tokens, S)
+    # the router launch alone over the same tokens, replayed the same way:
+    # the expert launch's duration is the difference of the two graphs
+    lg = eng.empty(E, torch.float32)
+    eng.capture_begin()
+    for t in range(W, n_tok):
+        eng.router_logits(t % L, xd[t], lg)
+    g_router = eng.capture_end()
+    eng.graph_launch(g_router)
+    eng.sync()
+    ev0.record(eng.stream)
+    eng.graph_launch(g_router)
+    ev1.record(eng.stream)
+    ev1.synchronize()
+    ms_router = ev0.elapsed_time(ev1)
+    eng.graph_destroy(g_router)
+
+    # the launches of an eager pass with HIP events on the engine stream around
+    # each (tells the one-launch experts from the two-launch ones; the eager
+    # events add the dispatch to each launch, so the graph difference above is
+    # the expert launch's duration)
+    n_prof = max(min(args.profile_tokens, S), 1)
     eng.profile(True)
     for t in range(W, W + n_prof):
         enqueue(t)
-    kern = {}
+    kern, eager = {}, {}
     for name, kind in (("router", pa.PROF_ROUTER), ("moe_ffn", pa.PROF_MOE_FFN),
                        ("gate_up", pa.PROF_EXPERT_GATE_UP), ("down_combine", pa.PROF_EXPERT_DOWN)):
         tot, cnt = eng.profile_read(kind)
         if cnt:
-            kern[name] = tot / cnt
+            eager[name] = tot / cnt
     eng.profile(False)
-    fused = "moe_ffn" in kern
+    fused = "moe_ffn" in eager
+    if fused:
+        kern = {"router": ms_router / S, "moe_ffn": (ms - ms_router) / S}
+    else:
+        kern = dict(eager)
     # streaming shape: all 32 experts of a layer copy in one gate_up launch
     act = eng.empty((E, HALF), torch.float32)
     all_e = eng.to_dev(np.arange(E, dtype=np.int32))
@@ -607,6 +629,9 @@ def measure_moe_layer(args):
                    "bytes_per_token": TOKEN_BYTES, "tokens_per_s": round(1e3 / ms_tok, 1),
                    "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "chained": True,
                    "kernel_us": {k: round(v * 1e3, 3) for k, v in kern.items()},
+                   "kernel_us_method": ("graph replays: router launches alone, and router + expert "
+                                        "launches; the expert launch = the difference" if fused else
+                                        "HIP events around each launch of an eager pass"),
                    "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
                    "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
                                                         / HBM_PEAK_GBPS, 4)},

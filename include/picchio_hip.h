@@ -222,6 +222,11 @@ int pk_expert_gate_up_dot(pk_engine *e, int layer, const int32_t *eids_dev, int 
 int pk_expert_down_dot(pk_engine *e, int layer, const int32_t *eids_dev, int n,
                        const int32_t *act_rec_dev, float *eo_dev);
 
+/* moe_forward's router (picchio.c:1316-1324): logits_dev[E] = R·x + b, the
+ * launch pk_moe_forward makes first (no top-k: its expert launch selects
+ * the experts). Asynchronous on the engine stream. */
+int pk_router_logits(pk_engine *e, int layer, const float *x_dev, float *logits_dev);
+
 /* moe_forward (picchio.c:1309-1466): out_dev = Σ_k (w_k·routed_scale)·expert_k(x).
  * Optional host outputs: sel_host[topk], w_host[topk] (softmaxed weights) —
  * passing either forces a stream sync. */

@@ -122,6 +122,7 @@ def lib():
         "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
+        "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
         "pk_expert_gate_up_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
         "pk_expert_down_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp]),
@@ -332,6 +333,10 @@ class Engine:
         lh.router = router.ctypes.data
         lh.router_bias = bias.ctypes.data
         check(self.L.pk_store_layer(self.h, layer, C.byref(lh)))
+
+    def router_logits(self, layer, x_dev, logits_dev):
+        """moe_forward's router launch alone: logits_dev[E] = R x + b."""
+        check(self.L.pk_router_logits(self.h, layer, ptr(x_dev), ptr(logits_dev)))
 
     def moe_forward(self, layer, x_dev, out_dev, want_routing=False):
         import numpy as np

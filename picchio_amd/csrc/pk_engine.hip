@@ -780,20 +780,28 @@ static bool moe_ffn_fits(const pk_engine *e) {
 
 // norm_w: x_dev is the raw residual row; the router normalises it (rmsnorm
 // fused) and writes the normalised row to e->hn, which the experts read.
+// The MoE layer's router launch (logits into `logits`; with norm_w the
+// normalised row into e->hn; with the integer dot the input's records).
+static int moe_router(pk_engine *e, int layer, const float *x_dev, const float *norm_w, bool dot,
+                      float *logits) {
+    const pk_cfg *c = &e->c;
+    const pk_layer_dev &d = e->L[layer];
+    return pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
+                                 c->routed_scale, logits, e->sel, e->w_scaled, e->w_soft, nullptr, e->stream,
+                                 norm_w, c->eps, norm_w ? e->hn : nullptr, dot ? e->hn_q : nullptr,
+                                 e->counters + PK_CTR_MOE_EPOCH);
+}
+
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
                  const float *residual, float *res_out, const float *norm_w) {
     const pk_cfg *c = &e->c;
-    const pk_layer_dev &d = e->L[layer];
-    // the router launch writes the logits only; the gate_up launch selects
+    // the router launch writes the logits only; the expert launch selects
     // the experts from them and publishes the routing (sel, weights)
     int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     // integer-dot arithmetic: the router also writes the input's records, the
     // gate_up epilogue those of its SwiGLU outputs for the down launch
     const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
-    PK_TRY(pk_launch_router_topk(x_dev, d.router, d.router_b, c->n_experts, c->hidden, c->topk,
-                                 c->routed_scale, e->r_logits, e->sel, e->w_scaled, e->w_soft,
-                                 nullptr, e->stream, norm_w, c->eps, norm_w ? e->hn : nullptr,
-                                 dot ? e->hn_q : nullptr, e->counters + PK_CTR_MOE_EPOCH));
+    PK_TRY(moe_router(e, layer, x_dev, norm_w, dot, e->r_logits));
     PK_TRY(pk_prof_end(e, ps));
     pk_route_args rt{};
     rt.logits = e->r_logits;
@@ -867,6 +875,15 @@ extern "C" int pk_set_moe_fused(pk_engine *e, int on) {
     }
     e->moe_fused = on != 0;
     return PK_OK;
+}
+
+extern "C" int pk_router_logits(pk_engine *e, int layer, const float *x_dev, float *logits_dev) {
+    PK_CHECK(e && x_dev && logits_dev, PK_ERR_ARG, "null argument");
+    PK_CHECK(layer >= 0 && layer < e->c.n_layers && e->L[layer].have_router, PK_ERR_MISSING,
+             "layer %d: router not loaded", layer);
+    const pk_cfg *c = &e->c;
+    const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
+    return moe_router(e, layer, x_dev, nullptr, dot, logits_dev);
 }
 
 extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,

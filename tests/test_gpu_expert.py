@@ -236,6 +236,10 @@ def test_moe_forward_parity(moe_setup, oracle):
         oracle.moe_forward(model, 0, x, out_ref, sel_ref, w_ref, logits)
         xd = eng.to_dev(x)
         od = eng.empty(D, torch.float32)
+        # the router launch alone (a fixed-tree sum: within 1e-5 absolute of the in-order one)
+        ld = eng.empty(E, torch.float32)
+        eng.router_logits(0, xd, ld)
+        assert np.allclose(eng.to_host(ld), logits, rtol=1e-5, atol=1e-5), t
         sel, w = eng.moe_forward(0, xd, od, want_routing=True)
         out = eng.to_host(od)
         srt = np.sort(logits)[::-1]
