@@ -40,10 +40,15 @@ EXPERT_BYTES = 12441600 + 1555200 + 34560          # packed + scales + biases
 ROUTER_BYTES = E * D * 4 + E * 4
 TOKEN_BYTES = K * EXPERT_BYTES + ROUTER_BYTES + 2 * D * 4      # 56,517,248
 
-# HBM bytes per 4-expert gate_up launch measured by rocprofv3 --pmc (profiles/
-# k_i4_gemv_gate_up_moe_config1.txt): FETCH_SIZE 18425.54 KiB x 2.000 +
-# WRITE_SIZE 45.04 KiB x 1.000, the factors being what the two counters read
-# for a plain copy kernel over 1 GiB.
+# HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, then
+# WRITE_SIZE, in passes of their own), scaled by what the two counters read
+# for a 1 GiB device copy in the same call (x 2.000 and x 1.000):
+#  * k_moe_ffn (the default, profiles/k_moe_ffn_moe_config1.txt), measured on
+#    commit d70a076: FETCH_SIZE 27792.77 KiB x 2 + WRITE_SIZE 168.84 KiB;
+#  * k_i4_gemv<SWIGLU> gate_up of the two-launch experts
+#    (pk_set_moe_fused(e, 0)), measured on commit 0a0ca63: FETCH_SIZE
+#    18425.54 KiB x 2 + WRITE_SIZE 45.04 KiB.
+MOE_FFN_TRAFFIC = 57092529
 GATE_UP_TRAFFIC = 37780589
 
 
@@ -594,7 +599,7 @@ def measure_moe_layer(args):
         dom, dom_bytes = "moe_ffn", gate_up_bytes(K) + down_bytes(K)
         dom_name = ("k_moe_ffn (gate_up + bias + SwiGLU, then down + bias + routing-weighted combine, "
                     "the token's 4 routed experts selected in the launch)")
-        traffic = None
+        traffic = MOE_FFN_TRAFFIC
     else:
         dom, dom_bytes = "gate_up", gate_up_bytes(K)
         dom_name = ("k_i4_gemv<SWIGLU> (gate_up + bias + SwiGLU, the layer's 4 routed experts "
