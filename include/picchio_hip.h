@@ -211,6 +211,13 @@ int pk_set_i4_dot(pk_engine *e, int on);
  * activations) or as a gate_up launch and a down launch. Same results either
  * way. Default on (PK_MOE_FUSED=0 in the environment at engine creation: off). */
 int pk_set_moe_fused(pk_engine *e, int on);
+/* Batch-1 decode attention (pk_forward_token, pk_generate; gqa_attention,
+ * picchio.c:504-623) and its output projection with the residual
+ * (picchio.c:615-616, :1690) as one launch per layer (k_attn_oproj: the
+ * projection's weight rows stream in while the attention runs) or as two
+ * launches. Same results either way. Default on (PK_ATT_FUSED=0 in the
+ * environment at engine creation: off). */
+int pk_set_attn_fused(pk_engine *e, int on);
 /* Records of x_dev[0..n) (n a multiple of 32) into rec_dev[n/32][24]. */
 int pk_act_records(pk_engine *e, const float *x_dev, int n, int32_t *rec_dev);
 /* pk_expert_gate_up / pk_expert_down on records: rec_dev = the input row's

@@ -122,6 +122,7 @@ def lib():
         "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
+        "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
         "pk_expert_gate_up_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
@@ -282,6 +283,11 @@ class Engine:
         """Batch-1 MoE layer's experts as one launch (default) or as a
         gate_up launch and a down launch; same results (pk_set_moe_fused)."""
         check(self.L.pk_set_moe_fused(self.h, 1 if on else 0))
+
+    def set_attn_fused(self, on):
+        """Batch-1 decode attention and its output projection as one launch
+        (default) or two; same results (pk_set_attn_fused)."""
+        check(self.L.pk_set_attn_fused(self.h, 1 if on else 0))
 
     def act_records(self, x_dev, rec_dev):
         """Half-group records of the integer-dot arithmetic for a device row."""

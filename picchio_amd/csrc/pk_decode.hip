@@ -10,6 +10,7 @@
 // appends it to the output list and advances the position.
 #include "pk_engine.h"
 #include "pk_dev.h"
+#include "pk_tagged.h"
 
 #include <math.h>
 #include <vector>
@@ -72,8 +73,10 @@ __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, cons
                                                        const float *__restrict__ nw, float eps,
                                                        const float *__restrict__ W, const float *__restrict__ b,
                                                        int D, int H, int KVH, int hd, const float *rope,
-                                                       float *qkv, float *Kl, float *Vl) {
+                                                       float *qkv, float *Kl, float *Vl, uint32_t *att_epoch) {
     __shared__ double npart[4];
+    // a new tag for the fused attention launch that follows
+    if (att_epoch && blockIdx.x == 0 && threadIdx.x == 0) *att_epoch = *att_epoch + 1u;
     __shared__ float pv[4];
     __shared__ __attribute__((aligned(16))) float xn[4 * 64 * QKV_U];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -241,13 +244,16 @@ __device__ __forceinline__ void att_window(int pos, int ctx, int sliding, int wi
 constexpr int ATT_THREADS = 256;
 constexpr int ATT_GH = 8;              // query heads per half-block (G <= 16)
 
+// Block (bx, by, bz) of a (gdx, gdy, rows) grid: k_attn_part's own blocks,
+// or the attention blocks of k_attn_oproj, which take the output as tagged
+// words att_t (row 0, tag) instead of att.
 template <int KD4>
-__global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
-                                                           const float *qkv, int64_t qkv_stride, const float *Kl,
-                                                           const float *Vl, int64_t kv_row, int H, int KVH,
-                                                           int hd, int ctx, int sliding, int window, float *part,
-                                                           int max_chunks, const float *sinks, float *att,
-                                                           uint32_t *ctr, int gs) {
+__device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_base, int pos_step, const float *qkv,
+                                                int64_t qkv_stride, const float *Kl, const float *Vl, int64_t kv_row,
+                                                int H, int KVH, int hd, int ctx, int sliding, int window,
+                                                float *part, int max_chunks, const float *sinks, float *att,
+                                                uint32_t *ctr, int gs, int bx, int by, int bz, int gdx, int gdy,
+                                                uint64_t *att_t, uint32_t tag) {
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     const int G = gs;                         // heads of this block
     float *q = att_lds;                       // [G][hd]
@@ -261,15 +267,15 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
     // own L2: the SUB blocks that read the same (KV head, chunk) tile get ids
     // equal mod 8, so the tile comes from HBM once.
     const int SUB = (H / KVH) / gs;
-    int b = blockIdx.x, c = blockIdx.y;
-    if (SUB > 1 && (KVH * (int)gridDim.y) % 8 == 0) {
-        const int L = blockIdx.x + gridDim.x * blockIdx.y;
+    int b = bx, c = by;
+    if (SUB > 1 && (KVH * gdy) % 8 == 0) {
+        const int L = bx + gdx * by;
         const int q8 = L >> 3, p8 = L & 7;
         const int pp = (q8 / SUB) * 8 + p8;            // (KV head, chunk) pair
         c = pp / KVH;
         b = (pp - c * KVH) * SUB + q8 % SUB;
     }
-    const int r = blockIdx.z;
+    const int r = bz;
     const int kvh = b / SUB;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int half = tid >> 7, tt = tid & 127;
@@ -411,7 +417,9 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
             const float e = expf(mh[j] - M);
             float S = expf(sinks[h] - M);
             S += ssum[j] * e;
-            att[(int64_t)r * H * hd + h * hd + i] = __builtin_fmaf(o, e, 0.0f) / S;
+            const float v = __builtin_fmaf(o, e, 0.0f) / S;
+            if (att_t) pk_put_tagged(att_t + h * hd + i, tag, __float_as_uint(v));
+            else att[(int64_t)r * H * hd + h * hd + i] = v;
         }
         return;
     }
@@ -425,7 +433,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
     // arrival: the last of the nc chunk blocks of (row, b) combines
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    uint32_t *cnt = ctr + (int64_t)r * gridDim.x + b;
+    uint32_t *cnt = ctr + (int64_t)r * gdx + b;
     if (tid == 0)
         last = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == (uint32_t)(nc - 1);
     __syncthreads();
@@ -482,7 +490,8 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
                 for (int u = 0; u < CB; ++u)
                     if (c0 + u < nc) o = __builtin_fmaf(ov[u], cm[j * nc + c0 + u], o);
             }
-            att[(int64_t)r * H * hd + h * hd + i] = o / hS[j];
+            if (att_t) pk_put_tagged(att_t + h * hd + i, tag, __float_as_uint(o / hS[j]));
+            else att[(int64_t)r * H * hd + h * hd + i] = o / hS[j];
         }
     } else {
         // windows longer than 128 chunks: the same arithmetic, reading the
@@ -522,16 +531,30 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, 
                 for (int u = 0; u < CB; ++u)
                     if (c0 + u < nc) o = __builtin_fmaf(ov[u], expf(mv[u] - M), o);
             }
-            att[(int64_t)r * H * hd + h * hd + i] = o / S;
+            if (att_t) pk_put_tagged(att_t + h * hd + i, tag, __float_as_uint(o / S));
+            else att[(int64_t)r * H * hd + h * hd + i] = o / S;
         }
     }
     if (tid == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <int KD4>
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_part(const pk_dstate *st, int pos_base, int pos_step,
+                                                           const float *qkv, int64_t qkv_stride, const float *Kl,
+                                                           const float *Vl, int64_t kv_row, int H, int KVH,
+                                                           int hd, int ctx, int sliding, int window, float *part,
+                                                           int max_chunks, const float *sinks, float *att,
+                                                           uint32_t *ctr, int gs) {
+    attn_part_block<KD4>(st, pos_base, pos_step, qkv, qkv_stride, Kl, Vl, kv_row, H, KVH, hd, ctx, sliding, window,
+                         part, max_chunks, sinks, att, ctr, gs, blockIdx.x, blockIdx.y, blockIdx.z, gridDim.x,
+                         gridDim.y, nullptr, 0);
 }
 
 // y[o] += (W[o] . x + b[o])  — attention output projection + residual
 // (picchio.c:615-616, :1690). One workgroup per 4 outputs (one per wave);
 // grid.y = row of a batch (x [rows][I], y [rows][O]).
 constexpr int RES_U = 16;              // float4 per lane loaded up front (4096 columns)
+constexpr int ATT_RPW = 2;             // k_attn_oproj: output rows per wave
 
 __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restrict__ x,
                                                   const float *__restrict__ W,
@@ -549,6 +572,8 @@ __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restr
     // (range-checked buffer loads, all issued before the first use; entries
     // past the row read as zero and are not used)
     const pk_buf_t wr = pk_buf(w4, (uint32_t)n4 * 16u), xr = pk_buf(x4, (uint32_t)n4 * 16u);
+    // the residual and the bias at entry (at the end each would cost a round trip)
+    const float yo = y[o], bo = b[o];
     pk_f32x4 wv[RES_U];
     float4 xv[RES_U];
 #pragma unroll
@@ -576,7 +601,104 @@ __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restr
     }
     for (int i = (n4 << 2) + lane; i < I; i += 64) acc = __builtin_fmaf(x[i], W[(int64_t)o * I + i], acc);
     acc = wave_sum(acc);
-    if (lane == 0) y[o] = y[o] + (acc + b[o]);
+    if (lane == 0) y[o] = yo + (acc + bo);
+}
+
+// Decode attention and its output projection in one launch (one row,
+// picchio.c:504-623 then :615-616, :1690). Blocks [0, gdx * gdy) are
+// k_attn_part's blocks; they hand the attention row over as tagged words
+// (pk_tagged.h, tag = *epoch, advanced by the QKV launch before). Each
+// other block computes y[o] += W[o] . att + b[o] for 4 * ATT_RPW rows o
+// (ATT_RPW per wave) with k_gemv_res's arithmetic per row: its weight rows
+// go out at entry, so that they stream in while the attention runs, then
+// the block reads the tagged row into LDS (one read per block: two rows
+// per wave halve those reads) and finishes. The attention blocks wait for nothing
+// (their chunk combine is a last-arrival count) and come first in dispatch
+// order, so the waiting blocks cannot hold them back.
+template <int KD4>
+__global__ __launch_bounds__(ATT_THREADS) void k_attn_oproj(const pk_dstate *st, const float *qkv, const float *Kl,
+                                                            const float *Vl, int H, int KVH, int hd, int ctx,
+                                                            int sliding, int window, float *part, int max_chunks,
+                                                            const float *sinks, uint32_t *ctr, int gs, int gdx,
+                                                            int gdy, uint64_t *att_t, const uint32_t *epoch,
+                                                            uint32_t *status, float *y, const float *__restrict__ W,
+                                                            const float *__restrict__ b, int O) {
+    extern __shared__ __attribute__((aligned(16))) float att_lds[];
+    const uint32_t tag = __builtin_amdgcn_readfirstlane(*epoch);
+    const int n_att = gdx * gdy;
+    if ((int)blockIdx.x < n_att) {
+        const int bx = blockIdx.x % gdx, by = blockIdx.x / gdx;
+        attn_part_block<KD4>(st, 0, 0, qkv, 0, Kl, Vl, 0, H, KVH, hd, ctx, sliding, window, part, max_chunks,
+                             sinks, nullptr, ctr, gs, bx, by, 0, gdx, gdy, att_t, tag);
+        return;
+    }
+    const int lane = threadIdx.x & 63;
+    const int o0 = (((int)blockIdx.x - n_att) * 4 + (threadIdx.x >> 6)) * ATT_RPW;   // this wave's rows
+    const int I = H * hd, n4 = I >> 2;                 // I <= 64 * RES_U * 4, I % 4 == 0
+    // the residual rows and biases first (read again at the end they would
+    // cost a round trip of their own), then the weight rows
+    float yv[ATT_RPW], bv[ATT_RPW];
+#pragma unroll
+    for (int k = 0; k < ATT_RPW; ++k) {
+        yv[k] = y[min(o0 + k, O - 1)];
+        bv[k] = b[min(o0 + k, O - 1)];
+    }
+    pk_f32x4 wv[ATT_RPW][RES_U];
+#pragma unroll
+    for (int k = 0; k < ATT_RPW; ++k) {
+        const pk_buf_t wr = pk_buf(W + (int64_t)min(o0 + k, O - 1) * I, (uint32_t)n4 * 16u);
+#pragma unroll
+        for (int u = 0; u < RES_U; ++u) wv[k][u] = pk_buf_load4_nt(wr, (uint32_t)(lane + u * 64) * 16u);
+    }
+    // the attention row: RES_U / 4 tagged words per thread, polled until all
+    // carry this launch's tag
+    constexpr int TW = RES_U * 64 * 4 / ATT_THREADS;
+    uint64_t tw[TW];
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+        const int i = threadIdx.x + k * ATT_THREADS;
+        tw[k] = i < I ? __hip_atomic_load(att_t + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
+    }
+    for (uint32_t n = 0;; ++n) {
+        bool stale = false;
+#pragma unroll
+        for (int k = 0; k < TW; ++k) stale |= (uint32_t)(tw[k] >> 32) != tag;
+        if (!__any(stale)) break;
+        if (n == PK_POLL_BOUND) {
+            if (lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int k = 0; k < TW; ++k)
+            if ((uint32_t)(tw[k] >> 32) != tag)
+                tw[k] = __hip_atomic_load(att_t + threadIdx.x + k * ATT_THREADS, __ATOMIC_RELAXED,
+                                          __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int k = 0; k < TW; ++k) {
+        const int i = threadIdx.x + k * ATT_THREADS;
+        if (i < I) att_lds[i] = __uint_as_float((uint32_t)tw[k]);
+    }
+    __syncthreads();
+    const float4 *x4 = reinterpret_cast<const float4 *>(att_lds);
+    float acc[ATT_RPW];
+#pragma unroll
+    for (int k = 0; k < ATT_RPW; ++k) acc[k] = 0.0f;
+#pragma unroll
+    for (int u = 0; u < RES_U; ++u) {
+        const int i = lane + u * 64;
+        if (i < n4) {
+            const float4 xv = x4[i];
+#pragma unroll
+            for (int k = 0; k < ATT_RPW; ++k) qkv_fma4(acc[k], xv, wv[k][u]);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < ATT_RPW; ++k) {
+        const float a = wave_sum(acc[k]);
+        if (lane == 0 && o0 + k < O) y[o0 + k] = yv[k] + (a + bv[k]);
+    }
 }
 
 // lm_head GEMV (fp32 or INT8 rows) and the greedy argmax of sample_logits
@@ -754,7 +876,8 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                  PK_ERR_UNSUPPORTED, "qkv: needs 16-byte aligned rows");
         const int n_pairs = (H + 2 * KVH) * hd / 2;
         hipLaunchKernelGGL(k_qkv_rope_norm, dim3((n_pairs + 1) / 2), dim3(256), 0, e->stream, st, xn, norm_w,
-                           c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl);
+                           c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl,
+                           e->counters + PK_CTR_ATT_EPOCH);
         PK_HIP(hipGetLastError());
     } else {
         if (exact)
@@ -795,12 +918,29 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
         const int f = atoi(v);
         if (f >= 1 && f <= G && G % f == 0) gs = f;
     }
+    // the decode row with the norm fused into QKV: attention and output
+    // projection in one launch (256-thread blocks: two heads per block)
+    const bool fuse = norm_w && e->attn_fused && n == 1 && G % 2 == 0 && (H * hd) % 4 == 0 &&
+                      H * hd <= 64 * RES_U * 4;
+    if (fuse && gs < 2) gs = 2;
     PK_CHECK((int64_t)n * (H / gs) <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d blocks", n,
              H / gs);
     const size_t att_lds = (size_t)gs * (hd + ATT_CHUNK + ATT_CHUNK * 4) * sizeof(float);
     // K / V rows held in registers: 16 float4 up to head_dim 64, else 32
     auto kern = hd <= 64 ? k_attn_part<16> : k_attn_part<32>;
     PK_CHECK(hd % 4 == 0 && hd <= 128, PK_ERR_UNSUPPORTED, "attention: head_dim %d", hd);
+    if (fuse) {
+        auto kf = hd <= 64 ? k_attn_oproj<16> : k_attn_oproj<32>;
+        const int gdx = H / gs;
+        const int rows_pb = 4 * ATT_RPW;
+        const size_t lds = std::max(att_lds, (size_t)H * hd * sizeof(float));
+        hipLaunchKernelGGL(kf, dim3(gdx * chunks + (D + rows_pb - 1) / rows_pb), dim3(ATT_THREADS), lds, e->stream, st, qkv, Kl, Vl,
+                           H, KVH, hd, c->ctx_len, sliding, c->sliding_window, part, max_chunks, d.sinks,
+                           e->counters + PK_CTR_ATTN, gs, gdx, chunks, e->att_t, e->counters + PK_CTR_ATT_EPOCH,
+                           e->counters + PK_CTR_MOE_STATUS, h, d.wo, d.bo, D);
+        PK_HIP(hipGetLastError());
+        return pk_prof_end(e, ps);
+    }
     hipLaunchKernelGGL(kern, dim3(H / gs, chunks, n), dim3(gs > 1 ? ATT_THREADS : ATT_CHUNK), att_lds,
                        e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,

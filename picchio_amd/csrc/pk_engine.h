@@ -35,7 +35,8 @@ struct pk_sampler_dev {
 // counters[] layout (uint32, zero-initialised, re-armed by their users)
 constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_MOE_EPOCH = 8;      // router launches so far: k_moe_ffn's hand-over tag
-constexpr int PK_CTR_MOE_STATUS = 40;    // k_moe_ffn: 1 once a wait gave up (checked by the host)
+constexpr int PK_CTR_ATT_EPOCH = 16;     // fused-QKV launches so far: k_attn_oproj's hand-over tag
+constexpr int PK_CTR_MOE_STATUS = 40;    // k_moe_ffn / k_attn_oproj: 1 once a wait gave up (checked by the host)
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
@@ -87,6 +88,10 @@ struct pk_engine {
     int32_t *act_q = nullptr;                 // [topk] SwiGLU outputs' records
     uint64_t *moe_act_t = nullptr;            // k_moe_ffn hand-over words: [topk][max(gu RB x 24, moe_inter/2)]
     uint64_t *moe_eo_t = nullptr;             // k_moe_ffn hand-over words: [topk][hidden]
+    // batch-1 decode attention and its output projection as one k_attn_oproj
+    // launch (PK_ATT_FUSED=0: two launches)
+    bool attn_fused = true;
+    uint64_t *att_t = nullptr;                // k_attn_oproj hand-over words: [heads x head_dim]
 
     bool capturing = false;                  // inside pk_capture_begin/end
 

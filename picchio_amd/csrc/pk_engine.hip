@@ -149,7 +149,7 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
-                    e->moe_act_t, e->moe_eo_t};
+                    e->moe_act_t, e->moe_eo_t, e->att_t};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -215,10 +215,13 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->moe_eo_t, (int64_t)K * D * 8);
     PK_HIP(hipMemsetAsync(e->moe_act_t, 0, (int64_t)K * act_words * 8, e->stream));
     PK_HIP(hipMemsetAsync(e->moe_eo_t, 0, (int64_t)K * D * 8, e->stream));
+    ALLOC(e->att_t, (int64_t)c->n_heads * c->head_dim * 8);
+    PK_HIP(hipMemsetAsync(e->att_t, 0, (int64_t)c->n_heads * c->head_dim * 8, e->stream));
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
     if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v) != 0;
+    if (const char *v = getenv("PK_ATT_FUSED")) e->attn_fused = atoi(v) != 0;
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -268,7 +271,7 @@ int pk_check_waits(pk_engine *e) {
     if (st) {
         PK_HIP(hipMemsetAsync(e->counters + PK_CTR_MOE_STATUS, 0, 4, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
-        pk_set_error("a device-side wait of the expert launch gave up: results are invalid");
+        pk_set_error("a device-side wait (expert or attention launch) gave up: results are invalid");
         return PK_ERR_HIP;
     }
     return PK_OK;
@@ -874,6 +877,18 @@ extern "C" int pk_set_moe_fused(pk_engine *e, int on) {
         e->step_cap = -1;
     }
     e->moe_fused = on != 0;
+    return PK_OK;
+}
+
+extern "C" int pk_set_attn_fused(pk_engine *e, int on) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_attn_fused: not available while capturing");
+    if (e->attn_fused != (on != 0) && e->step_exec) {   // the captured step holds the other kernels
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+        e->step_cap = -1;
+    }
+    e->attn_fused = on != 0;
     return PK_OK;
 }
 

@@ -16,6 +16,7 @@
 #include "pk_internal.h"
 
 #include "pk_i4_device.h"
+#include "pk_tagged.h"
 
 // ───────────────────────── tiled GEMV ─────────────────────────
 // grid = (RB, n_items); block = NW waves. Wave w handles groups w, w+NW, ...
@@ -294,14 +295,9 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
 // workgroups also take the down task of the same index (same item, so the
 // same expert) once their gate_up math is done. Every workgroup selects its
 // expert from the router logits (round `item` of the top-k).
-// Values that cross workgroups travel without fences, as 64-bit words
-// (tag << 32 | bits) written and read with device-scope atomics; the tag is
-// *epoch, a device word that the router launch before each expert launch
-// advances (never 0: the hand-over buffers start zeroed). A reader polls its
-// words until every tag matches: a word is single-copy atomic, so a
-// matching tag carries this launch's value.
-// The polls are bounded: past the bound a wave flags *status and goes on, so
-// that every wave ends (the host turns the flag into an error).
+// Values that cross workgroups travel as tagged words (pk_tagged.h); the
+// tag is *epoch, a device word that the router launch before each expert
+// launch advances.
 //  * gate_up task: the k_i4_gemv SwiGLU body (fp32 chains, or the integer
 //    dot on the input records); wave 0 publishes the row block's 32
 //    activations (fp32) or their record (integer dot) as tagged words.
@@ -319,27 +315,6 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
 // started yet always finds a slot whatever the dispatch order.
 // Wave 0 runs each epilogue at the highest wave priority (s_setprio): the
 // epilogues are the launch's critical path.
-constexpr uint32_t PK_POLL_BOUND = 1u << 18;
-
-// Polls the tagged word at p (lanes with use) until its tag is `tag` on
-// every such lane of the wave; returns the low halves.
-__device__ __forceinline__ uint32_t pk_wait_tagged(const uint64_t *p, bool use, uint32_t tag, uint32_t *status) {
-    uint64_t w = use ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
-    uint32_t n = 0;
-    while (__any((uint32_t)(w >> 32) != tag)) {
-        __builtin_amdgcn_s_sleep(1);
-        if ((uint32_t)(w >> 32) != tag) w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        if (++n == PK_POLL_BOUND) {
-            if ((threadIdx.x & 63) == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-    }
-    return (uint32_t)w;
-}
-
-__device__ __forceinline__ void pk_put_tagged(uint64_t *p, uint32_t tag, uint32_t bits) {
-    __hip_atomic_store(p, (uint64_t)tag << 32 | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
 
 // KM: an upper bound of the routed experts K. NW waves of GPW groups each
 // cover a row block's groups in one pass; WPE: waves per SIMD the launch

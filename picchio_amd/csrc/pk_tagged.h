@@ -1,0 +1,33 @@
+// pk_tagged.h — hand-over of values between workgroups of one launch.
+//
+// A value travels as a 64-bit word (tag << 32 | bits) written and read with
+// relaxed agent-scope atomics: a word is single-copy atomic, so a reader that
+// sees this launch's tag in a word sees the value that goes with it, and no
+// fence (an L2 write-back or invalidate) is needed. The tag is a counter that
+// the launch before advances (never 0: the buffers start zeroed).
+// Polls are bounded: past the bound a wave sets *status and goes on, so that
+// every wave ends; the host turns the flag into an error.
+#pragma once
+#include "pk_internal.h"
+
+constexpr uint32_t PK_POLL_BOUND = 1u << 18;
+
+// Polls the tagged word at p (lanes with use) until its tag is `tag` on
+// every such lane of the wave; returns the low halves.
+__device__ __forceinline__ uint32_t pk_wait_tagged(const uint64_t *p, bool use, uint32_t tag, uint32_t *status) {
+    uint64_t w = use ? __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
+    uint32_t n = 0;
+    while (__any((uint32_t)(w >> 32) != tag)) {
+        __builtin_amdgcn_s_sleep(1);
+        if ((uint32_t)(w >> 32) != tag) w = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (++n == PK_POLL_BOUND) {
+            if ((threadIdx.x & 63) == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            break;
+        }
+    }
+    return (uint32_t)w;
+}
+
+__device__ __forceinline__ void pk_put_tagged(uint64_t *p, uint32_t tag, uint32_t bits) {
+    __hip_atomic_store(p, (uint64_t)tag << 32 | bits, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
