@@ -218,12 +218,6 @@ int pk_set_moe_fused(pk_engine *e, int on);
  * launches. Same results either way. Default on (PK_ATT_FUSED=0 in the
  * environment at engine creation: off). */
 int pk_set_attn_fused(pk_engine *e, int on);
-/* With the attention launch fused (pk_set_attn_fused), the MoE layer's
- * router (post-attention RMSNorm and logits, picchio.c:1316-1324) runs in
- * it too, on the residual row its output projection hands over, instead of
- * as a launch of its own. Same results either way. Default on
- * (PK_ROUTER_FUSED=0 in the environment at engine creation: off). */
-int pk_set_router_fused(pk_engine *e, int on);
 /* Records of x_dev[0..n) (n a multiple of 32) into rec_dev[n/32][24]. */
 int pk_act_records(pk_engine *e, const float *x_dev, int n, int32_t *rec_dev);
 /* pk_expert_gate_up / pk_expert_down on records: rec_dev = the input row's

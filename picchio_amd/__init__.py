@@ -123,7 +123,6 @@ def lib():
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
-        "pk_set_router_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
         "pk_expert_gate_up_dot": (C.c_int, [vp, C.c_int, vp, C.c_int, vp, vp, vp]),
@@ -289,11 +288,6 @@ class Engine:
         """Batch-1 decode attention and its output projection as one launch
         (default) or two; same results (pk_set_attn_fused)."""
         check(self.L.pk_set_attn_fused(self.h, 1 if on else 0))
-
-    def set_router_fused(self, on):
-        """With the fused attention launch, the MoE router in it (default) or
-        in a launch of its own; same results (pk_set_router_fused)."""
-        check(self.L.pk_set_router_fused(self.h, 1 if on else 0))
 
     def act_records(self, x_dev, rec_dev):
         """Half-group records of the integer-dot arithmetic for a device row."""

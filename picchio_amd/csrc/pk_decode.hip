@@ -11,7 +11,6 @@
 #include "pk_engine.h"
 #include "pk_dev.h"
 #include "pk_tagged.h"
-#include "pk_router.h"
 
 #include <math.h>
 #include <vector>
@@ -605,79 +604,6 @@ __global__ __launch_bounds__(256) void k_gemv_res(float *y, const float *__restr
     if (lane == 0) y[o] = yo + (acc + bo);
 }
 
-// The router of the MoE layer that follows, folded into k_attn_oproj: E
-// workgroups, one per expert, each with k_router_topk's arithmetic for its
-// logit (pk_router.h) on the residual row that the output projection's
-// waves hand over as tagged words h_t.
-struct pk_attn_router {
-    const float *R, *rb, *nw;  // router [E][D], its bias, the post-attention norm weights
-    float eps;
-    int E;                     // 0: no router in the launch
-    float *logits, *hn;        // outputs: logits (+ bias), normalised row slices
-    int32_t *hq;               // integer-dot records of the normalised row (or null)
-    uint32_t *moe_epoch;       // advanced once: the expert launch's tag
-    uint64_t *h_t;             // [D] the residual row as tagged words
-};
-
-__device__ __forceinline__ void attn_router_block(const pk_attn_router &rt, int e, int D, uint32_t tag,
-                                                  uint32_t *status, float *xs) {
-    __shared__ float red[4];
-    __shared__ double npart[4];
-    if (e == 0 && threadIdx.x == 0) *rt.moe_epoch = *rt.moe_epoch + 1u;
-    // the router row and the norm weights go out first (D <= 3072)
-    const int n4 = D >> 2;
-    const pk_buf_t wr = pk_buf(rt.R + (int64_t)e * D, (uint32_t)n4 * 16u), nr = pk_buf(rt.nw, (uint32_t)n4 * 16u);
-    float4 wf[PK_ROUTER_U], xw[PK_ROUTER_U];
-#pragma unroll
-    for (int u = 0; u < PK_ROUTER_U; ++u) {
-        const uint32_t off = ((uint32_t)threadIdx.x + u * 256u) * 16u;
-        wf[u] = pk_buf_load4(wr, off);
-        xw[u] = pk_buf_load4(nr, off);
-    }
-    const float be = rt.rb[e];
-    // the residual row: 12 tagged words per thread, polled until all carry
-    // this launch's tag, into LDS
-    uint64_t tw[12];
-#pragma unroll
-    for (int k = 0; k < 12; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        tw[k] = i < D ? __hip_atomic_load(rt.h_t + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
-    }
-    for (uint32_t n = 0;; ++n) {
-        bool stale = false;
-#pragma unroll
-        for (int k = 0; k < 12; ++k) stale |= (uint32_t)(tw[k] >> 32) != tag;
-        if (!__any(stale)) break;
-        if (n == PK_POLL_BOUND) {
-            if ((threadIdx.x & 63) == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            break;
-        }
-        __builtin_amdgcn_s_sleep(1);
-#pragma unroll
-        for (int k = 0; k < 12; ++k)
-            if ((uint32_t)(tw[k] >> 32) != tag)
-                tw[k] = __hip_atomic_load(rt.h_t + threadIdx.x + 256 * k, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    float hv[12];
-#pragma unroll
-    for (int k = 0; k < 12; ++k) {
-        const int i = threadIdx.x + 256 * k;
-        hv[k] = i < D ? __uint_as_float((uint32_t)tw[k]) : 0.0f;
-        if (i < D) xs[i] = hv[k];
-    }
-    __syncthreads();
-    const float4 *xs4 = reinterpret_cast<const float4 *>(xs);
-    float4 xh[PK_ROUTER_U];
-#pragma unroll
-    for (int u = 0; u < PK_ROUTER_U; ++u) {
-        const int i = threadIdx.x + u * 256;
-        xh[u] = i < n4 ? xs4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-    }
-    const float v = pk_router_norm_logit(hv, xh, wf, xw, xs, rt.R + (int64_t)e * D, rt.nw, D, rt.eps, e, rt.E,
-                                         rt.hn, rt.hq, red, npart);
-    if (threadIdx.x == 0) rt.logits[e] = v + be;
-}
-
 // Decode attention and its output projection in one launch (one row,
 // picchio.c:504-623 then :615-616, :1690). Blocks [0, gdx * gdy) are
 // k_attn_part's blocks; they hand the attention row over as tagged words
@@ -686,12 +612,9 @@ __device__ __forceinline__ void attn_router_block(const pk_attn_router &rt, int 
 // (ATT_RPW per wave) with k_gemv_res's arithmetic per row: its weight rows
 // go out at entry, so that they stream in while the attention runs, then
 // the block reads the tagged row into LDS (one read per block: two rows
-// per wave halve those reads) and finishes. With rt.E > 0 the last E
-// blocks run the router of the MoE layer that follows (attn_router_block)
-// on the residual rows the projection's waves hand over. The attention blocks wait for nothing
+// per wave halve those reads) and finishes. The attention blocks wait for nothing
 // (their chunk combine is a last-arrival count) and come first in dispatch
-// order, so the waiting blocks cannot hold them back; the router blocks,
-// last, wait only for the projection's.
+// order, so the waiting blocks cannot hold them back.
 template <int KD4>
 __global__ __launch_bounds__(ATT_THREADS) void k_attn_oproj(const pk_dstate *st, const float *qkv, const float *Kl,
                                                             const float *Vl, int H, int KVH, int hd, int ctx,
@@ -699,16 +622,10 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_oproj(const pk_dstate *st,
                                                             const float *sinks, uint32_t *ctr, int gs, int gdx,
                                                             int gdy, uint64_t *att_t, const uint32_t *epoch,
                                                             uint32_t *status, float *y, const float *__restrict__ W,
-                                                            const float *__restrict__ b, int O,
-                                                            pk_attn_router rt) {
+                                                            const float *__restrict__ b, int O) {
     extern __shared__ __attribute__((aligned(16))) float att_lds[];
     const uint32_t tag = __builtin_amdgcn_readfirstlane(*epoch);
     const int n_att = gdx * gdy;
-    const int n_op = (O + 4 * ATT_RPW - 1) / (4 * ATT_RPW);
-    if ((int)blockIdx.x >= n_att + n_op) {
-        attn_router_block(rt, (int)blockIdx.x - n_att - n_op, O, tag, status, att_lds);
-        return;
-    }
     if ((int)blockIdx.x < n_att) {
         const int bx = blockIdx.x % gdx, by = blockIdx.x / gdx;
         attn_part_block<KD4>(st, 0, 0, qkv, 0, Kl, Vl, 0, H, KVH, hd, ctx, sliding, window, part, max_chunks,
@@ -780,11 +697,7 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_oproj(const pk_dstate *st,
 #pragma unroll
     for (int k = 0; k < ATT_RPW; ++k) {
         const float a = wave_sum(acc[k]);
-        if (lane == 0 && o0 + k < O) {
-            const float v = yv[k] + (a + bv[k]);
-            y[o0 + k] = v;
-            if (rt.h_t) pk_put_tagged(rt.h_t + o0 + k, tag, __float_as_uint(v));
-        }
+        if (lane == 0 && o0 + k < O) y[o0 + k] = yv[k] + (a + bv[k]);
     }
 }
 
@@ -947,7 +860,7 @@ int pk_check_model(pk_engine *e) {
 // and adds the output projection into h [n][D] (residual).
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
                       int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
-                      const float *norm_w, bool exact, bool *routed) {
+                      const float *norm_w, bool exact) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[l];
     const int H = c->n_heads, KVH = c->n_kv_heads, hd = c->head_dim, D = c->hidden;
@@ -1020,28 +933,11 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
         auto kf = hd <= 64 ? k_attn_oproj<16> : k_attn_oproj<32>;
         const int gdx = H / gs;
         const int rows_pb = 4 * ATT_RPW;
-        const size_t lds = std::max(att_lds, (size_t)std::max(H * hd, D) * sizeof(float));
-        // the MoE layer's router in the same launch (the caller then skips
-        // its router launch): the arguments of pk_moe_layer's
-        pk_attn_router rt{};
-        if (routed && e->router_fused && d.have_router && d.post_ln && D <= 12 * 256 &&
-            ((uintptr_t)d.router & 15) == 0 && ((uintptr_t)d.post_ln & 15) == 0) {
-            rt.R = d.router;
-            rt.rb = d.router_b;
-            rt.nw = d.post_ln;
-            rt.eps = c->eps;
-            rt.E = c->n_experts;
-            rt.logits = e->r_logits;
-            rt.hn = e->hn;
-            rt.hq = pk_moe_dot(e) ? e->hn_q : nullptr;
-            rt.moe_epoch = e->counters + PK_CTR_MOE_EPOCH;
-            rt.h_t = e->h_t;
-            *routed = true;
-        }
-        hipLaunchKernelGGL(kf, dim3(gdx * chunks + (D + rows_pb - 1) / rows_pb + rt.E), dim3(ATT_THREADS), lds,
-                           e->stream, st, qkv, Kl, Vl, H, KVH, hd, c->ctx_len, sliding, c->sliding_window, part,
-                           max_chunks, d.sinks, e->counters + PK_CTR_ATTN, gs, gdx, chunks, e->att_t,
-                           e->counters + PK_CTR_ATT_EPOCH, e->counters + PK_CTR_MOE_STATUS, h, d.wo, d.bo, D, rt);
+        const size_t lds = std::max(att_lds, (size_t)H * hd * sizeof(float));
+        hipLaunchKernelGGL(kf, dim3(gdx * chunks + (D + rows_pb - 1) / rows_pb), dim3(ATT_THREADS), lds, e->stream, st, qkv, Kl, Vl,
+                           H, KVH, hd, c->ctx_len, sliding, c->sliding_window, part, max_chunks, d.sinks,
+                           e->counters + PK_CTR_ATTN, gs, gdx, chunks, e->att_t, e->counters + PK_CTR_ATT_EPOCH,
+                           e->counters + PK_CTR_MOE_STATUS, h, d.wo, d.bo, D);
         PK_HIP(hipGetLastError());
         return pk_prof_end(e, ps);
     }
@@ -1073,11 +969,9 @@ struct att_cap_scope {
 
 // Decode attention of layer l on the residual row h (in_ln rmsnorm fused
 // into the QKV GEMV); adds the output projection into h.
-// With routed, the MoE layer's router may run in the same launch
-// (*routed = true then).
-static int attention_layer(pk_engine *e, int l, bool *routed = nullptr) {
+static int attention_layer(pk_engine *e, int l) {
     return pk_attention_rows(e, l, e->dstate, 0, 0, 0, 0, 1, e->h, e->qkv, e->attn_part, e->att, e->h,
-                             e->L[l].in_ln, false, routed);
+                             e->L[l].in_ln);
 }
 
 // One forward_token step with tok/pos in device state; logits optional.
@@ -1088,10 +982,9 @@ static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int o
                        e->h, e->hn, e->L[0].in_ln, D, c->eps);
     PK_HIP(hipGetLastError());
     for (int l = 0; l < c->n_layers; ++l) {
-        bool routed = false;
-        PK_TRY(attention_layer(e, l, &routed));
+        PK_TRY(attention_layer(e, l));
         // h += moe(rmsnorm(h)): the router normalises h and writes hn for the experts
-        PK_TRY(pk_moe_layer(e, l, e->h, nullptr, e->h, e->h, e->L[l].post_ln, routed));
+        PK_TRY(pk_moe_layer(e, l, e->h, nullptr, e->h, e->h, e->L[l].post_ln));
     }
     PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->final_norm, D, c->eps, 1, e->stream));
     return pk_lm_head_step(e, e->hn, logits_dev, out_toks, out_cap);

@@ -3,7 +3,6 @@
 #include "pk_internal.h"
 #include "pk_dev.h"
 #include "pk_i4_device.h"
-#include "pk_router.h"
 #include "pk_synth.h"
 
 // ───────────────────────── wave reductions ─────────────────────────
@@ -454,6 +453,7 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
     __shared__ int last;
     const int e = blockIdx.x;
     float v;
+    float rn = 1.0f;
     if (nw) {
         const float4 *w4 = reinterpret_cast<const float4 *>(R + (int64_t)e * D);
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
@@ -468,28 +468,64 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
         // it read as zero and are not used), then the first chunk's inputs
         const pk_buf_t wr = pk_buf(w4, (uint32_t)n4 * 16u), xr = pk_buf(x4, (uint32_t)n4 * 16u),
                        nr = pk_buf(n4w, (uint32_t)n4 * 16u);
-        float4 wf[PK_ROUTER_U], xh[PK_ROUTER_U], xw[PK_ROUTER_U];
+        float4 wf[GEMV_U], xh[GEMV_U], xw[GEMV_U];
 #pragma unroll
-        for (int u = 0; u < PK_ROUTER_U; ++u) {
+        for (int u = 0; u < GEMV_U; ++u) {
             const uint32_t off = ((uint32_t)threadIdx.x + u * 256u) * 16u;
             wf[u] = pk_buf_load4(wr, off);
             xh[u] = pk_buf_load4(xr, off);
             xw[u] = pk_buf_load4(nr, off);
         }
-        v = pk_router_norm_logit(hv, xh, wf, xw, x, R + (int64_t)e * D, nw, D, eps, e, E, hn, hq, red, npart);
+        rn = pk_rms_finish(hv, x, D, eps, npart);
+        if (!hq) {
+            const int span = (D + E - 1) / E;
+            for (int i = e * span + threadIdx.x; i < min(D, (e + 1) * span); i += 256) hn[i] = x[i] * rn * nw[i];
+        }
+        float acc = 0.0f;
+        for (int i0 = threadIdx.x; i0 < n4; i0 += 256 * GEMV_U) {
+            if (i0 != (int)threadIdx.x) {
+#pragma unroll
+                for (int u = 0; u < GEMV_U; ++u) {
+                    const uint32_t off = ((uint32_t)i0 + u * 256u) * 16u;
+                    wf[u] = pk_buf_load4(wr, off);
+                    xh[u] = pk_buf_load4(xr, off);
+                    xw[u] = pk_buf_load4(nr, off);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < GEMV_U; ++u) {
+                const int i = i0 + u * 256;
+                if (i < n4) {
+                    const float4 xv = pk_norm4(xh[u], rn, xw[u]);
+                    acc = __builtin_fmaf(xv.x, wf[u].x, acc);
+                    acc = __builtin_fmaf(xv.y, wf[u].y, acc);
+                    acc = __builtin_fmaf(xv.z, wf[u].z, acc);
+                    acc = __builtin_fmaf(xv.w, wf[u].w, acc);
+                }
+            }
+        }
+        for (int i = (n4 << 2) + threadIdx.x; i < D; i += 256)
+            acc = __builtin_fmaf(x[i] * rn * nw[i], R[(int64_t)e * D + i], acc);
+        acc = pk_wave_sum(acc);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = acc;
+        __syncthreads();
+        v = (red[0] + red[1]) + (red[2] + red[3]);
     } else {
         v = pk_row_dot_block(x, R + (int64_t)e * D, D, red);
-        if (hq) {
-            // the experts' input (x) as half-group records of the
-            // integer-dot arithmetic: one wave per 32 values, whole
-            // half-groups per workgroup
-            const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-            const int nhg = (D + 31) >> 5, per = (nhg + E - 1) / E;
-            for (int hg = e * per + wv; hg < min(nhg, (e + 1) * per); hg += 4) {
-                const int i = hg * 32 + lane;
-                const bool has = lane < 32 && i < D;
-                pk_write_digits<1>(x[has ? i : 0], has, hq + (int64_t)hg * PK_XQ_INTS);
-            }
+    }
+    if (hq) {
+        // the experts' input (the normalised row, or x) as half-group records
+        // of the integer-dot arithmetic: one wave per 32 values, whole
+        // half-groups per workgroup (with the norm, hn is written here too)
+        const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+        const int nhg = (D + 31) >> 5, per = (nhg + E - 1) / E;
+        for (int hg = e * per + wv; hg < min(nhg, (e + 1) * per); hg += 4) {
+            const int i = hg * 32 + lane;
+            const bool has = lane < 32 && i < D;
+            const int ic = has ? i : 0;
+            const float xv = nw ? x[ic] * rn * nw[ic] : x[ic];
+            if (has && nw) hn[i] = xv;
+            pk_write_digits<1>(xv, has, hq + (int64_t)hg * PK_XQ_INTS);
         }
     }
     // without a counter the block only publishes its logit: the expert

@@ -91,9 +91,7 @@ struct pk_engine {
     // batch-1 decode attention and its output projection as one k_attn_oproj
     // launch (PK_ATT_FUSED=0: two launches)
     bool attn_fused = true;
-    bool router_fused = true;                 // ... with the MoE router in it (PK_ROUTER_FUSED=0: own launch)
     uint64_t *att_t = nullptr;                // k_attn_oproj hand-over words: [heads x head_dim]
-    uint64_t *h_t = nullptr;                  // k_attn_oproj hand-over words: [hidden] (the residual row)
 
     bool capturing = false;                  // inside pk_capture_begin/end
 
@@ -176,14 +174,8 @@ int pk_prof_begin(pk_engine *e, int kind);
 int pk_prof_end(pk_engine *e, int slot);
 
 // internal MoE pieces reused by the decode and prompt drivers
-// routed: the router already ran for this token (logits, hn / hn_q, epoch:
-// k_attn_oproj's router workgroups), only the experts remain.
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
-                 const float *residual, float *res_out, const float *norm_w = nullptr, bool routed = false);
-// the batch-1 MoE layer's experts on the integer-dot arithmetic
-inline bool pk_moe_dot(const pk_engine *e) {
-    return e->i4_dot && e->c.hidden % 64 == 0 && e->c.moe_inter % 128 == 0;
-}
+                 const float *residual, float *res_out, const float *norm_w = nullptr);
 int pk_check_layer_experts(pk_engine *e, int layer);
 pk_i4_items pk_expert_items(pk_engine *e, int layer, bool down);
 
@@ -222,7 +214,7 @@ int pk_set_state(pk_engine *e, int tok, int pos);
 // exact: the prompt rows in the reference's operation order (pk_exact.hip).
 int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, int pos_step, int seq0,
                       int seq_step, int n, const float *xn, float *qkv, float *part, float *att, float *h,
-                      const float *norm_w = nullptr, bool exact = false, bool *routed = nullptr);
+                      const float *norm_w = nullptr, bool exact = false);
 // the prompt path's dense steps in the reference's order (pk_exact.hip)
 int pk_launch_gemm_chain8(const float *X, int64_t ldx, const float *W, const float *bias, float *out, int64_t ldo,
                           int S, int I, int O, bool add_res, hipStream_t st);

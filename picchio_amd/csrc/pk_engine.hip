@@ -149,7 +149,7 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
-                    e->moe_act_t, e->moe_eo_t, e->att_t, e->h_t};
+                    e->moe_act_t, e->moe_eo_t, e->att_t};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -217,14 +217,11 @@ static int engine_init(pk_engine *e) {
     PK_HIP(hipMemsetAsync(e->moe_eo_t, 0, (int64_t)K * D * 8, e->stream));
     ALLOC(e->att_t, (int64_t)c->n_heads * c->head_dim * 8);
     PK_HIP(hipMemsetAsync(e->att_t, 0, (int64_t)c->n_heads * c->head_dim * 8, e->stream));
-    ALLOC(e->h_t, (int64_t)D * 8);
-    PK_HIP(hipMemsetAsync(e->h_t, 0, (int64_t)D * 8, e->stream));
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
     if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v) != 0;
     if (const char *v = getenv("PK_ATT_FUSED")) e->attn_fused = atoi(v) != 0;
-    if (const char *v = getenv("PK_ROUTER_FUSED")) e->router_fused = atoi(v) != 0;
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -799,18 +796,16 @@ static int moe_router(pk_engine *e, int layer, const float *x_dev, const float *
 }
 
 int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
-                 const float *residual, float *res_out, const float *norm_w, bool routed) {
+                 const float *residual, float *res_out, const float *norm_w) {
     const pk_cfg *c = &e->c;
     // the router launch writes the logits only; the expert launch selects
     // the experts from them and publishes the routing (sel, weights)
+    int ps = pk_prof_begin(e, PK_PROF_ROUTER);
     // integer-dot arithmetic: the router also writes the input's records, the
     // gate_up epilogue those of its SwiGLU outputs for the down launch
-    const bool dot = pk_moe_dot(e);
-    if (!routed) {
-        int ps = pk_prof_begin(e, PK_PROF_ROUTER);
-        PK_TRY(moe_router(e, layer, x_dev, norm_w, dot, e->r_logits));
-        PK_TRY(pk_prof_end(e, ps));
-    }
+    const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
+    PK_TRY(moe_router(e, layer, x_dev, norm_w, dot, e->r_logits));
+    PK_TRY(pk_prof_end(e, ps));
     pk_route_args rt{};
     rt.logits = e->r_logits;
     rt.E = c->n_experts;
@@ -853,7 +848,7 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
         a.eo_t = e->moe_eo_t;
         a.epoch = e->counters + PK_CTR_MOE_EPOCH;
         a.status = e->counters + PK_CTR_MOE_STATUS;
-        const int ps = pk_prof_begin(e, PK_PROF_MOE_FFN);
+        ps = pk_prof_begin(e, PK_PROF_MOE_FFN);
         PK_TRY(pk_launch_moe_ffn(a, e->stream));
         return pk_prof_end(e, ps);
     }
@@ -885,18 +880,6 @@ extern "C" int pk_set_moe_fused(pk_engine *e, int on) {
     return PK_OK;
 }
 
-extern "C" int pk_set_router_fused(pk_engine *e, int on) {
-    PK_CHECK(e, PK_ERR_ARG, "engine is null");
-    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_router_fused: not available while capturing");
-    if (e->router_fused != (on != 0) && e->step_exec) {   // the captured step holds the other kernels
-        (void)hipGraphExecDestroy(e->step_exec);
-        e->step_exec = nullptr;
-        e->step_cap = -1;
-    }
-    e->router_fused = on != 0;
-    return PK_OK;
-}
-
 extern "C" int pk_set_attn_fused(pk_engine *e, int on) {
     PK_CHECK(e, PK_ERR_ARG, "engine is null");
     PK_CHECK(!e->capturing, PK_ERR_ARG, "set_attn_fused: not available while capturing");
@@ -913,7 +896,9 @@ extern "C" int pk_router_logits(pk_engine *e, int layer, const float *x_dev, flo
     PK_CHECK(e && x_dev && logits_dev, PK_ERR_ARG, "null argument");
     PK_CHECK(layer >= 0 && layer < e->c.n_layers && e->L[layer].have_router, PK_ERR_MISSING,
              "layer %d: router not loaded", layer);
-    return moe_router(e, layer, x_dev, nullptr, pk_moe_dot(e), logits_dev);
+    const pk_cfg *c = &e->c;
+    const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
+    return moe_router(e, layer, x_dev, nullptr, dot, logits_dev);
 }
 
 extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float *out_dev,

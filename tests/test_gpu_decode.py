@@ -111,44 +111,36 @@ def test_replay_graph_recaptured_past_its_position_bound(gpu):
         eng.close()
 
 
-@pytest.mark.parametrize("dot", [0, 1])
-def test_attention_one_launch_matches_two(gpu, dot):
-    """Decode attention, its output projection and the MoE router in one
-    launch (the projection's workgroups waiting on the attention row's
-    tagged words, the router's on the residual row's) give the same bits as
-    the router in its own launch and as three launches: forward_token's
-    logits over one-chunk and eight-chunk windows (layer 0 sliding, layer 1
-    full), on picchio's fp32 expert chains and on the integer dot (whose
-    records the router writes), and the replayed step graph's tokens; no
-    device-side wait gave up."""
+def test_attention_one_launch_matches_two(gpu):
+    """Decode attention and its output projection as one launch (the
+    projection's workgroups waiting on the attention row's tagged words)
+    give the same bits as the two launches: forward_token's logits over
+    one-chunk and eight-chunk windows (layer 0 sliding, layer 1 full), and
+    the replayed step graph's tokens; no device-side wait gave up."""
     import torch
     import picchio_amd as pa
     cfg = pa.gptoss_cfg(n_layers=2, n_experts=4, ctx_len=2100, vocab=2000)
     eng = pa.Engine(cfg)
-    modes = [(1, 1), (1, 0), (0, 0), (1, 1)]           # (attention fused, router fused)
     try:
         eng.build_synthetic(5, what=7)
-        eng.set_i4_dot(dot)
         lg = eng.empty(cfg.vocab, torch.float32)
         for n_ctx in (40, 1000):
             eng.kv_fill_synthetic(0, n_ctx, 9)
             for i in range(3):
                 outs = []
-                for att, rt in modes:
-                    eng.set_attn_fused(att)
-                    eng.set_router_fused(rt)
+                for fused in (1, 0, 1):
+                    eng.set_attn_fused(fused)
                     nxt = eng.forward_token(7 + i, n_ctx + i, lg)
                     outs.append((nxt, eng.to_host(lg)))
                 for nxt, v in outs[1:]:
                     assert nxt == outs[0][0], (n_ctx, i)
                     assert np.array_equal(v.view(np.uint32), outs[0][1].view(np.uint32)), (n_ctx, i)
         streams = []
-        for att, rt in modes[:3]:
-            eng.set_attn_fused(att)
-            eng.set_router_fused(rt)
+        for fused in (1, 0):
+            eng.set_attn_fused(fused)
             eng.kv_fill_synthetic(0, 1000, 9)
             streams.append(list(eng.decode_replay(7, 990, 12)))
-        assert streams[0] == streams[1] == streams[2]
+        assert streams[0] == streams[1]
         eng.sync()
     finally:
         eng.close()
