@@ -793,7 +793,24 @@ __global__ __launch_bounds__(1024) void k_argmax_blocks(const float *bval, const
     __shared__ int ri[16];
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int b = threadIdx.x; b < nb; b += blockDim.x) better(bv, bi, bval[b], bidx[b]);
+    // the pairs in rounds of AM_U per thread, every load of a round issued
+    // before the first comparison (range-checked: entries past nb are
+    // skipped); better() picks the same pair in any order
+    constexpr int AM_U = 32;
+    const pk_buf_t vr = pk_buf(bval, (uint32_t)nb * 4u), ir = pk_buf(bidx, (uint32_t)nb * 4u);
+    for (int b0 = 0; b0 < nb; b0 += AM_U * (int)blockDim.x) {
+        float v[AM_U];
+        int ix[AM_U];
+#pragma unroll
+        for (int u = 0; u < AM_U; ++u) {
+            const uint32_t off = (uint32_t)(b0 + (int)threadIdx.x + u * (int)blockDim.x) * 4u;
+            v[u] = pk_buf_load_f32(vr, off);
+            ix[u] = __float_as_int(pk_buf_load_f32(ir, off));
+        }
+#pragma unroll
+        for (int u = 0; u < AM_U; ++u)
+            if (b0 + (int)threadIdx.x + u * (int)blockDim.x < nb) better(bv, bi, v[u], ix[u]);
+    }
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(bv, o, 64);
