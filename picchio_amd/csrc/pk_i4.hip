@@ -15,6 +15,9 @@
 //    and all scaling by 16 is exact, so every rounding matches the reference.
 #include "pk_internal.h"
 
+#include <algorithm>
+#include <stdlib.h>
+
 #include "pk_i4_device.h"
 #include "pk_tagged.h"
 
@@ -145,6 +148,136 @@ __global__ __launch_bounds__(NW * 64) void k_i4_gemv(pk_i4_items it, int O, int 
         if (rt.logits && rb == 0 && item == 0) pk_wave_route_publish(rt);
 }
 
+// ───────────── persistent streaming GEMV (launches of many row blocks) ─────────────
+// The k_i4_gemv body for launches whose tasks (n_items x RB row blocks) are
+// well above the CUs: one 16-wave workgroup per CU walks tasks blockIdx.x,
+// + gridDim.x, ... . Waves 0..14 keep the next task's weights in flight
+// while they multiply the current one (a ring of two register slots; every
+// refill is issued, past the workgroup's last task a same-address dummy, so
+// that the load counter's waits stay exact) and write their partials to one
+// of two LDS buffers by task parity; wave 15 folds each task in group order
+// and writes its rows while the others move on. Two cumulative LDS counters
+// per buffer order them (partials in; fold done). The same per-row
+// arithmetic as k_i4_gemv, hence the same bits. Measured: 32 experts'
+// gate_up in one launch 4.3 -> 4.5 TB/s, the 512-token prompt of config 2
+// (its per-pair expert GEMVs) 0.43 -> 0.41 s; a ring of three slots was no
+// faster.
+constexpr int ST_NW = 15, ST_GPW = 3;     // load waves x groups per wave: NG <= 45
+
+__device__ __forceinline__ void st_signal(int *c) {
+    if ((threadIdx.x & 63) == 0) __hip_atomic_fetch_add(c, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+__device__ __forceinline__ void st_wait(int *c, int target) {
+    while (__hip_atomic_load(c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) < target) __builtin_amdgcn_s_sleep(1);
+}
+
+template <int EPI, bool DOT>
+__global__ __launch_bounds__((ST_NW + 1) * 64) void k_i4_gemv_stream(pk_i4_items it, int O, int NG, int RB,
+                                                                     float lim, float alpha) {
+    extern __shared__ float lds[];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int n_task = it.n_items * RB, W = gridDim.x;
+    const int my_n = (int)blockIdx.x < n_task ? (n_task - 1 - (int)blockIdx.x) / W + 1 : 0;
+    float *part = lds;                                      // [2][NG][64]
+    float *scl = lds + 2 * NG * 64;                         // [2][NG][64] (fp32 chains)
+    int *cnt = reinterpret_cast<int *>(lds + (DOT ? 2 : 4) * NG * 64);   // partials in [2], folds done [2]
+    if (threadIdx.x < 4) cnt[threadIdx.x] = 0;
+    __syncthreads();
+    const pk_cptr<int32_t> slots = pk_const(it.slots);
+    // task k of this workgroup: item, row block, the item's expert slot
+    auto task = [&](int k, int &item, int &rb) -> const uint8_t * {
+        const int t = (int)blockIdx.x + k * W;
+        item = t / RB;
+        rb = t - item * RB;
+        const int slot = it.slot_base + (it.slots ? slots[item] : 0);
+        return it.base + (int64_t)slot * it.slot_stride;
+    };
+
+    if (wave < ST_NW) {
+        uint4 wa0[ST_GPW], wb0[ST_GPW], wa1[ST_GPW], wb1[ST_GPW];
+        float s0[ST_GPW], s1[ST_GPW];
+        auto issue = [&](int k, uint4 (&wa)[ST_GPW], uint4 (&wb)[ST_GPW], float (&s)[ST_GPW]) {
+            const bool real = k < my_n;
+            int item, rb;
+            const uint8_t *base = task(real ? k : 0, item, rb);
+            const uint4 *tiles =
+                reinterpret_cast<const uint4 *>(base + it.off_tiles) + (int64_t)rb * NG * (PK_TILE_BYTES / 16);
+            const float *sc = reinterpret_cast<const float *>(base + it.off_scales) + (int64_t)rb * NG * 64;
+            const int l = real ? lane : 0;
+#pragma unroll
+            for (int u = 0; u < ST_GPW; ++u) {
+                const int g = min(wave + u * ST_NW, NG - 1);
+                wa[u] = pk_load_nt(&tiles[g * 128 + l]);
+                wb[u] = pk_load_nt(&tiles[g * 128 + 64 + l]);
+                s[u] = sc[g * 64 + l];
+            }
+        };
+        auto consume = [&](int k, const uint4 (&wa)[ST_GPW], const uint4 (&wb)[ST_GPW], const float (&s)[ST_GPW]) {
+            const int b = k & 1;
+            int item, rb;
+            (void)task(k, item, rb);
+            // buffer b is free once task k-2's fold is done
+            if (k >= 2) st_wait(&cnt[2 + b], k >> 1);
+            float *pb = part + b * NG * 64, *sb = scl + b * NG * 64;
+            if constexpr (DOT) {
+                const pk_cptr<int32_t> xq = pk_const(it.xq + (int64_t)(item / it.x_div) * it.xq_stride);
+#pragma unroll
+                for (int u = 0; u < ST_GPW; ++u) {
+                    const int g = wave + u * ST_NW;
+                    if (g < NG)
+                        pb[g * 64 + lane] = pk_dot_group(wa[u], wb[u], xq + 2 * g * PK_XQ_INTS,
+                                                         xq + (2 * g + 1) * PK_XQ_INTS, s[u]);
+                }
+            } else {
+                const pk_cptr<float> x = pk_const(it.x + (int64_t)(item / it.x_div) * it.x_stride);
+#pragma unroll
+                for (int u = 0; u < ST_GPW; ++u) {
+                    const int g = wave + u * ST_NW;
+                    if (g < NG) {
+                        pb[g * 64 + lane] = pk_group_dot(wa[u], wb[u], x + g * 64);
+                        sb[g * 64 + lane] = s[u];
+                    }
+                }
+            }
+            st_signal(&cnt[b]);
+        };
+        issue(0, wa0, wb0, s0);
+        issue(1, wa1, wb1, s1);
+        for (int k = 0; k < my_n; k += 2) {
+            consume(k, wa0, wb0, s0);
+            issue(k + 2, wa0, wb0, s0);
+            if (k + 1 < my_n) consume(k + 1, wa1, wb1, s1);
+            issue(k + 3, wa1, wb1, s1);
+        }
+        return;
+    }
+
+    // wave ST_NW: fold and epilogue of each task
+    for (int k = 0; k < my_n; ++k) {
+        const int b = k & 1;
+        int item, rb;
+        const uint8_t *base = task(k, item, rb);
+        const int row = rb * 64 + lane;
+        const float bias = it.off_bias >= 0 ? reinterpret_cast<const float *>(base + it.off_bias)[min(row, O - 1)]
+                                            : 0.0f;
+        st_wait(&cnt[b], ST_NW * ((k >> 1) + 1));
+        float acc = pk_fold_groups<DOT>(part + b * NG * 64, scl + b * NG * 64, NG);
+        st_signal(&cnt[2 + b]);
+        if (it.off_bias >= 0 && row < O) acc = acc + bias;
+        float *y = it.y + (int64_t)item * it.y_stride;
+        if constexpr (EPI == PK_EPI_SWIGLU) {
+            const float up = __shfl_down(acc, 1, 64);
+            const bool has = (lane & 1) == 0 && row + 1 < O;
+            const float a = pk_swiglu(acc, up, lim, alpha);
+            if (has) y[row >> 1] = a;
+            if (it.yq) pk_write_digits<2>(a, has, it.yq + (int64_t)item * it.yq_stride + rb * PK_XQ_INTS);
+        } else {
+            if (row < O) y[row] = acc;
+        }
+    }
+}
+
 // ─────────────── integer-dot GEMV over expert-grouped pairs ───────────────
 // grid = (RB, max_tiles); workgroup (rb, t) covers tile t's pairs (one expert,
 // at most DT_M pairs): each wave loads its 3 groups of the expert's 64-row
@@ -250,6 +383,24 @@ int pk_launch_act_records(const float *x, int n, int32_t *rec, hipStream_t st) {
     return PK_OK;
 }
 
+// compute units of the current device (cached per device)
+static int pk_device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess) cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+// PK_I4_STREAM=0 in the environment: the one-row-block-per-workgroup kernel only
+static bool pk_i4_stream_on() {
+    static const int on = getenv("PK_I4_STREAM") ? atoi(getenv("PK_I4_STREAM")) : 1;
+    return on != 0;
+}
+
 int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue,
                       float lim, float alpha, const pk_combine_args *comb, hipStream_t st,
                       const pk_route_args *route) {
@@ -270,6 +421,29 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
     PK_CHECK(sh.NG > 0 && sh.RB > 0 && it.n_items > 0, PK_ERR_ARG, "i4 gemv: empty shape");
     PK_CHECK(sh.NG <= 128, PK_ERR_UNSUPPORTED, "i4 gemv: I=%d above 8192", sh.I);
     PK_CHECK(!it.yq || epilogue == PK_EPI_SWIGLU, PK_ERR_ARG, "i4 gemv: output records need the SwiGLU epilogue");
+    // many row blocks without routing: the persistent streaming kernel (one
+    // workgroup per CU, the next row block's weights in flight meanwhile)
+    const int n_cu = pk_device_cus();
+    if (!route && epilogue != PK_EPI_COMBINE && sh.NG <= ST_NW * ST_GPW && n_cu > 0 &&
+        (int64_t)it.n_items * sh.RB >= 2 * (int64_t)n_cu && pk_i4_stream_on()) {
+        const bool dot = it.xq != nullptr;
+        // partials + scales in two buffers, the counters; at least half the
+        // CU's LDS so that one workgroup runs per CU
+        const size_t need = (size_t)(dot ? 2 : 4) * sh.NG * 64 * sizeof(float) + 4 * sizeof(int);
+        const size_t lds = std::max(need, (size_t)82 * 1024);
+        const dim3 grid((unsigned)std::min<int64_t>(n_cu, (int64_t)it.n_items * sh.RB));
+#define PK_I4_STREAM(E, D)                                                                              \
+    hipLaunchKernelGGL((k_i4_gemv_stream<E, D>), grid, dim3((ST_NW + 1) * 64), lds, st, it, sh.O, sh.NG, \
+                       sh.RB, lim, alpha)
+        if (epilogue == PK_EPI_SWIGLU) {
+            if (dot) PK_I4_STREAM(PK_EPI_SWIGLU, true); else PK_I4_STREAM(PK_EPI_SWIGLU, false);
+        } else {
+            if (dot) PK_I4_STREAM(PK_EPI_PLAIN, true); else PK_I4_STREAM(PK_EPI_PLAIN, false);
+        }
+#undef PK_I4_STREAM
+        PK_HIP(hipGetLastError());
+        return PK_OK;
+    }
     const dim3 grid(sh.RB, it.n_items);
     const size_t lds = (size_t)sh.NG * 64 * 2 * sizeof(float);
     // 15 waves x 3 groups covers the 45 groups of a 2880-wide row in one pass.

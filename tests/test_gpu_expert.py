@@ -25,9 +25,13 @@ def _rand(shape, seed, scale=1.0):
 # ───────────────────────── INT4 GEMV ─────────────────────────
 
 @pytest.mark.parametrize("O,I,S", [(5760, 2880, 1), (2880, 2880, 1), (2880, 2880, 3),
-                                   (100, 128, 2), (64, 64, 1), (720, 2880, 1)])
+                                   (100, 128, 2), (64, 64, 1), (720, 2880, 1),
+                                   (5760, 2880, 8), (2880, 2880, 12), (100, 128, 600)])
 def test_i4_gs64_gemv_tiled_bitexact(gpu, oracle, O, I, S):
-    """Tiled HBM layout + cvt_off decode reproduce matmul_i4_gs bit for bit."""
+    """Tiled HBM layout + cvt_off decode reproduce matmul_i4_gs bit for bit;
+    the last three shapes have 540-720 row blocks per launch, so they run on
+    the persistent streaming kernel (one workgroup per CU walking the row
+    blocks with the next block's weights in flight)."""
     import picchio_amd as pa
     import torch
     cfg = pa.gptoss_cfg(n_layers=1, n_experts=4, ctx_len=16, vocab=64)
@@ -220,6 +224,40 @@ def test_expert_gate_up_down_batched(moe_setup, oracle):
         ref = np.zeros(D, np.float32)
         oracle.expert_apply(model, 0, int(eid), x, ref, 1.0)
         assert rel_l2(got[k], ref) < 1e-6
+
+
+@pytest.mark.parametrize("dot", [0, 1])
+def test_expert_gate_up_streaming_matches_tiled(moe_setup, oracle, dot):
+    """gate_up over all 8 experts in one launch (720 row blocks: the
+    persistent streaming kernel) gives, for experts 6, 1 and 3, the bits of
+    gate_up over those three alone (270 row blocks: one workgroup per row
+    block), on picchio's fp32 chains and on the integer dot (outputs and
+    their records)."""
+    import torch
+    cfg, model, eng = moe_setup
+    D, H, E = cfg.hidden, cfg.moe_inter // 2, cfg.n_experts
+    x = _token_x(oracle, cfg, 4711)
+    xd = eng.to_dev(x)
+    all_e = np.arange(E, dtype=np.int32)[::-1].copy()
+    three = np.array([6, 1, 3], np.int32)
+    outs = {}
+    for name, ids in (("all", all_e), ("three", three)):
+        act = eng.empty((len(ids), H), torch.float32)
+        if dot:
+            rec = eng.empty(((D + 31) // 32) * 24, torch.int32)
+            eng.act_records(xd, rec)
+            arec = eng.empty((len(ids), (cfg.moe_inter // 64) * 24), torch.int32)
+            eng.expert_gate_up_dot(0, eng.to_dev(ids), rec, act, arec)
+            outs[name] = (eng.to_host(act), eng.to_host(arec))
+        else:
+            eng.expert_gate_up(0, eng.to_dev(ids), xd, act)
+            outs[name] = (eng.to_host(act), None)
+    for k, eid in enumerate(three):
+        j = int(np.where(all_e == eid)[0][0])
+        assert bits_equal(outs["all"][0][j], outs["three"][0][k]), eid
+        if dot:
+            assert np.array_equal(outs["all"][1][j], outs["three"][1][k]), eid
+    eng.sync()
 
 
 def test_moe_forward_parity(moe_setup, oracle):
