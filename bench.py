@@ -441,14 +441,18 @@ def cpu_pairs_baseline(seed, budget_s, x, sel, w):
 
 def run_prefill(args):
     """T=2048 tokens through one GPT-OSS-20B MoE layer as
-    expert-grouped INT4 GEMMs on the int8 matrix cores (8192 pairs, Zipf 1.1
-    routing). value = algorithmic TFLOP/s (2 x pairs x (5760x2880 + 2880x2880))."""
+    expert-grouped INT4 GEMMs on the matrix cores (8192 pairs, Zipf 1.1
+    routing): f16 activation pairs on v_mfma_f32_32x32x16_f16 (default) or
+    int8 limbs (--grouped int8). value = algorithmic TFLOP/s
+    (2 x pairs x (5760x2880 + 2880x2880))."""
     import torch
     import picchio_amd as pa
     T = 2048
     cfg = pa.gptoss_cfg(n_layers=1, n_experts=E, ctx_len=16, vocab=64)
     eng = pa.Engine(cfg)
     eng.build_synthetic(args.seed, what=1)
+    f16 = args.grouped == "f16"
+    eng.set_grouped_f16(f16)
     sel, w, counts = zipf_routing(T, E, K, args.seed)
     x = np.random.default_rng(args.seed + 7).standard_normal((T, D)).astype(np.float32)
     xd, sd, wd = eng.to_dev(x), eng.to_dev(sel), eng.to_dev(w)
@@ -480,22 +484,30 @@ def run_prefill(args):
         cpu = cpu_pairs_baseline(args.seed, args.cpu_seconds, x, sel, w)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     tfs = flops / (ms * 1e-3) / 1e12
+    # MFMA work issued: every 32-pair half tile runs whole (f16: 2 halves per
+    # activation, 64-pair tiles whose empty second half is skipped; int8: 3
+    # limbs, 32-pair tiles)
+    limbs, peak = (2, 2500.0) if f16 else (3, 5000.0)
+    kern = "k_moe_f16<SWIGLU>" if f16 else "k_moe_mfma<SWIGLU>"
     line = {
         "metric": METRIC, "value": round(tfs, 2), "unit": "TFLOP/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "int8x3 (int4 weights)",
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16x2 (int4 weights, fp32 sums)" if f16 else "int8x3 (int4 weights)",
         "data": "synthetic",
         "config": {"workload": "config3: prefill MoE layer, T=2048 tokens, 8192 (token, expert) pairs "
                                "over 32 INT4 gs64 experts (Zipf 1.1, 16..512 per expert), expert-grouped "
-                               "int8 MFMA GEMMs (3 activation limbs)",
-                   "tokens": T, "pairs": P, "tiles_of_32": tiles,
+                               + ("f16 MFMA GEMMs (2 activation halves)" if f16 else
+                                  "int8 MFMA GEMMs (3 activation limbs)"),
+                   "tokens": T, "pairs": P, "half_tiles_of_32": tiles,
                    "pairs_per_expert": [int(c) for c in counts],
                    "flops": flops, "gate_up_ms": round(gu_ms, 4), "down_ms": round(dn_ms, 4),
-                   "int8_mfma_ops_executed": 3 * 2 * tiles * 32 * (INTER * D + D * HALF)},
+                   ("f16" if f16 else "int8") + "_mfma_flops_issued": limbs * 2 * tiles * 32 * (INTER * D + D * HALF)},
         "roofline": {"bound": "mfma", "achieved": round(gu_flops / (gu_ms * 1e-3) / 1e12, 1),
-                     "peak": 5000.0, "unit": "TFLOP/s",
-                     "frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / 5000.0, 4), "traffic": None,
-                     "kernel": "k_moe_mfma<SWIGLU> (gate_up, algorithmic flops vs the int8 dense peak)",
+                     "peak": peak, "unit": "TFLOP/s",
+                     "frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / peak, 4), "traffic": None,
+                     "kernel": kern + " (gate_up, algorithmic flops vs the dense " +
+                               ("fp16" if f16 else "int8") + " peak)",
                      "flops_per_launch": gu_flops, "mean_us": round(gu_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
@@ -659,6 +671,8 @@ def main():
     ap.add_argument("--profile-tokens", type=int, default=400)
     ap.add_argument("--dot", type=int, default=-1,
                     help="config 1 expert arithmetic: 1 integer dot, 0 fp32 chains, -1 the engine's default")
+    ap.add_argument("--grouped", choices=["f16", "int8"], default="f16",
+                    help="config 3 arithmetic: f16 hi/lo activation pairs (default) or exact int8 limbs")
     ap.add_argument("--decode-steps", type=int, default=128,
                     help="default run: decode steps of configs 2 and 4")
     ap.add_argument("--sample", default="",

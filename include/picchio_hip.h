@@ -268,11 +268,13 @@ int pk_prefill_seq(pk_engine *e, int seq, const int32_t *ids, int n, int pos_bas
 int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host, int pos, int n_steps,
                     int32_t *out_host);
 
-/* Expert-grouped prefill MoE on the int8 matrix cores (forward_prefill's
- * MoE, picchio.c:1829-1916, as one grouped GEMM per projection): the T*topk
- * (token, expert) pairs are grouped by expert; activations are quantized by
- * pk_quantize_act_i8x3; per 64-column scale group the int32 dot products are
- * exact, then folded in fp32 (within ~1e-6 of the reference's fp32 path).
+/* Expert-grouped prefill MoE on the matrix cores (forward_prefill's MoE,
+ * picchio.c:1829-1916, as one grouped GEMM per projection): the T*topk
+ * (token, expert) pairs are grouped by expert; per 64-column scale group the
+ * dot products run on the f16 MFMA with the activations split in two halves
+ * (default), or exactly on int8 limbs of pk_quantize_act_i8x3
+ * (pk_set_grouped_f16(e, 0)), then fold in fp32 (within ~1e-6 of the
+ * reference's fp32 path either way).
  * sel_dev [T][topk] / w_dev [T][topk] (combine weights, softmax x
  * routed_scale): the routing to use, both or neither (null: the layer's
  * router). out_dev [T][hidden] = each token's weighted sum in the batch's
@@ -282,6 +284,15 @@ int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host, int pos, 
 int pk_moe_forward_grouped(pk_engine *e, int layer, const float *x_dev, int T,
                            const int32_t *sel_dev, const float *w_dev, float *out_dev,
                            float *act_dev, float *eo_dev);
+
+/* Arithmetic of pk_moe_forward_grouped (and of the prompt's MoE on the matrix
+ * cores). on = 1 (the default): activations as two halves, hi = f16(x') and
+ * lo = f16(x' - hi) with x' = x 2^(15-k), weights exactly q in f16, sums in
+ * fp32 on v_mfma_f32_32x32x16_f16 (~1e-7 from the reference's fp32 path, the
+ * MFMA's own summation order). on = 0: the exact int8 limbs of
+ * pk_quantize_act_i8x3 (bit-reproducible by a CPU restatement). No reference
+ * counterpart: the reference has one fp32 path. Not while capturing. */
+int pk_set_grouped_f16(pk_engine *e, int on);
 
 /* Integer activation quantization of the grouped path: per row, k = binary
  * exponent of max|x| (x = m 2^k, m in [0.5,1)), A = rint(x 2^(20-k)), split

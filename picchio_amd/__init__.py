@@ -121,6 +121,7 @@ def lib():
         "pk_reset_history": (C.c_int, [vp]),
         "pk_set_sampling_fast_sums": (C.c_int, [vp, C.c_int]),
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
+        "pk_set_grouped_f16": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
@@ -278,6 +279,11 @@ class Engine:
         """Batch-1 MoE experts on the integer-dot arithmetic, or on picchio's
         fp32 chains, bit-identical (the default) (pk_set_i4_dot)."""
         check(self.L.pk_set_i4_dot(self.h, 1 if on else 0))
+
+    def set_grouped_f16(self, on):
+        """Grouped MoE arithmetic: f16 hi/lo activations on the f16 MFMA (the
+        default) or the exact int8 limbs (pk_set_grouped_f16)."""
+        check(self.L.pk_set_grouped_f16(self.h, 1 if on else 0))
 
     def set_moe_fused(self, on):
         """Batch-1 MoE layer's experts as one launch (default) or as a

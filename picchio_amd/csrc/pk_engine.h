@@ -138,7 +138,10 @@ struct pk_engine {
     int32_t *bd_toks = nullptr;
     // grouped MFMA scratch for up to g_cap pairs (pk_prefill.hip)
     int64_t g_cap = 0;
-    int8_t *g_limbs = nullptr;
+    int8_t *g_limbs = nullptr;                 // int8 limbs (3 planes) or f16 hi/lo (2 planes of halves)
+    // grouped arithmetic: true = f16 hi/lo on v_mfma_f32_32x32x16_f16 (the
+    // default), false = exact int8 limbs (PK_GROUPED_F16 / pk_set_grouped_f16)
+    bool grouped_f16 = true;
     int32_t *g_exps = nullptr, *g_pairs = nullptr, *g_tiles = nullptr;
     // sampler (pk_sample.hip): device state, host mirror of its parameters,
     // kept entries (value, index) for vocabularies up to samp_cap entries
@@ -189,6 +192,9 @@ struct pk_mfma_args {
     int64_t plane;                             // bytes between limb planes
     int lrow;                                  // bytes per activation row (= its columns)
     const int32_t *exps;                       // per activation row: scale exponent
+    const uint16_t *xf;                        // half-precision path: hi plane, lo plane at + fplane (halves)
+    int64_t fplane;
+    int frow;                                  // halves per activation row (= its columns)
     const int32_t *pairs;                      // pair ids grouped by expert
     int x_div;                                 // activation row of pair p = p / x_div
     const int32_t *tile_exp, *tile_beg, *tile_cnt, *n_tiles;
@@ -203,6 +209,12 @@ int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int3
                           int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
                           int tile_pairs = 0);
 int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
+// half-precision pair arithmetic (pk_mfma.hip): activation planes, grouped GEMM
+// over tiles of PK_F16_TILE pairs
+constexpr int PK_F16_TILE = 64;
+int pk_launch_act_f16(const float *x, int64_t x_stride, int rows, int cols, uint16_t *xf, int64_t fplane,
+                      int32_t *exps, hipStream_t st);
+int pk_launch_moe_f16(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
 
 // decode driver pieces (pk_decode.hip) reused by the prompt driver
 int pk_decode_reserve(pk_engine *e);

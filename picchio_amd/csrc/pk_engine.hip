@@ -218,6 +218,7 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->att_t, (int64_t)c->n_heads * c->head_dim * 8);
     PK_HIP(hipMemsetAsync(e->att_t, 0, (int64_t)c->n_heads * c->head_dim * 8, e->stream));
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
+    if (const char *v = getenv("PK_GROUPED_F16")) e->grouped_f16 = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
     if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v) != 0;
@@ -865,6 +866,13 @@ extern "C" int pk_set_i4_dot(pk_engine *e, int on) {
         e->step_cap = -1;
     }
     e->i4_dot = on != 0;
+    return PK_OK;
+}
+
+extern "C" int pk_set_grouped_f16(pk_engine *e, int on) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_grouped_f16: not available while capturing");
+    e->grouped_f16 = on != 0;
     return PK_OK;
 }
 

@@ -21,6 +21,7 @@
 #include "pk_engine.h"
 #include "pk_i4_device.h"
 #include "pk_dev.h"
+#include <type_traits>
 
 namespace {
 
@@ -307,6 +308,432 @@ __global__ __launch_bounds__(NTHR, 4) void k_moe_mfma(pk_mfma_args a) {
             *reinterpret_cast<float4 *>(yr + row) = make_float4(y[4 * b], y[4 * b + 1], y[4 * b + 2], y[4 * b + 3]);
         }
     }
+}
+
+// ───────────── half-precision pair arithmetic (v_mfma_f32_32x32x16_f16) ─────────────
+// The same grouped GEMM with the activations as two halves and fp32 sums:
+//  * Activations: row x gets the factor 2^(15-k) (k the binary exponent of
+//    max|x|, as above), x' = x 2^(15-k), |x'| <= 2^15, stored as hi = f16(x')
+//    and lo = f16(x' - hi): hi + lo equals x' to ~2^-22 of |x'|.
+//  * Weights: a stored nibble t (the two's complement of q) placed under the
+//    exponent of 1024 reads 1024 + (t ^ 8) = 1032 + q; minus 1032 (packed
+//    half adds) it is exactly q.
+//  * Per 64-column group, 8 MFMAs (hi and lo over 4 x 16 columns) give
+//    z = sum (hi + lo) q in fp32 (every product exact); the groups fold in
+//    order, acc = fma(16 s_g, z_g, acc), and y = acc 2^(k-19) + bias.
+// The MFMA adds in its own order, so this path is held to a tolerance
+// against picchio's fp32 arithmetic (~1e-7 relative), not restated bit for
+// bit. Per group and 32 x 32 tile it spends 16 VALU instructions on the
+// fold (the int8 limbs need 80) and 44 on the weight expansion, shared by
+// up to 64 pairs.
+//
+// Work items: (tile j of up to 64 pairs, row group r of 512 rows). The
+// workgroup's 8 waves each take one 64-row block (two 32-row MFMA tiles) for
+// both 32-pair halves of the tile (the second skipped when the tile holds
+// at most 32 pairs). The MFMA runs with the activations as its first
+// operand, so a lane's 16 results are 16 pairs of one output row: one scale
+// per lane and row tile in the fold. Items i = r * n_tiles + j are dealt to
+// the 8 XCDs (workgroup L runs on XCD L % 8) in contiguous runs, so that the
+// workgroups resident on one XCD share an expert's weights in its L2.
+namespace {
+typedef _Float16 pk_v8h __attribute__((ext_vector_type(8)));
+typedef float pk_v16f __attribute__((ext_vector_type(16)));
+
+constexpr int FT = PK_F16_TILE;      // pairs per tile
+constexpr int FW = 8;                // waves per workgroup
+constexpr int FTHR = FW * 64;
+constexpr int FROWS = FW * 64;       // rows per work item
+
+// Stored position (0..7) of column u of an 8-column chunk: the expansion
+// of one weight dword yields columns 0,4,1,5,2,6,3,7.
+__device__ __forceinline__ int f16_pos(int u) { return ((u & 3) << 1) | (u >> 2); }
+
+// 8 nibbles (columns 0..7 of a chunk, two's complement t) -> 8 halves q in
+// the order above: ((w >> 4i) & M) ^ Y puts t ^ 8 = q + 8 under the
+// exponent of 1024 in both halves of a dword (M = 0x000F000F,
+// Y = 0x64086408; one three-input bit operation each when both are held in
+// registers), then one packed half add per dword subtracts 1032.
+__device__ __forceinline__ pk_v8h expand_f16(uint32_t w, uint32_t M, uint32_t Y) {
+    typedef uint32_t pk_v4u __attribute__((ext_vector_type(4)));
+    const pk_v4u p = {(w & M) ^ Y, ((w >> 4) & M) ^ Y, ((w >> 8) & M) ^ Y, ((w >> 12) & M) ^ Y};
+    return __builtin_bit_cast(pk_v8h, p) + (_Float16)-1032.0f;
+}
+}  // namespace
+
+// One row per workgroup: exponent k of max|x|, the hi and lo planes (columns
+// permuted by f16_pos inside each 8-column chunk).
+__global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ x, int64_t x_stride, int cols,
+                                                 uint16_t *__restrict__ xf, int64_t fplane,
+                                                 int32_t *__restrict__ exps) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float *xr = x + (int64_t)r * x_stride;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < cols; i += 256) m = fmaxf(m, fabsf(xr[i]));
+    m = pk_wave_max_f(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int k = 0;
+    if (m > 0.0f) (void)frexpf(m, &k);
+    if (threadIdx.x == 0) exps[r] = k;
+    _Float16 *hr = reinterpret_cast<_Float16 *>(xf) + (int64_t)r * cols;
+    for (int c = threadIdx.x; c < cols / 8; c += 256) {
+        pk_v8h hi, lo;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float v = ldexpf(xr[8 * c + u], 15 - k);
+            const _Float16 vh = (_Float16)v;
+            hi[f16_pos(u)] = vh;
+            lo[f16_pos(u)] = (_Float16)(v - (float)vh);
+        }
+        *reinterpret_cast<pk_v8h *>(hr + 8 * c) = hi;
+        *reinterpret_cast<pk_v8h *>(hr + fplane + 8 * c) = lo;
+    }
+}
+
+// Stage buffers: rings in LDS filled by direct global -> LDS loads (no
+// registers), three stages ahead: activations and weights FR = 4 stages,
+// scales FS = 8 (read one phase later, by the fold). Per stage and wave five
+// load instructions, always issued, so that the wait for a stage is a fixed
+// count of the wave's later loads.
+//
+// Schedule: the 8 waves form two groups, one wave of each on every SIMD (the
+// first and second wave the hardware placed there). Work alternates in
+// phases that end at a workgroup barrier: in one phase a group runs the
+// stage's 32 MFMAs while the other group, on the same SIMDs, folds its
+// previous stage and expands its next weights; group 1 runs one phase behind
+// group 0. So every SIMD's matrix core has one wave's MFMAs to run while the
+// other wave's VALU work may co-issue (measured: a VALU instruction issues
+// in ~32 % of the MFMA-busy cycles; the VALU work is what bounds the kernel).
+//   phase 2g:   group 0 folds g-1, expands g    | group 1 MFMA of g-1
+//   phase 2g+1: group 0 MFMA of g                | group 1 folds g-1, expands g
+constexpr int FR = 4, FS = 8;
+typedef __attribute__((address_space(3))) void pk_lds_void;
+
+// 64 lanes x 16 (or 4) bytes from per-lane global addresses to LDS at
+// lds + 16 (4) x lane; lds is the same for the whole wave. Issued as inline
+// assembly: the compiler then does not pair these loads with the kernel's
+// LDS reads (it would wait for every outstanding load before each read);
+// the kernel's own waits order them instead. M0 carries the LDS address.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void pk_dma16(const void *src, void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(pk_lds_void *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, off" ::"s"(m), "v"(src)
+                 : "memory", "m0");
+}
+__device__ __forceinline__ void pk_dma4(const void *src, void *lds) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(pk_lds_void *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, off" ::"s"(m), "v"(src)
+                 : "memory", "m0");
+}
+#pragma clang diagnostic pop
+// s_waitcnt: at most N of the wave's vector-memory loads outstanding and no
+// LDS read (gfx9 encoding: vmcnt[3:0], expcnt[6:4], lgkmcnt[11:8], vmcnt[5:4] at 15:14)
+template <int N>
+__device__ __forceinline__ void pk_wait_vm_lds() {
+    __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
+}
+// workgroup barrier after the wave's LDS reads are done; memory accesses are
+// not moved across it by the compiler
+__device__ __forceinline__ void pk_phase_barrier() {
+    asm volatile("" ::: "memory");
+    pk_wait_vm_lds<63>();
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+template <int EPI>
+__global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
+    // activations [slot][hi, lo][token][64 halves: 8 chunks of 16 bytes, chunk q
+    // of token t at position q ^ f(t), f(t) = (t ^ t / 8) % 8: any 16 tokens in a
+    // row, even and odd apart, take distinct positions, so 16-byte reads of 8 or
+    // 16 lanes hit distinct banks], weights [slot][wave][tile bytes],
+    // scales [slot][row]
+    __shared__ __attribute__((aligned(16))) _Float16 bring[FR][2][FT][64];
+    __shared__ __attribute__((aligned(16))) uint8_t wring[FR][FW][PK_TILE_BYTES];
+    __shared__ __attribute__((aligned(16))) float sring[FS][FROWS];
+    __shared__ int tok_row[FT], tok_exp[FT], tok_pair[FT], simd_of[FW];
+    // this workgroup's item
+    const int nt = *a.n_tiles;
+    const int n_item = nt * ((a.O + FROWS - 1) / FROWS);
+    const int run = (n_item + 7) >> 3;
+    const int s = blockIdx.x >> 3;
+    if (s >= run) return;
+    const int item = (int)(blockIdx.x & 7) * run + s;
+    if (item >= n_item) return;
+    const int rg = item / nt, j = item - rg * nt;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // the SIMD this wave runs on (HW_ID bits 5:4); the groups pair the two
+    // waves of each SIMD, whatever the placement
+    const int simd = __builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11));
+    if (lane == 0) simd_of[wave] = simd;
+    const int e = a.tile_exp[j], beg = a.tile_beg[j], cnt = a.tile_cnt[j];
+    if (threadIdx.x < FT) {
+        const int t = threadIdx.x;
+        const int pr = a.pairs[beg + (t < cnt ? t : 0)];
+        const int row = pr / a.x_div;
+        tok_row[t] = row;
+        tok_exp[t] = a.exps[row];
+        tok_pair[t] = pr;
+    }
+    const bool two = cnt > 32;                               // second 32-pair half in use
+    const uint8_t *base = a.base + (int64_t)(a.slot_base + e) * a.slot_stride;
+    const int RB = a.O >> 6;
+    const int rb = (rg * FROWS >> 6) + wave;                 // this wave's 64-row block
+    const bool active = rb < RB;
+    const int rbc = min(rb, RB - 1);
+    const int h = lane >> 5, n = lane & 31;
+    const int NG = a.NG;
+    uint32_t M = 0x000F000Fu, Y = 0x64086408u;
+    asm volatile("" : "+v"(M), "+v"(Y));                    // held in registers (see expand_f16)
+    __syncthreads();
+    int rank = 0;
+    for (int w = 0; w < wave; ++w) rank += simd_of[w] == simd;
+    const int grp = rank & 1;
+    // this wave's loads per stage: activation rows 8 b .. 8 b + 7 of limb l for
+    // b = 2 wave & 7 and b + 1 (l = wave / 4: waves 0..3 hi, 4..7 lo), its row
+    // block's two weight halves and 64 scales
+    const int blk = 8 * ((2 * wave) & 7);
+    const int l = wave >> 2;
+    const int ta = blk + (lane >> 3), tb = ta + 8, pos = lane & 7;
+    const _Float16 *xb = reinterpret_cast<const _Float16 *>(a.xf) + l * a.fplane;
+    const _Float16 *srca = xb + (int64_t)tok_row[ta] * a.frow + 8 * (pos ^ ((ta ^ (ta >> 3)) & 7));
+    const _Float16 *srcb = xb + (int64_t)tok_row[tb] * a.frow + 8 * (pos ^ ((tb ^ (tb >> 3)) & 7));
+    const uint8_t *wsrc = base + a.off_tiles + (int64_t)rbc * a.NG * PK_TILE_BYTES + 16 * lane;
+    const float *ssrc = reinterpret_cast<const float *>(base + a.off_scales) + (int64_t)rbc * a.NG * 64 + lane;
+    auto issue = [&](int g) {
+        const int sl = g & (FR - 1);
+        pk_dma16(srca + g * 64, &bring[sl][l][blk][0]);
+        pk_dma16(srcb + g * 64, &bring[sl][l][blk + 8][0]);
+        pk_dma16(wsrc + (int64_t)g * PK_TILE_BYTES, &wring[sl][wave][0]);
+        pk_dma16(wsrc + (int64_t)g * PK_TILE_BYTES + 1024, &wring[sl][wave][1024]);
+        pk_dma4(ssrc + g * 64, &sring[g & (FS - 1)][wave * 64]);
+    };
+    pk_v16f acc00 = {}, acc01 = {}, acc10 = {}, acc11 = {};   // [row tile][pair half]
+    pk_v16f z00 = {}, z01 = {}, z10 = {}, z11 = {};           // the last stage's group sums
+    pk_v8h A00, A01, A02, A03, A10, A11, A12, A13;           // the next stage's weights
+    const int sw0 = (n ^ (n >> 3)) & 7;                      // f(n), f(32 + n)
+    const int sw1 = (n ^ (4 + (n >> 3))) & 7;
+    // weights (this wave's own loads) and scales of a stage, read into
+    // registers during the wave's MFMA phase for the fold / expand phase after it
+    uint4 wr0 = make_uint4(0, 0, 0, 0), wr1 = wr0;
+    float sr0 = 0.0f, sr1 = 0.0f;
+    auto read_w = [&](int g) {
+        const int sl = g & (FR - 1);
+        wr0 = *reinterpret_cast<const uint4 *>(&wring[sl][wave][h * 1024 + 16 * n]);
+        wr1 = *reinterpret_cast<const uint4 *>(&wring[sl][wave][h * 1024 + 512 + 16 * n]);
+    };
+    auto read_s = [&](int g) {                               // the lane's rows n and 32 + n
+        sr0 = sring[g & (FS - 1)][wave * 64 + n];
+        sr1 = sring[g & (FS - 1)][wave * 64 + 32 + n];
+    };
+    // weights -> MFMA operands
+    auto expand = [&]() {
+        A00 = expand_f16(wr0.x, M, Y); A01 = expand_f16(wr0.y, M, Y);
+        A02 = expand_f16(wr0.z, M, Y); A03 = expand_f16(wr0.w, M, Y);
+        A10 = expand_f16(wr1.x, M, Y); A11 = expand_f16(wr1.y, M, Y);
+        A12 = expand_f16(wr1.z, M, Y); A13 = expand_f16(wr1.w, M, Y);
+    };
+    // Loads: stages 0..2 up front; phase 2g+1 issues stage g+3 into the slot
+    // of stage g-1, whose last reader was group 1's MFMA in phase 2g, before
+    // the barrier that ended it, then waits for the wave's own loads of stage
+    // g+1 (those of g+2, g+3 may still run). So stage g is in every wave's
+    // LDS share from phase 2g-1 on. Every wave passes 2 NG + 2 barriers.
+    // The wave's loads of a stage are in once at most those of the `later`
+    // stages issued after it (5 each) are still outstanding.
+    auto wait_stage = [&](int later) {
+        asm volatile("" ::: "memory");
+        if (later >= 2) pk_wait_vm_lds<10>();
+        else if (later == 1) pk_wait_vm_lds<5>();
+        else pk_wait_vm_lds<0>();
+        asm volatile("" ::: "memory");
+    };
+    issue(0);
+    if (NG > 1) issue(1);
+    if (NG > 2) issue(2);
+    wait_stage(min(2, NG - 1));                              // stage 0
+    auto odd_phase_loads = [&](int g) {                      // phase 2g+1
+        if (g + 3 < NG) issue(g + 3);
+        if (g + 1 < NG) wait_stage(min(g + 3, NG - 1) - (g + 1));   // stage g+1
+    };
+    if (!active) {
+        // no rows here: this wave's share of the loads and the barriers
+        for (int g = 0; g <= NG; ++g) {
+            pk_phase_barrier();
+            odd_phase_loads(g);
+            pk_phase_barrier();
+        }
+        return;
+    }
+    const pk_v16f zero = {};
+    // The stage loop for tiles with one (TWO false) or two 32-pair halves,
+    // compiled apart so that neither carries the other's branches.
+    auto stages = [&](auto two_c) {
+        constexpr bool TWO = decltype(two_c)::value;
+        // the stage's group sums for both row tiles (and pair halves): per
+        // 16-column step m, the activation operands (hi, lo of each half) are
+        // read from LDS two steps ahead of their MFMAs, so that the LDS latency
+        // is covered by the MFMAs of the step in between
+        auto mfma = [&](int g) {
+            const int sl = g & (FR - 1);
+            const _Float16 *bh = &bring[sl][0][n][0], *bl = &bring[sl][1][n][0];
+            auto ld = [&](int m, pk_v8h &h0, pk_v8h &l0, pk_v8h &h1, pk_v8h &l1) {
+                const int q0 = 8 * ((4 * h + m) ^ sw0);
+                h0 = *reinterpret_cast<const pk_v8h *>(bh + q0);
+                l0 = *reinterpret_cast<const pk_v8h *>(bl + q0);
+                if constexpr (TWO) {
+                    const int q1 = 8 * ((4 * h + m) ^ sw1);
+                    h1 = *reinterpret_cast<const pk_v8h *>(bh + 32 * 64 + q1);
+                    l1 = *reinterpret_cast<const pk_v8h *>(bl + 32 * 64 + q1);
+                }
+            };
+            auto step = [&](bool first, const pk_v8h &A0, const pk_v8h &A1, const pk_v8h &h0, const pk_v8h &l0,
+                            const pk_v8h &h1, const pk_v8h &l1) {
+                z00 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h0, A0, first ? zero : z00, 0, 0, 0);
+                z10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h0, A1, first ? zero : z10, 0, 0, 0);
+                z00 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, A0, z00, 0, 0, 0);
+                z10 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l0, A1, z10, 0, 0, 0);
+                if constexpr (TWO) {
+                    z01 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h1, A0, first ? zero : z01, 0, 0, 0);
+                    z11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(h1, A1, first ? zero : z11, 0, 0, 0);
+                    z01 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, A0, z01, 0, 0, 0);
+                    z11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, A1, z11, 0, 0, 0);
+                }
+            };
+            // three operand sets: a read never lands in registers that the MFMAs
+            // just issued still name (each set is refilled a step after its last use)
+            pk_v8h xh0, xl0, xh1, xl1, yh0, yl0, yh1, yl1, uh0, ul0, uh1, ul1, vh0, vl0, vh1, vl1;
+            auto keep = [&](const pk_v8h &p, const pk_v8h &q, const pk_v8h &r, const pk_v8h &t) {
+                if constexpr (TWO) asm volatile("" ::"v"(p), "v"(q), "v"(r), "v"(t));
+                else asm volatile("" ::"v"(p), "v"(q));
+            };
+            ld(0, xh0, xl0, xh1, xl1);
+            ld(1, yh0, yl0, yh1, yl1);
+            step(true, A00, A10, xh0, xl0, xh1, xl1);
+            ld(2, uh0, ul0, uh1, ul1);
+            step(false, A01, A11, yh0, yl0, yh1, yl1);
+            keep(xh0, xl0, xh1, xl1);
+            ld(3, vh0, vl0, vh1, vl1);
+            step(false, A02, A12, uh0, ul0, uh1, ul1);
+            keep(yh0, yl0, yh1, yl1);
+            step(false, A03, A13, vh0, vl0, vh1, vl1);
+            keep(uh0, ul0, uh1, ul1);
+        };
+        // acc += 16 s_g z_g in group order (the scales read by read_s)
+        auto fold = [&]() {
+#pragma unroll
+            for (int k = 0; k < 16; ++k) {
+                acc00[k] = __builtin_fmaf(sr0, z00[k], acc00[k]);
+                acc10[k] = __builtin_fmaf(sr1, z10[k], acc10[k]);
+                if constexpr (TWO) {
+                    acc01[k] = __builtin_fmaf(sr0, z01[k], acc01[k]);
+                    acc11[k] = __builtin_fmaf(sr1, z11[k], acc11[k]);
+                }
+            }
+        };
+        // phases 0, 1; then per stage g = 1 .. NG-1 the phases 2g, 2g+1; then
+        // phases 2 NG, 2 NG + 1 (the last fold)
+        if (grp == 0) {
+            read_w(0);
+            expand();                                        // phase 0
+            pk_phase_barrier();
+            odd_phase_loads(0);                              // phase 1
+            read_w(min(1, NG - 1));
+            read_s(0);
+            mfma(0);
+            pk_phase_barrier();
+            for (int g = 1; g < NG; ++g) {
+                fold();                                      // phase 2g: fold g-1, expand g
+                expand();
+                pk_phase_barrier();
+                odd_phase_loads(g);                          // phase 2g+1: MFMA of g
+                read_w(min(g + 1, NG - 1));
+                read_s(g);
+                mfma(g);
+                pk_phase_barrier();
+            }
+            fold();                                          // phase 2 NG
+            pk_phase_barrier();
+            odd_phase_loads(NG);                             // phase 2 NG + 1
+            pk_phase_barrier();
+        } else {
+            read_w(0);                                       // phase 0
+            pk_phase_barrier();
+            odd_phase_loads(0);                              // phase 1
+            expand();
+            pk_phase_barrier();
+            for (int g = 1; g < NG; ++g) {
+                read_w(g);                                   // phase 2g: MFMA of g-1
+                read_s(g - 1);
+                mfma(g - 1);
+                pk_phase_barrier();
+                odd_phase_loads(g);                          // phase 2g+1: fold g-1, expand g
+                fold();
+                expand();
+                pk_phase_barrier();
+            }
+            read_s(NG - 1);                                  // phase 2 NG
+            mfma(NG - 1);
+            pk_phase_barrier();
+            odd_phase_loads(NG);                             // phase 2 NG + 1
+            fold();
+            pk_phase_barrier();
+        }
+    };
+    if (two) stages(std::true_type{});
+    else stages(std::false_type{});
+    // lane (n, h) holds output row 32 rt + n of its block for the 16 pairs
+    // 32 ts + 8 b + 4 h + i of the tile (element 4 b + i)
+    const float *bias = a.off_bias >= 0 ? reinterpret_cast<const float *>(base + a.off_bias) : nullptr;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+        const int row = rb * 64 + 32 * rt + n;
+        const float bv = bias ? bias[row] : 0.0f;
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts) {
+            if (ts == 1 && !two) break;
+            const pk_v16f &c = rt ? (ts ? acc11 : acc10) : (ts ? acc01 : acc00);
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+                const int tn = 32 * ts + 8 * (v >> 2) + 4 * h + (v & 3);
+                float y = ldexpf(c[v], tok_exp[tn] - 19);
+                if (bias) y = y + bv;
+                if constexpr (EPI == PK_EPI_SWIGLU) {
+                    const float up = __shfl_xor(y, 1, 64);    // row + 1 (lane n ^ 1) for even n
+                    if (!(n & 1) && tn < cnt)
+                        a.y[(int64_t)tok_pair[tn] * a.y_stride + (row >> 1)] = pk_swiglu(y, up, a.lim, a.alpha);
+                } else {
+                    if (tn < cnt) a.y[(int64_t)tok_pair[tn] * a.y_stride + row] = y;
+                }
+            }
+        }
+    }
+}
+
+int pk_launch_act_f16(const float *x, int64_t x_stride, int rows, int cols, uint16_t *xf, int64_t fplane,
+                      int32_t *exps, hipStream_t st) {
+    PK_CHECK(rows > 0 && cols > 0 && cols % 8 == 0 && fplane >= (int64_t)rows * cols, PK_ERR_ARG,
+             "act f16: bad shape");
+    hipLaunchKernelGGL(k_act_f16, dim3(rows), dim3(256), 0, st, x, x_stride, cols, xf, fplane, exps);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+int pk_launch_moe_f16(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st) {
+    PK_CHECK(a.O % 64 == 0 && a.O > 0 && a.NG > 0 && max_tiles > 0 && a.frow == a.NG * 64 && a.xf && a.fplane > 0,
+             PK_ERR_UNSUPPORTED, "f16 grouped gemm: O=%d NG=%d", a.O, a.NG);
+    const int64_t n = (int64_t)max_tiles * ((a.O + FROWS - 1) / FROWS);
+    PK_CHECK(n < (1 << 30), PK_ERR_UNSUPPORTED, "f16 grouped gemm: %lld items", (long long)n);
+    const dim3 grid((unsigned)((n + 7) & ~(int64_t)7));
+    if (epilogue == PK_EPI_SWIGLU)
+        hipLaunchKernelGGL(k_moe_f16<PK_EPI_SWIGLU>, grid, dim3(FTHR), 0, st, a);
+    else
+        hipLaunchKernelGGL(k_moe_f16<PK_EPI_PLAIN>, grid, dim3(FTHR), 0, st, a);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
 }
 
 int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, int8_t *limbs, int64_t plane,

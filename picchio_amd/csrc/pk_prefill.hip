@@ -227,7 +227,7 @@ static int grouped_reserve(pk_engine *e, int T) {
     e->g_cap = 0;
     const int64_t plane = std::max((int64_t)T * c->hidden, P * (c->moe_inter / 2));
     const int64_t max_tiles = (P + 31) / 32 + c->n_experts;
-    PK_TRY(pk_dev_alloc(e, (void **)&e->g_limbs, 3 * plane));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_limbs, 4 * plane));     // 3 int8 planes or 2 half planes
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_exps, std::max((int64_t)T, P) * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_pairs, P * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_tiles, (3 * max_tiles + 1) * 4));
@@ -235,10 +235,11 @@ static int grouped_reserve(pk_engine *e, int T) {
     return PK_OK;
 }
 
-// The same MoE as moe_rows on the int8 matrix cores: pairs grouped by expert,
-// activations as three int8 limbs, gate_up (+SwiGLU) and down as grouped
-// GEMMs over 32-pair tiles (pk_mfma.hip), then the per-token sum in the
-// batch's expert order. sel_in / w_in: routing supplied by the caller
+// The same MoE as moe_rows on the matrix cores: pairs grouped by expert,
+// activations as two halves (hi, lo) on the f16 MFMA over 64-pair tiles, or
+// as three int8 limbs over 32-pair tiles (grouped_f16 off), gate_up
+// (+SwiGLU) and down as grouped GEMMs (pk_mfma.hip), then the per-token sum
+// in the batch's expert order. sel_in / w_in: routing supplied by the caller
 // (device [T][K], combine weights already x routed_scale), else the router's.
 static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
                          const int32_t *sel_in, const float *w_in, bool decode_order = false) {
@@ -257,10 +258,13 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, e->b_sel, T, K, E, e->b_perm);
         PK_HIP(hipGetLastError());
     }
-    const int max_tiles = (P + 31) / 32 + E;
+    const bool f16 = e->grouped_f16;
+    const int tile = f16 ? PK_F16_TILE : 32;
+    const int max_tiles = (P + tile - 1) / tile + E;           // within the 32-pair tiles' buffer
     int32_t *tile_exp = e->g_tiles, *tile_beg = tile_exp + max_tiles, *tile_cnt = tile_beg + max_tiles;
     int32_t *n_tiles = tile_cnt + max_tiles;
-    PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->g_pairs, tile_exp, tile_beg, tile_cnt, n_tiles, e->stream));
+    PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->g_pairs, tile_exp, tile_beg, tile_cnt, n_tiles, e->stream,
+                                 tile));
     const int64_t plane = std::max((int64_t)T * D, (int64_t)P * half);
     pk_mfma_args a{};
     a.base = e->store;
@@ -268,26 +272,33 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
     a.slot_base = layer * E;
     a.limbs = e->g_limbs;
     a.plane = plane;
+    a.xf = reinterpret_cast<const uint16_t *>(e->g_limbs);
+    a.fplane = plane;
+    uint16_t *xf = reinterpret_cast<uint16_t *>(e->g_limbs);
     a.exps = e->g_exps;
     a.pairs = e->g_pairs;
     a.tile_exp = tile_exp; a.tile_beg = tile_beg; a.tile_cnt = tile_cnt; a.n_tiles = n_tiles;
     a.lim = c->swiglu_limit;
     a.alpha = c->swiglu_alpha;
     // gate_up + SwiGLU: activation rows are the T tokens
-    PK_TRY(pk_launch_act_limbs(x, D, T, D, e->g_limbs, plane, e->g_exps, 1, e->stream));
+    if (f16) PK_TRY(pk_launch_act_f16(x, D, T, D, xf, plane, e->g_exps, e->stream));
+    else PK_TRY(pk_launch_act_limbs(x, D, T, D, e->g_limbs, plane, e->g_exps, 1, e->stream));
     a.off_tiles = e->ex.off_gu_tiles; a.off_scales = e->ex.off_gu_scales; a.off_bias = e->ex.off_gu_bias;
-    a.O = c->moe_inter; a.NG = D / 64; a.lrow = D; a.x_div = K;
+    a.O = c->moe_inter; a.NG = D / 64; a.lrow = D; a.frow = D; a.x_div = K;
     a.y = e->b_act; a.y_stride = half;
     int ps = pk_prof_begin(e, PK_PROF_EXPERT_GATE_UP);
-    PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_SWIGLU, e->stream));
+    if (f16) PK_TRY(pk_launch_moe_f16(a, max_tiles, PK_EPI_SWIGLU, e->stream));
+    else PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_SWIGLU, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     // down: activation rows are the P pairs' SwiGLU outputs
-    PK_TRY(pk_launch_act_limbs(e->b_act, half, P, half, e->g_limbs, plane, e->g_exps, 1, e->stream));
+    if (f16) PK_TRY(pk_launch_act_f16(e->b_act, half, P, half, xf, plane, e->g_exps, e->stream));
+    else PK_TRY(pk_launch_act_limbs(e->b_act, half, P, half, e->g_limbs, plane, e->g_exps, 1, e->stream));
     a.off_tiles = e->ex.off_dn_tiles; a.off_scales = e->ex.off_dn_scales; a.off_bias = e->ex.off_dn_bias;
-    a.O = D; a.NG = half / 64; a.lrow = half; a.x_div = 1;
+    a.O = D; a.NG = half / 64; a.lrow = half; a.frow = half; a.x_div = 1;
     a.y = e->b_eo; a.y_stride = D;
     ps = pk_prof_begin(e, PK_PROF_EXPERT_DOWN);
-    PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_PLAIN, e->stream));
+    if (f16) PK_TRY(pk_launch_moe_f16(a, max_tiles, PK_EPI_PLAIN, e->stream));
+    else PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_PLAIN, e->stream));
     PK_TRY(pk_prof_end(e, ps));
     hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
                        e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);

@@ -2,12 +2,15 @@
 
 Config 3: one GPT-OSS-20B MoE layer (32 experts) over T = 2048 tokens with
 the Zipf(1.1) routing of the benchmark (8192 (token, expert) pairs, 16..512
-pairs per expert), through the expert-grouped int8 MFMA GEMMs
-(pk_moe_forward_grouped). Bars: activation limbs and exponents of all rows
-bit-exact with the oracle's restatement; sampled pairs' down outputs
-bit-exact given the same activations; per-token outputs of 160 sampled
-tokens within relative L2 1e-5 of picchio's fp32 expert_apply arithmetic in
-forward_prefill's first-request expert order (picchio.c:1829-1916).
+pairs per expert), through the expert-grouped MFMA GEMMs
+(pk_moe_forward_grouped), both arithmetics. Int8 limbs: activation limbs
+and exponents of all rows bit-exact with the oracle's restatement; sampled
+pairs' down outputs bit-exact given the same activations. Half-precision
+pairs (the default): sampled pairs' SwiGLU activations and down outputs
+within relative L2 2e-6 of picchio's fp32 GEMV (matmul_i4_gs). Both:
+per-token outputs of 160 sampled tokens within relative L2 1e-5 of picchio's
+fp32 expert_apply arithmetic in forward_prefill's first-request expert order
+(picchio.c:1829-1916).
 
 Config 4: the GPT-OSS-120B shape (36 layers, 128 experts) with 4096-position
 synthetic KV contexts, at batch 1 (the replayed decode step) and batch 32
@@ -42,7 +45,8 @@ def _margin(lg):
 
 # ───────────────────────────── config 3 ─────────────────────────────
 
-def test_config3_grouped_prefill_full_shape(gpu, oracle):
+@pytest.mark.parametrize("f16", [True, False], ids=["f16", "int8"])
+def test_config3_grouped_prefill_full_shape(gpu, oracle, f16):
     import torch
     import picchio_amd as pa
     from bench import zipf_routing
@@ -60,22 +64,45 @@ def test_config3_grouped_prefill_full_shape(gpu, oracle):
         out = eng.empty((T, D), torch.float32)
         act = eng.empty((T * K, half), torch.float32)
         eo = eng.empty((T * K, D), torch.float32)
+        eng.set_grouped_f16(f16)
         eng.moe_forward_grouped(0, xd, out, eng.to_dev(sel), eng.to_dev(w), act, eo)
         out, act, eo = eng.to_host(out), eng.to_host(act), eng.to_host(eo)
+        pairs = [0, 5, 1023, 2048, 4097, 6000, 8191, 7777]
+        experts = {}
+        if f16:
+            # sampled pairs against picchio's fp32 GEMV on the same inputs
+            for p in pairs:
+                t, k = divmod(p, K)
+                e = int(sel[t, k])
+                if e not in experts:
+                    experts[e] = oracle.expert_arrays(model, 0, e, cfg)
+                gq, gs, dq, ds, gb, db = experts[e]
+                y = np.empty(cfg.moe_inter, np.float32)
+                oracle.matmul_i4_gs(y, np.ascontiguousarray(x[t]), gq, gs, 1, D, cfg.moe_inter, cfg.group_size)
+                y += gb
+                oracle.swiglu_clamped(y, cfg.moe_inter, cfg.swiglu_limit, cfg.swiglu_alpha)
+                assert rel_l2(act[p], y[:half]) < 2e-6, p
+                eo_ref = np.empty(D, np.float32)
+                oracle.matmul_i4_gs(eo_ref, np.ascontiguousarray(act[p]), dq, ds, 1, half, D, cfg.group_size)
+                eo_ref += db
+                assert rel_l2(eo[p], eo_ref) < 2e-6, p
+            pairs = []
 
         # activation limbs of every row
-        limbs = eng.empty((3, T, D), torch.int8)
-        exps = eng.empty(T, torch.int32)
-        eng.quantize_act_i8x3(xd, limbs, exps)
-        xl = np.empty((3, T, D), np.int8)
-        xe = np.empty(T, np.int32)
-        oracle.act_limbs(x, T, D, xl, xe)
-        assert np.array_equal(eng.to_host(exps), xe)
-        assert np.array_equal(eng.to_host(limbs), xl)
+        if f16:
+            xl = xe = None
+        else:
+            limbs = eng.empty((3, T, D), torch.int8)
+            exps = eng.empty(T, torch.int32)
+            eng.quantize_act_i8x3(xd, limbs, exps)
+            xl = np.empty((3, T, D), np.int8)
+            xe = np.empty(T, np.int32)
+            oracle.act_limbs(x, T, D, xl, xe)
+            assert np.array_equal(eng.to_host(exps), xe)
+            assert np.array_equal(eng.to_host(limbs), xl)
 
         # sampled pairs: the integer path restated (gate_up to 1e-6, down bit-exact)
-        experts = {}
-        for p in [0, 5, 1023, 2048, 4097, 6000, 8191, 7777]:
+        for p in pairs:
             t, k = divmod(p, K)
             e = int(sel[t, k])
             if e not in experts:
@@ -104,7 +131,8 @@ def test_config3_grouped_prefill_full_shape(gpu, oracle):
             err = rel_l2(out[t], acc)
             worst = max(worst, err)
             assert err < 1e-5, (int(t), err)
-        print(f"config 3: worst token rel-L2 {worst:.2e} over 160 tokens", flush=True)
+        print(f"config 3 ({'f16' if f16 else 'int8'}): worst token rel-L2 {worst:.2e} over 160 tokens",
+              flush=True)
     finally:
         eng.close()
         oracle.model_free(model)

@@ -1,13 +1,17 @@
-"""GPU parity of the expert-grouped MoE on the int8 matrix cores
-(pk_moe_forward_grouped, pk_quantize_act_i8x3).
+"""GPU parity of the expert-grouped MoE on the matrix cores
+(pk_moe_forward_grouped, pk_quantize_act_i8x3, pk_set_grouped_f16).
 
-Bars: activation limbs and exponents bit-exact with the oracle's
-restatement; down-projection outputs bit-exact with the oracle's restatement
-of the same integer arithmetic given the same activations; SwiGLU activations
-within relative L2 1e-6 of it (the device expf may differ in the last bit);
-per-token MoE outputs within relative L2 1e-5 of picchio's fp32 arithmetic
-(forward_prefill's expert order, oracle expert_apply), i.e. an order of
-magnitude inside the north star's 1e-4.
+Int8 limbs (pk_set_grouped_f16(e, 0)): activation limbs and exponents
+bit-exact with the oracle's restatement; down-projection outputs bit-exact
+with the oracle's restatement of the same integer arithmetic given the same
+activations; SwiGLU activations within relative L2 1e-6 of it (the device
+expf may differ in the last bit).
+Half-precision pairs (the default): every pair's SwiGLU activations and
+down outputs within relative L2 2e-6 of picchio's fp32 GEMV (matmul_i4_gs)
+on the same inputs; the MFMA sums in its own order, so no bit-exact bar.
+Both: per-token MoE outputs within relative L2 1e-5 of picchio's fp32
+arithmetic (forward_prefill's expert order, oracle expert_apply), i.e. an
+order of magnitude inside the north star's 1e-4.
 """
 import numpy as np
 import pytest
@@ -69,20 +73,47 @@ def _routing(eng, cfg, xd, T):
     return sd, wd, out
 
 
-def test_grouped_parity(grp, oracle):
+def _grouped_run(eng, cfg, x, f16):
     import torch
-    cfg, model, eng = grp
     D, K, half = cfg.hidden, cfg.topk, cfg.moe_inter // 2
-    T = 100                                        # 400 pairs over 8 experts: several tiles each
-    x = np.random.default_rng(6).standard_normal((T, D)).astype(np.float32)
+    T = x.shape[0]
     xd = eng.to_dev(x)
     sd, wd, out_exact = _routing(eng, cfg, xd, T)
     out = eng.empty((T, D), torch.float32)
     act = eng.empty((T * K, half), torch.float32)
     eo = eng.empty((T * K, D), torch.float32)
-    eng.moe_forward_grouped(0, xd, out, sd, wd, act, eo)
-    sel, w = eng.to_host(sd), eng.to_host(wd)
-    out, act, eo, out_exact = (eng.to_host(t) for t in (out, act, eo, out_exact))
+    eng.set_grouped_f16(f16)
+    try:
+        eng.moe_forward_grouped(0, xd, out, sd, wd, act, eo)
+    finally:
+        eng.set_grouped_f16(True)
+    return tuple(eng.to_host(t) for t in (sd, wd, out, act, eo, out_exact))
+
+
+def _check_tokens(cfg, model, oracle, x, sel, w, out, out_exact):
+    """Per-token outputs against picchio's fp32 arithmetic in the batch's expert order."""
+    D, K = cfg.hidden, cfg.topk
+    rank = {}
+    for e in sel.ravel():
+        rank.setdefault(int(e), len(rank))
+    worst = 0.0
+    for t in range(0, x.shape[0], 9):
+        acc = np.zeros(D, np.float32)
+        for k in sorted(range(K), key=lambda k: rank[int(sel[t, k])]):
+            oracle.expert_apply(model, 0, int(sel[t, k]), x[t], acc, float(w[t, k]))
+        err = rel_l2(out[t], acc)
+        worst = max(worst, err)
+        assert err < 1e-5, (t, err)
+    assert rel_l2(out, out_exact) < 1e-5
+    return worst
+
+
+def test_grouped_parity(grp, oracle):
+    cfg, model, eng = grp
+    D, K, half = cfg.hidden, cfg.topk, cfg.moe_inter // 2
+    T = 100                                        # 400 pairs over 8 experts: several tiles each
+    x = np.random.default_rng(6).standard_normal((T, D)).astype(np.float32)
+    sel, w, out, act, eo, out_exact = _grouped_run(eng, cfg, x, False)
 
     # integer path restated: a sample of (token, expert) pairs
     xl = np.empty((3, T, D), np.int8)
@@ -107,20 +138,43 @@ def test_grouped_parity(grp, oracle):
         oracle.mfma_matvec(dq, ds, db, D, half, al[0, 0], al[1, 0], al[2, 0], int(ae[0]), eo_ref)
         assert bits_equal(eo[p], eo_ref), (p, first_mismatch(eo[p], eo_ref))
 
-    # per-token output against picchio's fp32 arithmetic in the batch's expert order
-    rank = {}
-    for e in sel.ravel():
-        rank.setdefault(int(e), len(rank))
-    worst = 0.0
-    for t in range(0, T, 9):
-        acc = np.zeros(D, np.float32)
-        for k in sorted(range(K), key=lambda k: rank[int(sel[t, k])]):
-            oracle.expert_apply(model, 0, int(sel[t, k]), x[t], acc, float(w[t, k]))
-        err = rel_l2(out[t], acc)
-        worst = max(worst, err)
-        assert err < 1e-5, (t, err)
-    assert rel_l2(out, out_exact) < 1e-5
-    print(f"grouped vs fp32 reference: worst token rel-L2 {worst:.2e}")
+    worst = _check_tokens(cfg, model, oracle, x, sel, w, out, out_exact)
+    print(f"grouped (int8 limbs) vs fp32 reference: worst token rel-L2 {worst:.2e}")
+
+
+@pytest.mark.parametrize("T", [100, 7, 300])
+def test_grouped_f16_parity(grp, oracle, T):
+    """The half-precision pair arithmetic against picchio's fp32 GEMV, per
+    pair: T = 100 (tiles of 64 and partial halves), 7 (every tile one
+    32-pair half), 300 (1200 pairs, full tiles)."""
+    cfg, model, eng = grp
+    D, K, inter, half, gs = cfg.hidden, cfg.topk, cfg.moe_inter, cfg.moe_inter // 2, cfg.group_size
+    rng = np.random.default_rng(60 + T)
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    x[0] *= 1e-3                                   # a small-magnitude row (its own exponent)
+    sel, w, out, act, eo, out_exact = _grouped_run(eng, cfg, x, True)
+    experts = {}
+    worst_a = worst_e = 0.0
+    for p in sorted({0, 1, 3, K * T // 2, K * T - 1} | set(range(5, K * T, max(1, K * T // 40)))):
+        t, k = divmod(p, K)
+        e = int(sel[t, k])
+        if e not in experts:
+            experts[e] = oracle.expert_arrays(model, 0, e, cfg)
+        gq, gsc, dq, dsc, gb, db = experts[e]
+        y = np.empty(inter, np.float32)
+        oracle.matmul_i4_gs(y, np.ascontiguousarray(x[t]), gq, gsc, 1, D, inter, gs)
+        y += gb
+        oracle.swiglu_clamped(y, inter, cfg.swiglu_limit, cfg.swiglu_alpha)
+        ea = rel_l2(act[p], y[:half])
+        eo_ref = np.empty(D, np.float32)
+        oracle.matmul_i4_gs(eo_ref, np.ascontiguousarray(act[p]), dq, dsc, 1, half, D, gs)
+        eo_ref += db
+        ee = rel_l2(eo[p], eo_ref)
+        worst_a, worst_e = max(worst_a, ea), max(worst_e, ee)
+        assert ea < 2e-6 and ee < 2e-6, (p, ea, ee)
+    worst = _check_tokens(cfg, model, oracle, x, sel, w, out, out_exact)
+    print(f"grouped (f16 pairs) T={T}: pair act {worst_a:.2e}, pair down {worst_e:.2e}, "
+          f"worst token rel-L2 {worst:.2e}")
 
 
 def test_grouped_uses_router_when_no_routing_given(grp, oracle):
