@@ -406,8 +406,10 @@ __global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ x, in
 // group 0. So every SIMD's matrix core has one wave's MFMAs to run while the
 // other wave's VALU work may co-issue (measured: a VALU instruction issues
 // in ~32 % of the MFMA-busy cycles; the VALU work is what bounds the kernel).
-//   phase 2g:   group 0 folds g-1, expands g    | group 1 MFMA of g-1
-//   phase 2g+1: group 0 MFMA of g                | group 1 folds g-1, expands g
+//   phase 2g:   group 0 folds g-1                | group 1 MFMA of g-1, expands g
+//   phase 2g+1: group 0 MFMA of g, expands g+1   | group 1 folds g-1
+// (a wave expands its next weights between its own MFMAs, operand by
+// operand as they are consumed).
 constexpr int FR = 4, FS = 8;
 typedef __attribute__((address_space(3))) void pk_lds_void;
 
@@ -435,13 +437,16 @@ template <int N>
 __device__ __forceinline__ void pk_wait_vm_lds() {
     __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (0 << 8) | ((N >> 4) << 14));
 }
-// workgroup barrier after the wave's LDS reads are done; memory accesses are
-// not moved across it by the compiler
+// workgroup barrier after the wave's LDS reads are done; the compiler moves
+// no instruction across it (memory accesses, MFMAs and VALU work stay in
+// their phase)
 __device__ __forceinline__ void pk_phase_barrier() {
+    __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     pk_wait_vm_lds<63>();
     __builtin_amdgcn_s_barrier();
     asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
 }
 
 template <int EPI>
@@ -603,24 +608,27 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
                     z11 = __builtin_amdgcn_mfma_f32_32x32x16_f16(l1, A1, z11, 0, 0, 0);
                 }
             };
-            // three operand sets: a read never lands in registers that the MFMAs
-            // just issued still name (each set is refilled a step after its last use)
-            pk_v8h xh0, xl0, xh1, xl1, yh0, yl0, yh1, yl1, uh0, ul0, uh1, ul1, vh0, vl0, vh1, vl1;
-            auto keep = [&](const pk_v8h &p, const pk_v8h &q, const pk_v8h &r, const pk_v8h &t) {
-                if constexpr (TWO) asm volatile("" ::"v"(p), "v"(q), "v"(r), "v"(t));
-                else asm volatile("" ::"v"(p), "v"(q));
-            };
+            // two operand sets alternate; after step m's MFMAs have issued (an
+            // MFMA reads its operands at issue), its weight operands are
+            // re-expanded from the next stage's weights (wr0 / wr1), so that
+            // this VALU work issues between the MFMAs of the following steps
+            pk_v8h xh0, xl0, xh1, xl1, yh0, yl0, yh1, yl1;
             ld(0, xh0, xl0, xh1, xl1);
             ld(1, yh0, yl0, yh1, yl1);
             step(true, A00, A10, xh0, xl0, xh1, xl1);
-            ld(2, uh0, ul0, uh1, ul1);
+            A00 = expand_f16(wr0.x, M, Y); A10 = expand_f16(wr1.x, M, Y);
+            ld(2, xh0, xl0, xh1, xl1);
             step(false, A01, A11, yh0, yl0, yh1, yl1);
-            keep(xh0, xl0, xh1, xl1);
-            ld(3, vh0, vl0, vh1, vl1);
-            step(false, A02, A12, uh0, ul0, uh1, ul1);
-            keep(yh0, yl0, yh1, yl1);
-            step(false, A03, A13, vh0, vl0, vh1, vl1);
-            keep(uh0, ul0, uh1, ul1);
+            A01 = expand_f16(wr0.y, M, Y); A11 = expand_f16(wr1.y, M, Y);
+            ld(3, yh0, yl0, yh1, yl1);
+            step(false, A02, A12, xh0, xl0, xh1, xl1);
+            A02 = expand_f16(wr0.z, M, Y); A12 = expand_f16(wr1.z, M, Y);
+            step(false, A03, A13, yh0, yl0, yh1, yl1);
+            A03 = expand_f16(wr0.w, M, Y); A13 = expand_f16(wr1.w, M, Y);
+            // the expansion stays in this phase (the compiler may not sink it
+            // to the next use), interleaved with the MFMAs above
+            asm volatile("" : "+v"(A00), "+v"(A01), "+v"(A02), "+v"(A03), "+v"(A10), "+v"(A11), "+v"(A12),
+                         "+v"(A13));
         };
         // acc += 16 s_g z_g in group order (the scales read by read_s)
         auto fold = [&]() {
@@ -643,13 +651,12 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
             odd_phase_loads(0);                              // phase 1
             read_w(min(1, NG - 1));
             read_s(0);
-            mfma(0);
+            mfma(0);                                         // (expands stage 1 on the way)
             pk_phase_barrier();
             for (int g = 1; g < NG; ++g) {
-                fold();                                      // phase 2g: fold g-1, expand g
-                expand();
+                fold();                                      // phase 2g: fold g-1
                 pk_phase_barrier();
-                odd_phase_loads(g);                          // phase 2g+1: MFMA of g
+                odd_phase_loads(g);                          // phase 2g+1: MFMA of g, expand g+1
                 read_w(min(g + 1, NG - 1));
                 read_s(g);
                 mfma(g);
@@ -666,13 +673,12 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
             expand();
             pk_phase_barrier();
             for (int g = 1; g < NG; ++g) {
-                read_w(g);                                   // phase 2g: MFMA of g-1
+                read_w(g);                                   // phase 2g: MFMA of g-1, expand g
                 read_s(g - 1);
                 mfma(g - 1);
                 pk_phase_barrier();
-                odd_phase_loads(g);                          // phase 2g+1: fold g-1, expand g
+                odd_phase_loads(g);                          // phase 2g+1: fold g-1
                 fold();
-                expand();
                 pk_phase_barrier();
             }
             read_s(NG - 1);                                  // phase 2 NG
