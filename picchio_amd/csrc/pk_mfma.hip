@@ -360,6 +360,18 @@ __device__ __forceinline__ pk_v8h expand_f16(uint32_t w, uint32_t M, uint32_t Y)
 }
 }  // namespace
 
+// The clamped SwiGLU of picchio.c:1416-1424 with the hardware exp2 and
+// reciprocal (1-2 ulp) in place of the correctly rounded expf: this path is
+// held to a tolerance, and these few instructions replace a double-precision
+// exp per pair.
+__device__ __forceinline__ float swiglu_f16path(float gate, float up, float lim, float alpha) {
+    if (gate > lim) gate = lim;
+    if (up > lim) up = lim;
+    if (up < -lim) up = -lim;
+    const float e = __builtin_amdgcn_exp2f(-(alpha * gate) * 1.44269504088896341f);
+    return (up + 1.0f) * gate * __builtin_amdgcn_rcpf(1.0f + e);
+}
+
 // One row per workgroup: exponent k of max|x|, the hi and lo planes (columns
 // permuted by f16_pos inside each 8-column chunk).
 __global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ x, int64_t x_stride, int cols,
@@ -702,17 +714,32 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
         for (int ts = 0; ts < 2; ++ts) {
             if (ts == 1 && !two) break;
             const pk_v16f &c = rt ? (ts ? acc11 : acc10) : (ts ? acc01 : acc00);
+            float y[16];
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
                 const int tn = 32 * ts + 8 * (v >> 2) + 4 * h + (v & 3);
-                float y = ldexpf(c[v], tok_exp[tn] - 19);
-                if (bias) y = y + bv;
-                if constexpr (EPI == PK_EPI_SWIGLU) {
-                    const float up = __shfl_xor(y, 1, 64);    // row + 1 (lane n ^ 1) for even n
-                    if (!(n & 1) && tn < cnt)
-                        a.y[(int64_t)tok_pair[tn] * a.y_stride + (row >> 1)] = pk_swiglu(y, up, a.lim, a.alpha);
-                } else {
-                    if (tn < cnt) a.y[(int64_t)tok_pair[tn] * a.y_stride + row] = y;
+                y[v] = ldexpf(c[v], tok_exp[tn] - 19);
+                if (bias) y[v] = y[v] + bv;
+            }
+            if constexpr (EPI == PK_EPI_SWIGLU) {
+                // rows 2i (gate, even lane) and 2i+1 (up, odd lane): the even
+                // lane finishes elements 0..7, the odd lane 8..15
+                const bool odd = n & 1;
+#pragma unroll
+                for (int v = 0; v < 8; ++v) {
+                    const float other = __shfl_xor(odd ? y[v] : y[v + 8], 1, 64);
+                    const float mine = odd ? y[v + 8] : y[v];
+                    const int va = odd ? v + 8 : v;
+                    const int tn = 32 * ts + 8 * (va >> 2) + 4 * h + (va & 3);
+                    if (tn < cnt)
+                        a.y[(int64_t)tok_pair[tn] * a.y_stride + (row >> 1)] =
+                            swiglu_f16path(odd ? other : mine, odd ? mine : other, a.lim, a.alpha);
+                }
+            } else {
+#pragma unroll
+                for (int v = 0; v < 16; ++v) {
+                    const int tn = 32 * ts + 8 * (v >> 2) + 4 * h + (v & 3);
+                    if (tn < cnt) a.y[(int64_t)tok_pair[tn] * a.y_stride + row] = y[v];
                 }
             }
         }
