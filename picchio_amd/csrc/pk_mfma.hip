@@ -406,22 +406,16 @@ __global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ x, in
 
 // Stage buffers: rings in LDS filled by direct global -> LDS loads (no
 // registers), three stages ahead: activations and weights FR = 4 stages,
-// scales FS = 8 (read one phase later, by the fold). Per stage and wave five
-// load instructions, always issued, so that the wait for a stage is a fixed
-// count of the wave's later loads.
+// scales FS = 8. Per stage and wave five load instructions, always issued,
+// so that the wait for a stage is a fixed count of the wave's later loads.
 //
-// Schedule: the 8 waves form two groups, one wave of each on every SIMD (the
-// first and second wave the hardware placed there). Work alternates in
-// phases that end at a workgroup barrier: in one phase a group runs the
-// stage's 32 MFMAs while the other group, on the same SIMDs, folds its
-// previous stage and expands its next weights; group 1 runs one phase behind
-// group 0. So every SIMD's matrix core has one wave's MFMAs to run while the
-// other wave's VALU work may co-issue (measured: a VALU instruction issues
-// in ~32 % of the MFMA-busy cycles; the VALU work is what bounds the kernel).
-//   phase 2g:   group 0 folds g-1                | group 1 MFMA of g-1, expands g
-//   phase 2g+1: group 0 MFMA of g, expands g+1   | group 1 folds g-1
-// (a wave expands its next weights between its own MFMAs, operand by
-// operand as they are consumed).
+// Schedule, per 64-column stage g and wave: fold stage g-1 into the
+// accumulators | workgroup barrier | issue stage g+3, read this stage's
+// scales and the next stage's weights, run the 32 MFMAs of stage g and,
+// between them, expand the next stage's weights operand by operand as the
+// MFMAs consume the current ones. Measured against a two-group schedule in
+// which the waves of each SIMD alternate MFMA and fold/expand phases (two
+// barriers per stage): 607-626 against 650-657 us per gate_up launch.
 constexpr int FR = 4, FS = 8;
 typedef __attribute__((address_space(3))) void pk_lds_void;
 
@@ -451,8 +445,8 @@ __device__ __forceinline__ void pk_wait_vm_lds() {
 }
 // workgroup barrier after the wave's LDS reads are done; the compiler moves
 // no instruction across it (memory accesses, MFMAs and VALU work stay in
-// their phase)
-__device__ __forceinline__ void pk_phase_barrier() {
+// their stage)
+__device__ __forceinline__ void pk_stage_barrier() {
     __builtin_amdgcn_sched_barrier(0);
     asm volatile("" ::: "memory");
     pk_wait_vm_lds<63>();
@@ -471,7 +465,7 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     __shared__ __attribute__((aligned(16))) _Float16 bring[FR][2][FT][64];
     __shared__ __attribute__((aligned(16))) uint8_t wring[FR][FW][PK_TILE_BYTES];
     __shared__ __attribute__((aligned(16))) float sring[FS][FROWS];
-    __shared__ int tok_row[FT], tok_exp[FT], tok_pair[FT], simd_of[FW];
+    __shared__ int tok_row[FT], tok_exp[FT], tok_pair[FT];
     // this workgroup's item
     const int nt = *a.n_tiles;
     const int n_item = nt * ((a.O + FROWS - 1) / FROWS);
@@ -483,10 +477,6 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     const int rg = item / nt, j = item - rg * nt;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // the SIMD this wave runs on (HW_ID bits 5:4); the groups pair the two
-    // waves of each SIMD, whatever the placement
-    const int simd = __builtin_amdgcn_s_getreg(4 | (4 << 6) | (1 << 11));
-    if (lane == 0) simd_of[wave] = simd;
     const int e = a.tile_exp[j], beg = a.tile_beg[j], cnt = a.tile_cnt[j];
     if (threadIdx.x < FT) {
         const int t = threadIdx.x;
@@ -507,9 +497,6 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     uint32_t M = 0x000F000Fu, Y = 0x64086408u;
     asm volatile("" : "+v"(M), "+v"(Y));                    // held in registers (see expand_f16)
     __syncthreads();
-    int rank = 0;
-    for (int w = 0; w < wave; ++w) rank += simd_of[w] == simd;
-    const int grp = rank & 1;
     // this wave's loads per stage: activation rows 8 b .. 8 b + 7 of limb l for
     // b = 2 wave & 7 and b + 1 (l = wave / 4: waves 0..3 hi, 4..7 lo), its row
     // block's two weight halves and 64 scales
@@ -535,7 +522,7 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     const int sw0 = (n ^ (n >> 3)) & 7;                      // f(n), f(32 + n)
     const int sw1 = (n ^ (4 + (n >> 3))) & 7;
     // weights (this wave's own loads) and scales of a stage, read into
-    // registers during the wave's MFMA phase for the fold / expand phase after it
+    // registers ahead of the stage that uses them (the fold, the expansion)
     uint4 wr0 = make_uint4(0, 0, 0, 0), wr1 = wr0;
     float sr0 = 0.0f, sr1 = 0.0f;
     auto read_w = [&](int g) {
@@ -554,13 +541,13 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
         A10 = expand_f16(wr1.x, M, Y); A11 = expand_f16(wr1.y, M, Y);
         A12 = expand_f16(wr1.z, M, Y); A13 = expand_f16(wr1.w, M, Y);
     };
-    // Loads: stages 0..2 up front; phase 2g+1 issues stage g+3 into the slot
-    // of stage g-1, whose last reader was group 1's MFMA in phase 2g, before
-    // the barrier that ended it, then waits for the wave's own loads of stage
-    // g+1 (those of g+2, g+3 may still run). So stage g is in every wave's
-    // LDS share from phase 2g-1 on. Every wave passes 2 NG + 2 barriers.
-    // The wave's loads of a stage are in once at most those of the `later`
-    // stages issued after it (5 each) are still outstanding.
+    // Loads: stages 0..2 up front; after the barrier that opens stage g a
+    // wave issues stage g+3 into the slot of stage g-1 (every wave's last read
+    // of it came before that barrier), then waits for its own loads of stage
+    // g+1 (those of g+2, g+3 may still run): so stage g+1 is in every wave's
+    // LDS share before the barrier that opens it. Every wave passes NG
+    // barriers. The wave's loads of a stage are in once at most those of the
+    // `later` stages issued after it (5 each) are still outstanding.
     auto wait_stage = [&](int later) {
         asm volatile("" ::: "memory");
         if (later >= 2) pk_wait_vm_lds<10>();
@@ -572,16 +559,15 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     if (NG > 1) issue(1);
     if (NG > 2) issue(2);
     wait_stage(min(2, NG - 1));                              // stage 0
-    auto odd_phase_loads = [&](int g) {                      // phase 2g+1
+    auto stage_loads = [&](int g) {
         if (g + 3 < NG) issue(g + 3);
         if (g + 1 < NG) wait_stage(min(g + 3, NG - 1) - (g + 1));   // stage g+1
     };
     if (!active) {
         // no rows here: this wave's share of the loads and the barriers
-        for (int g = 0; g <= NG; ++g) {
-            pk_phase_barrier();
-            odd_phase_loads(g);
-            pk_phase_barrier();
+        for (int g = 0; g < NG; ++g) {
+            pk_stage_barrier();
+            stage_loads(g);
         }
         return;
     }
@@ -637,7 +623,7 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
             A02 = expand_f16(wr0.z, M, Y); A12 = expand_f16(wr1.z, M, Y);
             step(false, A03, A13, yh0, yl0, yh1, yl1);
             A03 = expand_f16(wr0.w, M, Y); A13 = expand_f16(wr1.w, M, Y);
-            // the expansion stays in this phase (the compiler may not sink it
+            // the expansion stays in this stage (the compiler may not sink it
             // to the next use), interleaved with the MFMAs above
             asm volatile("" : "+v"(A00), "+v"(A01), "+v"(A02), "+v"(A03), "+v"(A10), "+v"(A11), "+v"(A12),
                          "+v"(A13));
@@ -654,52 +640,18 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
                 }
             }
         };
-        // phases 0, 1; then per stage g = 1 .. NG-1 the phases 2g, 2g+1; then
-        // phases 2 NG, 2 NG + 1 (the last fold)
-        if (grp == 0) {
-            read_w(0);
-            expand();                                        // phase 0
-            pk_phase_barrier();
-            odd_phase_loads(0);                              // phase 1
-            read_w(min(1, NG - 1));
-            read_s(0);
-            mfma(0);                                         // (expands stage 1 on the way)
-            pk_phase_barrier();
-            for (int g = 1; g < NG; ++g) {
-                fold();                                      // phase 2g: fold g-1
-                pk_phase_barrier();
-                odd_phase_loads(g);                          // phase 2g+1: MFMA of g, expand g+1
-                read_w(min(g + 1, NG - 1));
-                read_s(g);
-                mfma(g);
-                pk_phase_barrier();
-            }
-            fold();                                          // phase 2 NG
-            pk_phase_barrier();
-            odd_phase_loads(NG);                             // phase 2 NG + 1
-            pk_phase_barrier();
-        } else {
-            read_w(0);                                       // phase 0
-            pk_phase_barrier();
-            odd_phase_loads(0);                              // phase 1
-            expand();
-            pk_phase_barrier();
-            for (int g = 1; g < NG; ++g) {
-                read_w(g);                                   // phase 2g: MFMA of g-1, expand g
-                read_s(g - 1);
-                mfma(g - 1);
-                pk_phase_barrier();
-                odd_phase_loads(g);                          // phase 2g+1: fold g-1
-                fold();
-                pk_phase_barrier();
-            }
-            read_s(NG - 1);                                  // phase 2 NG
-            mfma(NG - 1);
-            pk_phase_barrier();
-            odd_phase_loads(NG);                             // phase 2 NG + 1
-            fold();
-            pk_phase_barrier();
+        // per stage g: fold g-1 | barrier | loads, MFMA of g (expanding g+1)
+        read_w(0);
+        expand();
+        for (int g = 0; g < NG; ++g) {
+            if (g >= 1) fold();
+            pk_stage_barrier();
+            stage_loads(g);
+            read_w(min(g + 1, NG - 1));
+            read_s(g);
+            mfma(g);
         }
+        fold();
     };
     if (two) stages(std::true_type{});
     else stages(std::false_type{});
