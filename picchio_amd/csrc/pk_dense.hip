@@ -1,6 +1,7 @@
 // pk_dense.hip — fp32 / int8 GEMV, RMSNorm, router top-k, combine, and the
 // on-device synthetic weight generator.
 #include "pk_internal.h"
+#include <algorithm>
 #include "pk_dev.h"
 #include "pk_i4_device.h"
 #include "pk_synth.h"
@@ -130,117 +131,173 @@ __global__ __launch_bounds__(256) void k_gemv_f32_rows(float *__restrict__ y, co
 
 // ───────────────── skinny fp32 GEMM on the matrix cores ─────────────────
 // Y[s][o] = (residual ? Y[s][o] : 0) + (X[s] . W[o] + bias[o]) for s < S <= 32.
-// A workgroup of 8 waves owns 16 output rows; wave w takes the w-th eighth
-// of the K range. Per 32 columns a lane loads two float4 of its W row
-// (o = o0 + lane % 16, columns k0 + 8 (lane / 16) .. +7: the four lane groups
-// read 128 contiguous bytes of each row) and the same columns of its two X
-// rows (s = lane % 16 and 16 + lane % 16), then issues 16
-// v_mfma_f32_16x16x4_f32 (8 steps x 2 halves of the inputs); step i takes
-// element i of every lane's 8 columns, so the four k slots of one MFMA are
-// columns k0 + i, k0 + 8 + i, k0 + 16 + i, k0 + 24 + i. W runs three steps
-// ahead in a register ring, X (L2-resident) one step ahead. The eight
-// partial tiles meet in LDS and are added in wave order. fp32 products and
-// sums throughout (not the reference's 8-lane order: within 1e-6 relative,
+// A workgroup of 4 waves owns 64 output rows (16 per wave) over one K range.
+// The 32 input rows' columns of the range pass through LDS once per
+// workgroup (SK_ST steps of 32 columns per stage, double-buffered, staged a
+// stage ahead by all threads), so that in L2 traffic the input rows cost
+// half the weight bytes rather than twice (one read per 16 rows). Per 32
+// columns a lane loads two float4 of its W row (o = o0 + 16 wave + lane % 16,
+// columns k0 + 8 (lane / 16) .. +7: the four lane groups read 128 contiguous
+// bytes of each row; W runs four steps ahead in a register ring), reads the
+// same columns of its two input rows (s = lane % 16 and 16 + lane % 16) from
+// LDS, then issues 16 v_mfma_f32_16x16x4_f32 (8 steps x 2 halves of the
+// inputs); step i takes element i of every lane's 8 columns. Few output rows
+// split K over grid.y workgroups: their partial tiles go to a workspace that
+// k_gemm_splits adds in split order (deterministic). fp32 products and sums
+// throughout (not the reference's 8-lane order: within 1e-6 relative,
 // checked in tests).
 typedef float pk_f32x4v __attribute__((ext_vector_type(4)));
-constexpr int MF_WAVES = 8;
+constexpr int SK_WAVES = 4, SK_ROWS = 16 * SK_WAVES;
+constexpr int SK_ST = 4;                  // 32-column steps per LDS stage
+constexpr int SK_PAD = 36;                // floats per LDS input row (32 + 4: conflict-free 16-byte reads)
 
-__global__ __launch_bounds__(64 * MF_WAVES) void k_gemm_mfma32(float *__restrict__ Y, const float *__restrict__ X,
+__global__ __launch_bounds__(64 * SK_WAVES) void k_gemm_mfma32(float *__restrict__ Y, const float *__restrict__ X,
                                                                const float *__restrict__ W,
                                                                const float *__restrict__ bias, int S, int I,
-                                                               int O, int residual) {
-    __shared__ __attribute__((aligned(16))) float red[MF_WAVES][2][4][64];   // [wave][half][v][lane]
+                                                               int O, int residual, int kchunk,
+                                                               float *__restrict__ ws) {
+    __shared__ __attribute__((aligned(16))) float xs[2][SK_ST][32][SK_PAD];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int o0 = blockIdx.x * 16;
+    const int o0 = blockIdx.x * SK_ROWS + 16 * wave;
     const int r16 = lane & 15, kq = lane >> 4;
     const float *wrow = W + (int64_t)min(o0 + r16, O - 1) * I;
-    const float *x0 = X + (int64_t)min(r16, S - 1) * I;
-    const float *x1 = X + (int64_t)min(16 + r16, S - 1) * I;
-    const int slice = ((I + 32 * MF_WAVES - 1) / (32 * MF_WAVES)) * 32;   // columns per wave
-    const int kb = min(I, wave * slice), ke = min(I, kb + slice);
-
+    const int kb = blockIdx.y * kchunk, ke = min(I, kb + kchunk);
+    const int nstage = (ke - kb + 32 * SK_ST - 1) / (32 * SK_ST);
+    // stage loads: thread t carries float4 e = t + 256 u (u < 4) of the
+    // stage's 32 rows x 128 columns: row e / 32, column 4 (e % 32)
+    float4 xr[4];
+    auto load_x = [&](int t) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = threadIdx.x + 64 * SK_WAVES * u, sr = e >> 5, c = kb + 128 * t + 4 * (e & 31);
+            xr[u] = c < ke ? *reinterpret_cast<const float4 *>(X + (int64_t)min(sr, S - 1) * I + c)
+                           : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = threadIdx.x + 64 * SK_WAVES * u, sr = e >> 5, c4 = e & 31;
+            *reinterpret_cast<float4 *>(&xs[buf][c4 >> 3][sr][4 * (c4 & 7)]) = xr[u];
+        }
+    };
+    // this lane's 8 columns of W at K0 (zero past ke)
+    auto load_w = [&](int k0, float4 (&wv)[2]) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int k = k0 + 8 * kq + 4 * j;
+            if (k < ke) {
+                const pk_f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4v *>(wrow + k));
+                wv[j] = make_float4(t.x, t.y, t.z, t.w);
+            } else {
+                wv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+    };
     pk_f32x4v acc0 = {0.f, 0.f, 0.f, 0.f}, acc1 = {0.f, 0.f, 0.f, 0.f};
-    float4 w0[2], w1[2], w2[2], a[2], b[2], an[2], bn[2];
-    // this lane's 8 columns of the step at K0 (zero past ke)
-#define PK_MF_W(K0, WV)                                                                           \
-    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                              \
-        const int k = (K0) + 8 * kq + 4 * j;                                                      \
-        if (k < ke) {                                                                             \
-            const pk_f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4v *>(wrow + k)); \
-            WV[j] = make_float4(t.x, t.y, t.z, t.w);                                              \
-        } else {                                                                                  \
-            WV[j] = make_float4(0.f, 0.f, 0.f, 0.f);                                              \
-        }                                                                                         \
-    }
-#define PK_MF_X(K0, AV, BV)                                                                       \
-    _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                              \
-        const int k = (K0) + 8 * kq + 4 * j;                                                      \
-        const bool ok = k < ke;                                                                   \
-        AV[j] = ok ? *reinterpret_cast<const float4 *>(x0 + k) : make_float4(0.f, 0.f, 0.f, 0.f); \
-        BV[j] = ok ? *reinterpret_cast<const float4 *>(x1 + k) : make_float4(0.f, 0.f, 0.f, 0.f); \
-    }
-#define PK_MF_STEP(K0, WV)                                                                        \
-    if ((K0) < ke) {                                                                              \
-        PK_MF_X((K0) + 32, an, bn)                                                                \
-        _Pragma("unroll") for (int j = 0; j < 2; ++j) {                                          \
-            const float wv_[4] = {WV[j].x, WV[j].y, WV[j].z, WV[j].w};                            \
-            const float av_[4] = {a[j].x, a[j].y, a[j].z, a[j].w};                                \
-            const float bv_[4] = {b[j].x, b[j].y, b[j].z, b[j].w};                                \
-            _Pragma("unroll") for (int i = 0; i < 4; ++i) {                                      \
-                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av_[i], wv_[i], acc0, 0, 0, 0);      \
-                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv_[i], wv_[i], acc1, 0, 0, 0);      \
-            }                                                                                     \
-        }                                                                                         \
-        PK_MF_W((K0) + 96, WV)                                                                    \
-        _Pragma("unroll") for (int j = 0; j < 2; ++j) { a[j] = an[j]; b[j] = bn[j]; }            \
-    }
-    PK_MF_W(kb, w0)
-    PK_MF_W(kb + 32, w1)
-    PK_MF_W(kb + 64, w2)
-    PK_MF_X(kb, a, b)
-    for (int k0 = kb; k0 < ke; k0 += 96) {
-        PK_MF_STEP(k0, w0)
-        PK_MF_STEP(k0 + 32, w1)
-        PK_MF_STEP(k0 + 64, w2)
-    }
-#undef PK_MF_STEP
-#undef PK_MF_X
-#undef PK_MF_W
-    // D layout of a 16x16 MFMA: lane l, element v -> input 4 (l / 16) + v, row l % 16
-#pragma unroll
-    for (int v = 0; v < 4; ++v) {
-        red[wave][0][v][lane] = acc0[v];
-        red[wave][1][v][lane] = acc1[v];
-    }
+    float4 w0[2], w1[2], w2[2], w3[2];
+    load_w(kb, w0);
+    load_w(kb + 32, w1);
+    load_w(kb + 64, w2);
+    load_w(kb + 96, w3);
+    load_x(0);
+    store_x(0);
     __syncthreads();
-    {
-        const int idx = threadIdx.x;                    // (half, v, lane)
-        const int h = idx >> 8, v = (idx >> 6) & 3, l = idx & 63;
-        const int srow = 16 * h + 4 * (l >> 4) + v, orow = o0 + (l & 15);
-        if (srow < S && orow < O) {
-            float sum = red[0][h][v][l];
+    auto step = [&](int buf, int i, float4 (&wv)[2]) {
+        const float *xa = &xs[buf][i][r16][8 * kq], *xb = &xs[buf][i][16 + r16][8 * kq];
 #pragma unroll
-            for (int q = 1; q < MF_WAVES; ++q) sum = sum + red[q][h][v][l];
-            if (bias) sum = sum + bias[orow];
+        for (int j = 0; j < 2; ++j) {
+            const float4 a = *reinterpret_cast<const float4 *>(xa + 4 * j);
+            const float4 b = *reinterpret_cast<const float4 *>(xb + 4 * j);
+            const float wv_[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+            const float av_[4] = {a.x, a.y, a.z, a.w};
+            const float bv_[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc0 = __builtin_amdgcn_mfma_f32_16x16x4f32(av_[e], wv_[e], acc0, 0, 0, 0);
+                acc1 = __builtin_amdgcn_mfma_f32_16x16x4f32(bv_[e], wv_[e], acc1, 0, 0, 0);
+            }
+        }
+    };
+    for (int t = 0; t < nstage; ++t) {
+        const int buf = t & 1, k0 = kb + 128 * t;
+        if (t + 1 < nstage) load_x(t + 1);
+        // past ke the W ring holds zeros and the staged columns are zero
+        step(buf, 0, w0);
+        load_w(k0 + 128, w0);
+        step(buf, 1, w1);
+        load_w(k0 + 160, w1);
+        step(buf, 2, w2);
+        load_w(k0 + 192, w2);
+        step(buf, 3, w3);
+        load_w(k0 + 224, w3);
+        if (t + 1 < nstage) store_x(buf ^ 1);
+        __syncthreads();
+    }
+    // D layout of a 16x16 MFMA: lane l, element v -> input 4 (l / 16) + v, row l % 16
+    const int orow = o0 + r16;
+    if (orow >= O) return;
+    const bool split = gridDim.y > 1;
+    const float bv = !split && bias ? bias[orow] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+        const int srow = (v < 4 ? 0 : 16) + 4 * kq + (v & 3);
+        if (srow >= S) continue;
+        const float sum = v < 4 ? acc0[v] : acc1[v - 4];
+        if (split) {
+            ws[((int64_t)blockIdx.y * 32 + srow) * O + orow] = sum;
+        } else {
             float *yp = Y + (int64_t)srow * O + orow;
-            *yp = residual ? *yp + sum : sum;
+            const float val = bias ? sum + bv : sum;
+            *yp = residual ? *yp + val : val;
         }
     }
 }
 
+// The split-K partial tiles of k_gemm_mfma32 added in split order, + bias,
+// (+ Y when residual).
+__global__ __launch_bounds__(256) void k_gemm_splits(float *__restrict__ Y, const float *__restrict__ ws,
+                                                     const float *__restrict__ bias, int S, int O, int splits,
+                                                     int residual) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (int64_t)S * O) return;
+    const int srow = (int)(i / O), orow = (int)(i - (int64_t)srow * O);
+    float sum = ws[(int64_t)srow * O + orow];
+    for (int k = 1; k < splits; ++k) sum = sum + ws[((int64_t)k * 32 + srow) * O + orow];
+    if (bias) sum = sum + bias[orow];
+    Y[i] = residual ? Y[i] + sum : sum;
+}
+
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
-                          int residual, hipStream_t st) {
+                          int residual, hipStream_t st, float *ws, int64_t ws_floats) {
     PK_CHECK(S > 0 && S <= 32 && I > 0 && O > 0, PK_ERR_ARG, "skinny gemm: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0, PK_ERR_UNSUPPORTED,
              "skinny gemm: needs 16-byte aligned rows (I=%d)", I);
-    hipLaunchKernelGGL(k_gemm_mfma32, dim3((O + 15) / 16), dim3(64 * MF_WAVES), 0, st, y, x, W, bias, S, I, O,
-                       residual);
+    const int rb = (O + SK_ROWS - 1) / SK_ROWS;
+    // split K when the row blocks alone leave CUs idle: ~512 workgroups,
+    // at least two LDS stages (256 columns) each, as the workspace allows
+    int splits = 1, kchunk = (I + 127) / 128 * 128;
+    if (ws && rb < 512) {
+        const int want = std::min((512 + rb - 1) / rb, std::max(1, I / 256));
+        const int cap = (int)std::min<int64_t>(want, ws_floats / ((int64_t)32 * O));
+        if (cap > 1) {
+            kchunk = ((I + cap - 1) / cap + 127) / 128 * 128;
+            splits = (I + kchunk - 1) / kchunk;
+        }
+    }
+    hipLaunchKernelGGL(k_gemm_mfma32, dim3(rb, splits), dim3(64 * SK_WAVES), 0, st, y, x, W, bias, S, I, O,
+                       residual, kchunk, ws);
     PK_HIP(hipGetLastError());
+    if (splits > 1) {
+        hipLaunchKernelGGL(k_gemm_splits, dim3((unsigned)(((int64_t)S * O + 255) / 256)), dim3(256), 0, st, y, ws,
+                           bias, S, O, splits, residual);
+        PK_HIP(hipGetLastError());
+    }
     return PK_OK;
 }
 
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
-                       int S, int I, int O, hipStream_t st) {
+                       int S, int I, int O, hipStream_t st, float *ws, int64_t ws_floats) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv f32: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0,
              PK_ERR_UNSUPPORTED, "gemv f32: needs 16-byte aligned rows (I=%d)", I);
@@ -248,7 +305,7 @@ int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bi
         // several inputs: one weight read per block of up to 32 inputs
         for (int s0 = 0; s0 < S; s0 += 32)
             PK_TRY(pk_launch_gemm_skinny(y + (int64_t)s0 * O, x + (int64_t)s0 * I, W, bias,
-                                         S - s0 < 32 ? S - s0 : 32, I, O, 0, st));
+                                         S - s0 < 32 ? S - s0 : 32, I, O, 0, st, ws, ws_floats));
         return PK_OK;
     }
     if (O <= 2048) {

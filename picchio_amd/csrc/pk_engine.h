@@ -124,6 +124,8 @@ struct pk_engine {
     // batched MoE scratch for up to batch_cap tokens (pk_prefill.hip)
     int64_t batch_cap = 0;
     float *b_logits = nullptr, *b_w = nullptr, *b_act = nullptr, *b_eo = nullptr;
+    // split-K workspace of the skinny fp32 GEMM over several rows (PK_SKINNY_WS floats)
+    float *skinny_ws = nullptr;
     int32_t *b_sel = nullptr, *b_perm = nullptr;
     int32_t *b_xq = nullptr, *b_actq = nullptr;   // integer-dot records (rows, pairs' SwiGLU outputs)
     int32_t *b_pairs = nullptr, *b_tiles = nullptr;  // pairs grouped by expert (tiles of 4)
@@ -209,6 +211,7 @@ int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int3
                           int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
                           int tile_pairs = 0);
 int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
+constexpr int64_t PK_SKINNY_WS = (int64_t)2 << 20;   // floats: 12 K splits x 32 rows x 5120 outputs
 // half-precision pair arithmetic (pk_mfma.hip): activation planes, grouped GEMM
 // over tiles of PK_F16_TILE pairs
 constexpr int PK_F16_TILE = 64;

@@ -149,7 +149,7 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
-                    e->moe_act_t, e->moe_eo_t, e->att_t};
+                    e->moe_act_t, e->moe_eo_t, e->att_t, e->skinny_ws};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {

@@ -204,11 +204,13 @@ int pk_launch_i4_repack(const uint8_t *q4, const float *s, int O, int I,
 int pk_launch_quantize_i4(const float *w, int O, int I, int gs, uint8_t *packed,
                           float *scales, hipStream_t st);
 
+// ws / ws_floats (optional): workspace that lets the skinny GEMM split K
+// (partial tiles [splits][32][O]); without it every row block takes all of K
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
-                       int S, int I, int O, hipStream_t st);
+                       int S, int I, int O, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0);
 // Y[s][o] = (residual ? Y[s][o] : 0) + X[s].W[o] + bias[o] for up to 32 inputs, one read of W.
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
-                          int residual, hipStream_t st);
+                          int residual, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0);
 int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
                       int S, int I, int O, hipStream_t st);
 int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, const float *s,

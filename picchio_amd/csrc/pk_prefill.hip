@@ -111,6 +111,7 @@ static int batch_reserve(pk_engine *e, int T) {
     // pairs grouped by expert for the tiled integer-dot launches (tiles of 4)
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_pairs, TK * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->b_tiles, (3 * (TK / 4 + 1 + c->n_experts) + 1) * 4));
+    if (!e->skinny_ws) PK_TRY(pk_dev_alloc(e, (void **)&e->skinny_ws, PK_SKINNY_WS * 4));
     e->batch_cap = T;
     return PK_OK;
 }
@@ -650,7 +651,8 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
         if (c->lm_head_fmt == PK_FMT_INT8)
             PK_TRY(pk_launch_gemv_q8(e->bd_logits, e->p_XN, e->lm_q8, e->lm_s, n_seq, D, V, e->stream));
         else
-            PK_TRY(pk_launch_gemv_f32(e->bd_logits, e->p_XN, e->lm_f32, nullptr, n_seq, D, V, e->stream));
+            PK_TRY(pk_launch_gemv_f32(e->bd_logits, e->p_XN, e->lm_f32, nullptr, n_seq, D, V, e->stream,
+                                      e->skinny_ws, e->skinny_ws ? PK_SKINNY_WS : 0));
         hipLaunchKernelGGL(k_argmax_rows, dim3(n_seq), dim3(256), 0, e->stream, e->bd_logits, V,
                            e->bd_toks + (int64_t)(step + 1) * n_seq);
         PK_HIP(hipGetLastError());
