@@ -341,7 +341,9 @@ __device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_bas
         for (int jj = 0; jj < ATT_GH; ++jj) sc[jj] = dot[jj] * scale;
     }
     // V rows: thread = (column group c4 of hd/4, position group g of PG) of
-    // its half, positions g * PER + j, j < PER (PER = hd / 4 <= KD4)
+    // its half, positions g * PER + j, j < PER (PER = hd / 4 <= KD4). (Issued
+    // with the K rows they cost registers: 3 instead of 4 blocks per SIMD,
+    // slower at batch 1 and 32.)
     const int PG = ATT_CHUNK / D4, PER = ATT_CHUNK / PG;
     const int c4 = tt % D4, g = tt / D4;
     const float4 *v4 = reinterpret_cast<const float4 *>(Vl + (int64_t)t0 * kv_dim + kvh * hd) + c4;
@@ -959,7 +961,11 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
         PK_HIP(hipGetLastError());
         return pk_prof_end(e, ps);
     }
-    hipLaunchKernelGGL(kern, dim3(H / gs, chunks, n), dim3(gs > 1 ? ATT_THREADS : ATT_CHUNK), att_lds,
+    // one 128-thread half per block while a thread's registers hold the
+    // block's heads (both halves of a 256-thread block would read the same
+    // K and V rows: batch-32 full-context layers 192 -> 167 us)
+    const int thr = gs <= ATT_GH ? ATT_CHUNK : ATT_THREADS;
+    hipLaunchKernelGGL(kern, dim3(H / gs, chunks, n), dim3(thr), att_lds,
                        e->stream, st, pos_base, pos_step,
                        qkv, (int64_t)qkv_dim, Kl, Vl, kv_row, H, KVH, hd, c->ctx_len, sliding, c->sliding_window,
                        part, max_chunks, d.sinks, att, e->counters + PK_CTR_ATTN, gs);
