@@ -177,9 +177,21 @@ __device__ __forceinline__ int row_pos(const pk_dstate *st, int pos_base, int st
 // with the host-built cos/sin table (attn_factor folded in), then kv_store
 // (picchio.c:492-498): K/V rows of this layer at that position. grid.y = row;
 // row r's cache starts kv_row * r floats after Kl / Vl.
+// With ws (the split partial tiles [splits][32][qkv_stride] of a skinny
+// GEMM over at most 32 rows), each value is first k_gemm_splits' sum of the
+// row's partials + bias, written to qkv.
+__device__ __forceinline__ float splits_sum(const float *ws, int splits, int r, int O, int col, const float *bias) {
+    float sum = ws[(int64_t)r * O + col];
+    for (int k = 1; k < splits; ++k) sum = sum + ws[((int64_t)k * 32 + r) * O + col];
+    if (bias) sum = sum + bias[col];
+    return sum;
+}
+
 __global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float *qkv, int64_t qkv_stride,
-                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl, int64_t kv_row) {
+                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl, int64_t kv_row,
+                          const float *ws = nullptr, int splits = 1, const float *bias = nullptr) {
     const int pos = row_pos(st, pos_base, pos_step, blockIdx.y);
+    const int r = blockIdx.y;
     qkv += (int64_t)blockIdx.y * qkv_stride;
     Kl += (int64_t)blockIdx.y * kv_row;
     Vl += (int64_t)blockIdx.y * kv_row;
@@ -192,7 +204,8 @@ __global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float
         float *v = qkv + head * hd;                     // q heads then k heads
         const float cs = rope[((int64_t)pos * half + j) * 2 + 0];
         const float sn = rope[((int64_t)pos * half + j) * 2 + 1];
-        const float a = v[j], b = v[j + half];
+        const float a = ws ? splits_sum(ws, splits, r, (int)qkv_stride, head * hd + j, bias) : v[j];
+        const float b = ws ? splits_sum(ws, splits, r, (int)qkv_stride, head * hd + j + half, bias) : v[j + half];
         const float r0 = __builtin_fmaf(a, cs, -(b * sn));   // a*cs - b*sn (contracted)
         const float r1 = __builtin_fmaf(a, sn, b * cs);      // a*sn + b*cs (contracted)
         v[j] = r0;
@@ -204,7 +217,14 @@ __global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float
         }
     } else if (i < n_pairs + kv_dim) {
         const int c = i - n_pairs;
-        Vl[(int64_t)pos * kv_dim + c] = qkv[(H + KVH) * hd + c];
+        float val;
+        if (ws) {
+            val = splits_sum(ws, splits, r, (int)qkv_stride, (H + KVH) * hd + c, bias);
+            qkv[(H + KVH) * hd + c] = val;
+        } else {
+            val = qkv[(H + KVH) * hd + c];
+        }
+        Vl[(int64_t)pos * kv_dim + c] = val;
     }
 }
 
@@ -968,14 +988,21 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                            e->counters + PK_CTR_ATT_EPOCH);
         PK_HIP(hipGetLastError());
     } else {
+        // 4..32 rows with the workspace: the split sums + bias go into the RoPE launch
+        int splits = 1;
+        const bool split_rope = !exact && e->skinny_ws && n >= 4 && n <= 32 && qkv_dim >= 256;
         if (exact)
             PK_TRY(pk_launch_gemm_chain8(xn, D, d.wqkv, d.bqkv, qkv, qkv_dim, n, D, qkv_dim, false, e->stream));
+        else if (split_rope)
+            PK_TRY(pk_launch_gemm_skinny(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, 0, e->stream, e->skinny_ws,
+                                         PK_SKINNY_WS, &splits));
         else
             PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream, e->skinny_ws,
                                       e->skinny_ws ? PK_SKINNY_WS : 0));
         const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
         hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base,
-                           pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row);
+                           pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row,
+                           splits > 1 ? e->skinny_ws : nullptr, splits, d.bqkv);
         PK_HIP(hipGetLastError());
     }
     const int sliding = c->layer_type[l] == 0;

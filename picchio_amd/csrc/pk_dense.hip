@@ -269,7 +269,7 @@ __global__ __launch_bounds__(256) void k_gemm_splits(float *__restrict__ Y, cons
 }
 
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
-                          int residual, hipStream_t st, float *ws, int64_t ws_floats) {
+                          int residual, hipStream_t st, float *ws, int64_t ws_floats, int *splits_out) {
     PK_CHECK(S > 0 && S <= 32 && I > 0 && O > 0, PK_ERR_ARG, "skinny gemm: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0, PK_ERR_UNSUPPORTED,
              "skinny gemm: needs 16-byte aligned rows (I=%d)", I);
@@ -288,7 +288,8 @@ int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float 
     hipLaunchKernelGGL(k_gemm_mfma32, dim3(rb, splits), dim3(64 * SK_WAVES), 0, st, y, x, W, bias, S, I, O,
                        residual, kchunk, ws);
     PK_HIP(hipGetLastError());
-    if (splits > 1) {
+    if (splits_out) *splits_out = splits;
+    if (splits > 1 && !splits_out) {
         hipLaunchKernelGGL(k_gemm_splits, dim3((unsigned)(((int64_t)S * O + 255) / 256)), dim3(256), 0, st, y, ws,
                            bias, S, O, splits, residual);
         PK_HIP(hipGetLastError());

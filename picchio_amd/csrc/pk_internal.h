@@ -209,8 +209,12 @@ int pk_launch_quantize_i4(const float *w, int O, int I, int gs, uint8_t *packed,
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
                        int S, int I, int O, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0);
 // Y[s][o] = (residual ? Y[s][o] : 0) + X[s].W[o] + bias[o] for up to 32 inputs, one read of W.
+// splits_out (optional): when K is split, the partial tiles stay in ws
+// ([splits][32][O]) for the caller to add (*splits_out = splits, the sums
+// and bias / residual not applied); 1 when y holds the result.
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
-                          int residual, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0);
+                          int residual, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0,
+                          int *splits_out = nullptr);
 int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
                       int S, int I, int O, hipStream_t st);
 int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, const float *s,
