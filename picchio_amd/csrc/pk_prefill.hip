@@ -506,16 +506,36 @@ extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int po
 namespace {
 
 // Greedy id of each row of logits [rows][V] (first maximum, picchio.c:1555-1560).
-__global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int V, int32_t *out) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+__global__ __launch_bounds__(1024) void k_argmax_rows(const float *logits, int V, int32_t *out) {
+    __shared__ float bv[16];
+    __shared__ int bi[16];
     const float *lg = logits + (int64_t)blockIdx.x * V;
     float v = -INFINITY;
     int i = 0x7fffffff;
-    for (int j = threadIdx.x; j < V; j += 256) {
-        const float x = lg[j];
-        if (x > v) { v = x; i = j; }              // j increases: first maximum within the thread
+    // a thread's indices increase: the first maximum within the thread
+    auto take = [&](float x, int j) {
+        if (x > v) { v = x; i = j; }
+    };
+    // 16-byte loads, eight in flight per thread (rows are 16-byte aligned when V % 4 == 0)
+    const int V4 = (V & 3) == 0 ? V >> 2 : 0;
+    const float4 *l4 = reinterpret_cast<const float4 *>(lg);
+    constexpr int U = 8;
+    for (int j0 = threadIdx.x; j0 < V4; j0 += 1024 * U) {
+        float4 q[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) q[u] = l4[min(j0 + 1024 * u, V4 - 1)];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int j = j0 + 1024 * u;
+            if (j < V4) {
+                take(q[u].x, 4 * j);
+                take(q[u].y, 4 * j + 1);
+                take(q[u].z, 4 * j + 2);
+                take(q[u].w, 4 * j + 3);
+            }
+        }
     }
+    for (int j = 4 * V4 + (int)threadIdx.x; j < V; j += 1024) take(lg[j], j);
 #pragma unroll
     for (int o = 32; o > 0; o >>= 1) {
         const float ov = __shfl_xor(v, o, 64);
@@ -525,7 +545,7 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int V,
     if ((threadIdx.x & 63) == 0) { bv[threadIdx.x >> 6] = v; bi[threadIdx.x >> 6] = i; }
     __syncthreads();
     if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; ++w)
+        for (int w = 1; w < 16; ++w)
             if (bv[w] > v || (bv[w] == v && bi[w] < i)) { v = bv[w]; i = bi[w]; }
         // the reference's scan starts at index 0 and moves on a strictly
         // greater value only: a NaN (or the maximum) at index 0 keeps 0
@@ -653,7 +673,7 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
         else
             PK_TRY(pk_launch_gemv_f32(e->bd_logits, e->p_XN, e->lm_f32, nullptr, n_seq, D, V, e->stream,
                                       e->skinny_ws, e->skinny_ws ? PK_SKINNY_WS : 0));
-        hipLaunchKernelGGL(k_argmax_rows, dim3(n_seq), dim3(256), 0, e->stream, e->bd_logits, V,
+        hipLaunchKernelGGL(k_argmax_rows, dim3(n_seq), dim3(1024), 0, e->stream, e->bd_logits, V,
                            e->bd_toks + (int64_t)(step + 1) * n_seq);
         PK_HIP(hipGetLastError());
         PK_TRY(pk_prof_end(e, ps));
