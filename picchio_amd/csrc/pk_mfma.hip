@@ -86,10 +86,28 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
     const bool staged = P <= GP_LDS;
     for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
     __syncthreads();
-    for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        const int e = sel[i];
-        if (staged) s_sel[i] = e;
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    if (staged && (int)blockDim.x * 16 >= GP_LDS) {
+        // every load in flight at once (a loop would wait for each)
+        int ev[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = threadIdx.x + u * blockDim.x;
+            ev[u] = i < P ? sel[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = threadIdx.x + u * blockDim.x;
+            if (i < P) {
+                s_sel[i] = ev[u];
+                if (ev[u] >= 0 && ev[u] < E) atomicAdd(&cnt[ev[u]], 1);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < P; i += blockDim.x) {
+            const int e = sel[i];
+            if (staged) s_sel[i] = e;
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
     // offsets of the experts' pairs and of their tiles: one wave scans the
@@ -115,14 +133,24 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
             tile_beg[j] = off[e] + b;
             tile_cnt[j] = min(tt, cnt[e] - b);
         }
+    // (eight 64-entry chunks read per round, so that the reads' latency
+    // overlaps; the chunks are placed in order)
     for (int e = wave; e < E; e += nw) {
         int run = off[e];
-        for (int b = 0; b < P; b += 64) {
-            const int i = b + lane;
-            const bool hit = i < P && (staged ? s_sel[i] : sel[i]) == e;
-            const uint64_t m = __ballot(hit);
-            if (hit) pairs[run + __popcll(m & lt)] = i;
-            run += __popcll(m);
+        for (int b = 0; b < P; b += 512) {
+            int v[8];
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const int i = b + 64 * u + lane;
+                v[u] = i < P ? (staged ? s_sel[i] : sel[i]) : -1;
+            }
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+                const bool hit = v[u] == e;
+                const uint64_t m = __ballot(hit);
+                if (hit) pairs[run + __popcll(m & lt)] = b + 64 * u + lane;
+                run += __popcll(m);
+            }
         }
     }
 }
@@ -374,6 +402,56 @@ __device__ __forceinline__ float swiglu_f16path(float gate, float up, float lim,
 
 // One row per workgroup: exponent k of max|x|, the hi and lo planes (columns
 // permuted by f16_pos inside each 8-column chunk).
+// Rows of at most 4096 columns (16-byte aligned): the row is read once, two
+// 8-column chunks per thread held in registers for the max and the split.
+__global__ __launch_bounds__(256) void k_act_f16_reg(const float *__restrict__ x, int64_t x_stride, int cols,
+                                                     uint16_t *__restrict__ xf, int64_t fplane,
+                                                     int32_t *__restrict__ exps) {
+    __shared__ float red[4];
+    const int r = blockIdx.x;
+    const float *xr = x + (int64_t)r * x_stride;
+    const int nch = cols / 8;
+    float4 v[2][2];
+    float m = 0.0f;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = min((int)threadIdx.x + 256 * h, nch - 1);
+        v[h][0] = *reinterpret_cast<const float4 *>(xr + 8 * c);
+        v[h][1] = *reinterpret_cast<const float4 *>(xr + 8 * c + 4);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+        if ((int)threadIdx.x + 256 * h < nch)
+#pragma unroll
+            for (int q = 0; q < 2; ++q)
+                m = fmaxf(fmaxf(fmaxf(m, fabsf(v[h][q].x)), fmaxf(fabsf(v[h][q].y), fabsf(v[h][q].z))),
+                          fabsf(v[h][q].w));
+    m = pk_wave_max_f(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int k = 0;
+    if (m > 0.0f) (void)frexpf(m, &k);
+    if (threadIdx.x == 0) exps[r] = k;
+    _Float16 *hr = reinterpret_cast<_Float16 *>(xf) + (int64_t)r * cols;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int c = (int)threadIdx.x + 256 * h;
+        if (c >= nch) break;
+        const float xs[8] = {v[h][0].x, v[h][0].y, v[h][0].z, v[h][0].w, v[h][1].x, v[h][1].y, v[h][1].z, v[h][1].w};
+        pk_v8h hi, lo;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const float vv = ldexpf(xs[u], 15 - k);
+            const _Float16 vh = (_Float16)vv;
+            hi[f16_pos(u)] = vh;
+            lo[f16_pos(u)] = (_Float16)(vv - (float)vh);
+        }
+        *reinterpret_cast<pk_v8h *>(hr + 8 * c) = hi;
+        *reinterpret_cast<pk_v8h *>(hr + fplane + 8 * c) = lo;
+    }
+}
+
 __global__ __launch_bounds__(256) void k_act_f16(const float *__restrict__ x, int64_t x_stride, int cols,
                                                  uint16_t *__restrict__ xf, int64_t fplane,
                                                  int32_t *__restrict__ exps) {
@@ -702,7 +780,10 @@ int pk_launch_act_f16(const float *x, int64_t x_stride, int rows, int cols, uint
                       int32_t *exps, hipStream_t st) {
     PK_CHECK(rows > 0 && cols > 0 && cols % 8 == 0 && fplane >= (int64_t)rows * cols, PK_ERR_ARG,
              "act f16: bad shape");
-    hipLaunchKernelGGL(k_act_f16, dim3(rows), dim3(256), 0, st, x, x_stride, cols, xf, fplane, exps);
+    if (cols <= 4096 && ((uintptr_t)x & 15) == 0 && (x_stride & 3) == 0)
+        hipLaunchKernelGGL(k_act_f16_reg, dim3(rows), dim3(256), 0, st, x, x_stride, cols, xf, fplane, exps);
+    else
+        hipLaunchKernelGGL(k_act_f16, dim3(rows), dim3(256), 0, st, x, x_stride, cols, xf, fplane, exps);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

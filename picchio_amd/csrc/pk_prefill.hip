@@ -34,14 +34,34 @@ __global__ __launch_bounds__(256) void k_embed_rows(const int32_t *ids, const fl
 // experts in rank order. perm[p][j] = k of the token's j-th expert. One
 // workgroup: first request of each expert by atomic min, rank = number of
 // experts requested earlier, then each token orders its k by rank.
+constexpr int UP_LDS = 16384;           // routing entries staged in LDS (all loads in flight at once)
 __global__ __launch_bounds__(1024) void k_uniq_perm(const int32_t *sel, int n, int K, int E, int32_t *perm) {
     __shared__ int first[128], rank[128];
+    __shared__ int s_sel[UP_LDS];
     const int P = n * K;
+    const bool staged = P <= UP_LDS && (int)blockDim.x * 16 >= UP_LDS;
     for (int e = threadIdx.x; e < E; e += blockDim.x) first[e] = 0x7fffffff;
     __syncthreads();
-    for (int i = threadIdx.x; i < P; i += blockDim.x) {
-        const int e = sel[i];
-        if (e >= 0 && e < E) atomicMin(&first[e], i);
+    if (staged) {
+        int ev[16];
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = threadIdx.x + u * blockDim.x;
+            ev[u] = i < P ? sel[i] : -1;
+        }
+#pragma unroll
+        for (int u = 0; u < 16; ++u) {
+            const int i = threadIdx.x + u * blockDim.x;
+            if (i < P) {
+                s_sel[i] = ev[u];
+                if (ev[u] >= 0 && ev[u] < E) atomicMin(&first[ev[u]], i);
+            }
+        }
+    } else {
+        for (int i = threadIdx.x; i < P; i += blockDim.x) {
+            const int e = sel[i];
+            if (e >= 0 && e < E) atomicMin(&first[e], i);
+        }
     }
     __syncthreads();
     for (int e = threadIdx.x; e < E; e += blockDim.x) {
@@ -51,7 +71,7 @@ __global__ __launch_bounds__(1024) void k_uniq_perm(const int32_t *sel, int n, i
     }
     __syncthreads();
     for (int p = threadIdx.x; p < n; p += blockDim.x) {
-        const int32_t *sp = sel + (int64_t)p * K;
+        const int32_t *sp = staged ? s_sel + p * K : sel + (int64_t)p * K;
         for (int k = 0; k < K; ++k) {
             const int ek = sp[k];
             const int rk = (ek >= 0 && ek < E) ? rank[ek] : 0x7fffffff;
@@ -69,6 +89,30 @@ __global__ __launch_bounds__(1024) void k_uniq_perm(const int32_t *sel, int n, i
 // moe = 0; moe = fma(w_k, eo_k, moe) in rank order (expert_apply's
 // dst += w * eo, picchio.c:1788); out = residual + moe (picchio.c:1910-1914)
 // or moe alone.
+// The same sums four columns per thread (D % 4 == 0, 16-byte aligned rows).
+__global__ __launch_bounds__(256) void k_combine_rows4(float *out, const float *residual, const float *eo,
+                                                       const float *w, const int32_t *perm, int K, int D) {
+    const int p = blockIdx.y;
+    const int i = (blockIdx.x * 256 + threadIdx.x) * 4;
+    if (i >= D) return;
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int j = 0; j < K; ++j) {
+        const int k = perm ? perm[p * K + j] : j;
+        const float wk = w[p * K + k];
+        const float4 e = *reinterpret_cast<const float4 *>(eo + ((int64_t)p * K + k) * D + i);
+        acc.x = __builtin_fmaf(wk, e.x, acc.x);
+        acc.y = __builtin_fmaf(wk, e.y, acc.y);
+        acc.z = __builtin_fmaf(wk, e.z, acc.z);
+        acc.w = __builtin_fmaf(wk, e.w, acc.w);
+    }
+    const int64_t o = (int64_t)p * D + i;
+    if (residual) {
+        const float4 rr = *reinterpret_cast<const float4 *>(residual + o);
+        acc = make_float4(rr.x + acc.x, rr.y + acc.y, rr.z + acc.z, rr.w + acc.w);
+    }
+    *reinterpret_cast<float4 *>(out + o) = acc;
+}
+
 __global__ __launch_bounds__(256) void k_combine_rows(float *out, const float *residual, const float *eo,
                                                       const float *w, const int32_t *perm, int K, int D) {
     const int p = blockIdx.y;
@@ -84,6 +128,20 @@ __global__ __launch_bounds__(256) void k_combine_rows(float *out, const float *r
 }
 
 }  // namespace
+
+// out[t] = (residual ? residual[t] : 0) + the weighted rows of token t's pairs
+static int launch_combine(pk_engine *e, float *out, const float *residual, const float *eo, const float *w,
+                          const int32_t *perm, int K, int D, int T) {
+    const bool v4 = (D & 3) == 0 && (((uintptr_t)out | (uintptr_t)eo | (uintptr_t)residual) & 15) == 0;
+    if (v4)
+        hipLaunchKernelGGL(k_combine_rows4, dim3((D / 4 + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
+                           eo, w, perm, K, D);
+    else
+        hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual, eo,
+                           w, perm, K, D);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
 
 static int batch_reserve(pk_engine *e, int T) {
     if (T <= e->batch_cap) return PK_OK;
@@ -203,10 +261,7 @@ static int moe_rows_on(pk_engine *e, const rows_scratch &sc, int layer, const fl
     else
         PK_TRY(pk_launch_i4_gemv(dn, e->ex.dn, PK_EPI_PLAIN, 0.f, 0.f, nullptr, e->stream));
     PK_TRY(pk_prof_end(e, ps));
-    hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
-                       sc.eo, sc.w, decode_order ? nullptr : sc.perm, K, D);
-    PK_HIP(hipGetLastError());
-    return PK_OK;
+    return launch_combine(e, out, residual, sc.eo, sc.w, decode_order ? nullptr : sc.perm, K, D, T);
 }
 
 static int moe_rows(pk_engine *e, int layer, const float *x, int T, float *out, const float *residual,
@@ -301,10 +356,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
     if (f16) PK_TRY(pk_launch_moe_f16(a, max_tiles, PK_EPI_PLAIN, e->stream));
     else PK_TRY(pk_launch_moe_mfma(a, max_tiles, PK_EPI_PLAIN, e->stream));
     PK_TRY(pk_prof_end(e, ps));
-    hipLaunchKernelGGL(k_combine_rows, dim3((D + 255) / 256, T), dim3(256), 0, e->stream, out, residual,
-                       e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D);
-    PK_HIP(hipGetLastError());
-    return PK_OK;
+    return launch_combine(e, out, residual, e->b_eo, e->b_w, decode_order ? nullptr : e->b_perm, K, D, T);
 }
 
 extern "C" int pk_moe_forward_grouped(pk_engine *e, int layer, const float *x_dev, int T,
