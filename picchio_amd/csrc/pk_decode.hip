@@ -278,7 +278,7 @@ __device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_bas
     const int G = gs;                         // heads of this block
     float *q = att_lds;                       // [G][hd]
     float *p = q + G * hd;                    // [G][128]
-    float *vred = p + G * ATT_CHUNK;          // [G][PG][hd]
+    float *vred = p;                          // [G][PG][hd] over p once the V sums have read it
     __shared__ float red[4][ATT_GH];
     __shared__ float mh[2 * ATT_GH];
     __shared__ float ssum[2 * ATT_GH];
@@ -423,6 +423,7 @@ __device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_bas
             acc[jj].w = __builtin_fmaf(pw, vv[j].w, acc[jj].w);
         }
     }
+    __syncthreads();                          // every read of p is done: vred overwrites it
 #pragma unroll
     for (int jj = 0; jj < ATT_GH; ++jj) {
         if (jj >= jn) break;
@@ -472,7 +473,7 @@ __device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_bas
     };
     constexpr int CB = 16;
     float *cm = p;                            // [G][nc] chunk maxima, then factors e_c
-    float *cs = vred;                         // [G][nc] chunk sums
+    float *cs = p + G * ATT_CHUNK;            // [G][nc] chunk sums (the V partials are stored)
     __shared__ float hS[2 * ATT_GH];
     // Windows of CB < nc <= CO chunks, or more outputs than threads: a thread
     // takes column pairs (i, i + 1) of a head, every chunk's two values in one
@@ -1041,7 +1042,8 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     if (fuse && gs < 2) gs = 2;
     PK_CHECK((int64_t)n * (H / gs) <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d blocks", n,
              H / gs);
-    const size_t att_lds = (size_t)gs * (hd + ATT_CHUNK + ATT_CHUNK * 4) * sizeof(float);
+    // q, then p [gs][128] shared with the V partials [gs][PG][hd] (PG * hd = 512)
+    const size_t att_lds = (size_t)gs * (hd + ATT_CHUNK * 4) * sizeof(float);
     // K / V rows held in registers: 16 float4 up to head_dim 64, else 32
     auto kern = hd <= 64 ? k_attn_part<16> : k_attn_part<32>;
     PK_CHECK(hd % 4 == 0 && hd <= 128, PK_ERR_UNSUPPORTED, "attention: head_dim %d", hd);
