@@ -262,9 +262,100 @@ int pk_launch_attn_rows_exact(int pos_base, int n, const float *qkv, int64_t qkv
     return PK_OK;
 }
 
+// The same sums with 16-byte loads (D % 4 == 0, aligned rows; 4 <= E <= 128):
+// the next 64 columns of the router rows and of the block's input rows load
+// into registers (at most 20 per thread, so that the load counter can wait
+// for them in order) while the current ones are multiplied; in LDS each
+// router row's chunk is contiguous, so a thread reads its 64 weights and
+// its row's 64 inputs as float4, 32 at a time, before the dependent adds.
+constexpr int RQ_P = RS_KC + 4;          // padded LDS row (floats)
+__global__ __launch_bounds__(128) void k_router_seq4(const float *__restrict__ X, const float *__restrict__ R,
+                                                     const float *__restrict__ bias, int S, int D, int E,
+                                                     float *logits) {
+    extern __shared__ float lds_rs[];
+    const int rows = 128 / E;
+    float *wt = lds_rs;                   // [E][RQ_P]
+    float *xt = lds_rs + E * RQ_P;        // [rows][RQ_P]
+    const int tid = threadIdx.x;
+    const int e = tid % E, rr = tid / E;
+    const int s = blockIdx.x * rows + rr;
+    const bool live = rr < rows && s < S;
+    float acc = live ? bias[e] : 0.0f;
+    constexpr int WN = 16, XN = 4;        // float4 per thread: E * 16 / 128 and rows * 16 / 128
+    const int nw4 = E * (RS_KC / 4), nx4 = rows * (RS_KC / 4);
+    float4 wv[WN], xv[XN];
+    auto load = [&](int c0) {
+        const int nc4 = min(RS_KC, D - c0) / 4;
+#pragma unroll
+        for (int u = 0; u < WN; ++u) {
+            const int q = min(tid + 128 * u, nw4 - 1), ee = q / (RS_KC / 4), c4 = q - ee * (RS_KC / 4);
+            const float4 v = *reinterpret_cast<const float4 *>(R + (int64_t)ee * D + c0 + 4 * min(c4, nc4 - 1));
+            wv[u] = c4 < nc4 ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < XN; ++u) {
+            const int q = min(tid + 128 * u, nx4 - 1), r2 = q / (RS_KC / 4), c4 = q - r2 * (RS_KC / 4);
+            const int s2 = min(blockIdx.x * rows + r2, S - 1);
+            const float4 v = *reinterpret_cast<const float4 *>(X + (int64_t)s2 * D + c0 + 4 * min(c4, nc4 - 1));
+            xv[u] = c4 < nc4 ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    load(0);
+    // (the bias is waited for here: inside the loop the compiler would wait
+    // for every outstanding load before the first add)
+    asm volatile("" ::"v"(acc));
+    for (int c0 = 0; c0 < D; c0 += RS_KC) {
+        const int nc = min(RS_KC, D - c0);
+        __syncthreads();                  // the previous chunk's reads are done
+#pragma unroll
+        for (int u = 0; u < WN; ++u) {
+            const int q = tid + 128 * u, ee = q / (RS_KC / 4), c4 = q - ee * (RS_KC / 4);
+            if (q < nw4) *reinterpret_cast<float4 *>(wt + ee * RQ_P + 4 * c4) = wv[u];
+        }
+#pragma unroll
+        for (int u = 0; u < XN; ++u) {
+            const int q = tid + 128 * u, r2 = q / (RS_KC / 4), c4 = q - r2 * (RS_KC / 4);
+            if (q < nx4) *reinterpret_cast<float4 *>(xt + r2 * RQ_P + 4 * c4) = xv[u];
+        }
+        __syncthreads();
+        if (c0 + RS_KC < D) load(c0 + RS_KC);
+        if (live) {
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                float4 xa[8], wa[8];
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    xa[j] = *reinterpret_cast<const float4 *>(xt + rr * RQ_P + 32 * h + 4 * j);
+                    wa[j] = *reinterpret_cast<const float4 *>(wt + e * RQ_P + 32 * h + 4 * j);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const float xs[4] = {xa[j].x, xa[j].y, xa[j].z, xa[j].w};
+                    const float ws[4] = {wa[j].x, wa[j].y, wa[j].z, wa[j].w};
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        if (32 * h + 4 * j + k < nc) {
+                            const float p = xs[k] * ws[k];
+                            acc = acc + p;
+                        }
+                }
+            }
+        }
+    }
+    if (live) logits[(int64_t)s * E + e] = acc;
+}
+
 int pk_launch_router_seq(const float *X, const float *R, const float *bias, int S, int D, int E, float *logits,
                          hipStream_t st) {
     PK_CHECK(S > 0 && D > 0 && E > 0 && E <= 128, PK_ERR_ARG, "router: bad shape");
+    if (E >= 4 && (D & 3) == 0 && (((uintptr_t)X | (uintptr_t)R) & 15) == 0) {
+        const int rows = 128 / E;
+        const size_t lds = ((size_t)E + rows) * RQ_P * 4;
+        hipLaunchKernelGGL(k_router_seq4, dim3((S + rows - 1) / rows), dim3(128), lds, st, X, R, bias, S, D, E,
+                           logits);
+        PK_HIP(hipGetLastError());
+        return PK_OK;
+    }
     const int rows = 128 / E;
     const size_t lds = ((size_t)RS_KC * E + (size_t)rows * RS_KC) * 4;
     hipLaunchKernelGGL(k_router_seq, dim3((S + rows - 1) / rows), dim3(128), lds, st, X, R, bias, S, D, E, logits);
