@@ -38,7 +38,11 @@ constexpr int CH_ROWS = 64, CH_OUTS = 32;
 
 // TW = int8_t: matmul_q8 (quant.h:152-186), the same chains over the weights
 // converted to float, the tail as contracted FMAs, the sum times the row scale.
-template <typename TW>
+// VEC (fp32 weights, 16-byte aligned rows, ldx and I multiples of 4): each
+// chunk's 64 x 64 inputs and 32 x 64 weights load as six float4 per thread,
+// the next chunk's while the current one is multiplied (the scalar loops
+// wait for every load on its own).
+template <typename TW, bool VEC = false>
 __global__ __launch_bounds__(256) void k_gemm_chain8(const float *__restrict__ X, int64_t ldx,
                                                      const TW *__restrict__ W, const float *__restrict__ rscale,
                                                      const float *__restrict__ bias, float *out, int64_t ldo,
@@ -54,21 +58,63 @@ __global__ __launch_bounds__(256) void k_gemm_chain8(const float *__restrict__ X
     for (int m = 0; m < 8; ++m)
 #pragma unroll
         for (int i = 0; i < 8; ++i) acc[m][i] = 0.0f;
+    float4 xv4[4], wv4[2];
+    // float4 e = tid + 256 u of the chunk: row e / 16, columns 4 (e % 16) .. +3
+    auto load = [&](int c0) {
+        const int nc = min(CH_KC, I8 - c0);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int e = tid + 256 * u, r = e >> 4, c = 4 * (e & 15), sr = min(s0 + r, S - 1);
+            const float4 v = *reinterpret_cast<const float4 *>(X + (int64_t)sr * ldx + c0 + min(c, nc - 4));
+            xv4[u] = c < nc && s0 + r < S ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const int e = tid + 256 * u, r = e >> 4, c = 4 * (e & 15), orow = min(o0 + r, O - 1);
+            const float4 v =
+                *reinterpret_cast<const float4 *>(reinterpret_cast<const float *>(W) + (int64_t)orow * I + c0 +
+                                                  min(c, nc - 4));
+            wv4[u] = c < nc && o0 + r < O ? v : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    if constexpr (VEC)
+        if (I8 > 0) load(0);
     for (int c0 = 0; c0 < I8; c0 += CH_KC) {
         const int nc = min(CH_KC, I8 - c0);    // a multiple of 8
         __syncthreads();
-        // X chunk: 64 rows x nc columns (zeros past S), 16 per thread
-        for (int e = tid; e < CH_ROWS * CH_KC; e += 256) {
-            const int r = e / CH_KC, c = e - r * CH_KC;
-            const int s = s0 + r;
-            xs[c >> 3][c & 7][r] = (c < nc && s < S) ? X[(int64_t)s * ldx + c0 + c] : 0.0f;
-        }
-        for (int e = tid; e < CH_OUTS * CH_KC; e += 256) {
-            const int r = e / CH_KC, c = e - r * CH_KC;
-            const int o = o0 + r;
-            ws[c >> 3][c & 7][r] = (c < nc && o < O) ? (float)W[(int64_t)o * I + c0 + c] : 0.0f;
+        if constexpr (VEC) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) {
+                const int e = tid + 256 * u, r = e >> 4, c = 4 * (e & 15);
+                xs[c >> 3][(c & 7) + 0][r] = xv4[u].x;
+                xs[c >> 3][(c & 7) + 1][r] = xv4[u].y;
+                xs[c >> 3][(c & 7) + 2][r] = xv4[u].z;
+                xs[c >> 3][(c & 7) + 3][r] = xv4[u].w;
+            }
+#pragma unroll
+            for (int u = 0; u < 2; ++u) {
+                const int e = tid + 256 * u, r = e >> 4, c = 4 * (e & 15);
+                ws[c >> 3][(c & 7) + 0][r] = wv4[u].x;
+                ws[c >> 3][(c & 7) + 1][r] = wv4[u].y;
+                ws[c >> 3][(c & 7) + 2][r] = wv4[u].z;
+                ws[c >> 3][(c & 7) + 3][r] = wv4[u].w;
+            }
+        } else {
+            // X chunk: 64 rows x nc columns (zeros past S), 16 per thread
+            for (int e = tid; e < CH_ROWS * CH_KC; e += 256) {
+                const int r = e / CH_KC, c = e - r * CH_KC;
+                const int s = s0 + r;
+                xs[c >> 3][c & 7][r] = (c < nc && s < S) ? X[(int64_t)s * ldx + c0 + c] : 0.0f;
+            }
+            for (int e = tid; e < CH_OUTS * CH_KC; e += 256) {
+                const int r = e / CH_KC, c = e - r * CH_KC;
+                const int o = o0 + r;
+                ws[c >> 3][c & 7][r] = (c < nc && o < O) ? (float)W[(int64_t)o * I + c0 + c] : 0.0f;
+            }
         }
         __syncthreads();
+        if constexpr (VEC)
+            if (c0 + CH_KC < I8) load(c0 + CH_KC);
         for (int k = 0; k < nc / 8; ++k) {
             const float4 xa = *reinterpret_cast<const float4 *>(&xs[k][j][8 * g]);
             const float4 xb = *reinterpret_cast<const float4 *>(&xs[k][j][8 * g + 4]);
@@ -232,8 +278,13 @@ int pk_launch_gemm_chain8(const float *X, int64_t ldx, const float *W, const flo
                           int S, int I, int O, bool add_res, hipStream_t st) {
     PK_CHECK(S > 0 && I > 0 && O > 0, PK_ERR_ARG, "gemm chain8: bad shape");
     PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
-    hipLaunchKernelGGL(k_gemm_chain8<float>, dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
-                       dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
+    const bool vec = (ldx & 3) == 0 && (I & 3) == 0 && (((uintptr_t)X | (uintptr_t)W) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL((k_gemm_chain8<float, true>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
+    else
+        hipLaunchKernelGGL((k_gemm_chain8<float, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }
@@ -242,7 +293,7 @@ int pk_launch_gemm_chain8_q8(const float *X, const int8_t *W, const float *scale
                              hipStream_t st) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && scale, PK_ERR_ARG, "gemm chain8 q8: bad argument");
     PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
-    hipLaunchKernelGGL(k_gemm_chain8<int8_t>, dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+    hipLaunchKernelGGL((k_gemm_chain8<int8_t, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
                        dim3(256), 0, st, X, (int64_t)I, W, scale, nullptr, out, (int64_t)O, S, I, O, 0);
     PK_HIP(hipGetLastError());
     return PK_OK;
