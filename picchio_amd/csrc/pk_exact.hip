@@ -272,47 +272,6 @@ __global__ __launch_bounds__(128) void k_router_seq(const float *__restrict__ X,
     if (live) logits[(int64_t)s * E + e] = acc;
 }
 
-}  // namespace
-
-int pk_launch_gemm_chain8(const float *X, int64_t ldx, const float *W, const float *bias, float *out, int64_t ldo,
-                          int S, int I, int O, bool add_res, hipStream_t st) {
-    PK_CHECK(S > 0 && I > 0 && O > 0, PK_ERR_ARG, "gemm chain8: bad shape");
-    PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
-    const bool vec = (ldx & 3) == 0 && (I & 3) == 0 && (((uintptr_t)X | (uintptr_t)W) & 15) == 0;
-    if (vec)
-        hipLaunchKernelGGL((k_gemm_chain8<float, true>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
-                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
-    else
-        hipLaunchKernelGGL((k_gemm_chain8<float, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
-                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
-    PK_HIP(hipGetLastError());
-    return PK_OK;
-}
-
-int pk_launch_gemm_chain8_q8(const float *X, const int8_t *W, const float *scale, float *out, int S, int I, int O,
-                             hipStream_t st) {
-    PK_CHECK(S > 0 && I > 0 && O > 0 && scale, PK_ERR_ARG, "gemm chain8 q8: bad argument");
-    PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
-    hipLaunchKernelGGL((k_gemm_chain8<int8_t, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
-                       dim3(256), 0, st, X, (int64_t)I, W, scale, nullptr, out, (int64_t)O, S, I, O, 0);
-    PK_HIP(hipGetLastError());
-    return PK_OK;
-}
-
-int pk_launch_attn_rows_exact(int pos_base, int n, const float *qkv, int64_t qkv_stride, const float *Kl,
-                              const float *Vl, int H, int KVH, int hd, int ctx, int sliding, int window,
-                              const float *sinks, float *att, hipStream_t st) {
-    PK_CHECK(n > 0 && n <= 65535 && H % KVH == 0, PK_ERR_ARG, "attention rows: bad shape");
-    const int last = pos_base + n - 1;
-    int span = (last < ctx ? last : ctx - 1) + 1;
-    if (sliding && span > window) span = window;
-    PK_CHECK((size_t)span * 4 <= 64 * 1024, PK_ERR_UNSUPPORTED, "attention rows: window of %d positions", span);
-    hipLaunchKernelGGL(k_attn_rows_exact, dim3(H, n), dim3(64), (size_t)span * 4, st, pos_base, qkv, qkv_stride,
-                       Kl, Vl, H, KVH, hd, ctx, sliding, window, sinks, att);
-    PK_HIP(hipGetLastError());
-    return PK_OK;
-}
-
 // The same sums with 16-byte loads (D % 4 == 0, aligned rows; 4 <= E <= 128):
 // the next 64 columns of the router rows and of the block's input rows load
 // into registers (at most 20 per thread, so that the load counter can wait
@@ -394,6 +353,47 @@ __global__ __launch_bounds__(128) void k_router_seq4(const float *__restrict__ X
         }
     }
     if (live) logits[(int64_t)s * E + e] = acc;
+}
+
+}  // namespace
+
+int pk_launch_gemm_chain8(const float *X, int64_t ldx, const float *W, const float *bias, float *out, int64_t ldo,
+                          int S, int I, int O, bool add_res, hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0, PK_ERR_ARG, "gemm chain8: bad shape");
+    PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
+    const bool vec = (ldx & 3) == 0 && (I & 3) == 0 && (((uintptr_t)X | (uintptr_t)W) & 15) == 0;
+    if (vec)
+        hipLaunchKernelGGL((k_gemm_chain8<float, true>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
+    else
+        hipLaunchKernelGGL((k_gemm_chain8<float, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+                           dim3(256), 0, st, X, ldx, W, nullptr, bias, out, ldo, S, I, O, add_res ? 1 : 0);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+int pk_launch_gemm_chain8_q8(const float *X, const int8_t *W, const float *scale, float *out, int S, int I, int O,
+                             hipStream_t st) {
+    PK_CHECK(S > 0 && I > 0 && O > 0 && scale, PK_ERR_ARG, "gemm chain8 q8: bad argument");
+    PK_CHECK((S + CH_ROWS - 1) / CH_ROWS <= 65535, PK_ERR_UNSUPPORTED, "gemm chain8: %d rows", S);
+    hipLaunchKernelGGL((k_gemm_chain8<int8_t, false>), dim3((O + CH_OUTS - 1) / CH_OUTS, (S + CH_ROWS - 1) / CH_ROWS),
+                       dim3(256), 0, st, X, (int64_t)I, W, scale, nullptr, out, (int64_t)O, S, I, O, 0);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+int pk_launch_attn_rows_exact(int pos_base, int n, const float *qkv, int64_t qkv_stride, const float *Kl,
+                              const float *Vl, int H, int KVH, int hd, int ctx, int sliding, int window,
+                              const float *sinks, float *att, hipStream_t st) {
+    PK_CHECK(n > 0 && n <= 65535 && H % KVH == 0, PK_ERR_ARG, "attention rows: bad shape");
+    const int last = pos_base + n - 1;
+    int span = (last < ctx ? last : ctx - 1) + 1;
+    if (sliding && span > window) span = window;
+    PK_CHECK((size_t)span * 4 <= 64 * 1024, PK_ERR_UNSUPPORTED, "attention rows: window of %d positions", span);
+    hipLaunchKernelGGL(k_attn_rows_exact, dim3(H, n), dim3(64), (size_t)span * 4, st, pos_base, qkv, qkv_stride,
+                       Kl, Vl, H, KVH, hd, ctx, sliding, window, sinks, att);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
 }
 
 int pk_launch_router_seq(const float *X, const float *R, const float *bias, int S, int D, int E, float *logits,
