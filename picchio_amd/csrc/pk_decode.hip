@@ -1040,10 +1040,11 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
     const bool fuse = norm_w && e->attn_fused && n == 1 && G % 2 == 0 && (H * hd) % 4 == 0 &&
                       H * hd <= 64 * RES_U * 4;
     if (fuse && gs < 2) gs = 2;
-    // long windows in the one-launch form: four heads per block (half the
-    // attention blocks ahead of the O-projection blocks; config 4 at 4096
-    // positions 369.5 against 367 tok/s, two heads again below 16 chunks)
-    if (fuse && chunks >= 16 && G % 4 == 0 && gs < 4 && !getenv("PK_ATT_GS")) gs = 4;
+    // long windows in the one-launch form: all G heads of a KV head per
+    // block (a quarter of the attention blocks ahead of the O-projection
+    // blocks, each K/V row read once; config 4 at 4096 positions 383 against
+    // 368 tok/s with two heads, 375 with four), two heads below 16 chunks
+    if (fuse && chunks >= 16 && !getenv("PK_ATT_GS")) gs = G;
     PK_CHECK((int64_t)n * (H / gs) <= PK_CTR_ATTN_N, PK_ERR_UNSUPPORTED, "attention: %d rows x %d blocks", n,
              H / gs);
     // q, then p [gs][128] shared with the V partials [gs][PG][hd] (PG * hd = 512)
