@@ -1,29 +1,35 @@
 #!/usr/bin/env python3
 """Benchmark of the INT4 expert path on one MI355X.
 
-Default run (no --mode): BASELINE config 1 is the headline `value`; config 2
-(20B-shaped greedy decode) and config 4 (120B-shaped decode at batch 1 and
-32) are timed in the same process and reported under `config`.
+Default run (no --mode): every BASELINE config in one process. Config 1 is
+the headline `value`; configs 0, 2, 3 and 4 are reported under `config`,
+each with its own roofline and same-run CPU baseline.
 
 Config 1: one GPT-OSS-20B-shaped MoE layer at
 batch-1 decode -- RMSNorm'd fp32 x [2880], fp32 router [32x2880] + bias,
 top-4 of 32 INT4 gs64 experts (gate_up 5760x2880, down 2880x2880, biases),
-clamped SwiGLU, softmax-weighted combine -- over fresh seeded tokens. A
-"step" is one token through that layer, three launches (router, gate_up
-with the in-launch top-4, down with the combine) replayed from a HIP graph.
-Token t uses layer copy t % L (L = 24, the 20B model's MoE layers, 10.8 GB of
+clamped SwiGLU, softmax-weighted combine. A "step" is the config's 1000
+fresh seeded tokens through that layer one after another (each token: the
+router launch, then the experts launch), replayed from a HIP graph. Token t
+uses layer copy t % L (L = 24, the 20B model's MoE layers, 10.8 GB of
 experts) so the expert bytes come from HBM, not from the 256 MB MALL.
 
 value = algorithmic HBM bytes per token (experts + router + x/out) x tokens/s.
-roofline = the dominant kernel (gate_up + SwiGLU, four routed experts per
-launch): its algorithmic bytes per launch / its mean duration, from HIP
-events on the engine stream around each of its launches in eager layers.
+roofline = the dominant kernel (the experts launch): its algorithmic bytes per
+launch / its mean duration (graph replays with HIP events on the engine
+stream: router + experts, minus the router launches alone).
 cpu_baseline = picchio's MoE layer on the host cores (oracle/_ref build of
 the reference when present, else the C restatement).
 """
+import os
+
+# picchio's CPU baseline runs under OpenMP with threads bound to cores
+# (BASELINE.md's run conditions); set before any OpenMP runtime starts
+os.environ.setdefault("OMP_PROC_BIND", "close")
+os.environ.setdefault("OMP_PLACES", "cores")
+
 import argparse
 import json
-import os
 import sys
 import time
 
@@ -39,6 +45,8 @@ D, INTER, HALF, E, K = 2880, 5760, 2880, 32, 4
 EXPERT_BYTES = 12441600 + 1555200 + 34560          # packed + scales + biases
 ROUTER_BYTES = E * D * 4 + E * 4
 TOKEN_BYTES = K * EXPERT_BYTES + ROUTER_BYTES + 2 * D * 4      # 56,517,248
+FFN_BYTES = EXPERT_BYTES + 2 * D * 4               # config 0: one expert, x in, y out: 14,054,400
+TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh seeded tokens"
 
 # HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE, then
 # WRITE_SIZE, in passes of their own), scaled by what the two counters read
@@ -111,36 +119,58 @@ def token_inputs(n, seed):
     return (x * r[:, None]).astype(np.float32)
 
 
-def cpu_baseline(x, seed, budget_s):
-    """picchio's moe_forward on the host (time-bounded sample of the same tokens)."""
+def cpu_threads():
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+
+
+def timed_loop(fn, budget_s):
+    """fn(i) for i = 0, 1, ... until budget_s seconds have passed (after one
+    untimed call that pages the model in); returns (calls, seconds)."""
+    fn(0)
+    n, t0 = 0, time.perf_counter()
+    while time.perf_counter() - t0 < budget_s:
+        fn(n)
+        n += 1
+    return n, time.perf_counter() - t0
+
+
+def cpu_moe_baselines(x1, x0, seed, budget1_s, budget0_s):
+    """picchio on the host cores, on one 20B-shaped MoE layer (32 experts
+    resident in RAM, the same seeded weights as the GPU store's layer 0):
+    moe_forward over config 1's tokens (time-bounded sample), and
+    expert_apply over config 0's inputs, one expert after another."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_ffi import Oracle, Reference, reference_available, make_cfg
     o = Oracle()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     cfg = make_cfg(n_layers=1, n_experts=E, ctx_len=16, vocab=64)
     model = o.model_build(cfg, seed, threads)
     kind = "port"
     if reference_available():
         ref = Reference()
         ref.attach(model, cfg)
-        run = lambda xt, out: ref.moe_forward(0, xt, out)
+        moe = lambda xt, out: ref.moe_forward(0, xt, out)
+        ffn = lambda e, xt, dst: ref.expert_apply(0, e, xt, dst, 1.0)
         kind = "reference"
     else:
         sel = np.empty(K, np.int32)
         w = np.empty(K, np.float32)
-        run = lambda xt, out: o.moe_forward(model, 0, xt, out, sel, w, None)
+        moe = lambda xt, out: o.moe_forward(model, 0, xt, out, sel, w, None)
+        ffn = lambda e, xt, dst: o.expert_apply(model, 0, e, xt, dst, 1.0)
     out = np.empty(D, np.float32)
-    run(x[0], out)                                   # warm-up (page in)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        run(x[n % len(x)], out)
-        n += 1
-    dt = time.perf_counter() - t0
+    n1, dt1 = timed_loop(lambda i: moe(x1[i % len(x1)], out), budget1_s)
+    dst = np.zeros(D, np.float32)
+    n0, dt0 = timed_loop(lambda i: ffn(i % E, x0[i % len(x0)], dst), budget0_s)
     o.model_free(model)
-    return {"value": round(n * TOKEN_BYTES / dt / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": kind, "tokens_per_s": round(n / dt, 2),
-            "sample": f"{n} tokens of the same MoE layer (1 layer, 32 experts resident in RAM), "
-                      f"{dt:.1f} s, OpenMP {threads} threads"}
+    c1 = {"value": round(n1 * TOKEN_BYTES / dt1 / 1e9, 3), "unit": "GB/s", "cores": threads,
+          "kind": kind, "tokens_per_s": round(n1 / dt1, 2),
+          "sample": f"{n1} tokens of the same MoE layer (1 layer, 32 experts resident in RAM), "
+                    f"{dt1:.1f} s, OpenMP {threads} threads"}
+    c0 = {"value": round(n0 * FFN_BYTES / dt0 / 1e9, 3), "unit": "GB/s", "cores": threads,
+          "kind": kind, "us_per_ffn": round(dt0 / n0 * 1e6, 1),
+          "sample": f"{n0} expert_apply calls (the 32 experts of one layer in turn), {dt0:.1f} s, "
+                    f"OpenMP {threads} threads"}
+    return c1, c0
 
 
 def decode_bytes_per_token(cfg, pos):
@@ -164,13 +194,15 @@ def decode_bytes_per_token(cfg, pos):
     return total + 4 * D + lm + 4 * D
 
 
-def cpu_decode_baseline(cfg, seed, budget_s, prompt):
-    """picchio's forward_token on the host cores for the same model shape
-    (time-bounded sample)."""
+def cpu_decode_baseline(cfg, seed, budget_s, prompt, pos0):
+    """picchio's forward_token on the host cores for the same model (same
+    seeded weights), time-bounded, at positions pos0, pos0 + 1, ... like the
+    GPU's decode steps. The KV rows below pos0 stay zero: the attention loops
+    do the same work whatever the rows hold."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_ffi import Oracle, Reference, reference_available
     o = Oracle()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    threads = cpu_threads()
     t0 = time.perf_counter()
     model = o.model_build(cfg, seed, threads)
     build_s = time.perf_counter() - t0
@@ -183,18 +215,62 @@ def cpu_decode_baseline(cfg, seed, budget_s, prompt):
     else:
         step = lambda tok, pos: o.forward_token(model, tok, pos, None)
         kind = "port"
-    tok = int(prompt[0])
-    tok = step(tok, 0)                                  # warm-up (page in)
-    n, t0 = 0, time.perf_counter()
-    while time.perf_counter() - t0 < budget_s:
-        tok = step(int(prompt[(n + 1) % len(prompt)]), n + 1)
-        n += 1
-    dt = time.perf_counter() - t0
+    n, dt = timed_loop(lambda i: step(int(prompt[i % len(prompt)]), pos0 + i), budget_s)
     o.model_free(model)
     return {"value": round(n / dt, 3), "unit": "tok/s", "cores": threads, "kind": kind,
-            "sample": f"{n} forward_token steps at positions 1..{n} of the same 20B-shaped model "
-                      f"(all experts resident in RAM, fp32 lm_head), {dt:.1f} s, OpenMP {threads} "
-                      f"threads; model build {build_s:.0f} s"}
+            "sample": f"{n} forward_token steps at positions {pos0}..{pos0 + n} of the same "
+                      f"{cfg.n_layers}-layer model ({cfg.n_experts} experts per layer resident in RAM, "
+                      f"fp32 lm_head), {dt:.1f} s, OpenMP {threads} threads; model build {build_s:.0f} s"}
+
+
+def cpu_decode120_baseline(seed, budget_s, prompt, pos0):
+    """picchio's forward_token for the 120B shape, from a host model that
+    fits the run: every layer at full width (128 experts, the same seeded
+    weights as the GPU model's layers 0 and 1) but two layers deep (one
+    sliding-window, one full-context layer, as the 36 alternate) and a
+    64-entry vocabulary; the 201,088 x 2880 fp32 lm_head GEMV (matmul_f32,
+    picchio.c:1744) is timed on its own. Per token at 36 layers:
+    18 x t(two layers) + t(lm_head)."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_ffi import Oracle, Reference, reference_available, make_cfg
+    o = Oracle()
+    threads = cpu_threads()
+    cfg = make_cfg(n_layers=2, n_experts=128, ctx_len=pos0 + 4096, vocab=64)
+    t0 = time.perf_counter()
+    model = o.model_build(cfg, seed, threads)
+    build_s = time.perf_counter() - t0
+    V = 201088
+    y = np.empty(V, np.float32)
+    xl = np.random.default_rng(seed).standard_normal(D).astype(np.float32)
+    # the GEMV's work does not depend on the weight values: a constant matrix
+    W = np.full((V, D), 0.01, np.float32)
+    if reference_available():
+        ref = Reference()
+        ref.attach(model, cfg)
+        ref.reset_kv()
+        step = lambda tok, pos: ref.forward_token(tok, pos)
+        lm = lambda: ref.matmul_f32(y, xl, W, 1, D, V)
+        kind = "reference"
+    else:
+        step = lambda tok, pos: o.forward_token(model, tok, pos, None)
+        lm = lambda: o.matmul_f32(y, xl, W, 1, D, V)
+        kind = "port"
+    n2, dt2 = timed_loop(lambda i: step(int(prompt[i % len(prompt)]) % 64, pos0 + i), budget_s)
+    nl, dtl = timed_loop(lambda i: lm(), budget_s / 3)
+    o.model_free(model)
+    del W
+    t2, tl = dt2 / n2, dtl / nl
+    t36 = 18 * t2 + tl
+    return {"value": round(1.0 / t36, 3), "unit": "tok/s", "cores": threads, "kind": kind,
+            "ms_per_token_36_layers": round(t36 * 1e3, 1),
+            "ms_two_layers": round(t2 * 1e3, 2), "ms_lm_head": round(tl * 1e3, 2),
+            "batch32_tok_s": round(1.0 / t36, 3),
+            "sample": f"{n2} forward_token steps at positions {pos0}..{pos0 + n2} of a two-layer "
+                      f"120B-width model (128 experts per layer resident in RAM, KV rows below {pos0} "
+                      f"zero) in {dt2:.1f} s, and {nl} fp32 lm_head GEMVs (201088 x 2880) in "
+                      f"{dtl:.1f} s; 36 layers = 18 x two layers + lm_head; OpenMP {threads} threads; "
+                      f"model build {build_s:.0f} s; picchio decodes one sequence at a time, so its "
+                      f"batch-32 rate is its batch-1 rate"}
 
 
 def parse_sampling(spec):
@@ -253,7 +329,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
     lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
     cpu = None
     if cpu_on:
-        cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt)
+        cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt, n_prompt)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     print(f"[bench] config 2: {tok_s:.1f} tok/s ({ms / steps * 1e3:.1f} us/token), prefill "
           f"{prefill_s:.3f} s", file=sys.stderr, flush=True)
@@ -263,7 +339,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "config2: GPT-OSS-20B-shaped " + ("sampled" if sampling else "greedy") +
-                               " decode, batch 1, 512-token random-id prompt then 256 steps, all "
+                               f" decode, batch 1, 512-token random-id prompt then {steps} steps, all "
                                "experts HBM-resident",
                    "sampling": ({"temperature": sampling[0], "top_p": sampling[1], "top_k": sampling[2],
                                  "rep_penalty": sampling[3], "seed": args.seed} if sampling else "greedy"),
@@ -344,7 +420,7 @@ def measure_decode120b(args, steps, warmup, cpu_on):
     lm_bytes = cfg.vocab * cfg.hidden * 4 + cfg.hidden * 4 + cfg.vocab * 4
     cpu = None
     if cpu_on:
-        cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, first)
+        cpu = cpu_decode120_baseline(args.seed, args.cpu_seconds, first, ctx)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     print(f"[bench] config 4: batch 1 {tok1:.1f} tok/s, batch 32 {tok32:.1f} tok/s", file=sys.stderr,
           flush=True)
@@ -439,7 +515,7 @@ def cpu_pairs_baseline(seed, budget_s, x, sel, w):
                       f"{dt:.1f} s, OpenMP {threads} threads"}
 
 
-def run_prefill(args):
+def measure_prefill(args, steps, warmup, cpu_on):
     """T=2048 tokens through one GPT-OSS-20B MoE layer as
     expert-grouped INT4 GEMMs on the matrix cores (8192 pairs, Zipf 1.1
     routing): f16 activation pairs on v_mfma_f32_32x32x16_f16 (default) or
@@ -457,16 +533,16 @@ def run_prefill(args):
     x = np.random.default_rng(args.seed + 7).standard_normal((T, D)).astype(np.float32)
     xd, sd, wd = eng.to_dev(x), eng.to_dev(sel), eng.to_dev(w)
     out = eng.empty((T, D), torch.float32)
-    for _ in range(max(args.warmup, 1)):
+    for _ in range(max(warmup, 1)):
         eng.moe_forward_grouped(0, xd, out, sd, wd)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
     ev0.record(eng.stream)
-    for _ in range(args.steps):
+    for _ in range(steps):
         eng.moe_forward_grouped(0, xd, out, sd, wd)
     ev1.record(eng.stream)
     ev1.synchronize()
-    ms = ev0.elapsed_time(ev1) / args.steps
+    ms = ev0.elapsed_time(ev1) / steps
     eng.profile(True)
     for _ in range(5):
         eng.moe_forward_grouped(0, xd, out, sd, wd)
@@ -480,7 +556,7 @@ def run_prefill(args):
     gu_flops = 2.0 * P * INTER * D
     tiles = int(sum((c + 31) // 32 for c in counts))
     cpu = None
-    if not args.no_cpu:
+    if cpu_on:
         cpu = cpu_pairs_baseline(args.seed, args.cpu_seconds, x, sel, w)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     tfs = flops / (ms * 1e-3) / 1e12
@@ -491,7 +567,7 @@ def run_prefill(args):
     kern = "k_moe_f16<SWIGLU>" if f16 else "k_moe_mfma<SWIGLU>"
     line = {
         "metric": METRIC, "value": round(tfs, 2), "unit": "TFLOP/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 5),
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 5),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "f16x2 (int4 weights, fp32 sums)" if f16 else "int8x3 (int4 weights)",
         "data": "synthetic",
@@ -511,11 +587,23 @@ def run_prefill(args):
                      "flops_per_launch": gu_flops, "mean_us": round(gu_ms * 1e3, 2)},
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line))
+    print(f"[bench] config 3: {ms:.3f} ms per layer, {tfs:.1f} TFLOP/s; gate_up {gu_ms * 1e3:.1f} us, "
+          f"down {dn_ms * 1e3:.1f} us", file=sys.stderr, flush=True)
+    return line
+
+
+def capture(eng, lo, hi, enqueue):
+    """One executable graph of enqueue(t) for t in lo..hi-1."""
+    eng.capture_begin()
+    for t in range(lo, hi):
+        enqueue(t)
+    return eng.capture_end()
 
 
 def measure_moe_layer(args):
-    """the batch-1 MoE layer over fresh seeded tokens."""
+    """the batch-1 MoE layer over fresh seeded tokens, each
+    step 1000 of them; and, on the same expert store, config 0: one expert's
+    FFN at a time over every distinct expert of the store."""
     import torch
     import picchio_amd as pa
 
@@ -530,81 +618,95 @@ def measure_moe_layer(args):
     print(f"[bench] store built: {L} layers x {E} experts, {eng.device_bytes() / 1e9:.2f} GB in "
           f"{build_s:.1f} s", file=sys.stderr, flush=True)
 
-    W, S = args.warmup, args.steps
-    n_tok = W + S
+    W, S, T = args.warmup, args.steps, TOKENS_PER_STEP
+    n_tok = (W + S) * T
     x = token_inputs(n_tok, 1000 + args.seed)
     xd = eng.to_dev(x)
     od = eng.empty((n_tok, D), torch.float32)
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
 
-    # timed region: S tokens, three launches each, replayed from one graph
+    # timed region: S steps of T tokens, each token the router launch and the
+    # experts launch; one graph per step, the steps' graphs replayed back to back
     def enqueue(t):
         eng.moe_forward(t % L, xd[t], od[t])
-    eng.capture_begin()
-    for t in range(W):
-        enqueue(t)
-    g_warm = eng.capture_end()
-    eng.capture_begin()
-    for t in range(W, n_tok):
-        enqueue(t)
-    g_run = eng.capture_end()
-    eng.graph_launch(g_warm)
+    graphs = [capture(eng, s * T, (s + 1) * T, enqueue) for s in range(W + S)]
+    for g in graphs[:W]:
+        eng.graph_launch(g)
     eng.sync()
     torch.cuda.synchronize()
     ev0.record(eng.stream)
-    eng.graph_launch(g_run)
+    for g in graphs[W:]:
+        eng.graph_launch(g)
     ev1.record(eng.stream)
     ev1.synchronize()
     ms = ev0.elapsed_time(ev1)
-    eng.graph_destroy(g_warm)
-    eng.graph_destroy(g_run)
+    for g in graphs:
+        eng.graph_destroy(g)
 
     # the router launch alone over the same tokens, replayed the same way:
-    # the expert launch's duration is the difference of the two graphs
+    # the experts launch's duration is the difference of the two
     lg = eng.empty(E, torch.float32)
-    eng.capture_begin()
-    for t in range(W, n_tok):
-        eng.router_logits(t % L, xd[t], lg)
-    g_router = eng.capture_end()
-    eng.graph_launch(g_router)
+    graphs = [capture(eng, s * T, (s + 1) * T, lambda t: eng.router_logits(t % L, xd[t], lg))
+              for s in range(W, W + S)]
+    eng.graph_launch(graphs[0])
     eng.sync()
     ev0.record(eng.stream)
-    eng.graph_launch(g_router)
+    for g in graphs:
+        eng.graph_launch(g)
     ev1.record(eng.stream)
     ev1.synchronize()
     ms_router = ev0.elapsed_time(ev1)
-    eng.graph_destroy(g_router)
+    for g in graphs:
+        eng.graph_destroy(g)
 
     # the launches of an eager pass with HIP events on the engine stream around
     # each (tells the one-launch experts from the two-launch ones; the eager
     # events add the dispatch to each launch, so the graph difference above is
-    # the expert launch's duration)
-    n_prof = max(min(args.profile_tokens, S), 1)
+    # the experts launch's duration)
+    n_prof = max(min(args.profile_tokens, S * T), 1)
     eng.profile(True)
-    for t in range(W, W + n_prof):
+    for t in range(W * T, W * T + n_prof):
         enqueue(t)
-    kern, eager = {}, {}
+    eager = {}
     for name, kind in (("router", pa.PROF_ROUTER), ("moe_ffn", pa.PROF_MOE_FFN),
                        ("gate_up", pa.PROF_EXPERT_GATE_UP), ("down_combine", pa.PROF_EXPERT_DOWN)):
         tot, cnt = eng.profile_read(kind)
         if cnt:
             eager[name] = tot / cnt
     eng.profile(False)
+    n_timed = S * T
     fused = "moe_ffn" in eager
     if fused:
-        kern = {"router": ms_router / S, "moe_ffn": (ms - ms_router) / S}
+        kern = {"router": ms_router / n_timed, "moe_ffn": (ms - ms_router) / n_timed}
     else:
         kern = dict(eager)
     # streaming shape: all 32 experts of a layer copy in one gate_up launch
     act = eng.empty((E, HALF), torch.float32)
     all_e = eng.to_dev(np.arange(E, dtype=np.int32))
     st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act))
+
+    # config 0: one expert FFN after another (gate_up + bias + SwiGLU, then
+    # down + bias), FFN i on expert (i // L) % E of layer copy i % L: all
+    # L x E distinct experts (10.8 GB) before any repeats; x ~ N(0,1)
+    n_ffn = L * E
+    x0 = np.random.default_rng(2000 + args.seed).standard_normal((n_ffn, D)).astype(np.float32)
+    x0d = eng.to_dev(x0)
+    act0 = eng.empty(HALF, torch.float32)
+    y0 = eng.empty((n_ffn, D), torch.float32)
+    eid = lambda i: all_e[(i // L) % E:(i // L) % E + 1]
+
+    def ffn(i):
+        eng.expert_gate_up(i % L, eid(i), x0d[i], act0)
+        eng.expert_down(i % L, eid(i), act0, y0[i])
+    ffn_ms = replay_ms(eng, ev0, ev1, n_ffn, ffn)
+    ffn_gu_ms = replay_ms(eng, ev0, ev1, n_ffn, lambda i: eng.expert_gate_up(i % L, eid(i), x0d[i], act0))
+
     dot_on = args.dot == 1 or (args.dot < 0 and os.environ.get("PK_I4_DOT", "0") not in ("", "0"))
     arith = "integer-dot" if dot_on else "fp32 chains (bit-exact with quant.h)"
     eng.close()
 
-    ms_tok = ms / S
+    ms_tok = ms / n_timed
     gbps = TOKEN_BYTES / (ms_tok * 1e-3) / 1e9
     if fused:
         # the dominant kernel: all routed experts of the token in one launch
@@ -618,14 +720,30 @@ def measure_moe_layer(args):
                     "per launch, top-4 selected in the launch)")
         traffic = GATE_UP_TRAFFIC
     achieved = dom_bytes / (kern[dom] * 1e-3) / 1e9
-    print(f"[bench] config 1: {S} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, {gbps:.1f} GB/s; "
+    ffn_gbps = FFN_BYTES / (ffn_ms * 1e-3) / 1e9
+    print(f"[bench] config 1: {n_timed} tokens in {ms:.2f} ms: {ms_tok * 1e3:.2f} us/token, {gbps:.1f} GB/s; "
           f"kernels (us) " + ", ".join(f"{k} {v * 1e3:.2f}" for k, v in kern.items()) +
           f"; {dom} {achieved:.1f} GB/s ({arith})", file=sys.stderr, flush=True)
-    cpu = None
+    print(f"[bench] config 0: {ffn_ms * 1e3:.2f} us per expert FFN ({ffn_gu_ms * 1e3:.2f} gate_up), "
+          f"{ffn_gbps:.1f} GB/s", file=sys.stderr, flush=True)
+    cpu = cpu0 = None
     if not args.no_cpu:
-        cpu = cpu_baseline(x[:4000], args.seed, args.cpu_seconds)
+        cpu, cpu0 = cpu_moe_baselines(x[:4000], x0, args.seed, args.cpu_seconds, args.cpu_seconds * 0.6)
         cpu.update(host_info())
-        print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
+        print(f"[bench] cpu baselines: config 1 {cpu}; config 0 {cpu0}", file=sys.stderr, flush=True)
+    config0 = {
+        "workload": "config0: one GPT-OSS-20B-shaped expert FFN at batch 1 (gate_up 5760x2880 + bias, "
+                    "clamped SwiGLU, down 2880x2880 + bias; INT4 gs64), x ~ N(0,1); FFNs one after another "
+                    f"over all {n_ffn} distinct experts of the store (10.8 GB), replayed from a HIP graph",
+        "us_per_ffn": round(ffn_ms * 1e3, 3), "bytes_per_ffn": FFN_BYTES,
+        "gbps": round(ffn_gbps, 1), "hbm_frac": round(ffn_gbps / HBM_PEAK_GBPS, 4),
+        "gate_up_us": round(ffn_gu_ms * 1e3, 3), "down_us": round((ffn_ms - ffn_gu_ms) * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(ffn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(ffn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "kernel": "k_i4_gemv<SWIGLU> (gate_up) then k_i4_gemv<PLAIN> (down), one expert",
+                     "bytes_per_launch": FFN_BYTES, "mean_us": round(ffn_ms * 1e3, 3)},
+        "cpu_baseline": cpu0,
+    }
     return {
         "metric": METRIC,
         "value": round(gbps, 2),
@@ -633,17 +751,19 @@ def measure_moe_layer(args):
         "n_gpus": 1,
         "steps": S,
         "warmup": W,
-        "ms_per_step": round(ms_tok, 5),
+        "ms_per_step": round(ms / S, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32",
         "data": "synthetic",
         "config": {"workload": "config1: GPT-OSS-20B MoE layer, batch-1 decode, top-4 of 32 "
-                               "INT4 gs64 experts, fresh seeded tokens",
+                               f"INT4 gs64 experts; a step = {T} fresh seeded tokens one after another",
+                   "tokens_per_step": T, "tokens_timed": n_timed,
                    "layer_copies": L, "experts": E, "topk": K, "hidden": D, "weights": "int4-gs64",
                    "expert_arithmetic": arith, "experts_one_launch": fused,
-                   "bytes_per_token": TOKEN_BYTES, "tokens_per_s": round(1e3 / ms_tok, 1),
+                   "bytes_per_token": TOKEN_BYTES, "us_per_token": round(ms_tok * 1e3, 3),
+                   "tokens_per_s": round(1e3 / ms_tok, 1),
                    "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4), "chained": True,
                    "kernel_us": {k: round(v * 1e3, 3) for k, v in kern.items()},
                    "kernel_us_method": ("graph replays: router launches alone, and router + expert "
@@ -651,7 +771,8 @@ def measure_moe_layer(args):
                                         "HIP events around each launch of an eager pass"),
                    "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
                    "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
-                                                        / HBM_PEAK_GBPS, 4)},
+                                                        / HBM_PEAK_GBPS, 4),
+                   "config0_expert_ffn": config0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,
                      "kernel": dom_name, "bytes_per_launch": dom_bytes, "mean_us": round(kern[dom] * 1e3, 3)},
@@ -662,9 +783,11 @@ def measure_moe_layer(args):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=1000, help="timed tokens (config 1) or decode steps")
-    ap.add_argument("--warmup", type=int, default=100)
-    ap.add_argument("--layers", type=int, default=24, help="distinct MoE layer copies (config 1)")
+    ap.add_argument("--steps", type=int, default=20,
+                    help="timed steps: config 1 steps of 1000 tokens (default run, kernels); decode or "
+                         "prefill steps in the single-config modes")
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=24, help="distinct MoE layer copies (configs 0 and 1)")
     ap.add_argument("--seed", type=int, default=1)
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
@@ -673,50 +796,57 @@ def main():
                     help="config 1 expert arithmetic: 1 integer dot, 0 fp32 chains, -1 the engine's default")
     ap.add_argument("--grouped", choices=["f16", "int8"], default="f16",
                     help="config 3 arithmetic: f16 hi/lo activation pairs (default) or exact int8 limbs")
-    ap.add_argument("--decode-steps", type=int, default=128,
-                    help="default run: decode steps of configs 2 and 4")
+    ap.add_argument("--decode-steps", type=int, default=256,
+                    help="default run: config 2's greedy decode steps (the config names 256)")
+    ap.add_argument("--decode120-steps", type=int, default=128,
+                    help="default run: config 4's decode steps (the config names 128)")
+    ap.add_argument("--prefill-steps", type=int, default=10, help="default run: config 3's timed layers")
     ap.add_argument("--sample", default="",
                     help="decode mode: draw tokens on the device with T,top_p,top_k,rep "
                          "(e.g. 1.0,0.95,50,1.1, picchio's defaults) instead of greedy")
     ap.add_argument("--mode", choices=["all", "kernels", "decode", "prefill", "decode120b"], default="all",
-                    help="all (default): config 1 headline with configs 2 and 4 under config; "
-                         "kernels: config 1 only; decode: config 2 (use --steps 256); prefill: "
-                         "config 3, grouped MFMA MoE (--steps 20); decode120b: config 4 (--steps 128)")
+                    help="all (default): config 1 headline with configs 0, 2, 3 and 4 under config; "
+                         "kernels: configs 1 and 0 only; decode: config 2 (use --steps 256); prefill: "
+                         "config 3, grouped MFMA MoE; decode120b: config 4 (use --steps 128)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the expert path is built and timed on a single MI355X "
               "(multi-GPU sharding is a design note, not a measured configuration).", file=sys.stderr)
         sys.exit(2)
+    cpu_on = not args.no_cpu
     if args.mode == "decode":
-        print(json.dumps(measure_decode20b(args, args.steps, args.warmup, not args.no_cpu)))
+        print(json.dumps(measure_decode20b(args, args.steps, args.warmup, cpu_on)))
         return
     if args.mode == "prefill":
-        run_prefill(args)
+        print(json.dumps(measure_prefill(args, args.steps, args.warmup, cpu_on)))
         return
     if args.mode == "decode120b":
-        print(json.dumps(measure_decode120b(args, args.steps, args.warmup, not args.no_cpu)))
+        print(json.dumps(measure_decode120b(args, args.steps, args.warmup, cpu_on)))
         return
     line = measure_moe_layer(args)
     if args.mode == "all":
-        # configs 2 and 4 in the same run: decode tok/s of both model shapes
-        # (the 120B CPU baseline is left out: its model build on the host
-        # takes minutes; --mode decode120b measures it)
-        ds = args.decode_steps
-        d20 = measure_decode20b(args, ds, 8, not args.no_cpu)
-        d120 = measure_decode120b(args, ds, 4, False)
+        # configs 2, 3 and 4 in the same run, each with its roofline and CPU baseline
+        ds, ds4 = args.decode_steps, args.decode120_steps
+        d20 = measure_decode20b(args, ds, 8, cpu_on)
+        pf = measure_prefill(args, args.prefill_steps, 2, cpu_on)
+        d120 = measure_decode120b(args, ds4, 4, cpu_on)
         line["config"]["decode_20b"] = {"tok_s": d20["value"], "ms_per_token": d20["ms_per_step"],
                                         "steps": ds, **{k: d20["config"][k] for k in
                                                         ("workload", "bytes_per_token", "hbm_gbps", "hbm_frac",
                                                          "prefill_tok_s", "attention_us_per_layer")},
                                         "lm_head_roofline": d20["roofline"], "cpu_baseline": d20["cpu_baseline"]}
+        line["config"]["prefill_grouped"] = {"tflops": pf["value"], "ms_per_layer": pf["ms_per_step"],
+                                             "steps": pf["steps"], "dtype": pf["dtype"],
+                                             **{k: pf["config"][k] for k in
+                                                ("workload", "pairs", "gate_up_ms", "down_ms")},
+                                             "roofline": pf["roofline"], "cpu_baseline": pf["cpu_baseline"]}
         line["config"]["decode_120b"] = {"batch1_tok_s": d120["config"]["batch1_tok_s"],
-                                         "steps": ds, **{k: d120["config"][k] for k in
-                                                         ("workload", "batch1_bytes_per_token", "batch1_hbm_gbps",
-                                                          "batch32_tok_s", "batch32_ms_per_step",
-                                                          "batch32_hbm_gbps")},
+                                         "steps": ds4, **{k: d120["config"][k] for k in
+                                                          ("workload", "batch1_bytes_per_token", "batch1_hbm_gbps",
+                                                           "batch32_tok_s", "batch32_ms_per_step",
+                                                           "batch32_hbm_gbps")},
                                          "lm_head_roofline": d120["roofline"],
-                                         "cpu_baseline": "not run by default (host model build takes minutes): "
-                                                         "bench.py --mode decode120b"}
+                                         "cpu_baseline": d120["cpu_baseline"]}
     print(json.dumps(line))
 
 

@@ -211,6 +211,14 @@ int pk_set_i4_dot(pk_engine *e, int on);
  * activations) or as a gate_up launch and a down launch. Same results either
  * way. Default on (PK_MOE_FUSED=0 in the environment at engine creation: off). */
 int pk_set_moe_fused(pk_engine *e, int on);
+/* Diagnostic (no reference counterpart; no device work): how the one-launch
+ * experts place their down tasks for gu_RB x K gate_up workgroups on a
+ * device of n_cu compute units. down_task[t] (optional, n_out >= gu_RB*K
+ * entries) receives the down task of workgroup t, a permutation of the
+ * workgroups for every n_cu. Returns 1 if the one-launch form runs on such a
+ * device (its waiting down tasks leave a free workgroup slot), 0 if the
+ * layer falls back to two launches, or a negative PK_ERR_* code. */
+int pk_moe_ffn_plan(int gu_RB, int dn_RB, int K, int n_cu, int dot, int *down_task, int n_out);
 /* Batch-1 decode attention (pk_forward_token, pk_generate; gqa_attention,
  * picchio.c:504-623) and its output projection with the residual
  * (picchio.c:615-616, :1690) as one launch per layer (k_attn_oproj: the

@@ -123,6 +123,7 @@ def lib():
         "pk_set_i4_dot": (C.c_int, [vp, C.c_int]),
         "pk_set_grouped_f16": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
+        "pk_moe_ffn_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),

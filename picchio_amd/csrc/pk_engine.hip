@@ -774,12 +774,14 @@ static int experts_ffn(pk_engine *e, int layer, const int32_t *sel_dev, int n, c
     return PK_OK;
 }
 
-// Shapes k_moe_ffn takes (pk_launch_moe_ffn checks the same).
-static bool moe_ffn_fits(const pk_engine *e) {
+// Shapes and devices k_moe_ffn takes (pk_launch_moe_ffn checks the same):
+// its waiting down tasks must leave a free workgroup slot on this device.
+static bool moe_ffn_fits(const pk_engine *e, bool dot) {
     const pk_cfg *c = &e->c;
     return e->ex.gu.NG <= 45 && e->ex.dn.NG <= 45 && e->ex.gu.O == e->ex.gu.RB * 64 &&
-           e->ex.dn.NG * 64 == e->ex.gu.O / 2 && c->topk <= 4 && e->ex.dn.RB * c->topk <= 240 &&
-           e->ex.dn.RB <= e->ex.gu.RB && e->ex.stride < ((int64_t)1 << 31);   // 32-bit offsets in a slot
+           e->ex.dn.NG * 64 == e->ex.gu.O / 2 && c->topk <= 4 && e->ex.dn.RB <= e->ex.gu.RB &&
+           e->ex.stride < ((int64_t)1 << 31) &&   // 32-bit offsets in a slot
+           pk_moe_ffn_supported(e->ex.gu.RB, e->ex.dn.RB, c->topk, e->n_cu, dot);
 }
 
 // norm_w: x_dev is the raw residual row; the router normalises it (rmsnorm
@@ -822,7 +824,7 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     cb.residual = residual;
     cb.counters = e->counters + PK_CTR_COMBINE;
     const float *xin = norm_w ? e->hn : x_dev;
-    if (e->moe_fused && moe_ffn_fits(e)) {
+    if (e->moe_fused && moe_ffn_fits(e, dot)) {
         pk_moe_ffn_args a{};
         a.store = e->store;
         a.slot_stride = e->ex.stride;

@@ -500,11 +500,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void k_moe_ffn(pk_moe_ffn_args a) {
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int task = blockIdx.x;
     const int item = task % a.K;
-    // the down task this workgroup also takes: the first ones go to the
-    // workgroups that have a CU to themselves (workgroups n_cu.. share the CUs
-    // of workgroups 0.. with them), so that the bytes per CU even out
-    const int n2 = max((int)gridDim.x - a.n_cu, 0);
-    const int dtask = task >= n2 && task < a.n_cu ? task - n2 : task < n2 ? a.n_cu - n2 + task : task;
+    // the down task this workgroup also takes (a permutation of the grid for
+    // any CU count; pk_moe_down_task)
+    const int dtask = pk_moe_down_task(task, (int)gridDim.x, a.n_cu);
     const bool has_down = dtask < a.dn_RB * a.K;
     const int ditem = dtask % a.K;
     const pk_wave_logits lg = pk_load_wave_logits(a.rt.logits, a.rt.E);
@@ -657,8 +655,52 @@ __global__ __launch_bounds__(NW * 64, WPE) void k_moe_ffn(pk_moe_ffn_args a) {
     if (row < O) a.out[row] = a.residual ? res + o : o;
 }
 
+namespace {
+constexpr int MF_NW = 15, MF_GPW = 3, MF_WPE = 8;
+// partials + scales of NW x GPW groups, then the combine weights
+constexpr size_t MF_LDS = (size_t)2 * MF_NW * MF_GPW * 64 * sizeof(float) + 16 * sizeof(float);
+
+// workgroups of k_moe_ffn one CU holds at once (0 if the query fails)
+int moe_ffn_wgs_per_cu(bool dot) {
+    static int occ[2] = {-1, -1};
+    int &o = occ[dot ? 1 : 0];
+    if (o < 0) {
+        int n = 0;
+        const hipError_t rc =
+            dot ? hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      &n, reinterpret_cast<const void *>(k_moe_ffn<true, 4, MF_NW, MF_GPW, MF_WPE>), MF_NW * 64, MF_LDS)
+                : hipOccupancyMaxActiveBlocksPerMultiprocessor(
+                      &n, reinterpret_cast<const void *>(k_moe_ffn<false, 4, MF_NW, MF_GPW, MF_WPE>), MF_NW * 64,
+                      MF_LDS);
+        if (rc != hipSuccess) return 0;           // (not cached: a later query may succeed)
+        o = n;
+    }
+    return o;
+}
+}  // namespace
+
+bool pk_moe_ffn_supported(int gu_RB, int dn_RB, int K, int n_cu, bool dot) {
+    (void)gu_RB;
+    if (n_cu <= 0 || K <= 0 || dn_RB <= 0) return false;
+    const int64_t resident = (int64_t)n_cu * moe_ffn_wgs_per_cu(dot);
+    return (int64_t)dn_RB * K < resident;
+}
+
+// Diagnostic: k_moe_ffn's placement for a device of n_cu CUs (grid =
+// gu_RB x K workgroups): down_task[task] for every task, and whether the
+// launcher would take the one-launch form (1) or refuse it (0). No device
+// work; the occupancy query needs the HIP runtime only.
+extern "C" int pk_moe_ffn_plan(int gu_RB, int dn_RB, int K, int n_cu, int dot, int *down_task, int n_out) {
+    PK_CHECK(gu_RB > 0 && dn_RB > 0 && K > 0 && n_cu > 0, PK_ERR_ARG, "moe ffn plan: bad shape");
+    const int grid = gu_RB * K;
+    PK_CHECK(down_task == nullptr || n_out >= grid, PK_ERR_ARG, "moe ffn plan: %d outputs for %d tasks", n_out, grid);
+    if (down_task)
+        for (int t = 0; t < grid; ++t) down_task[t] = pk_moe_down_task(t, grid, n_cu);
+    return pk_moe_ffn_supported(gu_RB, dn_RB, K, n_cu, dot != 0) ? 1 : 0;
+}
+
 int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st) {
-    constexpr int NW = 15, GPW = 3, WPE = 8;
+    constexpr int NW = MF_NW, GPW = MF_GPW, WPE = MF_WPE;
     PK_CHECK(a.rt.logits && a.rt.sel && a.rt.w_scaled && a.rt.E > 0 && a.rt.E <= 128 && a.K > 0 &&
                  a.K <= a.rt.E && a.rt.K == a.K,
              PK_ERR_ARG, "moe ffn: routing of K=%d over E=%d", a.K, a.rt.E);
@@ -671,13 +713,13 @@ int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st) {
                  a.dn_NG * 64 == a.gu_O / 2 && a.dn_RB * 64 >= a.dn_O && a.dn_RB <= a.gu_RB,
              PK_ERR_UNSUPPORTED, "moe ffn: shapes gate_up %d x %d groups, down %d x %d groups", a.gu_O, a.gu_NG,
              a.dn_O, a.dn_NG);
-    // workgroups in their down task wait; they must leave room for the rest
-    // (at least one 15-wave workgroup per CU fits on any gfx950 part)
-    PK_CHECK(a.dn_RB * a.K <= 240, PK_ERR_UNSUPPORTED, "moe ffn: %d down tasks", a.dn_RB * a.K);
     PK_CHECK(a.n_cu > 0, PK_ERR_ARG, "moe ffn: n_cu %d", a.n_cu);
+    // workgroups in their down task wait; they must leave room for the rest
+    PK_CHECK(pk_moe_ffn_supported(a.gu_RB, a.dn_RB, a.K, a.n_cu, a.dot), PK_ERR_UNSUPPORTED,
+             "moe ffn: %d down tasks do not leave a free slot among %d CUs x %d workgroups", a.dn_RB * a.K, a.n_cu,
+             moe_ffn_wgs_per_cu(a.dot));
     const int grid = a.gu_RB * a.K;
-    // partials + scales of NW x GPW groups, then the combine weights
-    const size_t lds = (size_t)2 * NW * GPW * 64 * sizeof(float) + 16 * sizeof(float);
+    const size_t lds = MF_LDS;
     if (a.dot) hipLaunchKernelGGL((k_moe_ffn<true, 4, NW, GPW, WPE>), dim3(grid), dim3(NW * 64), lds, st, a);
     else hipLaunchKernelGGL((k_moe_ffn<false, 4, NW, GPW, WPE>), dim3(grid), dim3(NW * 64), lds, st, a);
     PK_HIP(hipGetLastError());

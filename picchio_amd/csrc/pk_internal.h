@@ -180,6 +180,24 @@ struct pk_moe_ffn_args {
     uint32_t *status;              // set to 1 if a wait gave up
 };
 int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st);
+// Whether the one-launch experts can run on this device: every down task
+// waits, so the down tasks must stay below the workgroups the device holds at
+// once (n_cu x the kernel's occupancy per CU) — else the launcher refuses
+// and the caller runs the two-launch form.
+bool pk_moe_ffn_supported(int gu_RB, int dn_RB, int K, int n_cu, bool dot);
+
+// The down task of k_moe_ffn's workgroup `task` (grid workgroups, n_cu CUs):
+// the first down tasks go to the workgroups that have a CU to themselves
+// (with grid <= 2 n_cu, workgroups n_cu.. share the CUs of workgroups 0..);
+// with grid > 2 n_cu no workgroup is alone and the mapping is the identity.
+// A permutation of [0, grid) for every n_cu >= 1.
+__host__ __device__ inline int pk_moe_down_task(int task, int grid, int n_cu) {
+    const int n2 = grid > n_cu ? grid - n_cu : 0;     // workgroups sharing a CU with a later one
+    if (n2 >= n_cu) return task;
+    if (task >= n2 && task < n_cu) return task - n2;
+    if (task < n2) return n_cu - n2 + task;
+    return task;
+}
 
 // Pairs grouped by expert into tiles (k_group_pairs): tile t = expert
 // tile_exp[t], pairs[tile_beg[t] .. + tile_cnt[t]]; *n_tiles tiles (device).

@@ -521,7 +521,9 @@ int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_bas
     }
     if (batch < 1) batch = 1;
     const int B = batch < n ? batch : n;
-    // PK_PREFILL_MFMA=1: the chunk's MoE on the int8 matrix cores (grouped GEMM)
+    // PK_PREFILL_MFMA=1: the chunk's MoE on the grouped matrix-core GEMM
+    // (f16 hi/lo activations by default, held to a tolerance; the exact int8
+    // limbs with pk_set_grouped_f16 off)
     const char *mv = getenv("PK_PREFILL_MFMA");
     const bool mfma = mv && atoi(mv) != 0;
     PK_TRY(prefill_reserve(e, B));
@@ -549,6 +551,8 @@ extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int po
     pk_dstate s{};
     PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
+    // a one-token prompt runs the fused decode step, whose waits may give up
+    PK_TRY(pk_check_waits(e));
     if (next_host) *next_host = s.next;
     return PK_OK;
 }
@@ -658,6 +662,8 @@ extern "C" int pk_prefill_seq(pk_engine *e, int seq, const int32_t *ids, int n, 
     pk_dstate s{};
     PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
+    // a one-token prompt runs the fused decode step, whose waits may give up
+    PK_TRY(pk_check_waits(e));
     if (next_host) *next_host = s.next;
     return PK_OK;
 }
@@ -693,12 +699,14 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
         e->bd_steps = n_steps + 1;
     }
     // With PK_BATCH_MFMA_MIN=n (n > 0) and at least n sequences the MoE runs
-    // on the int8 matrix cores (pairs grouped by expert, three exact
-    // activation limbs; sums in another order than the per-pair GEMV, within
-    // 1e-6 relative). Off by default: at 32 sequences over 128 experts most
-    // experts get one or two pairs, and a 32-pair tile per expert costs more
-    // (25.5 against 22.3 ms per 120B-shaped step); without it every sequence
-    // gets forward_token's exact bits.
+    // on the grouped matrix-core GEMM (pairs grouped by expert; the f16 hi/lo
+    // activations by default, the exact int8 limbs with pk_set_grouped_f16
+    // off). Off by default: at 32 sequences over 128 experts most experts get
+    // one or two pairs, and a 32-pair tile per expert costs more (25.5
+    // against 22.3 ms per 120B-shaped step). Without it each row's MoE runs
+    // on the integer-dot arithmetic (within 2e-5 of picchio's; the experts of
+    // a step grouped by expert), or with PK_I4_DOT_BATCH=0 in the
+    // environment at engine creation on forward_token's exact bits.
     int mfma_min = 0;
     if (const char *v = getenv("PK_BATCH_MFMA_MIN")) mfma_min = atoi(v);
     const bool moe_mfma = mfma_min > 0 && n_seq >= mfma_min;

@@ -1,34 +1,52 @@
-/* picchio_service.c — picchio's SERVICE=1 mode over the C-ABI of
- * libpicchio_hip.so: a persistent multi-turn session on one GPU, speaking
- * service_loop's protocol (picchio.c:2697-2795) on stdin / stdout.
+/* picchio_service.c — a persistent multi-turn session on one GPU, speaking
+ * the wire protocol of picchio's SERVICE=1 mode (picchio.c:2697-2795) on
+ * stdin / stdout, over the C-ABI of libpicchio_hip.so.
  *
- *   start-up (picchio.c main, :2800-3082): MODEL (or argv[1]) = the converted
- *   checkpoint directory; CTX = KV capacity in positions (default 512, at
- *   most the config's max_position_embeddings, :2931-2936); TEMPERATURE,
- *   TOPP, TOPK, REP, SEED = the sampler's settings (defaults 1.0 / 0.95 / 50
- *   / 1.1 and a time seed, :1510-1513, :3031-3038). SERVICE must be set to a
- *   non-zero value: the interactive and batch modes of picchio's main (the
- *   tokenizer, the chat template) are not part of this program.
+ * Start-up (the parts of picchio.c main, :2800-3082, that this mode uses):
+ *   MODEL (or argv[1])  converted checkpoint directory
+ *   CTX                 KV capacity in positions (default 512, at most the
+ *                       config's max_position_embeddings, :2931-2936)
+ *   TEMPERATURE, TOPP, TOPK, REP, SEED
+ *                       sampler settings (defaults 1.0 / 0.95 / 50 / 1.1
+ *                       and a time seed, :1510-1513, :3031-3038)
+ *   SERVICE             must be non-zero: the interactive and batch modes
+ *                       (tokenizer, chat template) are not part of this
+ *                       program.
  *
- *   protocol (stdout carries only the protocol, stderr diagnostics):
- *     READY <cap> <vocab> <stop0> <stop1>
- *     TURN <max_new> <keep> <temp> <top_p> <top_k> <n_ids> <id>...
- *         -> TOKEN <id> ... then DONE <MAX_TOKENS|CONTEXT_FULL|RETURN|CALL>
- *            <produced> <pos>
- *         -> ERROR BAD_RANGE 0 ... / ERROR BAD_TOKEN 0 ... (session intact)
- *     RESET    -> DONE RESET 0 0
- *     SHUTDOWN -> exit 0
- *     anything else -> ERROR BAD_COMMAND 1 ..., exit 1; an unreadable TURN
- *     header -> ERROR BAD_HEADER 1 ..., exit 1.
- *   The TURN's sampling is applied (with its clamp) before the range check,
- *   and nothing in the KV cache changes before the ids are validated, as in
- *   the reference. `keep` positions of the cache are reused: the turn's ids
- *   go in at pos = keep.
+ * Protocol. stdout carries protocol frames only (one line each, flushed),
+ * stderr diagnostics. The input is a stream of whitespace-separated fields;
+ * a command is one field followed by its arguments:
  *
- *   No reference counterpart: a failing GPU call prints
- *   ERROR ENGINE 1 <message> and exits 1 (the CPU reference cannot fail
- *   there). */
+ *   (on start)  READY <cap> <vocab> <stop_return> <stop_call>
+ *   TURN <max_new> <keep> <temp> <top_p> <top_k> <n_ids> <id>*n_ids
+ *               TOKEN <id> per emitted token, then
+ *               DONE <MAX_TOKENS|CONTEXT_FULL|RETURN|CALL> <produced> <pos>
+ *               or ERROR BAD_RANGE 0 ... / ERROR BAD_TOKEN 0 ...
+ *               (the session is unchanged and continues)
+ *   RESET       DONE RESET 0 0
+ *   SHUTDOWN    exit status 0 (so does the end of the input)
+ *   other       ERROR BAD_COMMAND 1 ..., exit status 1; a TURN header that
+ *               does not parse: ERROR BAD_HEADER 1 ..., exit status 1; the
+ *               input ending inside a TURN's ids: exit status 1.
+ *
+ * Semantics a client relies on (the reference's):
+ *  - the turn's sampling settings take effect (clamped) even when the turn
+ *    is then refused;
+ *  - a turn is refused before anything changes: BAD_RANGE when the counts do
+ *    not fit the session (max_new < 0, keep outside [0, pos], n_ids outside
+ *    [1, cap - keep]), its ids still consumed; BAD_TOKEN when any id is
+ *    outside the vocabulary;
+ *  - `keep` positions of the cache are reused and the ids go in at keep;
+ *  - each emitted token is also fed forward, so after DONE `pos` counts the
+ *    cache's valid positions; a stop id is emitted, fed, then ends the turn;
+ *  - an out-of-vocabulary prediction continues as token 0.
+ *
+ * No reference counterpart: a failing GPU call answers
+ * ERROR ENGINE 1 <message> and exits with status 1. */
+#include <ctype.h>
+#include <errno.h>
 #include <limits.h>
+#include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
@@ -37,132 +55,259 @@
 
 #include "picchio_hip.h"
 
-/* picchio.c:410-412: <|return|>, <|call|> */
-enum { STOP_RETURN = 200002, STOP_CALL = 200012 };
+/* the stop ids of the GPT-OSS vocabulary: <|return|>, <|call|> (picchio.c:410-412) */
+#define STOP_RETURN 200002
+#define STOP_CALL 200012
 
-static int engine_failed(const char *what) {
-    printf("ERROR ENGINE 1 %s: %s\n", what, pk_last_error());
-    fflush(stdout);
+/* ───────────── input: whitespace-separated fields ───────────── */
+
+typedef struct {
+    FILE *in;
+    char field[64];   /* the current field, NUL-terminated (longer fields are cut) */
+} field_reader;
+
+/* Next field into r->field; 0 at the end of the input. */
+static int next_field(field_reader *r) {
+    int ch;
+    do {
+        ch = getc(r->in);
+    } while (ch != EOF && isspace(ch));
+    if (ch == EOF) return 0;
+    size_t n = 0;
+    while (ch != EOF && !isspace(ch)) {
+        if (n + 1 < sizeof r->field) r->field[n++] = (char)ch;
+        ch = getc(r->in);
+    }
+    r->field[n] = '\0';
     return 1;
 }
 
-static float env_f(const char *name, float def) {
-    const char *v = getenv(name);
-    return v ? (float)atof(v) : def;
+/* The next field as an integer / a float; 0 if missing or malformed. */
+static int field_long(field_reader *r, long *v) {
+    if (!next_field(r)) return 0;
+    char *end = NULL;
+    errno = 0;
+    *v = strtol(r->field, &end, 10);
+    return end != r->field && *end == '\0' && errno == 0;
 }
 
-static int service_loop(pk_engine *e, const pk_cfg *c, int cap) {
-    int pos = 0;
-    printf("READY %d %d %d %d\n", cap, c->vocab, STOP_RETURN, STOP_CALL);
+static int field_float(field_reader *r, float *v) {
+    if (!next_field(r)) return 0;
+    char *end = NULL;
+    *v = strtof(r->field, &end);
+    return end != r->field && *end == '\0';
+}
+
+/* ───────────── output: one flushed frame per call ───────────── */
+
+static void frame(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vfprintf(stdout, fmt, ap);
+    va_end(ap);
+    fputc('\n', stdout);
     fflush(stdout);
+}
 
-    char cmd[32];
-    while (scanf("%31s", cmd) == 1) {
-        if (strcmp(cmd, "SHUTDOWN") == 0) break;
+/* ───────────── the session ───────────── */
 
-        if (strcmp(cmd, "RESET") == 0) {
-            /* positions are overwritten from 0 on; the penalty history empties */
-            pos = 0;
-            if (pk_reset_history(e) != PK_OK) return engine_failed("reset");
-            printf("DONE RESET 0 0\n");
-            fflush(stdout);
-            continue;
-        }
+typedef struct {
+    pk_engine *engine;
+    int vocab;
+    int cap;            /* KV capacity in positions */
+    int pos;            /* valid positions in the KV cache */
+    int32_t *ids;       /* the current turn's ids (grown on demand) */
+    long ids_cap;
+    field_reader rd;
+} session;
 
-        if (strcmp(cmd, "TURN") != 0) {
-            printf("ERROR BAD_COMMAND 1 unknown command\n");
-            fflush(stdout);
+/* what a handler tells the command loop */
+typedef enum { NEXT_COMMAND, END_OK, END_FAIL } outcome;
+
+static outcome engine_failure(const char *what) {
+    frame("ERROR ENGINE 1 %s: %s", what, pk_last_error());
+    return END_FAIL;
+}
+
+/* The TURN header: the six fields after the command word. */
+typedef struct {
+    long max_new, keep, top_k, n_ids;
+    float temp, top_p;
+} turn_header;
+
+static int read_turn_header(field_reader *r, turn_header *h) {
+    return field_long(r, &h->max_new) && field_long(r, &h->keep) && field_float(r, &h->temp) &&
+           field_float(r, &h->top_p) && field_long(r, &h->top_k) && field_long(r, &h->n_ids);
+}
+
+/* Whether the turn's counts fit the session (nothing changes otherwise). */
+static int turn_fits(const session *s, const turn_header *h) {
+    const long room = (long)s->cap - h->keep;   /* positions left after the kept prefix */
+    return h->max_new >= 0 && h->keep >= 0 && h->keep <= s->pos && h->n_ids >= 1 && h->n_ids <= room &&
+           h->n_ids <= s->cap;
+}
+
+/* Reads n ids into s->ids; returns the number outside the vocabulary, or -1
+ * if the input ended first (or memory ran out). */
+static long read_ids(session *s, long n) {
+    if (n > s->ids_cap) {
+        int32_t *grown = (int32_t *)realloc(s->ids, (size_t)n * sizeof(int32_t));
+        if (!grown) return -1;
+        s->ids = grown;
+        s->ids_cap = n;
+    }
+    long outside = 0;
+    for (long i = 0; i < n; ++i) {
+        long v;
+        if (!field_long(&s->rd, &v)) return -1;
+        outside += v < 0 || v >= s->vocab;
+        s->ids[i] = (int32_t)v;
+    }
+    return outside;
+}
+
+/* Skips n ids of a refused turn; 0 if the input ended first. */
+static int skip_ids(session *s, long n) {
+    for (long i = 0; i < n; ++i) {
+        long v;
+        if (!field_long(&s->rd, &v)) return 0;
+    }
+    return 1;
+}
+
+/* Why a turn that has `produced` tokens out stops before the next emission
+ * (NULL: it goes on). The token budget is checked before the cache room. */
+static const char *budget_stop(const session *s, long produced, long max_new) {
+    if (produced >= max_new) return "MAX_TOKENS";
+    if (s->pos >= s->cap) return "CONTEXT_FULL";
+    return NULL;
+}
+
+/* Why an emitted (and already fed) token ends the turn (NULL: it does not). */
+static const char *stop_token(int32_t tok) {
+    switch (tok) {
+    case STOP_RETURN: return "RETURN";
+    case STOP_CALL: return "CALL";
+    default: return NULL;
+    }
+}
+
+/* Emits tokens from `tok` on: each is announced, then fed at the next
+ * position; the prediction of the last fed token is the next candidate. */
+static outcome generate(session *s, int32_t tok, long max_new) {
+    long produced = 0;
+    const char *why;
+    while ((why = budget_stop(s, produced, max_new)) == NULL) {
+        frame("TOKEN %d", tok);
+        ++produced;
+        int32_t predicted = 0;
+        if (pk_forward_token(s->engine, tok, s->pos, &predicted, NULL) != PK_OK) return engine_failure("forward");
+        ++s->pos;
+        if ((why = stop_token(tok)) != NULL) break;
+        tok = predicted >= 0 && predicted < s->vocab ? predicted : 0;
+    }
+    frame("DONE %s %ld %d", why, produced, s->pos);
+    return NEXT_COMMAND;
+}
+
+static outcome cmd_turn(session *s) {
+    turn_header h;
+    if (!read_turn_header(&s->rd, &h)) {
+        frame("ERROR BAD_HEADER 1 unreadable TURN header");
+        return END_FAIL;
+    }
+    /* the turn's sampling holds from here on, refused or not (the engine
+     * clamps it as picchio.c:2737-2743 does) */
+    const int top_k = h.top_k > INT_MAX ? INT_MAX : h.top_k < INT_MIN ? INT_MIN : (int)h.top_k;
+    if (pk_set_turn_sampling(s->engine, h.temp, h.top_p, top_k) != PK_OK) return engine_failure("sampling");
+    if (!turn_fits(s, &h)) {
+        frame("ERROR BAD_RANGE 0 keep/n_ids out of bounds (pos=%d cap=%d)", s->pos, s->cap);
+        return skip_ids(s, h.n_ids) ? NEXT_COMMAND : END_FAIL;
+    }
+    const long outside = read_ids(s, h.n_ids);
+    if (outside < 0) return END_FAIL;
+    if (outside > 0) {
+        frame("ERROR BAD_TOKEN 0 ID out of vocabulary");
+        return NEXT_COMMAND;
+    }
+    /* the prompt overwrites the cache from `keep` on */
+    int32_t first = 0;
+    if (pk_prefill_tokens(s->engine, s->ids, (int)h.n_ids, (int)h.keep, &first) != PK_OK)
+        return engine_failure("prefill");
+    s->pos = (int)(h.keep + h.n_ids);
+    return generate(s, first, h.max_new);
+}
+
+static outcome cmd_reset(session *s) {
+    /* positions are rewritten from 0; the penalty history empties */
+    s->pos = 0;
+    if (pk_reset_history(s->engine) != PK_OK) return engine_failure("reset");
+    frame("DONE RESET 0 0");
+    return NEXT_COMMAND;
+}
+
+static outcome cmd_shutdown(session *s) {
+    (void)s;
+    return END_OK;
+}
+
+static const struct {
+    const char *word;
+    outcome (*run)(session *);
+} COMMANDS[] = {
+    {"TURN", cmd_turn},
+    {"RESET", cmd_reset},
+    {"SHUTDOWN", cmd_shutdown},
+};
+
+/* Runs commands until SHUTDOWN, the end of the input or a fatal error;
+ * returns the exit status. */
+static int serve(session *s) {
+    frame("READY %d %d %d %d", s->cap, s->vocab, STOP_RETURN, STOP_CALL);
+    while (next_field(&s->rd)) {
+        outcome (*run)(session *) = NULL;
+        for (size_t i = 0; i < sizeof COMMANDS / sizeof COMMANDS[0]; ++i)
+            if (strcmp(s->rd.field, COMMANDS[i].word) == 0) run = COMMANDS[i].run;
+        if (!run) {
+            frame("ERROR BAD_COMMAND 1 unknown command");
             return 1;
         }
-
-        long max_new = 0, keep = 0, n_ids = 0, t_topk = 0;
-        float t_temp = 0.0f, t_topp = 0.0f;
-        if (scanf("%ld %ld %f %f %ld %ld", &max_new, &keep, &t_temp, &t_topp, &t_topk, &n_ids) != 6) {
-            printf("ERROR BAD_HEADER 1 unreadable TURN header\n");
-            fflush(stdout);
-            return 1;
-        }
-        /* the turn's sampling, clamped by the engine as picchio.c:2737-2743 */
-        if (pk_set_turn_sampling(e, t_temp, t_topp, t_topk > INT_MAX ? INT_MAX : (int)t_topk) != PK_OK)
-            return engine_failed("sampling");
-        if (max_new < 0 || keep < 0 || keep > pos || n_ids <= 0 || keep + n_ids > cap || n_ids > cap) {
-            printf("ERROR BAD_RANGE 0 keep/n_ids out of bounds (pos=%d cap=%d)\n", pos, cap);
-            fflush(stdout);
-            /* nothing changed: discard the turn's ids, the session stays usable */
-            for (long i = 0; i < n_ids; i++) {
-                long skip;
-                if (scanf("%ld", &skip) != 1) return 1;
-            }
-            continue;
-        }
-
-        int32_t *ids = (int32_t *)malloc((size_t)n_ids * sizeof(int32_t));
-        if (!ids) return 1;
-        int valid = 1;
-        for (long i = 0; i < n_ids; i++) {
-            long value;
-            if (scanf("%ld", &value) != 1) {
-                free(ids);
-                return 1;
-            }
-            if (value < 0 || value >= c->vocab) valid = 0;
-            ids[i] = (int32_t)value;
-        }
-        if (!valid) {
-            free(ids);
-            printf("ERROR BAD_TOKEN 0 ID out of vocabulary\n");
-            fflush(stdout);
-            continue;
-        }
-
-        /* the prefix up to `keep` stays; the turn's ids overwrite from there */
-        pos = (int)keep;
-        int32_t next = 0;
-        const int rc = pk_prefill_tokens(e, ids, (int)n_ids, pos, &next);
-        free(ids);
-        if (rc != PK_OK) return engine_failed("prefill");
-        pos += (int)n_ids;
-
-        const char *reason = "MAX_TOKENS";
-        int produced = 0;
-        int tok = next;
-        while (1) {
-            if (produced >= max_new) { reason = "MAX_TOKENS"; break; }
-            if (pos >= cap) { reason = "CONTEXT_FULL"; break; }
-            printf("TOKEN %d\n", tok);
-            fflush(stdout);
-            produced++;
-            int32_t following = 0;
-            if (pk_forward_token(e, tok, pos, &following, NULL) != PK_OK) return engine_failed("forward");
-            pos++;
-            if (tok == STOP_RETURN) { reason = "RETURN"; break; }
-            if (tok == STOP_CALL) { reason = "CALL"; break; }
-            tok = (following < 0 || following >= c->vocab) ? 0 : following;
-        }
-        printf("DONE %s %d %d\n", reason, produced, pos);
-        fflush(stdout);
+        const outcome o = run(s);
+        if (o != NEXT_COMMAND) return o == END_OK ? 0 : 1;
     }
     return 0;
+}
+
+/* ───────────── start-up ───────────── */
+
+static float env_float(const char *name, float fallback) {
+    const char *v = getenv(name);
+    return v ? (float)atof(v) : fallback;
+}
+
+static int env_int(const char *name, int fallback) {
+    const char *v = getenv(name);
+    return v ? atoi(v) : fallback;
+}
+
+static int fail_startup(pk_engine *e) {
+    fprintf(stderr, "error: %s\n", pk_last_error());
+    if (e) pk_engine_destroy(e);
+    return 1;
 }
 
 int main(int argc, char **argv) {
     const char *model = getenv("MODEL");
     if (!model && argc > 1) model = argv[1];
-    const char *svc = getenv("SERVICE");
-    if (!model || !svc || atoi(svc) == 0) {
+    if (!model || env_int("SERVICE", 0) == 0) {
         fprintf(stderr, "usage: SERVICE=1 MODEL=/path/to/checkpoint %s  (or SERVICE=1 %s /path)\n", argv[0],
                 argv[0]);
         return 1;
     }
 
     pk_cfg cfg;
-    if (pk_cfg_from_container(model, 0, &cfg) != PK_OK) {
-        fprintf(stderr, "error: %s\n", pk_last_error());
-        return 1;
-    }
-    int cap = 512;
-    const char *ctx = getenv("CTX");
-    if (ctx) cap = atoi(ctx);
+    if (pk_cfg_from_container(model, 0, &cfg) != PK_OK) return fail_startup(NULL);
+    int cap = env_int("CTX", 512);
     if (cap > cfg.ctx_len) cap = cfg.ctx_len;
     if (cap < 1) {
         fprintf(stderr, "error: KV capacity %d\n", cap);
@@ -171,33 +316,27 @@ int main(int argc, char **argv) {
     cfg.ctx_len = cap;
 
     pk_engine *e = NULL;
-    const char *dev = getenv("PK_DEVICE");
-    if (pk_engine_create(&cfg, dev ? atoi(dev) : 0, &e) != PK_OK) {
-        fprintf(stderr, "error: %s\n", pk_last_error());
-        return 1;
-    }
-    const char *io = getenv("IO_THREADS");
+    if (pk_engine_create(&cfg, env_int("PK_DEVICE", 0), &e) != PK_OK) return fail_startup(NULL);
     const clock_t t0 = clock();
-    if (pk_load_container(e, model, io ? atoi(io) : 8) != PK_OK) {
-        fprintf(stderr, "error: %s\n", pk_last_error());
-        pk_engine_destroy(e);
-        return 1;
-    }
+    if (pk_load_container(e, model, env_int("IO_THREADS", 8)) != PK_OK) return fail_startup(e);
     fprintf(stderr, "loaded %s: %d layers, %d experts, vocab %d, %.2f GB resident (%.1f s cpu)\n", model,
             cfg.n_layers, cfg.n_experts, cfg.vocab, (double)pk_engine_device_bytes(e) / 1e9,
             (double)(clock() - t0) / CLOCKS_PER_SEC);
 
     const char *seed = getenv("SEED");
-    const uint64_t s = seed ? (uint64_t)atoll(seed) : (uint64_t)time(NULL);
-    const char *topk = getenv("TOPK");
-    if (pk_set_sampling(e, env_f("TEMPERATURE", 1.0f), env_f("TOPP", 0.95f), topk ? atoi(topk) : 50,
-                        env_f("REP", 1.1f), s) != PK_OK) {
-        fprintf(stderr, "error: %s\n", pk_last_error());
-        pk_engine_destroy(e);
-        return 1;
-    }
+    const uint64_t rng_seed = seed ? (uint64_t)atoll(seed) : (uint64_t)time(NULL);
+    if (pk_set_sampling(e, env_float("TEMPERATURE", 1.0f), env_float("TOPP", 0.95f), env_int("TOPK", 50),
+                        env_float("REP", 1.1f), rng_seed) != PK_OK)
+        return fail_startup(e);
     fprintf(stderr, "service: persistent session, KV capacity %d positions\n", cap);
-    const int rc = service_loop(e, &cfg, cap);
+
+    session s = {0};
+    s.engine = e;
+    s.vocab = cfg.vocab;
+    s.cap = cap;
+    s.rd.in = stdin;
+    const int status = serve(&s);
+    free(s.ids);
     pk_engine_destroy(e);
-    return rc;
+    return status;
 }

@@ -44,10 +44,10 @@ def config_json(cfg):
 
 
 def quantize_int8_rows(w):
-    """Per-row symmetric INT8 (convert.py:106-126): s = amax / 127 (1e-8 for
-    an all-zero row), q = clip(round(w / s), -127, 127)."""
+    """Per-row symmetric INT8 (convert.py:106-126): s = amax / 127 (1.0 for
+    an all-zero row, convert.py:123), q = clip(round(w / s), -127, 127)."""
     amax = np.abs(w).max(axis=1).astype(np.float32)
-    s = np.where(amax > 0, amax / np.float32(127.0), np.float32(1e-8)).astype(np.float32)
+    s = np.where(amax > 0, amax / np.float32(127.0), np.float32(1.0)).astype(np.float32)
     q = np.clip(np.rint(w / s[:, None]), -127, 127).astype(np.int8)
     return q, s
 

@@ -115,3 +115,29 @@ def test_rope_attn_factor_default():
     import picchio_amd as pa
     assert abs(pa.gptoss_cfg().rope_attn_factor - (0.1 * math.log(32.0) + 1.0)) < 1e-6
     assert pa.gptoss_cfg(rope_factor=1.0).rope_attn_factor == 1.0
+
+
+@pytest.mark.parametrize("n_cu", [1, 32, 64, 104, 128, 179, 180, 255, 256, 304, 512])
+@pytest.mark.parametrize("gu_rb,dn_rb,k", [(90, 45, 4), (90, 45, 2), (90, 45, 1), (8, 4, 3)])
+def test_moe_ffn_down_tasks_are_a_permutation(lib, n_cu, gu_rb, dn_rb, k):
+    """k_moe_ffn's workgroup -> down-task placement is a permutation of the
+    grid for every CU count, so every down task is taken exactly once and no
+    task index is negative (device partitions report 32/64/128 CUs)."""
+    grid = gu_rb * k
+    out = (C.c_int * grid)()
+    rc = lib.pk_moe_ffn_plan(gu_rb, dn_rb, k, n_cu, 0, out, grid)
+    assert rc in (0, 1)
+    got = list(out)
+    assert sorted(got) == list(range(grid)), (n_cu, min(got))
+    # with a CU to spare for some workgroups, the down tasks go to those first
+    n2 = max(grid - n_cu, 0)
+    if 0 < n2 < n_cu:
+        alone = range(n2, n_cu)
+        assert all(got[t] < n_cu - n2 for t in alone)
+
+
+def test_moe_ffn_plan_checks_arguments(lib):
+    out = (C.c_int * 4)()
+    assert lib.pk_moe_ffn_plan(0, 45, 4, 256, 0, None, 0) == -1
+    assert lib.pk_moe_ffn_plan(90, 45, 4, 0, 0, None, 0) == -1
+    assert lib.pk_moe_ffn_plan(90, 45, 4, 256, 0, out, 4) == -1   # too few outputs

@@ -321,6 +321,24 @@ def test_moe_one_launch_matches_two(moe_setup, oracle, dot):
         eng.set_i4_dot(0)
 
 
+def test_moe_one_launch_fits_this_device_only(gpu):
+    """The one-launch experts run only where their waiting down tasks leave
+    a free workgroup slot: on this device (all its CUs) the 20B shape takes
+    that form, on a device partition of 64 CUs it falls back to two launches
+    (its 180 down tasks would fill every slot)."""
+    import ctypes as C
+    import torch
+    import picchio_amd as pa
+    lib = pa.lib()
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    out = (C.c_int * 360)()
+    assert lib.pk_moe_ffn_plan(90, 45, 4, n_cu, 0, out, 360) == 1
+    assert lib.pk_moe_ffn_plan(90, 45, 4, n_cu, 1, out, 360) == 1
+    assert sorted(out) == list(range(360))
+    assert lib.pk_moe_ffn_plan(90, 45, 4, 64, 0, out, 360) == 0
+    assert sorted(out) == list(range(360))
+
+
 def test_router_ties_take_lowest_index(moe_setup, oracle):
     """Equal router logits: the lowest expert index is taken first
     (picchio.c:1327-1339, strict '>' over experts in order), and equal
