@@ -79,6 +79,10 @@ def host_info():
             "numa_nodes": len(nodes), "nproc": os.cpu_count()}
 
 
+# read before any OpenMP runtime binds this thread to one core
+HOST = host_info()
+
+
 def gate_up_bytes(n):
     """Algorithmic bytes of one gate_up launch over n experts: packed nibbles,
     scales, bias of each, x in, SwiGLU activations out."""
@@ -120,7 +124,7 @@ def token_inputs(n, seed):
 
 
 def cpu_threads():
-    return int(os.environ.get("OMP_NUM_THREADS", "0")) or len(os.sched_getaffinity(0))
+    return int(os.environ.get("OMP_NUM_THREADS", "0")) or HOST["threads_available"]
 
 
 def timed_loop(fn, budget_s):
@@ -729,7 +733,7 @@ def measure_moe_layer(args):
     cpu = cpu0 = None
     if not args.no_cpu:
         cpu, cpu0 = cpu_moe_baselines(x[:4000], x0, args.seed, args.cpu_seconds, args.cpu_seconds * 0.6)
-        cpu.update(host_info())
+        cpu.update(HOST)
         print(f"[bench] cpu baselines: config 1 {cpu}; config 0 {cpu0}", file=sys.stderr, flush=True)
     config0 = {
         "workload": "config0: one GPT-OSS-20B-shaped expert FFN at batch 1 (gate_up 5760x2880 + bias, "
