@@ -205,12 +205,19 @@ int pk_expert_down(pk_engine *e, int layer, const int32_t *eids_dev, int n,
  * launch its SwiGLU outputs' records for the down launch. Default off
  * (also PK_I4_DOT=1 in the environment at engine creation). */
 int pk_set_i4_dot(pk_engine *e, int on);
-/* Batch-1 MoE layers (pk_moe_forward, pk_forward_token, pk_generate) as one
- * launch per layer (k_moe_ffn: gate_up + SwiGLU, then down + combine, the
- * down workgroups waiting on device-side counters for their expert's
- * activations) or as a gate_up launch and a down launch. Same results either
- * way. Default on (PK_MOE_FUSED=0 in the environment at engine creation: off). */
-int pk_set_moe_fused(pk_engine *e, int on);
+/* How batch-1 MoE layers (pk_moe_forward, pk_forward_token, pk_generate)
+ * run their routed experts (the router is a launch of its own):
+ *   1 (default) one launch of one workgroup per gate_up row block and
+ *     expert, the first of them also taking the down row blocks (k_moe_ffn);
+ *   2 one launch with every CU streaming the same bytes (k_moe_bal: one
+ *     workgroup per CU, each holding an equal share of the experts' 64x64
+ *     tiles, values handed between workgroups as tagged words; measured
+ *     slower than mode 1: three hand-overs follow the stream); where the
+ *     shape or the CU count does not allow it, mode 1;
+ *   0 a gate_up launch and a down launch.
+ * Same results in every mode. PK_MOE_FUSED=<mode> in the environment sets
+ * it at engine creation. */
+int pk_set_moe_fused(pk_engine *e, int mode);
 /* Diagnostic (no reference counterpart; no device work): how the one-launch
  * experts place their down tasks for gu_RB x K gate_up workgroups on a
  * device of n_cu compute units. down_task[t] (optional, n_out >= gu_RB*K
@@ -219,6 +226,13 @@ int pk_set_moe_fused(pk_engine *e, int on);
  * device (its waiting down tasks leave a free workgroup slot), 0 if the
  * layer falls back to two launches, or a negative PK_ERR_* code. */
 int pk_moe_ffn_plan(int gu_RB, int dn_RB, int K, int n_cu, int dot, int *down_task, int n_out);
+/* Diagnostic (no reference counterpart; no device work): the unit ranges of
+ * mode 2's W workgroups for K experts of gu_RB x gu_NG gate_up and dn_RB x
+ * dn_NG down tiles. ranges (optional, n_out >= 4 W) receives per workgroup
+ * [gate_up first, gate_up end, down first, down end) in the unit numbering
+ * (item, row block, group), group fastest. Returns 1 if mode 2 runs this
+ * shape on W workgroups, 0 if it falls back, or a negative PK_ERR_* code. */
+int pk_moe_bal_plan(int K, int gu_RB, int gu_NG, int dn_RB, int dn_NG, int W, int *ranges, int n_out);
 /* Batch-1 decode attention (pk_forward_token, pk_generate; gqa_attention,
  * picchio.c:504-623) and its output projection with the residual
  * (picchio.c:615-616, :1690) as one launch per layer (k_attn_oproj: the

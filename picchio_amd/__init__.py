@@ -124,6 +124,7 @@ def lib():
         "pk_set_grouped_f16": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_moe_ffn_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int]),
+        "pk_moe_bal_plan": (C.c_int, [C.c_int] * 6 + [vp, C.c_int]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
@@ -286,10 +287,12 @@ class Engine:
         default) or the exact int8 limbs (pk_set_grouped_f16)."""
         check(self.L.pk_set_grouped_f16(self.h, 1 if on else 0))
 
-    def set_moe_fused(self, on):
-        """Batch-1 MoE layer's experts as one launch (default) or as a
-        gate_up launch and a down launch; same results (pk_set_moe_fused)."""
-        check(self.L.pk_set_moe_fused(self.h, 1 if on else 0))
+    def set_moe_fused(self, mode):
+        """How a batch-1 MoE layer runs its experts (pk_set_moe_fused): 1 one
+        launch of row-block workgroups (default), 2 one launch with every CU
+        streaming the same bytes, 0 a gate_up launch and a down launch; same
+        results. True / False mean 1 / 0."""
+        check(self.L.pk_set_moe_fused(self.h, int(mode)))
 
     def set_attn_fused(self, on):
         """Batch-1 decode attention and its output projection as one launch

@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "libpicchio_hip.so")
 OBJ = os.path.join(HERE, "_build")
-SOURCES = ["pk_i4.hip", "pk_dense.hip", "pk_engine.hip", "pk_decode.hip",
+SOURCES = ["pk_i4.hip", "pk_moe.hip", "pk_dense.hip", "pk_engine.hip", "pk_decode.hip",
            "pk_prefill.hip", "pk_mfma.hip", "pk_sample.hip", "pk_exact.hip", "pk_container.cpp"]
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

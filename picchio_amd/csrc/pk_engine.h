@@ -82,12 +82,17 @@ struct pk_engine {
     // integer-dot expert arithmetic of the three-launch MoE layer (opt-in:
     // PK_I4_DOT=1 or pk_set_i4_dot; default picchio's fp32 chains, bit-identical)
     bool i4_dot = false;
-    bool moe_fused = true;                    // batch-1 MoE as one k_moe_ffn launch (PK_MOE_FUSED=0: two launches)
+    // batch-1 MoE experts: 1 one launch of one workgroup per gate_up row
+    // block and expert (k_moe_ffn), 2 one launch with every CU streaming the
+    // same bytes (k_moe_bal; k_moe_ffn where that does not fit), 0 two
+    // launches (PK_MOE_FUSED=n)
+    int moe_fused = 1;
     bool i4_dot_batch = true;                 // pk_decode_batch's MoE on it (PK_I4_DOT_BATCH=0: not)
     int32_t *hn_q = nullptr;                  // the layer input's half-group records
     int32_t *act_q = nullptr;                 // [topk] SwiGLU outputs' records
     uint64_t *moe_act_t = nullptr;            // k_moe_ffn hand-over words: [topk][max(gu RB x 24, moe_inter/2)]
     uint64_t *moe_eo_t = nullptr;             // k_moe_ffn hand-over words: [topk][hidden]
+    uint64_t *moe_cont_t = nullptr;           // k_moe_bal hand-over words: [topk x (gu RB + dn RB)][64]
     // batch-1 decode attention and its output projection as one k_attn_oproj
     // launch (PK_ATT_FUSED=0: two launches)
     bool attn_fused = true;

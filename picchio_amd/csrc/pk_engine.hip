@@ -149,7 +149,7 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
-                    e->moe_act_t, e->moe_eo_t, e->att_t, e->skinny_ws};
+                    e->moe_act_t, e->moe_eo_t, e->moe_cont_t, e->att_t, e->skinny_ws};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
@@ -215,13 +215,16 @@ static int engine_init(pk_engine *e) {
     ALLOC(e->moe_eo_t, (int64_t)K * D * 8);
     PK_HIP(hipMemsetAsync(e->moe_act_t, 0, (int64_t)K * act_words * 8, e->stream));
     PK_HIP(hipMemsetAsync(e->moe_eo_t, 0, (int64_t)K * D * 8, e->stream));
+    const int64_t cont_bytes = (int64_t)K * (e->ex.gu.RB + e->ex.dn.RB) * 64 * 8;
+    ALLOC(e->moe_cont_t, cont_bytes);
+    PK_HIP(hipMemsetAsync(e->moe_cont_t, 0, cont_bytes, e->stream));
     ALLOC(e->att_t, (int64_t)c->n_heads * c->head_dim * 8);
     PK_HIP(hipMemsetAsync(e->att_t, 0, (int64_t)c->n_heads * c->head_dim * 8, e->stream));
     if (const char *v = getenv("PK_I4_DOT")) e->i4_dot = atoi(v) != 0;
     if (const char *v = getenv("PK_GROUPED_F16")) e->grouped_f16 = atoi(v) != 0;
     if (const char *v = getenv("PK_DOT_TILES")) e->dot_tiles_off = atoi(v) == 0;
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
-    if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v) != 0;
+    if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v);
     if (const char *v = getenv("PK_ATT_FUSED")) e->attn_fused = atoi(v) != 0;
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
@@ -849,10 +852,14 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
         a.rt = rt;
         a.act_t = e->moe_act_t;
         a.eo_t = e->moe_eo_t;
+        a.cont_t = e->moe_cont_t;
         a.epoch = e->counters + PK_CTR_MOE_EPOCH;
         a.status = e->counters + PK_CTR_MOE_STATUS;
         ps = pk_prof_begin(e, PK_PROF_MOE_FFN);
-        PK_TRY(pk_launch_moe_ffn(a, e->stream));
+        if (e->moe_fused == 2 && pk_moe_bal_fits_cu(dot) && pk_moe_bal_supported(a, e->n_cu))
+            PK_TRY(pk_launch_moe_bal(a, e->stream));
+        else
+            PK_TRY(pk_launch_moe_ffn(a, e->stream));
         return pk_prof_end(e, ps);
     }
     PK_TRY(experts_ffn(e, layer, e->sel, c->topk, xin, 0, e->act, e->eo, &cb, &rt, dot));
@@ -878,15 +885,16 @@ extern "C" int pk_set_grouped_f16(pk_engine *e, int on) {
     return PK_OK;
 }
 
-extern "C" int pk_set_moe_fused(pk_engine *e, int on) {
+extern "C" int pk_set_moe_fused(pk_engine *e, int mode) {
     PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(mode >= 0 && mode <= 2, PK_ERR_ARG, "set_moe_fused: mode %d (0, 1 or 2)", mode);
     PK_CHECK(!e->capturing, PK_ERR_ARG, "set_moe_fused: not available while capturing");
-    if (e->moe_fused != (on != 0) && e->step_exec) {   // the captured step holds the other kernels
+    if (e->moe_fused != mode && e->step_exec) {   // the captured step holds the other kernels
         (void)hipGraphExecDestroy(e->step_exec);
         e->step_exec = nullptr;
         e->step_cap = -1;
     }
-    e->moe_fused = on != 0;
+    e->moe_fused = mode;
     return PK_OK;
 }
 

@@ -201,6 +201,36 @@ __device__ __forceinline__ int pk_wave_topk_nth(const float *logits, int E, int 
     return pk_wave_topk_nth(pk_load_wave_logits(logits, E), E, n, val);
 }
 
+// Rounds 0..K-1 of the same selection in one pass: idx[k] / val[k] = round
+// k's (index, logit), the same on every lane (KM: an upper bound of K).
+template <int KM>
+__device__ __forceinline__ void pk_wave_topk_all(const pk_wave_logits &lg, int E, int K, int *idx, float *val) {
+    const int lane = threadIdx.x & 63;
+    const float v0 = lg.v0, v1 = lg.v1;
+    const uint32_t k0 = (lane < E && v0 == v0) ? pk_fkey(v0 + 0.0f) : 0u;
+    const uint32_t k1 = (lane + 64 < E && v1 == v1) ? pk_fkey(v1 + 0.0f) : 0u;
+    const uint32_t floor_key = pk_fkey(-1e30f);
+    bool t0 = false, t1 = false;
+#pragma unroll
+    for (int k = 0; k < KM; ++k) {
+        int bi = 0;
+        float bv = -1e30f;
+        if (k < K) {
+            const uint32_t a0 = t0 ? 0u : k0, a1 = t1 ? 0u : k1;
+            const uint32_t M = pk_wave_max_u32(max(a0, a1));
+            if (M > floor_key) {
+                const uint64_t m0 = __ballot(a0 == M);
+                bi = m0 ? __builtin_ctzll(m0) : 64 + __builtin_ctzll(__ballot(a1 == M));
+                bv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(bi < 64 ? v0 : v1), bi & 63));
+            }
+            if (bi == lane) t0 = true;
+            if (bi == lane + 64) t1 = true;
+        }
+        idx[k] = bi;
+        val[k] = bv;
+    }
+}
+
 // Routing of one token from its logits, in the consumer of the router
 // logits (picchio.c:1353, quant.h:406-412: max, expf, sum and division in
 // routing order), with the arithmetic of k_router_topk's last block: ci[k] /

@@ -176,10 +176,17 @@ struct pk_moe_ffn_args {
     // hand-over words (tag << 32 | bits), zero-initialised:
     uint64_t *act_t;               // [K][dot ? gu_RB * PK_XQ_INTS : gu_O / 2]
     uint64_t *eo_t;                // [K][dn_O]
+    uint64_t *cont_t;              // k_moe_bal: [K x (gu_RB + dn_RB)][64] split row blocks' accumulators
     const uint32_t *epoch;         // the tag: advanced before each launch (router), never 0
     uint32_t *status;              // set to 1 if a wait gave up
 };
 int pk_launch_moe_ffn(const pk_moe_ffn_args &a, hipStream_t st);
+// The same work with every CU streaming the same bytes (k_moe_bal, grid =
+// a.n_cu workgroups, one per CU; pk_moe.hip). Supported: shape and CU count
+// (the ranges) and one workgroup per CU fitting the kernel's resources.
+int pk_launch_moe_bal(const pk_moe_ffn_args &a, hipStream_t st);
+bool pk_moe_bal_supported(const pk_moe_ffn_args &a, int W);
+bool pk_moe_bal_fits_cu(bool dot);
 // Whether the one-launch experts can run on this device: every down task
 // waits, so the down tasks must stay below the workgroups the device holds at
 // once (n_cu x the kernel's occupancy per CU) — else the launcher refuses

@@ -7,6 +7,7 @@ import re
 import subprocess
 import tempfile
 
+import numpy as np
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -141,3 +142,40 @@ def test_moe_ffn_plan_checks_arguments(lib):
     assert lib.pk_moe_ffn_plan(0, 45, 4, 256, 0, None, 0) == -1
     assert lib.pk_moe_ffn_plan(90, 45, 4, 0, 0, None, 0) == -1
     assert lib.pk_moe_ffn_plan(90, 45, 4, 256, 0, out, 4) == -1   # too few outputs
+
+
+@pytest.mark.parametrize("W", [256, 240, 304, 200])
+@pytest.mark.parametrize("K", [4, 3, 2])
+def test_moe_balanced_ranges_partition_the_tiles(lib, W, K):
+    """The balanced experts launch's ranges (the same function the kernel
+    evaluates): each workgroup's gate_up and down ranges are contiguous and
+    together cover every (item, row block, group) tile once; down ranges
+    start and end on thirds of a row block; every workgroup holds about the
+    same number of tiles; no row block spans more than two workgroups."""
+    gu_rb, ng, dn_rb = 90, 45, 45
+    out = (C.c_int * (4 * W))()
+    ok = lib.pk_moe_bal_plan(K, gu_rb, ng, dn_rb, ng, W, out, 4 * W)
+    r = np.array(list(out)).reshape(W, 4)
+    Ug, Ud = K * gu_rb * ng, K * dn_rb * ng
+    assert r[0, 0] == 0 and r[0, 2] == 0 and r[-1, 1] == Ug and r[-1, 3] == Ud
+    assert np.all(r[1:, 0] == r[:-1, 1]) and np.all(r[1:, 2] == r[:-1, 3])
+    assert np.all(r[:, 2] % 15 == 0) and np.all(r[:, 3] % 15 == 0)
+    tot = (r[:, 1] - r[:, 0]) + (r[:, 3] - r[:, 2])
+    assert tot.max() - tot.min() <= 1
+    if ok == 1:
+        for lo, hi, NG in ((0, 1, ng), (2, 3, ng)):
+            owners = {}
+            for c in range(W):
+                for u in (r[c, lo], r[c, hi] - 1):
+                    if r[c, hi] > r[c, lo]:
+                        owners.setdefault(u // NG, set()).add(c)
+            for R, cs in owners.items():
+                assert max(cs) - min(cs) <= 1, (R, cs)
+
+
+def test_moe_balanced_plan_refuses_what_does_not_fit(lib):
+    # 128 CUs: ~190 tiles per workgroup, beyond the kernel's 80 + 48 slots
+    assert lib.pk_moe_bal_plan(4, 90, 45, 45, 45, 128, None, 0) == 0
+    # a down input that does not split in thirds
+    assert lib.pk_moe_bal_plan(4, 90, 45, 45, 44, 256, None, 0) == 0
+    assert lib.pk_moe_bal_plan(0, 90, 45, 45, 45, 256, None, 0) == -1

@@ -293,10 +293,13 @@ def test_moe_forward_parity(moe_setup, oracle):
 
 @pytest.mark.parametrize("dot", [0, 1])
 def test_moe_one_launch_matches_two(moe_setup, oracle, dot):
-    """The batch-1 experts as one launch (down workgroups waiting on the
-    gate_up counters) give the same bits as the gate_up launch + down launch,
-    token after token (the counters re-arm themselves), on picchio's fp32
-    chains and on the integer dot; and no device-side wait gave up."""
+    """The batch-1 experts as one launch give the same bits as the gate_up
+    launch + down launch, token after token (the hand-over tags advance with
+    every launch), on picchio's fp32 chains and on the integer dot: the
+    default row-block form (mode 1), the form with every CU streaming the
+    same bytes (mode 2, whose row blocks are split between workgroups and
+    continued in group order), and mode 1 again after the others; and no
+    device-side wait gave up."""
     import torch
     cfg, model, eng = moe_setup
     D = cfg.hidden
@@ -306,19 +309,28 @@ def test_moe_one_launch_matches_two(moe_setup, oracle, dot):
             x = _token_x(oracle, cfg, 500 + t)
             xd = eng.to_dev(x)
             outs, sels = [], []
-            for fused in (1, 0, 1):
-                eng.set_moe_fused(fused)
+            for mode in (1, 0, 2, 1):
+                eng.set_moe_fused(mode)
                 od = eng.empty(D, torch.float32)
                 sel, w = eng.moe_forward(0, xd, od, want_routing=True)
                 outs.append(eng.to_host(od))
                 sels.append((list(sel), list(w)))
-            assert sels[0] == sels[1] == sels[2], (t, sels)
-            assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32)), t
-            assert np.array_equal(outs[2].view(np.uint32), outs[1].view(np.uint32)), t
+            assert sels[0] == sels[1] == sels[2] == sels[3], (t, sels)
+            for m in (0, 2, 3):
+                assert np.array_equal(outs[m].view(np.uint32), outs[1].view(np.uint32)), (t, m)
         eng.sync()
     finally:
         eng.set_moe_fused(1)
         eng.set_i4_dot(0)
+
+
+def test_moe_balanced_launch_runs_here(gpu):
+    """Mode 2's ranges hold for the 20B and 120B shapes (top-4) on this
+    device's CUs, so that mode runs the balanced launch, not its fallback."""
+    import torch
+    import picchio_amd as pa
+    n_cu = torch.cuda.get_device_properties(0).multi_processor_count
+    assert pa.lib().pk_moe_bal_plan(4, 90, 45, 45, 45, n_cu, None, 0) == 1
 
 
 def test_moe_one_launch_fits_this_device_only(gpu):
