@@ -58,6 +58,7 @@ TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh
 #    18425.54 KiB x 2 + WRITE_SIZE 45.04 KiB.
 MOE_FFN_TRAFFIC = 57092529
 GATE_UP_TRAFFIC = 37780589
+STREAM_DOT_TRAFFIC = None
 
 
 def host_info():
@@ -685,10 +686,17 @@ def measure_moe_layer(args):
         kern = {"router": ms_router / n_timed, "moe_ffn": (ms - ms_router) / n_timed}
     else:
         kern = dict(eager)
-    # streaming shape: all 32 experts of a layer copy in one gate_up launch
+    # streaming shape: all 32 experts of a layer copy in one gate_up launch,
+    # on picchio's fp32 chains and on the integer dot (input records made
+    # once per token, outside the timed launches: the GEMV's input format)
     act = eng.empty((E, HALF), torch.float32)
     all_e = eng.to_dev(np.arange(E, dtype=np.int32))
-    st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act))
+    st_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up(t, all_e, xd[t], act), reps=5)
+    rec = eng.empty((L, (D // 32) * 24), torch.int32)
+    for t in range(L):
+        eng.act_records(xd[t], rec[t])
+    arec = eng.empty((E, (INTER // 64) * 24), torch.int32)
+    st_dot_ms = replay_ms(eng, ev0, ev1, L, lambda t: eng.expert_gate_up_dot(t, all_e, rec[t], act, arec), reps=5)
 
     # config 0: one expert FFN after another (gate_up + bias + SwiGLU, then
     # down + bias), FFN i on expert (i // L) % E of layer copy i % L: all
@@ -735,6 +743,25 @@ def measure_moe_layer(args):
         cpu, cpu0 = cpu_moe_baselines(x[:4000], x0, args.seed, args.cpu_seconds, args.cpu_seconds * 0.6)
         cpu.update(HOST)
         print(f"[bench] cpu baselines: config 1 {cpu}; config 0 {cpu0}", file=sys.stderr, flush=True)
+    st_gbps = gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
+    st_dot_gbps = gate_up_bytes(E) / (st_dot_ms * 1e-3) / 1e9
+    print(f"[bench] INT4 GEMV streaming (gate_up of 32 experts per launch): integer dot {st_dot_ms * 1e3:.2f} us "
+          f"= {st_dot_gbps:.1f} GB/s; fp32 chains {st_ms * 1e3:.2f} us = {st_gbps:.1f} GB/s", file=sys.stderr,
+          flush=True)
+    streaming = {
+        "workload": "INT4 gs64 expert GEMV at its streaming shape: gate_up + bias + SwiGLU of all 32 experts of "
+                    "a layer in one launch (32 x 5760 x 2880, 299 MB), one input row, over the 24 layer copies "
+                    "(graph replay)",
+        "bytes_per_launch": gate_up_bytes(E),
+        "roofline": {"bound": "hbm", "achieved": round(st_dot_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(st_dot_gbps / HBM_PEAK_GBPS, 4), "traffic": STREAM_DOT_TRAFFIC,
+                     "kernel": "k_i4_gemv_stream<SWIGLU, integer dot> (one workgroup per CU-share of row "
+                               "blocks, next row block in flight)",
+                     "bytes_per_launch": gate_up_bytes(E), "mean_us": round(st_dot_ms * 1e3, 3)},
+        "fp32_chains": {"achieved": round(st_gbps, 1), "frac": round(st_gbps / HBM_PEAK_GBPS, 4),
+                        "mean_us": round(st_ms * 1e3, 3),
+                        "kernel": "k_i4_gemv_stream<SWIGLU, fp32 chains> (bit-exact with quant.h)"},
+    }
     config0 = {
         "workload": "config0: one GPT-OSS-20B-shaped expert FFN at batch 1 (gate_up 5760x2880 + bias, "
                     "clamped SwiGLU, down 2880x2880 + bias; INT4 gs64), x ~ N(0,1); FFNs one after another "
@@ -773,9 +800,7 @@ def measure_moe_layer(args):
                    "kernel_us_method": ("graph replays: router launches alone, and router + expert "
                                         "launches; the expert launch = the difference" if fused else
                                         "HIP events around each launch of an eager pass"),
-                   "gate_up_32_experts_gbps": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9, 1),
-                   "gate_up_32_experts_hbm_frac": round(gate_up_bytes(E) / (st_ms * 1e-3) / 1e9
-                                                        / HBM_PEAK_GBPS, 4),
+                   "int4_gemv_streaming": streaming,
                    "config0_expert_ffn": config0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": traffic,

@@ -431,7 +431,12 @@ int pk_launch_i4_gemv(const pk_i4_items &it, const pk_i4_shape &sh, int epilogue
         // CU's LDS so that one workgroup runs per CU
         const size_t need = (size_t)(dot ? 2 : 4) * sh.NG * 64 * sizeof(float) + 4 * sizeof(int);
         const size_t lds = std::max(need, (size_t)82 * 1024);
-        const dim3 grid((unsigned)std::min<int64_t>(n_cu, (int64_t)it.n_items * sh.RB));
+        // as many workgroups as give every one the same count of row blocks
+        // (2880 row blocks on 256 CUs: 240 x 12, not 64 x 12 + 192 x 11,
+        // whose last round would stream from 64 CUs alone)
+        const int64_t n_task = (int64_t)it.n_items * sh.RB;
+        const int64_t per_wg = (n_task + n_cu - 1) / n_cu;
+        const dim3 grid((unsigned)((n_task + per_wg - 1) / per_wg));
 #define PK_I4_STREAM(E, D)                                                                              \
     hipLaunchKernelGGL((k_i4_gemv_stream<E, D>), grid, dim3((ST_NW + 1) * 64), lds, st, it, sh.O, sh.NG, \
                        sh.RB, lim, alpha)
