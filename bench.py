@@ -52,13 +52,16 @@ TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh
 # WRITE_SIZE, in passes of their own), scaled by what the two counters read
 # for a 1 GiB device copy in the same call (x 2.000 and x 1.000):
 #  * k_moe_ffn (the default, profiles/k_moe_ffn_moe_config1.txt), measured on
-#    commit d70a076: FETCH_SIZE 27792.77 KiB x 2 + WRITE_SIZE 168.84 KiB;
+#    commit afc7a2d: FETCH_SIZE 27791.47 KiB x 2 + WRITE_SIZE 168.84 KiB;
 #  * k_i4_gemv<SWIGLU> gate_up of the two-launch experts
 #    (pk_set_moe_fused(e, 0)), measured on commit 0a0ca63: FETCH_SIZE
-#    18425.54 KiB x 2 + WRITE_SIZE 45.04 KiB.
-MOE_FFN_TRAFFIC = 57092529
+#    18425.54 KiB x 2 + WRITE_SIZE 45.04 KiB;
+#  * k_i4_gemv_stream<SWIGLU, integer dot>, 32 experts' gate_up
+#    (profiles/k_i4_gemv_stream_gate_up32.txt), commit afc7a2d: FETCH_SIZE
+#    149022.55 KiB x 2 + WRITE_SIZE 630.00 KiB.
+MOE_FFN_TRAFFIC = 57088267
 GATE_UP_TRAFFIC = 37780589
-STREAM_DOT_TRAFFIC = None
+STREAM_DOT_TRAFFIC = 305834925
 
 
 def host_info():
