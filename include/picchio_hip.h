@@ -433,6 +433,24 @@ int pk_sampler_state(pk_engine *e, uint64_t *rng, int32_t *history_host, int cap
 #define PK_PROF_N              8
 int pk_engine_profile(pk_engine *e, int enable);
 int pk_engine_profile_read(pk_engine *e, int kernel, double *total_ms, int64_t *launches);
+/* ── diagnostics (no device work of their own beyond copies; not while
+ *    capturing a graph) ──
+ * Router trace: while buf_dev is set, every MoE router launch appends its
+ * logits (+ bias) to buf_dev in launch order — batch-1 layers one row of
+ * n_experts floats each (pk_moe_forward, pk_forward_token), batched rows
+ * [rows][n_experts] per layer (pk_decode_batch, pk_prefill_*) — until
+ * cap_floats would be exceeded; pk_router_trace_used gives the floats
+ * written. The logits are what the top-k (picchio.c:1327-1339) ranks, so a
+ * caller sees how close each routing decision was. NULL turns it off. */
+int pk_set_router_trace(pk_engine *e, float *buf_dev, int64_t cap_floats);
+int64_t pk_router_trace_used(pk_engine *e);
+/* picchio's TRACE_NUMERIC (picchio.c:251-288, :1356-1360, :1666-1745): with
+ * on != 0 (or TRACE_NUMERIC=1 in the environment at engine creation) each
+ * eager pk_forward_token prints to stderr, per stage, the residual's min,
+ * max, rms and count of non-finite entries, per layer the routing (experts,
+ * softmax weights, and the 4th / 5th logit margin), and the top-10 logits.
+ * Synchronises the stream at every stage; replayed graphs print nothing. */
+int pk_set_numeric_trace(pk_engine *e, int on);
 /* Queues a bounded idle kernel (about `usec` microseconds, at most 1 s) so
  * that the host can queue work ahead of the GPU before a profiled pass. */
 int pk_engine_stall(pk_engine *e, int usec);

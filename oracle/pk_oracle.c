@@ -585,6 +585,18 @@ static void po_topk(const float *scores, int E, int K, int *sel, float *wsel) {
     }
 }
 
+/* Test diagnostics (no reference counterpart): while set, every
+ * po_moe_forward appends its router logits here, so that a test can see how
+ * close each routing decision along a token chain was. */
+static float *g_rtrace = NULL;
+static int64_t g_rtrace_cap = 0, g_rtrace_used = 0;
+void po_set_router_trace(float *buf, int64_t cap_floats) {
+    g_rtrace = buf;
+    g_rtrace_cap = buf ? cap_floats : 0;
+    g_rtrace_used = 0;
+}
+int64_t po_router_trace_used(void) { return g_rtrace_used; }
+
 /* picchio.c:1309-1466. Router logit = in-order dot, router bias added after
  * the dot (picchio.c:1317-1324). */
 void po_moe_forward(po_model *m, int layer, const float *x, float *out,
@@ -598,6 +610,10 @@ void po_moe_forward(po_model *m, int layer, const float *x, float *out,
         scores[e] = dot + ly->router_b[e];
     }
     if (logits) memcpy(logits, scores, (size_t)E * sizeof(float));
+    if (g_rtrace && g_rtrace_used + E <= g_rtrace_cap) {
+        memcpy(g_rtrace + g_rtrace_used, scores, (size_t)E * sizeof(float));
+        g_rtrace_used += E;
+    }
     int s_loc[64];
     float w_loc[64];
     po_topk(scores, E, K, s_loc, w_loc);

@@ -111,6 +111,10 @@ float po_yarn_inv_freq(const pk_cfg *c, int j);
 void po_embed(po_model *m, int tok, float *x);
 /* forward_token (picchio.c:1655-1756) with greedy sampling; logits optional. */
 int po_forward_token(po_model *m, int tok, int pos, float *logits);
+/* Test diagnostics: every po_moe_forward appends its router logits to buf
+ * (until cap_floats), NULL: off. */
+void po_set_router_trace(float *buf, int64_t cap_floats);
+int64_t po_router_trace_used(void);
 /* forward_prefill (picchio.c:1795-1932) for n tokens at pos_base. */
 int po_forward_prefill(po_model *m, const int *ids, int n, int pos_base);
 /* prefill_tokens (picchio.c:1936-1975): chunks of `batch` through forward_prefill. */

@@ -125,6 +125,9 @@ def lib():
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_moe_ffn_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int]),
         "pk_moe_bal_plan": (C.c_int, [C.c_int] * 6 + [vp, C.c_int]),
+        "pk_set_router_trace": (C.c_int, [vp, vp, C.c_int64]),
+        "pk_router_trace_used": (C.c_int64, [vp]),
+        "pk_set_numeric_trace": (C.c_int, [vp, C.c_int]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
@@ -286,6 +289,19 @@ class Engine:
         """Grouped MoE arithmetic: f16 hi/lo activations on the f16 MFMA (the
         default) or the exact int8 limbs (pk_set_grouped_f16)."""
         check(self.L.pk_set_grouped_f16(self.h, 1 if on else 0))
+
+    def set_router_trace(self, buf_dev):
+        """Every MoE router launch appends its logits to buf_dev (a float32
+        device tensor; None: off) until it is full (pk_set_router_trace)."""
+        check(self.L.pk_set_router_trace(self.h, ptr(buf_dev) if buf_dev is not None else None,
+                                         buf_dev.numel() if buf_dev is not None else 0))
+
+    def router_trace_used(self):
+        return int(self.L.pk_router_trace_used(self.h))
+
+    def set_numeric_trace(self, on):
+        """picchio's TRACE_NUMERIC lines on stderr for eager forward_token."""
+        check(self.L.pk_set_numeric_trace(self.h, 1 if on else 0))
 
     def set_moe_fused(self, mode):
         """How a batch-1 MoE layer runs its experts (pk_set_moe_fused): 1 one

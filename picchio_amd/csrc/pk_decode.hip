@@ -1109,13 +1109,17 @@ static int decode_step(pk_engine *e, float *logits_dev, int32_t *out_toks, int o
     hipLaunchKernelGGL(k_embed_rmsnorm, dim3(1), dim3(256), 0, e->stream, e->dstate, e->embed, c->vocab,
                        e->h, e->hn, e->L[0].in_ln, D, c->eps);
     PK_HIP(hipGetLastError());
+    PK_TRY(pk_trace_vec(e, "embedding", -1, e->h, D));
     for (int l = 0; l < c->n_layers; ++l) {
         PK_TRY(attention_layer(e, l));
+        PK_TRY(pk_trace_vec(e, "post_attention", l, e->h, D));
         // h += moe(rmsnorm(h)): the router normalises h and writes hn for the experts
         PK_TRY(pk_moe_layer(e, l, e->h, nullptr, e->h, e->h, e->L[l].post_ln));
+        PK_TRY(pk_trace_vec(e, "post_moe", l, e->h, D));
     }
     PK_TRY(pk_launch_rmsnorm(e->hn, e->h, e->final_norm, D, c->eps, 1, e->stream));
-    return pk_lm_head_step(e, e->hn, logits_dev, out_toks, out_cap);
+    PK_TRY(pk_lm_head_step(e, e->hn, logits_dev, out_toks, out_cap));
+    return pk_trace_top_logits(e, logits_dev ? logits_dev : e->logits);
 }
 
 // lm_head GEMV + greedy argmax of the normalised state hn for the token at

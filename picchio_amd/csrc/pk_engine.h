@@ -100,6 +100,13 @@ struct pk_engine {
 
     bool capturing = false;                  // inside pk_capture_begin/end
 
+    // diagnostics (outside graph capture only): every MoE router launch
+    // appends its logits [rows][E] to rtrace (pk_set_router_trace); with
+    // trace_numeric forward_token prints picchio's TRACE_NUMERIC lines
+    float *rtrace = nullptr;
+    int64_t rtrace_cap = 0, rtrace_used = 0;
+    bool trace_numeric = false;
+
     // decode step (pk_decode.hip)
     bool dec_ready = false;
     pk_dstate *dstate = nullptr;              // device
@@ -261,5 +268,11 @@ int pk_decode_token(pk_engine *e, int tok, int pos, int32_t *out_toks, int out_c
 int pk_prefill_run(pk_engine *e, int seq, const int32_t *ids, int n, int pos_base, int32_t *out_toks,
                    int out_cap);
 
+// Diagnostics: the router trace append (no-op unless set and not capturing),
+// and the numeric trace lines of forward_token (host syncs; trace_numeric only).
+int pk_trace_router(pk_engine *e, const float *logits_dev, int rows);
+int pk_trace_vec(pk_engine *e, const char *stage, int layer, const float *dev, int n);
+int pk_trace_route(pk_engine *e, int layer, const float *logits_dev);
+int pk_trace_top_logits(pk_engine *e, const float *logits_dev);
 // Reads (and clears) the k_moe_ffn wait flag after a stream sync.
 int pk_check_waits(pk_engine *e);

@@ -226,6 +226,7 @@ static int engine_init(pk_engine *e) {
     if (const char *v = getenv("PK_I4_DOT_BATCH")) e->i4_dot_batch = atoi(v) != 0;
     if (const char *v = getenv("PK_MOE_FUSED")) e->moe_fused = atoi(v);
     if (const char *v = getenv("PK_ATT_FUSED")) e->attn_fused = atoi(v) != 0;
+    if (const char *v = getenv("TRACE_NUMERIC")) e->trace_numeric = atoi(v) != 0;   // picchio.c:2826-2827
     PK_HIP(hipMemsetAsync(e->counters, 0, PK_CTR_N * 4, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -278,6 +279,116 @@ int pk_check_waits(pk_engine *e) {
         pk_set_error("a device-side wait (expert or attention launch) gave up: results are invalid");
         return PK_ERR_HIP;
     }
+    return PK_OK;
+}
+
+// ───────────────────────── diagnostics ─────────────────────────
+// The router logits of every MoE router launch, appended in launch order
+// (batch-1: one row per layer; batched rows: [rows][E] per layer), so that a
+// caller can see how close each routing decision was (the 4th / 5th logit
+// margin of moe_forward's top-k, picchio.c:1327-1339). Not while capturing.
+extern "C" int pk_set_router_trace(pk_engine *e, float *buf_dev, int64_t cap_floats) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_router_trace: not available while capturing");
+    PK_CHECK(buf_dev == nullptr || cap_floats > 0, PK_ERR_ARG, "router trace: capacity %lld", (long long)cap_floats);
+    e->rtrace = buf_dev;
+    e->rtrace_cap = buf_dev ? cap_floats : 0;
+    e->rtrace_used = 0;
+    return PK_OK;
+}
+
+extern "C" int64_t pk_router_trace_used(pk_engine *e) { return e ? e->rtrace_used : -1; }
+
+int pk_trace_router(pk_engine *e, const float *logits_dev, int rows) {
+    if (!e->rtrace || e->capturing) return PK_OK;
+    const int64_t n = (int64_t)rows * e->c.n_experts;
+    if (e->rtrace_used + n > e->rtrace_cap) return PK_OK;        // full: later launches are not kept
+    PK_HIP(hipMemcpyAsync(e->rtrace + e->rtrace_used, logits_dev, (size_t)n * 4, hipMemcpyDeviceToDevice,
+                          e->stream));
+    e->rtrace_used += n;
+    return PK_OK;
+}
+
+// picchio's TRACE_NUMERIC (picchio.c:251-288, :1356-1360, :1666-1745): per
+// stage of forward_token the vector's min, max, rms over its finite entries
+// and the count of non-finite ones; per layer the routing (and here also
+// the 4th / 5th logit margin); the top-10 logits. Lines go to stderr.
+extern "C" int pk_set_numeric_trace(pk_engine *e, int on) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    e->trace_numeric = on != 0;
+    return PK_OK;
+}
+
+static int trace_fetch(pk_engine *e, const float *dev, int n, std::vector<float> &host) {
+    host.resize((size_t)n);
+    PK_HIP(hipMemcpyAsync(host.data(), dev, (size_t)n * 4, hipMemcpyDeviceToHost, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+int pk_trace_vec(pk_engine *e, const char *stage, int layer, const float *dev, int n) {
+    if (!e->trace_numeric || e->capturing) return PK_OK;
+    std::vector<float> v;
+    PK_TRY(trace_fetch(e, dev, n, v));
+    int bad = 0;
+    float lo = INFINITY, hi = -INFINITY;
+    double ss = 0.0;
+    for (float x : v) {
+        if (!std::isfinite(x)) { ++bad; continue; }
+        lo = std::min(lo, x);
+        hi = std::max(hi, x);
+        ss += (double)x * x;
+    }
+    fprintf(stderr, "  numeric L=%d %-18s min=% .6g max=% .6g rms=%.6g bad=%d\n", layer, stage, lo, hi,
+            n > bad ? std::sqrt(ss / (n - bad)) : NAN, bad);
+    return PK_OK;
+}
+
+int pk_trace_route(pk_engine *e, int layer, const float *logits_dev) {
+    if (!e->trace_numeric || e->capturing) return PK_OK;
+    const int E = e->c.n_experts, K = e->c.topk;
+    std::vector<float> v;
+    PK_TRY(trace_fetch(e, logits_dev, E, v));
+    // repeated argmax with strict '>' (the lowest index wins a tie), as moe_forward
+    std::vector<int> sel;
+    std::vector<bool> taken((size_t)E, false);
+    for (int k = 0; k <= K && k < E; ++k) {
+        int bi = -1;
+        for (int i = 0; i < E; ++i)
+            if (!taken[i] && (bi < 0 || v[i] > v[bi])) bi = i;
+        taken[bi] = true;
+        sel.push_back(bi);
+    }
+    float m = -INFINITY, sum = 0.0f, w[16];
+    const int kk = std::min(K, 16);
+    for (int k = 0; k < kk; ++k) m = std::max(m, v[sel[k]]);
+    for (int k = 0; k < kk; ++k) { w[k] = std::exp(v[sel[k]] - m); sum += w[k]; }
+    fprintf(stderr, "  numeric route L=%d:", layer);
+    for (int k = 0; k < kk; ++k) fprintf(stderr, " e%d=%.7g", sel[k], w[k] / sum);
+    if ((int)sel.size() > K) fprintf(stderr, " margin%d/%d=%.3g", K, K + 1, v[sel[K - 1]] - v[sel[K]]);
+    fprintf(stderr, "\n");
+    return PK_OK;
+}
+
+int pk_trace_top_logits(pk_engine *e, const float *logits_dev) {
+    if (!e->trace_numeric || e->capturing) return PK_OK;
+    const int V = e->c.vocab;
+    std::vector<float> v;
+    PK_TRY(trace_fetch(e, logits_dev, V, v));
+    int ids[10], bad = 0;
+    float vals[10];
+    for (int k = 0; k < 10; ++k) { ids[k] = -1; vals[k] = -INFINITY; }
+    for (int i = 0; i < V; ++i) {
+        if (!std::isfinite(v[i])) { ++bad; continue; }
+        if (v[i] <= vals[9]) continue;
+        int k = 9;
+        while (k > 0 && vals[k - 1] < v[i]) { vals[k] = vals[k - 1]; ids[k] = ids[k - 1]; --k; }
+        vals[k] = v[i];
+        ids[k] = i;
+    }
+    fprintf(stderr, "  numeric logits bad=%d top10:", bad);
+    for (int k = 0; k < 10; ++k) fprintf(stderr, " %d=%.6g", ids[k], vals[k]);
+    fprintf(stderr, "\n");
     return PK_OK;
 }
 
@@ -812,6 +923,8 @@ int pk_moe_layer(pk_engine *e, int layer, const float *x_dev, float *out_dev,
     const bool dot = e->i4_dot && c->hidden % 64 == 0 && c->moe_inter % 128 == 0;
     PK_TRY(moe_router(e, layer, x_dev, norm_w, dot, e->r_logits));
     PK_TRY(pk_prof_end(e, ps));
+    PK_TRY(pk_trace_router(e, e->r_logits, 1));
+    PK_TRY(pk_trace_route(e, layer, e->r_logits));
     pk_route_args rt{};
     rt.logits = e->r_logits;
     rt.E = c->n_experts;

@@ -198,6 +198,7 @@ static int route_rows(pk_engine *e, const rows_scratch &sc, int layer, const flo
         PK_TRY(pk_launch_router_seq(x, d.router, d.router_b, T, c->hidden, c->n_experts, sc.logits, e->stream));
     else
         PK_TRY(pk_launch_gemv_f32(sc.logits, x, d.router, d.router_b, T, c->hidden, c->n_experts, e->stream));
+    PK_TRY(pk_trace_router(e, sc.logits, T));
     return pk_launch_topk_batch(sc.logits, T, c->n_experts, c->topk, c->routed_scale, sc.sel, sc.w, nullptr,
                                 e->stream);
 }

@@ -80,6 +80,8 @@ class Oracle:
         self.rope_apply = _bind(L, "po_rope_apply", None, C.POINTER(PkCfg), f32p, f32p, C.c_int)
         self.yarn_inv_freq = _bind(L, "po_yarn_inv_freq", C.c_float, C.POINTER(PkCfg), C.c_int)
         self.forward_token = _bind(L, "po_forward_token", C.c_int, vp, C.c_int, C.c_int, vp)
+        self.set_router_trace = _bind(L, "po_set_router_trace", None, vp, C.c_int64)
+        self.router_trace_used = _bind(L, "po_router_trace_used", C.c_int64)
         self.forward_prefill = _bind(L, "po_forward_prefill", C.c_int, vp, i32p, C.c_int, C.c_int)
         self.prefill_tokens = _bind(L, "po_prefill_tokens", C.c_int, vp, i32p, C.c_int, C.c_int, C.c_int)
         self.argmax = _bind(L, "po_argmax", C.c_int, f32p, C.c_int)

@@ -163,6 +163,65 @@ def test_forward_token_parity(dec_setup, oracle):
             assert nxt == nxt_ref, (pos, nxt, nxt_ref)
 
 
+def test_router_trace_and_numeric_trace(dec_setup, oracle, capfd):
+    """Diagnostics. pk_set_router_trace: forward_token appends each layer's
+    router logits (n_layers rows per token), which agree with the oracle's
+    in-order router along the same chain (po_set_router_trace) within the
+    fixed-tree sum's 1e-5, with the same top-4 wherever the 4th / 5th margin
+    exceeds that; a launch past the buffer's capacity is not kept. With the
+    numeric trace on, forward_token prints picchio's TRACE_NUMERIC lines
+    (picchio.c:251-288): stage statistics, the routing with its margin, the
+    top-10 logits led by the greedy id."""
+    import re
+    import torch
+    cfg, model, eng = dec_setup
+    L, E, K = cfg.n_layers, cfg.n_experts, cfg.topk
+    ids = [int(v) for v in np.random.default_rng(8).integers(0, cfg.vocab, 3)]
+    tr = eng.empty(3 * L * E + E - 1, torch.float32)
+    otr = np.zeros(3 * L * E, np.float32)
+    oracle.model_reset_kv(model)
+    eng.set_router_trace(tr)
+    oracle.set_router_trace(otr.ctypes.data, otr.size)
+    try:
+        for pos, tok in enumerate(ids):
+            eng.forward_token(tok, pos, None)
+            oracle.forward_token(model, tok, pos, None)
+        assert eng.router_trace_used() == 3 * L * E
+        assert oracle.router_trace_used() == 3 * L * E
+        eng.forward_token(ids[-1], 3, None)               # does not fit: not kept
+        assert eng.router_trace_used() == 3 * L * E
+    finally:
+        eng.set_router_trace(None)
+        oracle.set_router_trace(None, 0)
+    got = eng.to_host(tr)[:3 * L * E].reshape(3 * L, E)
+    ref = otr.reshape(3 * L, E)
+    assert np.max(np.abs(got - ref)) < 1e-5
+    for g, r in zip(got, ref):
+        srt = np.sort(r)[::-1]
+        if E == K or srt[K - 1] - srt[K] > 1e-5:
+            assert set(np.argsort(-g)[:K]) == set(np.argsort(-r)[:K])
+
+    capfd.readouterr()
+    eng.set_numeric_trace(True)
+    try:
+        lg = eng.empty(cfg.vocab, torch.float32)
+        nxt = eng.forward_token(ids[0], 4, lg)
+    finally:
+        eng.set_numeric_trace(False)
+    err = capfd.readouterr().err
+    assert "numeric L=-1 embedding" in err and "bad=0" in err
+    for l in range(L):
+        assert f"numeric L={l} post_attention" in err and f"numeric L={l} post_moe" in err
+        # (the 4th / 5th margin only where the layer has a 5th expert)
+        m = re.search(rf"numeric route L={l}:((?: e\d+=[^ \n]+)+)( margin4/5=(\S+))?\n", err)
+        assert m, err
+        assert len(re.findall(r"e\d+=", m.group(1))) == K
+        assert (m.group(3) is not None) == (E > K) and (E == K or float(m.group(3)) >= 0.0)
+    top = re.search(r"numeric logits bad=0 top10: (\d+)=", err)
+    assert top and int(top.group(1)) == nxt, err
+    assert int(np.argmax(eng.to_host(lg))) == nxt
+
+
 def test_out_of_range_token_embeds_zero(dec_setup, oracle):
     """embed_token gives a zero row for ids outside the vocabulary (picchio.c:1476-1480)."""
     import torch
