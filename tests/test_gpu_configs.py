@@ -1,4 +1,8 @@
-"""BASELINE configs 3 and 4 at their own shapes.
+"""BASELINE configs 1, 3 and 4 at their own shapes.
+
+Config 1: one GPT-OSS-20B MoE layer with all 32 experts at batch-1 decode
+(router launch + one-launch experts) against the oracle's moe_forward, the
+4th / 5th router-logit margin of every token logged, both arithmetics.
 
 Config 3: one GPT-OSS-20B MoE layer (32 experts) over T = 2048 tokens with
 the Zipf(1.1) routing of the benchmark (8192 (token, expert) pairs, 16..512
@@ -41,6 +45,64 @@ def _seq0_seed_like(seed, s):
 def _margin(lg):
     top = np.sort(lg)[-2:]
     return float(top[1] - top[0]), float(abs(top[1]))
+
+
+# ───────────────────────────── config 1 ─────────────────────────────
+
+@pytest.mark.parametrize("dot", [0, 1], ids=["fp32", "dot"])
+def test_config1_moe_layer_32_experts(gpu, oracle, dot):
+    """Config 1 at its own shape: one GPT-OSS-20B MoE layer with all 32
+    experts (router 32 x 2880 + bias), batch-1 tokens through pk_moe_forward
+    (router launch, then the one-launch experts) against the oracle's
+    moe_forward (picchio.c:1309-1466). Every token's 4th / 5th router-logit
+    margin is logged; the selected experts are identical wherever that
+    margin exceeds the router sums' difference (the GPU router adds in a
+    fixed tree, picchio in order: within 1e-5), and the layer output is
+    within relative L2 1e-4 (fp32 chains: ~3e-6, from the routing weights;
+    integer dot: ~2e-5)."""
+    import torch
+    import picchio_amd as pa
+    cfg = pa.gptoss_cfg(n_layers=1, n_experts=32, ctx_len=16, vocab=64)
+    D, E, K = cfg.hidden, cfg.n_experts, cfg.topk
+    model = oracle.model_build(cfg, 31337, 0)
+    eng = pa.Engine(cfg)
+    try:
+        for e in range(E):
+            eng.store_expert(0, e, *oracle.expert_arrays(model, 0, e, cfg))
+        eng.store_router(0, oracle.tensor(model, 6, 0, E * D), oracle.tensor(model, 7, 0, E))
+        eng.set_i4_dot(dot)
+        margins, worst, hist = [], 0.0, np.zeros(E, np.int64)
+        for t in range(40):
+            x = oracle.normal(4242, 1, t, 0, D)
+            xn = np.empty_like(x)
+            oracle.rmsnorm(xn, x, np.ones(D, np.float32), D, 1e-5)
+            out_ref = np.empty(D, np.float32)
+            sel_ref = np.empty(K, np.int32)
+            w_ref = np.empty(K, np.float32)
+            logits = np.empty(E, np.float32)
+            oracle.moe_forward(model, 0, xn, out_ref, sel_ref, w_ref, logits)
+            od = eng.empty(D, torch.float32)
+            sel, w = eng.moe_forward(0, eng.to_dev(xn), od, want_routing=True)
+            m = _route_margin(logits, K)
+            margins.append(m)
+            hist[list(sel_ref)] += 1
+            if m > 1e-5:
+                assert list(sel) == list(sel_ref), (t, list(sel), list(sel_ref), m)
+                err = rel_l2(eng.to_host(od), out_ref)
+                worst = max(worst, err)
+                assert err < 1e-4, (t, err)
+        eng.sync()
+        print(f"config 1 ({'integer dot' if dot else 'fp32 chains'}): 40 tokens, 4th/5th router margins min "
+              f"{min(margins):.2e} median {np.median(margins):.2e}; experts hit {int((hist > 0).sum())} of {E}; "
+              f"worst rel-L2 {worst:.2e}", flush=True)
+        assert (hist > 0).sum() >= 24                       # the tokens spread over the experts
+        # fp32 chains: the experts are picchio's bits; what differs is the
+        # routing weights' softmax of the fixed-tree router logits (~1e-6)
+        assert worst < (1e-5 if not dot else 1e-4)
+    finally:
+        eng.set_i4_dot(0)
+        eng.close()
+        oracle.model_free(model)
 
 
 # ───────────────────────────── config 3 ─────────────────────────────
