@@ -10,7 +10,9 @@
 // the converter's (convert.py:216-334, :440-470): F32 norms, biases, router,
 // sinks and attention; INT8-per-row (or F32) embedding and lm_head with a
 // ".qs" tensor of row scales; INT4 experts as uint8 [O][I/2] with ".qs" group
-// scales; expert biases F32, aggregated [E][n] or per expert.
+// scales; expert biases F32, aggregated [E][n] or per expert. Embedding,
+// lm_head and attention also take load_qt_i4's other forms (BF16 / F16
+// quantized to INT4 rows, INT4 rows or groups, INT8 rows).
 //
 // Host code only: it reads the shards with pread and hands each tensor to the
 // engine's store entry points (pk_store_expert / _layer / _globals).
@@ -499,47 +501,140 @@ int read_expert_bias(const StDb &db, int layer, int eid, const char *suffix, int
     return db.read(*t, out.data(), off, (int64_t)n * 4);
 }
 
-// Embedding as fp32 rows: F32 / BF16 / F16 as load_f32_tensor, INT8 per row
-// and INT4 dequantized with embed_token's arithmetic (picchio.c:1482-1502).
-int read_embedding(const StDb &db, int V, int D, std::vector<float> &out) {
-    const std::string name = "model.embed_tokens.weight";
-    const StTensor *t = db.find(name);
-    PK_CHECK(t, PK_ERR_MISSING, "container: %s not found", name.c_str());
-    if (t->dtype == ST_F32 || t->dtype == ST_BF16 || t->dtype == ST_F16)
-        return read_f32(db, name, (int64_t)V * D, out);
-    const StTensor *ts = db.find(name + ".qs");
-    PK_CHECK(ts && ts->dtype == ST_F32, PK_ERR_ARG, "container: %s.qs missing", name.c_str());
-    std::vector<float> sc(ts->numel());
-    PK_TRY(db.read(*ts, sc.data(), 0, (int64_t)sc.size() * 4));
-    out.resize((int64_t)V * D);
-    if (t->dtype == ST_I8) {
-        PK_CHECK(t->numel() == (int64_t)V * D && (int64_t)sc.size() == V, PK_ERR_ARG,
-                 "container: INT8 embedding of %lld values, %zu scales", (long long)t->numel(), sc.size());
-        std::vector<int8_t> q((int64_t)V * D);
-        PK_TRY(db.read(*t, q.data(), 0, (int64_t)q.size()));
-        for (int64_t r = 0; r < V; ++r)
-            for (int i = 0; i < D; ++i) out[r * D + i] = (float)q[r * D + i] * sc[r];
-        return PK_OK;
-    }
-    PK_CHECK(t->dtype == ST_U8, PK_ERR_UNSUPPORTED, "container: embedding dtype %d", (int)t->dtype);
-    const int64_t rb = (D + 1) / 2;
-    PK_CHECK(t->numel() == V * rb, PK_ERR_ARG, "container: INT4 embedding size");
-    const int64_t ns = (int64_t)sc.size();
-    const int gs = ns > V ? (int)((int64_t)V * D / ns) : 0;
-    const int ng = gs > 0 ? (D + gs - 1) / gs : 1;
-    PK_CHECK(ns == (int64_t)V * ng, PK_ERR_ARG, "container: INT4 embedding scales");
-    std::vector<uint8_t> q(V * rb);
-    PK_TRY(db.read(*t, q.data(), 0, (int64_t)q.size()));
-    for (int64_t r = 0; r < V; ++r) {
-        const float *s = sc.data() + r * ng;
-        for (int i = 0; i < D; i += 2) {
-            const uint8_t byte = q[r * rb + (i >> 1)];
-            out[r * D + i] = (float)((int)(byte & 0xF) - 8) * s[gs > 0 ? i / gs : 0];
-            if (i + 1 < D) out[r * D + i + 1] = (float)((int)(byte >> 4) - 8) * s[gs > 0 ? (i + 1) / gs : 0];
+// quantize_rows_i4 (quant.h:366-392): per row s = amax / 7 (at least
+// 1e-8), v = lrintf(w / s) clipped to [-8, 7]. Values are kept signed
+// (nibble - 8), one per byte.
+void quantize_rows_i4(const float *w, int64_t r0, int64_t r1, int I, int8_t *q, float *s) {
+    for (int64_t o = r0; o < r1; ++o) {
+        const float *wr = w + o * I;
+        float amax = 0.0f;
+        for (int i = 0; i < I; ++i) amax = std::max(amax, fabsf(wr[i]));
+        float sc = amax / 7.0f;
+        if (sc < 1e-8f) sc = 1e-8f;
+        s[o] = sc;
+        for (int i = 0; i < I; ++i) {
+            int v = (int)lrintf(wr[i] / sc);
+            q[o * I + i] = (int8_t)std::min(7, std::max(-8, v));
         }
     }
+}
+
+// A dense matrix [O][I] in the form load_qt_i4 (picchio.c:2443-2531) leaves
+// it: F32 kept F32; I8 rows with ".qs" row scales; U8 nibbles with ".qs"
+// row scales, group scales (more scales than rows: group size O*I/n), or
+// none (every row scale 1.0); BF16 / F16 quantized to INT4 rows. ROWS and
+// GROUPS hold the signed values (nibble - 8 for INT4) one per byte.
+struct QtHost {
+    enum Kind { F32, ROWS, GROUPS };
+    Kind kind = F32;
+    int O = 0, I = 0, gs = 0;
+    std::vector<float> f;
+    std::vector<int8_t> q;
+    std::vector<float> s;
+    // (float)q * scale per value: embed_token's product (picchio.c:1482-1502)
+    void dequant(std::vector<float> &out) const {
+        if (kind == F32) {
+            out = f;
+            return;
+        }
+        out.resize((int64_t)O * I);
+        const int ng = kind == GROUPS ? (I + gs - 1) / gs : 1;
+        for (int64_t o = 0; o < O; ++o)
+            for (int i = 0; i < I; ++i)
+                out[o * I + i] = (float)q[o * I + i] * s[o * ng + (kind == GROUPS ? i / gs : 0)];
+    }
+};
+
+// What load_qt_i4 makes of a tensor, from its dtype and the ".qs" beside it,
+// with the sizes checked (the reference reads what the shapes say; a short
+// tensor or scale vector is an error here).
+int qt_layout(const StDb &db, const std::string &name, int O, int I, QtHost::Kind &kind, int &gs) {
+    const StTensor *t = db.find(name);
+    if (!t) {
+        pk_set_error("container: tensor %s not found", name.c_str());
+        return PK_ERR_MISSING;
+    }
+    gs = 0;
+    const int64_t n = (int64_t)O * I;
+    const StTensor *ts = db.find(name + ".qs");
+    if (t->dtype == ST_F32 || t->dtype == ST_BF16 || t->dtype == ST_F16) {
+        PK_CHECK(t->numel() == n, PK_ERR_ARG, "container: %s has %lld values, expected %lld", name.c_str(),
+                 (long long)t->numel(), (long long)n);
+        kind = t->dtype == ST_F32 ? QtHost::F32 : QtHost::ROWS;
+        return PK_OK;
+    }
+    if (t->dtype == ST_I8) {
+        PK_CHECK(t->numel() == n && ts && ts->dtype == ST_F32 && ts->numel() == O, PK_ERR_ARG,
+                 "container: INT8 %s needs [%d,%d] values and %d F32 row scales", name.c_str(), O, I, O);
+        kind = QtHost::ROWS;
+        return PK_OK;
+    }
+    PK_CHECK(t->dtype == ST_U8, PK_ERR_UNSUPPORTED, "container: %s dtype %d", name.c_str(), (int)t->dtype);
+    PK_CHECK(t->numel() == (int64_t)O * ((I + 1) / 2), PK_ERR_ARG, "container: INT4 %s: %lld bytes for [%d,%d]",
+             name.c_str(), (long long)t->numel(), O, I);
+    kind = QtHost::ROWS;
+    if (!ts) return PK_OK;
+    PK_CHECK(ts->dtype == ST_F32, PK_ERR_ARG, "container: %s.qs is not F32", name.c_str());
+    const int64_t ns = ts->numel();
+    if (ns > O) {
+        gs = (int)(n / ns);
+        if (gs <= 0) gs = 64;
+        PK_CHECK(ns == (int64_t)O * ((I + gs - 1) / gs), PK_ERR_ARG,
+                 "container: %s: %lld scales for [%d,%d] and group size %d", name.c_str(), (long long)ns, O, I, gs);
+        kind = QtHost::GROUPS;
+        return PK_OK;
+    }
+    PK_CHECK(ns == O, PK_ERR_ARG, "container: %s: %lld scales for %d rows", name.c_str(), (long long)ns, O);
     return PK_OK;
 }
+
+int read_qt(const StDb &db, const std::string &name, int O, int I, int n_threads, QtHost &out) {
+    PK_TRY(qt_layout(db, name, O, I, out.kind, out.gs));
+    out.O = O;
+    out.I = I;
+    const StTensor *t = db.find(name);
+    const StTensor *ts = db.find(name + ".qs");
+    const int64_t n = (int64_t)O * I;
+    if (t->dtype == ST_F32) return read_f32(db, name, n, out.f);
+    if (t->dtype == ST_BF16 || t->dtype == ST_F16) {
+        std::vector<float> w;
+        PK_TRY(read_f32(db, name, n, w));
+        out.q.resize(n);
+        out.s.resize(O);
+        const int nt = std::max(1, std::min(n_threads, 64));
+        std::vector<std::thread> pool;
+        for (int k = 0; k < nt; ++k)
+            pool.emplace_back(quantize_rows_i4, w.data(), (int64_t)O * k / nt, (int64_t)O * (k + 1) / nt, I,
+                              out.q.data(), out.s.data());
+        for (auto &th : pool) th.join();
+        return PK_OK;
+    }
+    out.q.resize(n);
+    if (t->dtype == ST_I8) {
+        out.s.resize(O);
+        PK_TRY(db.read(*t, out.q.data(), 0, n));
+        return db.read(*ts, out.s.data(), 0, (int64_t)O * 4);
+    }
+    const int64_t rb = (I + 1) / 2;
+    std::vector<uint8_t> packed((int64_t)O * rb);
+    PK_TRY(db.read(*t, packed.data(), 0, (int64_t)packed.size()));
+    for (int64_t o = 0; o < O; ++o)
+        for (int i = 0; i < I; ++i) {
+            const uint8_t byte = packed[o * rb + (i >> 1)];
+            out.q[o * I + i] = (int8_t)(((i & 1) ? byte >> 4 : byte & 0x0F) - 8);
+        }
+    if (!ts) {
+        out.s.assign(O, 1.0f);
+        return PK_OK;
+    }
+    out.s.resize(ts->numel());
+    return db.read(*ts, out.s.data(), 0, (int64_t)out.s.size() * 4);
+}
+
+// The engine's lm_head formats for load_qt_i4's results: INT4 or INT8 rows
+// as INT8 rows (matmul_i4 and matmul_q8 are the same sum of x * q times the
+// row scale, quant.h:152-257); F32 and group-scaled INT4 as F32.
+int lm_head_fmt_of(QtHost::Kind k) { return k == QtHost::ROWS ? PK_FMT_INT8 : PK_FMT_F32; }
 
 // cfg_load's reads (picchio.c:349-420). The reference looks a key up
 // anywhere in the text, so the rope_scaling entries (factor, beta_fast, ...)
@@ -621,9 +716,10 @@ extern "C" int pk_cfg_from_container(const char *dir, int ctx_len, pk_cfg *out) 
             break;
         }
     }
-    const StTensor *lm = db.find("lm_head.weight");
-    PK_CHECK(lm, PK_ERR_MISSING, "container: lm_head.weight not found");
-    c.lm_head_fmt = lm->dtype == ST_I8 ? PK_FMT_INT8 : PK_FMT_F32;
+    QtHost::Kind lm_kind;
+    int lm_gs;
+    PK_TRY(qt_layout(db, "lm_head.weight", c.vocab, c.hidden, lm_kind, lm_gs));
+    c.lm_head_fmt = lm_head_fmt_of(lm_kind);
     *out = c;
     return PK_OK;
 }
@@ -638,30 +734,23 @@ extern "C" int pk_load_container(pk_engine *e, const char *dir, int n_threads) {
 
     // ── globals (load_dense_weights, picchio.c:2546-2575) ──
     {
+        const int nt = std::max(1, std::min(n_threads > 0 ? n_threads : 8, 64));
         std::vector<float> emb, lmf, fn;
-        PK_TRY(read_embedding(db, V, D, emb));
-        const StTensor *lm = db.find("lm_head.weight");
-        PK_CHECK(lm, PK_ERR_MISSING, "container: lm_head.weight not found");
+        {
+            QtHost et;
+            PK_TRY(read_qt(db, "model.embed_tokens.weight", V, D, nt, et));
+            et.dequant(emb);
+        }
+        QtHost lt;
+        PK_TRY(read_qt(db, "lm_head.weight", V, D, nt, lt));
+        PK_CHECK(lm_head_fmt_of(lt.kind) == c->lm_head_fmt, PK_ERR_ARG,
+                 "container: lm_head format %d, engine built for %d", lm_head_fmt_of(lt.kind), c->lm_head_fmt);
         pk_qt_host eh{PK_FMT_F32, emb.data(), nullptr, V, D, 0};
         pk_qt_host lh{};
-        std::vector<int8_t> lq;
-        std::vector<float> ls;
-        if (lm->dtype == ST_I8) {
-            // INT8 per row with its row scales (load_qt_i4's I8 branch, picchio.c:2485-2511)
-            const StTensor *ts = db.find("lm_head.weight.qs");
-            PK_CHECK(lm->numel() == (int64_t)V * D && ts && ts->numel() == V, PK_ERR_ARG,
-                     "container: INT8 lm_head needs [%d,%d] and %d row scales", V, D, V);
-            lq.resize((int64_t)V * D);
-            ls.resize(V);
-            PK_TRY(db.read(*lm, lq.data(), 0, (int64_t)lq.size()));
-            PK_TRY(db.read(*ts, ls.data(), 0, (int64_t)V * 4));
-            lh = pk_qt_host{PK_FMT_INT8, lq.data(), ls.data(), V, D, 0};
+        if (lt.kind == QtHost::ROWS) {
+            lh = pk_qt_host{PK_FMT_INT8, lt.q.data(), lt.s.data(), V, D, 0};
         } else {
-            // F32 (kept F32); BF16/F16 would be quantized to INT4 rows by the
-            // reference (picchio.c:2524-2530), a format this lm_head does not hold
-            PK_CHECK(lm->dtype == ST_F32, PK_ERR_UNSUPPORTED, "container: lm_head dtype %d (F32 or INT8)",
-                     (int)lm->dtype);
-            PK_TRY(read_f32(db, "lm_head.weight", (int64_t)V * D, lmf));
+            lt.dequant(lmf);
             lh = pk_qt_host{PK_FMT_F32, lmf.data(), nullptr, V, D, 0};
         }
         PK_TRY(read_f32_or(db, "model.norm.weight", D, 1.0f, fn));
@@ -674,19 +763,23 @@ extern "C" int pk_load_container(pk_engine *e, const char *dir, int n_threads) {
         auto p = [l](const char *rest) { return fmtname("model.layers.%d.", l) + rest; };
         PK_TRY(read_f32_or(db, p("input_layernorm.weight"), D, 1.0f, in_ln));
         PK_TRY(read_f32_or(db, p("post_attention_layernorm.weight"), D, 1.0f, post_ln));
-        // attention stays F32 in the converter's output (convert.py:305-309);
-        // BF16/F16 would be quantized to INT4 rows by load_qt_i4
-        for (const char *w : {"self_attn.q_proj.weight", "self_attn.k_proj.weight", "self_attn.v_proj.weight",
-                              "self_attn.o_proj.weight"}) {
-            const StTensor *t = db.find(p(w));
-            PK_CHECK(t, PK_ERR_MISSING, "container: %s not found", p(w).c_str());
-            PK_CHECK(t->dtype == ST_F32, PK_ERR_UNSUPPORTED, "container: %s dtype %d (F32 attention)",
-                     p(w).c_str(), (int)t->dtype);
+        // attention is F32 in the converter's output (convert.py:305-309) and
+        // stays F32; load_qt_i4's other forms (INT8 rows, INT4 rows or groups,
+        // BF16/F16 quantized to INT4 rows) are held as their fp32 values
+        // q * scale, so the projections compute sum(x * q * s) where
+        // matmul_q8 / matmul_i4 compute sum(x * q) * s
+        {
+            QtHost t;
+            const int nt = std::max(1, std::min(n_threads > 0 ? n_threads : 8, 64));
+            PK_TRY(read_qt(db, p("self_attn.q_proj.weight"), H * hd, D, nt, t));
+            t.dequant(wq);
+            PK_TRY(read_qt(db, p("self_attn.k_proj.weight"), KVH * hd, D, nt, t));
+            t.dequant(wk);
+            PK_TRY(read_qt(db, p("self_attn.v_proj.weight"), KVH * hd, D, nt, t));
+            t.dequant(wv);
+            PK_TRY(read_qt(db, p("self_attn.o_proj.weight"), D, H * hd, nt, t));
+            t.dequant(wo);
         }
-        PK_TRY(read_f32(db, p("self_attn.q_proj.weight"), (int64_t)H * hd * D, wq));
-        PK_TRY(read_f32(db, p("self_attn.k_proj.weight"), (int64_t)KVH * hd * D, wk));
-        PK_TRY(read_f32(db, p("self_attn.v_proj.weight"), (int64_t)KVH * hd * D, wv));
-        PK_TRY(read_f32(db, p("self_attn.o_proj.weight"), (int64_t)D * H * hd, wo));
         PK_TRY(read_f32_or(db, p("self_attn.q_proj.bias"), H * hd, 0.0f, bq));
         PK_TRY(read_f32_or(db, p("self_attn.k_proj.bias"), KVH * hd, 0.0f, bk));
         PK_TRY(read_f32_or(db, p("self_attn.v_proj.bias"), KVH * hd, 0.0f, bv));

@@ -20,7 +20,6 @@ namespace {
 constexpr int ATT_CHUNK = 128;         // positions per attention partial
 
 __device__ __forceinline__ float wave_sum(float v) { return pk_wave_sum_f(v); }
-__device__ __forceinline__ double wave_sum_d(double v) { return pk_wave_sum_d(v); }
 
 // Token row -> h (zeros for an out-of-range id, picchio.c:1476-1480), and
 // hn = rmsnorm(h) (quant.h:396-402: double sum of squares).

@@ -3,13 +3,80 @@
 safetensors shards holding F32 norms / biases / router / sinks / attention,
 F32 or INT8-per-row (+ ".qs" row scales) embedding and lm_head, INT4 experts
 as uint8 [O][I/2] + ".qs" group scales, and F32 expert biases (aggregated
-[E][n] or per expert). Test infrastructure: the tensors come from the
-oracle's model or from numpy."""
+[E][n] or per expert). Dense tensors may also be BF16 / F16 / INT8 / INT4
+(load_qt_i4's other inputs, picchio.c:2443-2531). Test infrastructure: the
+tensors come from the oracle's model or from numpy."""
 import json
 import os
+import struct
 
 import numpy as np
-from safetensors.numpy import save_file
+
+_ST_DTYPE = {np.dtype(np.float32): "F32", np.dtype(np.float16): "F16", np.dtype(np.int8): "I8",
+             np.dtype(np.uint8): "U8", np.dtype(np.int32): "I32", np.dtype(np.float64): "F64"}
+
+
+class BF16:
+    """A tensor to be stored as BF16: fp32 values rounded to nearest even."""
+
+    def __init__(self, f32):
+        f32 = np.ascontiguousarray(f32, np.float32)
+        u = f32.view(np.uint32).astype(np.uint64)
+        self.bits = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+        self.shape = f32.shape
+
+    def to_f32(self):
+        """load_f32_tensor's BF16 rule (picchio.c:2404-2411): the high half."""
+        return (self.bits.astype(np.uint32) << 16).view(np.float32).reshape(self.shape)
+
+
+def f16_to_f32(h):
+    """load_f32_tensor's F16 rule (picchio.c:2412-2429): subnormals become
+    signed zero."""
+    f = np.asarray(h, np.float16).astype(np.float32)
+    sub = (np.asarray(h, np.float16).view(np.uint16) & 0x7C00) == 0
+    return np.where(sub, np.copysign(np.float32(0), f), f).astype(np.float32)
+
+
+def save_shard(path, tensors):
+    """A safetensors file: u64 header length, JSON header (dtype, shape,
+    data_offsets), then the tensors' bytes in order."""
+    header, blobs, off = {}, [], 0
+    for name, v in tensors.items():
+        if isinstance(v, BF16):
+            dt, shape, raw = "BF16", v.shape, v.bits.tobytes()
+        else:
+            v = np.ascontiguousarray(v)
+            dt, shape, raw = _ST_DTYPE[v.dtype], v.shape, v.tobytes()
+        header[name] = {"dtype": dt, "shape": list(shape), "data_offsets": [off, off + len(raw)]}
+        blobs.append(raw)
+        off += len(raw)
+    h = json.dumps(header).encode()
+    h += b" " * (-len(h) % 8)
+    with open(path, "wb") as f:
+        f.write(struct.pack("<Q", len(h)))
+        f.write(h)
+        for b in blobs:
+            f.write(b)
+
+
+def pack_i4(q):
+    """Signed values in [-8, 7] of [O][I] as picchio's nibbles (value + 8,
+    even index in the low half, quant.h:386-390)."""
+    q = np.asarray(q, np.int16) + 8
+    O, I = q.shape
+    if I % 2:
+        q = np.concatenate([q, np.full((O, 1), 8, np.int16)], axis=1)
+    return (q[:, 0::2] | (q[:, 1::2] << 4)).astype(np.uint8)
+
+
+def unpack_i4(packed, I):
+    """pack_i4's inverse: signed int8 values [O][I]."""
+    lo = (packed & 0x0F).astype(np.int8) - 8
+    hi = (packed >> 4).astype(np.int8) - 8
+    out = np.empty((packed.shape[0], packed.shape[1] * 2), np.int8)
+    out[:, 0::2], out[:, 1::2] = lo, hi
+    return out[:, :I]
 
 
 def config_json(cfg):
@@ -66,8 +133,7 @@ def write_container(path, cfg, tensors, experts, per_expert_names=False, lm_int8
         dense["lm_head.weight"], dense["lm_head.weight.qs"] = lm_int8
     if embed_int8 is not None:
         dense["model.embed_tokens.weight"], dense["model.embed_tokens.weight.qs"] = embed_int8
-    save_file({k: np.ascontiguousarray(v) for k, v in dense.items()},
-              os.path.join(path, "model-00000.safetensors"))
+    save_shard(os.path.join(path, "model-00000.safetensors"), dense)
     E = cfg.n_experts
     shards = [dict() for _ in range(expert_shards)]
     for l, layer in enumerate(experts):
@@ -88,8 +154,7 @@ def write_container(path, cfg, tensors, experts, per_expert_names=False, lm_int8
                 sh[f"{p}.down_proj.{e}"], sh[f"{p}.down_proj.{e}.qs"] = dq, ds
     for i, sh in enumerate(shards):
         if sh:
-            save_file({k: np.ascontiguousarray(v) for k, v in sh.items()},
-                      os.path.join(path, f"model-{i + 1:05d}.safetensors"))
+            save_shard(os.path.join(path, f"model-{i + 1:05d}.safetensors"), sh)
 
 
 def oracle_tensors(oracle, model, cfg):

@@ -98,3 +98,97 @@ def test_container_errors(tmp_path):
     with pytest.raises(pa.PkError) as e:
         pa.cfg_from_container(str(tmp_path))
     assert e.value.code == -1
+
+
+def _lm_head_variants(cfg, rng):
+    """lm_head.weight in each form load_qt_i4 accepts (picchio.c:2443-2531),
+    with the engine format it maps to."""
+    from container_writer import BF16, pack_i4
+    V, D = cfg.vocab, cfg.hidden
+    lm = (rng.standard_normal((V, D)) * 0.02).astype(np.float32)
+    q = rng.integers(-8, 8, (V, D)).astype(np.int8)
+    return [({"lm_head.weight": BF16(lm)}, "INT8"),
+            ({"lm_head.weight": lm.astype(np.float16)}, "INT8"),
+            ({"lm_head.weight": pack_i4(q), "lm_head.weight.qs": rng.random(V, np.float32)}, "INT8"),
+            ({"lm_head.weight": pack_i4(q)}, "INT8"),                        # no .qs: scales 1.0
+            ({"lm_head.weight": pack_i4(q), "lm_head.weight.qs": rng.random(V * D // 32, np.float32)}, "F32"),
+            ({"lm_head.weight": lm}, "F32")]
+
+
+def test_cfg_lm_head_format_of_each_form(tmp_path):
+    """INT4 or INT8 rows become the INT8-row lm_head (BF16 / F16 are
+    quantized to INT4 rows by load_qt_i4), F32 and group-scaled INT4 the F32
+    one."""
+    import picchio_amd as pa
+    cfg = _tiny(pa)
+    rng = np.random.default_rng(8)
+    ex = _random_experts(cfg, rng)
+    for i, (lm, fmt) in enumerate(_lm_head_variants(cfg, rng)):
+        d = str(tmp_path / f"v{i}")
+        write_container(d, cfg, {**lm, "model.norm.weight": np.ones(cfg.hidden, np.float32)}, ex)
+        assert pa.cfg_from_container(d).lm_head_fmt == getattr(pa, "FMT_" + fmt), i
+
+
+def test_cfg_rejects_inconsistent_int4_scales(tmp_path):
+    """A U8 lm_head whose .qs count is neither the row count nor a whole
+    number of groups per row is an error, not a read past the scales."""
+    import picchio_amd as pa
+    from container_writer import pack_i4
+    cfg = _tiny(pa)
+    rng = np.random.default_rng(9)
+    q = rng.integers(-8, 8, (cfg.vocab, cfg.hidden)).astype(np.int8)
+    for ns in (cfg.vocab - 1, cfg.vocab * 3):
+        d = str(tmp_path / f"n{ns}")
+        write_container(d, cfg, {"lm_head.weight": pack_i4(q), "lm_head.weight.qs": np.ones(ns, np.float32)},
+                        _random_experts(cfg, rng))
+        with pytest.raises(pa.PkError) as e:
+            pa.cfg_from_container(d)
+        assert e.value.code == -1, ns
+
+
+@pytest.mark.parametrize("I", [64, 128, 2880])
+def test_int4_rows_product_is_the_int8_row_product(oracle, I):
+    """The INT8-row lm_head holds INT4 rows as q = nibble - 8 with the row
+    scale: matmul_i4 (quant.h:191-257) and matmul_q8 (quant.h:152-186) sum
+    x * q in the same eight chains and scale once, so for I a multiple of 16
+    the two agree bit for bit."""
+    from container_writer import unpack_i4
+    rng = np.random.default_rng(I)
+    O = 24
+    w = rng.standard_normal((O, I)).astype(np.float32)
+    q4, s = np.empty((O, I // 2), np.uint8), np.empty(O, np.float32)
+    oracle.quantize_rows_i4(w, O, I, q4, s)
+    x = rng.standard_normal((3, I)).astype(np.float32)
+    y4, y8 = np.empty((3, O), np.float32), np.empty((3, O), np.float32)
+    oracle.matmul_i4(y4, x, q4, s, 3, I, O)
+    oracle.matmul_q8(y8, x, np.ascontiguousarray(unpack_i4(q4, I)), s, 3, I, O)
+    assert np.array_equal(y4.view(np.uint32), y8.view(np.uint32))
+
+
+@pytest.mark.parametrize("gs", [0, 64])
+def test_int4_attention_as_fp32_values(oracle, gs):
+    """Attention in INT4 is held as its fp32 values q * s: sum(x * q * s)
+    against matmul_i4's sum(x * q) * s (or matmul_i4_gs's per group) differs
+    by rounding only, bounded here by 1e-6 of sum |x * q * s|."""
+    from container_writer import unpack_i4
+    rng = np.random.default_rng(11 + gs)
+    O, I = 64, 2880
+    w = (rng.standard_normal((O, I)) * 0.02).astype(np.float32)
+    if gs:
+        q4, s = oracle.quant_gs(w, gs)
+    else:
+        q4, s = np.empty((O, I // 2), np.uint8), np.empty(O, np.float32)
+        oracle.quantize_rows_i4(w, O, I, q4, s)
+    s = s.reshape(O, -1)
+    q = unpack_i4(q4, I).astype(np.float32)
+    deq = (q * np.repeat(s, I // s.shape[1], axis=1)).astype(np.float32)
+    x = rng.standard_normal((2, I)).astype(np.float32)
+    yq, yf = np.empty((2, O), np.float32), np.empty((2, O), np.float32)
+    if gs:
+        oracle.matmul_i4_gs(yq, x, q4, s, 2, I, O, gs)
+    else:
+        oracle.matmul_i4(yq, x, q4, s.ravel(), 2, I, O)
+    oracle.matmul_f32(yf, x, deq, 2, I, O)
+    bound = 1e-6 * (np.abs(x.astype(np.float64)) @ np.abs(deq.astype(np.float64)).T)
+    assert (np.abs(yq.astype(np.float64) - yf) <= bound).all()
+    assert not np.array_equal(yq, yf)                     # the two orders do differ
