@@ -331,6 +331,19 @@ def measure_decode20b(args, steps, warmup, cpu_on):
     lm_ms, _ = eng.profile_read(pa.PROF_LM_HEAD)
     att_ms, att_n = eng.profile_read(pa.PROF_ATTENTION)
     eng.profile(False)
+    # the same steps with the experts on the integer-dot arithmetic (an
+    # option, not picchio's fp32 chains): rate and whether the stream matches
+    dot = None
+    if not sampling:
+        eng.set_i4_dot(True)
+        eng.decode_replay(nxt, n_prompt, max(warmup, 1))
+        ev0.record(eng.stream)
+        toks_dot = eng.decode_replay(nxt, n_prompt, steps)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        dot = {"tok_s": round(steps / (ev0.elapsed_time(ev1) * 1e-3), 2),
+               "same_stream": bool(list(toks_dot) == list(toks))}
+        eng.set_i4_dot(False)
     eng.close()
     tok_s = steps / (ms * 1e-3)
     bpt = sum(decode_bytes_per_token(cfg, n_prompt + i) for i in range(steps)) / steps
@@ -340,7 +353,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
         cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt, n_prompt)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     print(f"[bench] config 2: {tok_s:.1f} tok/s ({ms / steps * 1e3:.1f} us/token), prefill "
-          f"{prefill_s:.3f} s", file=sys.stderr, flush=True)
+          f"{prefill_s:.3f} s; integer-dot experts {dot}", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms / steps, 5),
@@ -357,6 +370,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
                    "hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
                    "prefill_s": round(prefill_s, 3), "prefill_tok_s": round(n_prompt / prefill_s, 1),
                    "attention_us_per_layer": round(att_ms / max(att_n, 1) * 1e3, 2),
+                   "integer_dot_experts": dot,
                    "first_tokens": [int(nxt)] + [int(t) for t in toks[:8]]},
         "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
