@@ -212,6 +212,7 @@ struct pk_mfma_args {
     const int32_t *pairs;                      // pair ids grouped by expert
     int x_div;                                 // activation row of pair p = p / x_div
     const int32_t *tile_exp, *tile_beg, *tile_cnt, *n_tiles;
+    const int32_t *tile_grp;                   // per tile: the expert's first tile, tile count (or null)
     float *y;                                  // output rows by pair id
     int64_t y_stride;
     float lim, alpha;                          // SwiGLU clamp / slope
@@ -221,7 +222,7 @@ int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, in
 // tile_pairs: pairs per tile (0: the MFMA GEMM's 32)
 int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int32_t *tile_exp,
                           int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
-                          int tile_pairs = 0);
+                          int tile_pairs = 0, int32_t *tile_grp = nullptr);
 int pk_launch_moe_mfma(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
 constexpr int64_t PK_SKINNY_WS = (int64_t)2 << 20;   // floats: 12 K splits x 32 rows x 5120 outputs
 // half-precision pair arithmetic (pk_mfma.hip): activation planes, grouped GEMM

@@ -71,14 +71,17 @@ __global__ __launch_bounds__(256) void k_act_limbs(const float *__restrict__ x, 
 }
 
 // Stable grouping of the P = T*K (token, expert) pairs by expert, and the
-// tile list: tile j = up to 32 consecutive pairs of one expert. One
-// workgroup: counts by LDS atomics, then each wave places the pairs of its
-// experts in order with ballots (routing staged in LDS when it fits).
+// tile list: tile j = up to 32 consecutive pairs of one expert (with
+// tile_grp: also the expert's first tile and tile count, tile_grp[2j] and
+// [2j + 1]). One workgroup: counts by LDS atomics, then each wave places
+// the pairs of its experts in order with ballots (routing staged in LDS
+// when it fits).
 constexpr int GP_LDS = 16384;
 __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict__ sel, int P, int E,
                                                       int32_t *__restrict__ pairs, int32_t *__restrict__ tile_exp,
                                                       int32_t *__restrict__ tile_beg,
-                                                      int32_t *__restrict__ tile_cnt, int32_t *n_tiles, int tt) {
+                                                      int32_t *__restrict__ tile_cnt, int32_t *n_tiles, int tt,
+                                                      int32_t *__restrict__ tile_grp) {
     __shared__ int cnt[128], off[129];
     __shared__ int s_sel[GP_LDS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
@@ -132,6 +135,10 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
             tile_exp[j] = e;
             tile_beg[j] = off[e] + b;
             tile_cnt[j] = min(tt, cnt[e] - b);
+            if (tile_grp) {
+                tile_grp[2 * j] = toff[e];
+                tile_grp[2 * j + 1] = (cnt[e] + tt - 1) / tt;
+            }
         }
     // (eight 64-entry chunks read per round, so that the reads' latency
     // overlaps; the chunks are placed in order)
@@ -552,7 +559,22 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     if (s >= run) return;
     const int item = (int)(blockIdx.x & 7) * run + s;
     if (item >= n_item) return;
-    const int rg = item / nt, j = item - rg * nt;
+    // item -> (row group, tile): row-group-major over all tiles, or (with
+    // tile_grp) expert by expert and within an expert row-group-major over
+    // its tiles, so that the workgroups resident on one XCD together share
+    // the activation rows of their tiles as well as the expert's weights
+    int rg, j;
+    if (a.tile_grp) {
+        const int RG = (a.O + FROWS - 1) / FROWS;
+        const int p = item / RG;
+        const int first = a.tile_grp[2 * p], n_e = a.tile_grp[2 * p + 1];
+        const int local = item - RG * first;
+        rg = local / n_e;
+        j = first + (local - rg * n_e);
+    } else {
+        rg = item / nt;
+        j = item - rg * nt;
+    }
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int e = a.tile_exp[j], beg = a.tile_beg[j], cnt = a.tile_cnt[j];
@@ -813,10 +835,10 @@ int pk_launch_act_limbs(const float *x, int64_t x_stride, int rows, int cols, in
 
 int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int32_t *tile_exp,
                           int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
-                          int tile_pairs) {
+                          int tile_pairs, int32_t *tile_grp) {
     PK_CHECK(P > 0 && E > 0 && E <= 128, PK_ERR_ARG, "group pairs: P=%d E=%d", P, E);
     hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, st, sel, P, E, pairs, tile_exp, tile_beg,
-                       tile_cnt, n_tiles, tile_pairs > 0 ? tile_pairs : TT);
+                       tile_cnt, n_tiles, tile_pairs > 0 ? tile_pairs : TT, tile_grp);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

@@ -287,7 +287,7 @@ static int grouped_reserve(pk_engine *e, int T) {
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_limbs, 4 * plane));     // 3 int8 planes or 2 half planes
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_exps, std::max((int64_t)T, P) * 4));
     PK_TRY(pk_dev_alloc(e, (void **)&e->g_pairs, P * 4));
-    PK_TRY(pk_dev_alloc(e, (void **)&e->g_tiles, (3 * max_tiles + 1) * 4));
+    PK_TRY(pk_dev_alloc(e, (void **)&e->g_tiles, (5 * max_tiles + 1) * 4));
     e->g_cap = P;
     return PK_OK;
 }
@@ -320,8 +320,9 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
     const int max_tiles = (P + tile - 1) / tile + E;           // within the 32-pair tiles' buffer
     int32_t *tile_exp = e->g_tiles, *tile_beg = tile_exp + max_tiles, *tile_cnt = tile_beg + max_tiles;
     int32_t *n_tiles = tile_cnt + max_tiles;
+    int32_t *tile_grp = f16 ? n_tiles + 1 : nullptr;            // [2 x max_tiles]
     PK_TRY(pk_launch_group_pairs(e->b_sel, P, E, e->g_pairs, tile_exp, tile_beg, tile_cnt, n_tiles, e->stream,
-                                 tile));
+                                 tile, tile_grp));
     const int64_t plane = std::max((int64_t)T * D, (int64_t)P * half);
     pk_mfma_args a{};
     a.base = e->store;
@@ -335,6 +336,7 @@ static int moe_rows_mfma(pk_engine *e, int layer, const float *x, int T, float *
     a.exps = e->g_exps;
     a.pairs = e->g_pairs;
     a.tile_exp = tile_exp; a.tile_beg = tile_beg; a.tile_cnt = tile_cnt; a.n_tiles = n_tiles;
+    a.tile_grp = tile_grp;
     a.lim = c->swiglu_limit;
     a.alpha = c->swiglu_alpha;
     // gate_up + SwiGLU: activation rows are the T tokens
