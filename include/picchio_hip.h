@@ -454,6 +454,22 @@ int pk_set_numeric_trace(pk_engine *e, int on);
 /* Queues a bounded idle kernel (about `usec` microseconds, at most 1 s) so
  * that the host can queue work ahead of the GPU before a profiled pass. */
 int pk_engine_stall(pk_engine *e, int usec);
+/* No reference counterpart (picchio runs on the host). The one-launch forms
+ * (pk_set_moe_fused modes 1 and 2, pk_set_attn_fused) hand values between
+ * workgroups of one launch and so need all of them resident at once. On a
+ * device shared with other work a device-side wait can reach its bound; all
+ * waves still end. The engine then turns both options off, so that the
+ * separate launches (no waits) run from then on, and the call that saw it
+ * runs again:
+ *   - pk_forward_token (with next_host), pk_generate, pk_decode_replay,
+ *     pk_prefill_tokens, pk_prefill_seq and pk_moe_forward (with host outputs,
+ *     not in place) redo the call themselves;
+ *   - pk_engine_sync returns PK_ERR_HIP, since the queued work is unknown.
+ * pk_wait_fallbacks counts these switches. pk_set_poll_bound sets the polls
+ * a wait makes before it gives up (0: the default, 2^18, several ms); a test
+ * sets a tiny one to take the path. */
+int pk_set_poll_bound(pk_engine *e, uint32_t polls);
+int64_t pk_wait_fallbacks(pk_engine *e);
 
 /* ── HIP graphs (no reference counterpart: launch amortisation) ──
  * Everything the engine queues between pk_capture_begin and pk_capture_end

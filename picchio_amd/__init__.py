@@ -128,6 +128,8 @@ def lib():
         "pk_set_router_trace": (C.c_int, [vp, vp, C.c_int64]),
         "pk_router_trace_used": (C.c_int64, [vp]),
         "pk_set_numeric_trace": (C.c_int, [vp, C.c_int]),
+        "pk_set_poll_bound": (C.c_int, [vp, C.c_uint32]),
+        "pk_wait_fallbacks": (C.c_int64, [vp]),
         "pk_set_attn_fused": (C.c_int, [vp, C.c_int]),
         "pk_router_logits": (C.c_int, [vp, C.c_int, vp, vp]),
         "pk_act_records": (C.c_int, [vp, vp, C.c_int, vp]),
@@ -298,6 +300,15 @@ class Engine:
 
     def router_trace_used(self):
         return int(self.L.pk_router_trace_used(self.h))
+
+    def set_poll_bound(self, polls):
+        """Polls a device-side wait makes before it gives up (0: the default;
+        pk_set_poll_bound)."""
+        check(self.L.pk_set_poll_bound(self.h, int(polls)))
+
+    def wait_fallbacks(self):
+        """Calls redone with the separate launches after a wait gave up."""
+        return int(self.L.pk_wait_fallbacks(self.h))
 
     def set_numeric_trace(self, on):
         """picchio's TRACE_NUMERIC lines on stderr for eager forward_token."""

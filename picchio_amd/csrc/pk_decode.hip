@@ -750,12 +750,13 @@ __global__ __launch_bounds__(ATT_THREADS) void k_attn_oproj(const pk_dstate *st,
         const int i = threadIdx.x + k * ATT_THREADS;
         tw[k] = i < I ? __hip_atomic_load(att_t + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : (uint64_t)tag << 32;
     }
+    const uint32_t bound = pk_poll_bound(status);
     for (uint32_t n = 0;; ++n) {
         bool stale = false;
 #pragma unroll
         for (int k = 0; k < TW; ++k) stale |= (uint32_t)(tw[k] >> 32) != tag;
         if (!__any(stale)) break;
-        if (n == PK_POLL_BOUND) {
+        if (n >= bound) {
             if (lane == 0) __hip_atomic_store(status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             break;
         }
@@ -1193,7 +1194,9 @@ extern "C" int pk_forward_token(pk_engine *e, int tok, int pos, int32_t *next_ho
         pk_dstate s{};
         PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
-        PK_TRY(pk_check_waits(e));
+        bool redo = false;
+        PK_TRY(pk_wait_fallback(e, &redo));
+        if (redo) return pk_forward_token(e, tok, pos, next_host, logits_dev);   // rewrites this position's K/V
         *next_host = s.next;
     }
     return PK_OK;
@@ -1220,6 +1223,7 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
     int32_t *out_dev = nullptr;
     PK_TRY(pk_dev_alloc(e, (void **)&out_dev, (int64_t)n_steps * 4));
     int rc = PK_OK;
+    bool redo = false;
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
     do {
@@ -1246,13 +1250,15 @@ extern "C" int pk_generate(pk_engine *e, const int32_t *prompt, int n_prompt, in
         if (rc != PK_OK) break;
         if (hipMemcpyAsync(out, out_dev, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream) != hipSuccess ||
             hipStreamSynchronize(e->stream) != hipSuccess) { rc = PK_ERR_HIP; break; }
-        rc = pk_check_waits(e);
+        rc = pk_wait_fallback(e, &redo);
     } while (0);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     (void)hipStreamSynchronize(e->stream);
     pk_dev_free(e, out_dev);
     e->device_bytes -= (int64_t)n_steps * 4;
+    // the prompt's prefill rewrites every position the failed run wrote
+    if (rc == PK_OK && redo) return pk_generate(e, prompt, n_prompt, n_steps, out);
     return rc;
 }
 
@@ -1306,5 +1312,8 @@ extern "C" int pk_decode_replay(pk_engine *e, int tok, int pos, int n_steps, int
     for (int i = 0; i < n_steps; ++i) PK_HIP(hipGraphLaunch(e->step_exec, e->stream));
     PK_HIP(hipMemcpyAsync(out, e->step_out, (size_t)n_steps * 4, hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
-    return pk_check_waits(e);
+    bool redo = false;
+    PK_TRY(pk_wait_fallback(e, &redo));
+    // from (tok, pos) again: every step rewrites its own position's K/V rows
+    return redo ? pk_decode_replay(e, tok, pos, n_steps, out) : PK_OK;
 }

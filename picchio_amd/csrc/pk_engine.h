@@ -37,6 +37,7 @@ constexpr int PK_CTR_ROUTER = 0;          // router+top-k arrivals
 constexpr int PK_CTR_MOE_EPOCH = 8;      // router launches so far: k_moe_ffn's hand-over tag
 constexpr int PK_CTR_ATT_EPOCH = 16;     // fused-QKV launches so far: k_attn_oproj's hand-over tag
 constexpr int PK_CTR_MOE_STATUS = 40;    // k_moe_ffn / k_attn_oproj: 1 once a wait gave up (checked by the host)
+constexpr int PK_CTR_POLL_BOUND = 41;    // their bound on polls per wait (0: the default)
 constexpr int PK_CTR_COMBINE = 64;        // [row blocks] down+combine arrivals
 constexpr int PK_CTR_ATTN = 4096;         // [rows x heads] attention chunk arrivals
 constexpr int PK_CTR_ATTN_N = 4096;
@@ -96,6 +97,7 @@ struct pk_engine {
     // batch-1 decode attention and its output projection as one k_attn_oproj
     // launch (PK_ATT_FUSED=0: two launches)
     bool attn_fused = true;
+    int64_t wait_fallbacks = 0;          // calls redone with the separate launches
     uint64_t *att_t = nullptr;                // k_attn_oproj hand-over words: [heads x head_dim]
 
     bool capturing = false;                  // inside pk_capture_begin/end
@@ -275,5 +277,7 @@ int pk_trace_router(pk_engine *e, const float *logits_dev, int rows);
 int pk_trace_vec(pk_engine *e, const char *stage, int layer, const float *dev, int n);
 int pk_trace_route(pk_engine *e, int layer, const float *logits_dev);
 int pk_trace_top_logits(pk_engine *e, const float *logits_dev);
-// Reads (and clears) the k_moe_ffn wait flag after a stream sync.
-int pk_check_waits(pk_engine *e);
+// After a stream sync: if a device-side wait gave up, the one-launch forms
+// are switched off (the separate launches do not wait) and *redo is set, so
+// that the caller runs its call again; an error if it happened with them off.
+int pk_wait_fallback(pk_engine *e, bool *redo);

@@ -268,19 +268,54 @@ extern "C" int pk_engine_destroy(pk_engine *e) {
 
 extern "C" void *pk_engine_stream(pk_engine *e) { return e ? (void *)e->stream : nullptr; }
 
-// After a stream sync: an error if a device-side wait of k_moe_ffn gave up
-// (its results are then not to be trusted); the flag is cleared.
-int pk_check_waits(pk_engine *e) {
+// After a stream sync: whether a device-side wait of k_moe_ffn, k_moe_bal or
+// k_attn_oproj gave up since the last look (the flag is cleared).
+static int take_wait_failure(pk_engine *e, bool *failed) {
     uint32_t st = 0;
     PK_HIP(hipMemcpy(&st, e->counters + PK_CTR_MOE_STATUS, 4, hipMemcpyDeviceToHost));
+    *failed = st != 0;
     if (st) {
         PK_HIP(hipMemsetAsync(e->counters + PK_CTR_MOE_STATUS, 0, 4, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
-        pk_set_error("a device-side wait (expert or attention launch) gave up: results are invalid");
-        return PK_ERR_HIP;
     }
     return PK_OK;
 }
+
+// The one-launch forms hand values between workgroups of one launch, so all
+// their workgroups must be resident at once; on a device shared with other
+// work a wait can give up (all waves still end). The engine then takes the
+// separate launches, which wait for nothing, from here on: the captured step
+// graph is dropped and the caller redoes its call.
+int pk_wait_fallback(pk_engine *e, bool *redo) {
+    *redo = false;
+    bool failed = false;
+    PK_TRY(take_wait_failure(e, &failed));
+    if (!failed) return PK_OK;
+    if (e->moe_fused == 0 && !e->attn_fused) {
+        pk_set_error("a device-side wait gave up with the one-launch forms off: results are invalid");
+        return PK_ERR_HIP;
+    }
+    if (e->step_exec) {
+        (void)hipGraphExecDestroy(e->step_exec);
+        e->step_exec = nullptr;
+        e->step_cap = -1;
+    }
+    e->moe_fused = 0;
+    e->attn_fused = false;
+    e->wait_fallbacks += 1;
+    *redo = true;
+    return PK_OK;
+}
+
+extern "C" int pk_set_poll_bound(pk_engine *e, uint32_t polls) {
+    PK_CHECK(e, PK_ERR_ARG, "engine is null");
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "set_poll_bound: not available while capturing");
+    PK_HIP(hipMemcpyAsync(e->counters + PK_CTR_POLL_BOUND, &polls, 4, hipMemcpyHostToDevice, e->stream));
+    PK_HIP(hipStreamSynchronize(e->stream));
+    return PK_OK;
+}
+
+extern "C" int64_t pk_wait_fallbacks(pk_engine *e) { return e ? e->wait_fallbacks : 0; }
 
 // ───────────────────────── diagnostics ─────────────────────────
 // The router logits of every MoE router launch, appended in launch order
@@ -395,7 +430,14 @@ int pk_trace_top_logits(pk_engine *e, const float *logits_dev) {
 extern "C" int pk_engine_sync(pk_engine *e) {
     PK_CHECK(e, PK_ERR_ARG, "engine is null");
     PK_HIP(hipStreamSynchronize(e->stream));
-    return pk_check_waits(e);
+    bool redo = false;
+    PK_TRY(pk_wait_fallback(e, &redo));
+    if (redo) {
+        pk_set_error("a device-side wait gave up: the work queued since the last sync is invalid and is to be "
+                     "queued again (the engine now runs the separate launches)");
+        return PK_ERR_HIP;
+    }
+    return PK_OK;
 }
 
 extern "C" int64_t pk_engine_device_bytes(pk_engine *e) { return e ? e->device_bytes : -1; }
@@ -1045,7 +1087,15 @@ extern "C" int pk_moe_forward(pk_engine *e, int layer, const float *x_dev, float
         if (w_host)
             PK_HIP(hipMemcpyAsync(w_host, e->w_soft, e->c.topk * 4, hipMemcpyDeviceToHost, e->stream));
         PK_HIP(hipStreamSynchronize(e->stream));
-        PK_TRY(pk_check_waits(e));
+        bool redo = false;
+        PK_TRY(pk_wait_fallback(e, &redo));
+        if (redo) {
+            // the input is intact unless the layer ran in place
+            PK_CHECK(x_dev != out_dev, PK_ERR_HIP,
+                     "a device-side wait gave up in an in-place moe_forward: the output is invalid (the engine now "
+                     "runs the separate launches)");
+            return pk_moe_forward(e, layer, x_dev, out_dev, sel_host, w_host);
+        }
     }
     return PK_OK;
 }

@@ -371,12 +371,13 @@ __global__ __launch_bounds__(BW * 64, 1) void k_moe_bal(pk_moe_ffn_args a) {
             w[i] = used(i) ? __hip_atomic_load(src(i), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                            : (uint64_t)tag << 32;
         uint32_t n_poll = 0;
+        const uint32_t bound = pk_poll_bound(a.status);
         for (;;) {
             bool wait = false;
 #pragma unroll
             for (int i = 0; i < NU; ++i) wait |= (uint32_t)(w[i] >> 32) != tag;
             if (!__any(wait)) break;
-            if (++n_poll == PK_POLL_BOUND) {
+            if (++n_poll >= bound) {
                 if (lane == 0) __hip_atomic_store(a.status, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
             }

@@ -555,7 +555,9 @@ extern "C" int pk_prefill_tokens(pk_engine *e, const int32_t *ids, int n, int po
     PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     // a one-token prompt runs the fused decode step, whose waits may give up
-    PK_TRY(pk_check_waits(e));
+    bool redo = false;
+    PK_TRY(pk_wait_fallback(e, &redo));
+    if (redo) return pk_prefill_tokens(e, ids, n, pos_base, next_host);
     if (next_host) *next_host = s.next;
     return PK_OK;
 }
@@ -666,7 +668,9 @@ extern "C" int pk_prefill_seq(pk_engine *e, int seq, const int32_t *ids, int n, 
     PK_HIP(hipMemcpyAsync(&s, e->dstate, sizeof(s), hipMemcpyDeviceToHost, e->stream));
     PK_HIP(hipStreamSynchronize(e->stream));
     // a one-token prompt runs the fused decode step, whose waits may give up
-    PK_TRY(pk_check_waits(e));
+    bool redo = false;
+    PK_TRY(pk_wait_fallback(e, &redo));
+    if (redo) return pk_prefill_seq(e, seq, ids, n, pos_base, next_host);
     if (next_host) *next_host = s.next;
     return PK_OK;
 }
