@@ -58,10 +58,22 @@ TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh
 #    18425.54 KiB x 2 + WRITE_SIZE 45.04 KiB;
 #  * k_i4_gemv_stream<SWIGLU, integer dot>, 32 experts' gate_up
 #    (profiles/k_i4_gemv_stream_gate_up32.txt), commit afc7a2d: FETCH_SIZE
-#    149022.55 KiB x 2 + WRITE_SIZE 630.00 KiB.
+#    149022.55 KiB x 2 + WRITE_SIZE 630.00 KiB;
+#  * measured again on commit 85f4c9b (passes over --mode decode and
+#    --mode kernels): k_moe_ffn FETCH_SIZE 27790.06 KiB x 2 + WRITE_SIZE
+#    168.84 KiB = 57,085,388 B (the constant above within 0.01 %);
+#    k_lm_head<fp32> FETCH_SIZE 1131188.06 KiB x 2 + WRITE_SIZE 2358.62 KiB;
+#    config 0's expert FFN, k_i4_gemv<SWIGLU> FETCH_SIZE 4726.50 KiB x 2 +
+#    WRITE_SIZE 11.25 KiB, then k_i4_gemv<PLAIN> 2433.75 KiB x 2 + 11.25 KiB;
+#  * k_moe_f16<SWIGLU>, config 3's gate_up
+#    (profiles/k_moe_f16_prefill_config3.txt, commit e0c51b1): FETCH_SIZE
+#    3.705e5 KiB x 2 + WRITE_SIZE 1.022e5 KiB.
 MOE_FFN_TRAFFIC = 57088267
 GATE_UP_TRAFFIC = 37780589
 STREAM_DOT_TRAFFIC = 305834925
+LM_HEAD_TRAFFIC = 2319025051
+FFN_TRAFFIC = 9691127 + 4995704
+F16_GATE_UP_TRAFFIC = 863436800
 
 
 def host_info():
@@ -375,7 +387,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
         "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(lm_bytes / (lm_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4),
-                     "traffic": None, "kernel": "k_lm_head<fp32> (201088 x 2880 GEMV, per-block maxima)",
+                     "traffic": LM_HEAD_TRAFFIC, "kernel": "k_lm_head<fp32> (201088 x 2880 GEMV, per-block maxima)",
                      "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
         "cpu_baseline": cpu,
     }
@@ -466,7 +478,7 @@ def measure_decode120b(args, steps, warmup, cpu_on):
                    "first_tokens_batch32_seq0": [int(t) for t in out32[:6, 0]]},
         "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(lm_bytes / (lm_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(lm_bytes / (lm_ms * 1e-3) / 1e9 / HBM_PEAK_GBPS, 4), "traffic": LM_HEAD_TRAFFIC,
                      "kernel": "k_lm_head<fp32> (201088 x 2880 GEMV, per-block maxima)",
                      "bytes_per_launch": lm_bytes, "mean_us": round(lm_ms * 1e3, 3)},
         "cpu_baseline": cpu,
@@ -603,7 +615,8 @@ def measure_prefill(args, steps, warmup, cpu_on):
                    ("f16" if f16 else "int8") + "_mfma_flops_issued": limbs * 2 * tiles * 32 * (INTER * D + D * HALF)},
         "roofline": {"bound": "mfma", "achieved": round(gu_flops / (gu_ms * 1e-3) / 1e12, 1),
                      "peak": peak, "unit": "TFLOP/s",
-                     "frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / peak, 4), "traffic": None,
+                     "frac": round(gu_flops / (gu_ms * 1e-3) / 1e12 / peak, 4),
+                     "traffic": F16_GATE_UP_TRAFFIC if f16 else None,
                      "kernel": kern + " (gate_up, algorithmic flops vs the dense " +
                                ("fp16" if f16 else "int8") + " peak)",
                      "flops_per_launch": gu_flops, "mean_us": round(gu_ms * 1e3, 2)},
@@ -787,7 +800,7 @@ def measure_moe_layer(args):
         "gbps": round(ffn_gbps, 1), "hbm_frac": round(ffn_gbps / HBM_PEAK_GBPS, 4),
         "gate_up_us": round(ffn_gu_ms * 1e3, 3), "down_us": round((ffn_ms - ffn_gu_ms) * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(ffn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(ffn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+                     "frac": round(ffn_gbps / HBM_PEAK_GBPS, 4), "traffic": FFN_TRAFFIC,
                      "kernel": "k_i4_gemv<SWIGLU> (gate_up) then k_i4_gemv<PLAIN> (down), one expert",
                      "bytes_per_launch": FFN_BYTES, "mean_us": round(ffn_ms * 1e3, 3)},
         "cpu_baseline": cpu0,
