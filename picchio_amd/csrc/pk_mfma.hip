@@ -547,9 +547,12 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     // row, even and odd apart, take distinct positions, so 16-byte reads of 8 or
     // 16 lanes hit distinct banks], weights [slot][wave][tile bytes],
     // scales [slot][row]
-    __shared__ __attribute__((aligned(16))) _Float16 bring[FR][2][FT][64];
-    __shared__ __attribute__((aligned(16))) uint8_t wring[FR][FW][PK_TILE_BYTES];
-    __shared__ __attribute__((aligned(16))) float sring[FS][FROWS];
+    // (one LDS block: after the last stage the output tile is staged in it)
+    constexpr int B_BYTES = FR * 2 * FT * 64 * 2, W_BYTES = FR * FW * PK_TILE_BYTES, S_BYTES = FS * FROWS * 4;
+    __shared__ __attribute__((aligned(16))) uint8_t lds[B_BYTES + W_BYTES + S_BYTES];
+    auto &bring = *reinterpret_cast<_Float16 (*)[FR][2][FT][64]>(lds);
+    auto &wring = *reinterpret_cast<uint8_t (*)[FR][FW][PK_TILE_BYTES]>(lds + B_BYTES);
+    auto &sring = *reinterpret_cast<float (*)[FS][FROWS]>(lds + B_BYTES + W_BYTES);
     __shared__ int tok_row[FT], tok_exp[FT], tok_pair[FT];
     // this workgroup's item
     const int nt = *a.n_tiles;
@@ -663,14 +666,6 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
         if (g + 3 < NG) issue(g + 3);
         if (g + 1 < NG) wait_stage(min(g + 3, NG - 1) - (g + 1));   // stage g+1
     };
-    if (!active) {
-        // no rows here: this wave's share of the loads and the barriers
-        for (int g = 0; g < NG; ++g) {
-            pk_stage_barrier();
-            stage_loads(g);
-        }
-        return;
-    }
     const pk_v16f zero = {};
     // The stage loop for tiles with one (TWO false) or two 32-pair halves,
     // compiled apart so that neither carries the other's branches.
@@ -753,47 +748,82 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
         }
         fold();
     };
-    if (two) stages(std::true_type{});
-    else stages(std::false_type{});
-    // lane (n, h) holds output row 32 rt + n of its block for the 16 pairs
-    // 32 ts + 8 b + 4 h + i of the tile (element 4 b + i)
-    const float *bias = a.off_bias >= 0 ? reinterpret_cast<const float *>(base + a.off_bias) : nullptr;
+    if (!active) {
+        // no rows here: this wave's share of the loads and the barriers
+        for (int g = 0; g < NG; ++g) {
+            pk_stage_barrier();
+            stage_loads(g);
+        }
+    } else if (two) {
+        stages(std::true_type{});
+    } else {
+        stages(std::false_type{});
+    }
+    // Epilogue: the item's outputs go through LDS (every wave is past its last
+    // read of the rings), [pair][output column of the item], so that each
+    // lane then writes 16 contiguous bytes of a pair's row: a quarter of the
+    // store instructions of writing the lanes' values in place, and each
+    // wave's store covers whole 1 KB runs of rows.
+    constexpr int OC = EPI == PK_EPI_SWIGLU ? FROWS / 2 : FROWS;   // output columns per item
+    constexpr int OT = OC + 4;                                      // staged row (padded: banks)
+    static_assert(FT * OT * 4 <= B_BYTES + W_BYTES + S_BYTES, "output tile exceeds the LDS block");
+    float (*ot)[OT] = reinterpret_cast<float (*)[OT]>(lds);
+    __syncthreads();
+    if (active) {
+        // lane (n, h) holds output row 32 rt + n of its block for the 16 pairs
+        // 32 ts + 8 b + 4 h + i of the tile (element 4 b + i)
+        const float *bias = a.off_bias >= 0 ? reinterpret_cast<const float *>(base + a.off_bias) : nullptr;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-        const int row = rb * 64 + 32 * rt + n;
-        const float bv = bias ? bias[row] : 0.0f;
+        for (int rt = 0; rt < 2; ++rt) {
+            const int row = rb * 64 + 32 * rt + n;
+            const int lrow = wave * 64 + 32 * rt + n;                // row within the item
+            const float bv = bias ? bias[row] : 0.0f;
 #pragma unroll
-        for (int ts = 0; ts < 2; ++ts) {
-            if (ts == 1 && !two) break;
-            const pk_v16f &c = rt ? (ts ? acc11 : acc10) : (ts ? acc01 : acc00);
-            float y[16];
-#pragma unroll
-            for (int v = 0; v < 16; ++v) {
-                const int tn = 32 * ts + 8 * (v >> 2) + 4 * h + (v & 3);
-                y[v] = ldexpf(c[v], tok_exp[tn] - 19);
-                if (bias) y[v] = y[v] + bv;
-            }
-            if constexpr (EPI == PK_EPI_SWIGLU) {
-                // rows 2i (gate, even lane) and 2i+1 (up, odd lane): the even
-                // lane finishes elements 0..7, the odd lane 8..15
-                const bool odd = n & 1;
-#pragma unroll
-                for (int v = 0; v < 8; ++v) {
-                    const float other = __shfl_xor(odd ? y[v] : y[v + 8], 1, 64);
-                    const float mine = odd ? y[v + 8] : y[v];
-                    const int va = odd ? v + 8 : v;
-                    const int tn = 32 * ts + 8 * (va >> 2) + 4 * h + (va & 3);
-                    if (tn < cnt)
-                        a.y[(int64_t)tok_pair[tn] * a.y_stride + (row >> 1)] =
-                            swiglu_f16path(odd ? other : mine, odd ? mine : other, a.lim, a.alpha);
-                }
-            } else {
+            for (int ts = 0; ts < 2; ++ts) {
+                if (ts == 1 && !two) break;
+                const pk_v16f &c = rt ? (ts ? acc11 : acc10) : (ts ? acc01 : acc00);
+                float y[16];
 #pragma unroll
                 for (int v = 0; v < 16; ++v) {
                     const int tn = 32 * ts + 8 * (v >> 2) + 4 * h + (v & 3);
-                    if (tn < cnt) a.y[(int64_t)tok_pair[tn] * a.y_stride + row] = y[v];
+                    y[v] = ldexpf(c[v], tok_exp[tn] - 19);
+                    if (bias) y[v] = y[v] + bv;
+                }
+                if constexpr (EPI == PK_EPI_SWIGLU) {
+                    // rows 2i (gate, even lane) and 2i+1 (up, odd lane): the even
+                    // lane finishes elements 0..7, the odd lane 8..15
+                    const bool odd = n & 1;
+#pragma unroll
+                    for (int v = 0; v < 8; ++v) {
+                        const float other = __shfl_xor(odd ? y[v] : y[v + 8], 1, 64);
+                        const float mine = odd ? y[v + 8] : y[v];
+                        const int va = odd ? v + 8 : v;
+                        const int tn = 32 * ts + 8 * (va >> 2) + 4 * h + (va & 3);
+                        ot[tn][lrow >> 1] = swiglu_f16path(odd ? other : mine, odd ? mine : other, a.lim, a.alpha);
+                    }
+                } else {
+#pragma unroll
+                    for (int v = 0; v < 16; ++v) ot[32 * ts + 8 * (v >> 2) + 4 * h + (v & 3)][lrow] = y[v];
                 }
             }
+        }
+    }
+    __syncthreads();
+    // the item's valid output columns (rows of active waves), then per pair
+    // of the tile its runs of 4 columns
+    const int oc0 = (EPI == PK_EPI_SWIGLU ? rg * FROWS / 2 : rg * FROWS);
+    const int noc = min(OC, (EPI == PK_EPI_SWIGLU ? a.O / 2 : a.O) - oc0);
+    const bool v4 = (a.y_stride & 3) == 0 && ((uintptr_t)a.y & 15) == 0;
+    constexpr int Q = OC / 4;
+    for (int k = threadIdx.x; k < cnt * Q; k += FTHR) {
+        const int p = k / Q, c = 4 * (k - p * Q);
+        if (c >= noc) continue;
+        float *dst = a.y + (int64_t)tok_pair[p] * a.y_stride + oc0 + c;
+        const float4 v = *reinterpret_cast<const float4 *>(&ot[p][c]);
+        if (v4) {
+            *reinterpret_cast<float4 *>(dst) = v;
+        } else {
+            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
         }
     }
 }
