@@ -813,18 +813,12 @@ __global__ __launch_bounds__(FTHR, 2) void k_moe_f16(pk_mfma_args a) {
     // of the tile its runs of 4 columns
     const int oc0 = (EPI == PK_EPI_SWIGLU ? rg * FROWS / 2 : rg * FROWS);
     const int noc = min(OC, (EPI == PK_EPI_SWIGLU ? a.O / 2 : a.O) - oc0);
-    const bool v4 = (a.y_stride & 3) == 0 && ((uintptr_t)a.y & 15) == 0;
     constexpr int Q = OC / 4;
     for (int k = threadIdx.x; k < cnt * Q; k += FTHR) {
         const int p = k / Q, c = 4 * (k - p * Q);
-        if (c >= noc) continue;
-        float *dst = a.y + (int64_t)tok_pair[p] * a.y_stride + oc0 + c;
-        const float4 v = *reinterpret_cast<const float4 *>(&ot[p][c]);
-        if (v4) {
-            *reinterpret_cast<float4 *>(dst) = v;
-        } else {
-            dst[0] = v.x; dst[1] = v.y; dst[2] = v.z; dst[3] = v.w;
-        }
+        if (c < noc)
+            *reinterpret_cast<float4 *>(a.y + (int64_t)tok_pair[p] * a.y_stride + oc0 + c) =
+                *reinterpret_cast<const float4 *>(&ot[p][c]);
     }
 }
 
@@ -843,6 +837,9 @@ int pk_launch_act_f16(const float *x, int64_t x_stride, int rows, int cols, uint
 int pk_launch_moe_f16(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st) {
     PK_CHECK(a.O % 64 == 0 && a.O > 0 && a.NG > 0 && max_tiles > 0 && a.frow == a.NG * 64 && a.xf && a.fplane > 0,
              PK_ERR_UNSUPPORTED, "f16 grouped gemm: O=%d NG=%d", a.O, a.NG);
+    // the epilogue writes 16-byte runs of output rows
+    PK_CHECK((a.y_stride & 3) == 0 && ((uintptr_t)a.y & 15) == 0, PK_ERR_UNSUPPORTED,
+             "f16 grouped gemm: output rows must be 16-byte aligned (stride %lld)", (long long)a.y_stride);
     const int64_t n = (int64_t)max_tiles * ((a.O + FROWS - 1) / FROWS);
     PK_CHECK(n < (1 << 30), PK_ERR_UNSUPPORTED, "f16 grouped gemm: %lld items", (long long)n);
     const dim3 grid((unsigned)((n + 7) & ~(int64_t)7));
