@@ -71,19 +71,24 @@ __global__ __launch_bounds__(256) void k_act_limbs(const float *__restrict__ x, 
 }
 
 // Stable grouping of the P = T*K (token, expert) pairs by expert, and the
-// tile list: tile j = up to 32 consecutive pairs of one expert (with
+// tile list: tile j = up to tt consecutive pairs of one expert (with
 // tile_grp: also the expert's first tile and tile count, tile_grp[2j] and
-// [2j + 1]). One workgroup: counts by LDS atomics, then each wave places
-// the pairs of its experts in order with ballots (routing staged in LDS
-// when it fits).
+// [2j + 1]). Workgroup x (grid = E) places expert x. It counts every
+// expert's pairs (LDS atomics; the offsets need them all) and scans the
+// counts. Its waves then count their segment's pairs of x, and after a
+// prefix over the 16 waves each wave places its pairs of x in order with
+// ballots. No workgroup waits for another. (One workgroup placing every
+// expert scanned the routing once per expert: for 8192 pairs and 32
+// experts, 26 of its 33 µs.)
 constexpr int GP_LDS = 16384;
 __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict__ sel, int P, int E,
                                                       int32_t *__restrict__ pairs, int32_t *__restrict__ tile_exp,
                                                       int32_t *__restrict__ tile_beg,
                                                       int32_t *__restrict__ tile_cnt, int32_t *n_tiles, int tt,
                                                       int32_t *__restrict__ tile_grp) {
-    __shared__ int cnt[128], off[129];
+    __shared__ int cnt[128], off[129], toff[128], wcnt[16];
     __shared__ int s_sel[GP_LDS];
+    const int x = blockIdx.x;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
     const bool staged = P <= GP_LDS;
@@ -114,8 +119,7 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
     }
     __syncthreads();
     // offsets of the experts' pairs and of their tiles: one wave scans the
-    // counts (lane l holds experts l and l + 64), then every expert writes its tiles
-    __shared__ int toff[128];
+    // counts (lane l holds experts l and l + 64)
     if (wave == 0) {
         const int c0 = lane < E ? cnt[lane] : 0, c1 = lane + 64 < E ? cnt[lane + 64] : 0;
         int p0 = c0, p1 = c1, q0 = (c0 + tt - 1) / tt, q1 = (c1 + tt - 1) / tt;
@@ -127,38 +131,40 @@ __global__ __launch_bounds__(1024) void k_group_pairs(const int32_t *__restrict_
         const int pt = __shfl(p0, 63, 64), qt = __shfl(q0, 63, 64);   // first half's totals
         if (lane < E) { off[lane] = p0 - c0; toff[lane] = q0 - (c0 + tt - 1) / tt; }
         if (lane + 64 < E) { off[lane + 64] = pt + p1 - c1; toff[lane + 64] = qt + q1 - (c1 + tt - 1) / tt; }
-        if (lane == 63) { off[E] = pt + p1; *n_tiles = qt + q1; }
+        if (lane == 63) {
+            off[E] = pt + p1;
+            if (x == 0) *n_tiles = qt + q1;
+        }
     }
     __syncthreads();
-    for (int e = threadIdx.x; e < E; e += blockDim.x)
-        for (int b = 0, j = toff[e]; b < cnt[e]; b += tt, ++j) {
-            tile_exp[j] = e;
-            tile_beg[j] = off[e] + b;
-            tile_cnt[j] = min(tt, cnt[e] - b);
-            if (tile_grp) {
-                tile_grp[2 * j] = toff[e];
-                tile_grp[2 * j + 1] = (cnt[e] + tt - 1) / tt;
-            }
+    // expert x's tiles
+    const int cx = cnt[x], nx = (cx + tt - 1) / tt;
+    for (int k = threadIdx.x; k < nx; k += blockDim.x) {
+        const int j = toff[x] + k;
+        tile_exp[j] = x;
+        tile_beg[j] = off[x] + k * tt;
+        tile_cnt[j] = min(tt, cx - k * tt);
+        if (tile_grp) {
+            tile_grp[2 * j] = toff[x];
+            tile_grp[2 * j + 1] = nx;
         }
-    // (eight 64-entry chunks read per round, so that the reads' latency
-    // overlaps; the chunks are placed in order)
-    for (int e = wave; e < E; e += nw) {
-        int run = off[e];
-        for (int b = 0; b < P; b += 512) {
-            int v[8];
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const int i = b + 64 * u + lane;
-                v[u] = i < P ? (staged ? s_sel[i] : sel[i]) : -1;
-            }
-#pragma unroll
-            for (int u = 0; u < 8; ++u) {
-                const bool hit = v[u] == e;
-                const uint64_t m = __ballot(hit);
-                if (hit) pairs[run + __popcll(m & lt)] = b + 64 * u + lane;
-                run += __popcll(m);
-            }
-        }
+    }
+    // wave w's segment of the routing: its pairs of x, counted, then placed
+    // after those of the waves before it
+    const int seg = ((P + nw - 1) / nw + 63) & ~63;
+    const int b0 = min(P, wave * seg), b1 = min(P, b0 + seg);
+    auto sel_at = [&](int i) { return i < b1 ? (staged ? s_sel[i] : sel[i]) : -1; };
+    int mine = 0;
+    for (int b = b0; b < b1; b += 64) mine += __popcll(__ballot(sel_at(b + lane) == x));
+    if (lane == 0) wcnt[wave] = mine;
+    __syncthreads();
+    int run = off[x];
+    for (int w = 0; w < wave; ++w) run += wcnt[w];
+    for (int b = b0; b < b1; b += 64) {
+        const bool hit = sel_at(b + lane) == x;
+        const uint64_t m = __ballot(hit);
+        if (hit) pairs[run + __popcll(m & lt)] = b + lane;
+        run += __popcll(m);
     }
 }
 
@@ -864,7 +870,7 @@ int pk_launch_group_pairs(const int32_t *sel, int P, int E, int32_t *pairs, int3
                           int32_t *tile_beg, int32_t *tile_cnt, int32_t *n_tiles, hipStream_t st,
                           int tile_pairs, int32_t *tile_grp) {
     PK_CHECK(P > 0 && E > 0 && E <= 128, PK_ERR_ARG, "group pairs: P=%d E=%d", P, E);
-    hipLaunchKernelGGL(k_group_pairs, dim3(1), dim3(1024), 0, st, sel, P, E, pairs, tile_exp, tile_beg,
+    hipLaunchKernelGGL(k_group_pairs, dim3(E), dim3(1024), 0, st, sel, P, E, pairs, tile_exp, tile_beg,
                        tile_cnt, n_tiles, tile_pairs > 0 ? tile_pairs : TT, tile_grp);
     PK_HIP(hipGetLastError());
     return PK_OK;
