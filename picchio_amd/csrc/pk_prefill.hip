@@ -70,17 +70,23 @@ __global__ __launch_bounds__(1024) void k_uniq_perm(const int32_t *sel, int n, i
         rank[e] = first[e] == 0x7fffffff ? 0x7fffffff : r;
     }
     __syncthreads();
+    // the token's K ranks into registers first (K <= 16, the engine's
+    // bound): read once, not again after every store to perm
     for (int p = threadIdx.x; p < n; p += blockDim.x) {
         const int32_t *sp = staged ? s_sel + p * K : sel + (int64_t)p * K;
-        for (int k = 0; k < K; ++k) {
-            const int ek = sp[k];
-            const int rk = (ek >= 0 && ek < E) ? rank[ek] : 0x7fffffff;
+        int r[16];
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            const int ek = k < K ? sp[k] : -1;
+            r[k] = (ek >= 0 && ek < E) ? rank[ek] : 0x7fffffff;
+        }
+#pragma unroll
+        for (int k = 0; k < 16; ++k) {
+            if (k >= K) break;
             int pos = 0;
-            for (int k2 = 0; k2 < K; ++k2) {
-                const int e2 = sp[k2];
-                const int r2 = (e2 >= 0 && e2 < E) ? rank[e2] : 0x7fffffff;
-                pos += (r2 < rk) || (r2 == rk && k2 < k);
-            }
+#pragma unroll
+            for (int k2 = 0; k2 < 16; ++k2)
+                if (k2 < K) pos += (r[k2] < r[k]) || (r[k2] == r[k] && k2 < k);
             perm[(int64_t)p * K + pos] = k;
         }
     }
