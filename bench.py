@@ -66,14 +66,14 @@ TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh
 #    config 0's expert FFN, k_i4_gemv<SWIGLU> FETCH_SIZE 4726.50 KiB x 2 +
 #    WRITE_SIZE 11.25 KiB, then k_i4_gemv<PLAIN> 2433.75 KiB x 2 + 11.25 KiB;
 #  * k_moe_f16<SWIGLU>, config 3's gate_up
-#    (profiles/k_moe_f16_prefill_config3.txt, commit e0c51b1): FETCH_SIZE
-#    3.705e5 KiB x 2 + WRITE_SIZE 1.022e5 KiB.
+#    (profiles/k_moe_f16_prefill_config3.txt, commit 73774fc): FETCH_SIZE
+#    369465.17 KiB x 2 + WRITE_SIZE 92160.00 KiB.
 MOE_FFN_TRAFFIC = 57088267
 GATE_UP_TRAFFIC = 37780589
 STREAM_DOT_TRAFFIC = 305834925
 LM_HEAD_TRAFFIC = 2319025051
 FFN_TRAFFIC = 9691127 + 4995704
-F16_GATE_UP_TRAFFIC = 863436800
+F16_GATE_UP_TRAFFIC = 851036516
 
 
 def host_info():
