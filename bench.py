@@ -695,6 +695,43 @@ def measure_moe_layer(args):
     for g in graphs:
         eng.graph_destroy(g)
 
+    # the same tokens on the integer-dot arithmetic (within 2e-5 of picchio's
+    # fp32 chains, the north star's 1e-4 per layer; the same 256-step greedy
+    # stream in config 2), timed the same way over fewer steps, when the run
+    # is on the default fp32 chains
+    dot_on = args.dot == 1 or (args.dot < 0 and os.environ.get("PK_I4_DOT", "0") not in ("", "0"))
+    alt = None
+    if args.dot < 0 and not dot_on:
+        eng.set_i4_dot(True)
+        S2 = min(S, 5)
+
+        def replay(steps, fn):
+            gs = [capture(eng, s * T, (s + 1) * T, fn) for s in steps]
+            eng.graph_launch(gs[0])
+            eng.sync()
+            ev0.record(eng.stream)
+            for g in gs:
+                eng.graph_launch(g)
+            ev1.record(eng.stream)
+            ev1.synchronize()
+            for g in gs:
+                eng.graph_destroy(g)
+            return ev0.elapsed_time(ev1)
+        steps2 = range(W, W + S2)
+        ms2 = replay(steps2, enqueue)
+        ms2_router = replay(steps2, lambda t: eng.router_logits(t % L, xd[t], lg))
+        eng.set_i4_dot(False)
+        n2 = S2 * T
+        moe2 = (ms2 - ms2_router) / n2
+        alt = {"expert_arithmetic": "integer-dot", "tokens_timed": n2,
+               "us_per_token": round(ms2 / n2 * 1e3, 3),
+               "gbps": round(TOKEN_BYTES / (ms2 / n2 * 1e-3) / 1e9, 1),
+               "kernel_us": {"router": round(ms2_router / n2 * 1e3, 3), "moe_ffn": round(moe2 * 1e3, 3)},
+               "moe_ffn_gbps": round((gate_up_bytes(K) + down_bytes(K)) / (moe2 * 1e-3) / 1e9, 1)}
+        print(f"[bench] config 1 on the integer dot: {alt['us_per_token']:.2f} us/token, {alt['gbps']:.1f} GB/s; "
+              f"moe_ffn {alt['kernel_us']['moe_ffn']:.2f} us = {alt['moe_ffn_gbps']:.1f} GB/s", file=sys.stderr,
+              flush=True)
+
     # the launches of an eager pass with HIP events on the engine stream around
     # each (tells the one-launch experts from the two-launch ones; the eager
     # events add the dispatch to each launch, so the graph difference above is
@@ -744,7 +781,6 @@ def measure_moe_layer(args):
     ffn_ms = replay_ms(eng, ev0, ev1, n_ffn, ffn)
     ffn_gu_ms = replay_ms(eng, ev0, ev1, n_ffn, lambda i: eng.expert_gate_up(i % L, eid(i), x0d[i], act0))
 
-    dot_on = args.dot == 1 or (args.dot < 0 and os.environ.get("PK_I4_DOT", "0") not in ("", "0"))
     arith = "integer-dot" if dot_on else "fp32 chains (bit-exact with quant.h)"
     eng.close()
 
@@ -830,6 +866,7 @@ def measure_moe_layer(args):
                    "kernel_us_method": ("graph replays: router launches alone, and router + expert "
                                         "launches; the expert launch = the difference" if fused else
                                         "HIP events around each launch of an eager pass"),
+                   "integer_dot_experts": alt,
                    "int4_gemv_streaming": streaming,
                    "config0_expert_ffn": config0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
