@@ -23,8 +23,9 @@ the reference when present, else the C restatement).
 """
 import os
 
-# picchio's CPU baseline runs under OpenMP with threads bound to cores
-# (BASELINE.md's run conditions); set before any OpenMP runtime starts
+# picchio's CPU baseline runs under OpenMP with threads bound to cores (the
+# conditions its published CPU figures were taken under); set before any
+# OpenMP runtime starts
 os.environ.setdefault("OMP_PROC_BIND", "close")
 os.environ.setdefault("OMP_PLACES", "cores")
 
