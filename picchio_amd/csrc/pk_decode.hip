@@ -71,7 +71,7 @@ __device__ __forceinline__ void qkv_fma4(float &a, float4 x, pk_f32x4 w) {
 __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, const float *__restrict__ h,
                                                        const float *__restrict__ nw, float eps,
                                                        const float *__restrict__ W, const float *__restrict__ b,
-                                                       int D, int H, int KVH, int hd, const float *rope,
+                                                       int D, int H, int KVH, int hd, int ctx, const float *rope,
                                                        float *qkv, float *Kl, float *Vl, uint32_t *att_epoch) {
     __shared__ double npart[4];
     // a new tag for the fused attention launch that follows
@@ -153,9 +153,8 @@ __global__ __launch_bounds__(256) void k_qkv_rope_norm(const pk_dstate *st, cons
         qkv[r0] = q0;
         qkv[r1] = q1;
         if (head >= H) {
-            float *kr = Kl + (int64_t)pos * kv_dim + (head - H) * hd;
-            kr[j] = q0;
-            kr[j + half] = q1;
+            Kl[pk_k_off(pos, head - H, j, ctx, KVH, hd)] = q0;
+            Kl[pk_k_off(pos, head - H, j + half, ctx, KVH, hd)] = q1;
         }
     } else {
         qkv[r0] = v0;
@@ -187,7 +186,7 @@ __device__ __forceinline__ float splits_sum(const float *ws, int splits, int r, 
 }
 
 __global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float *qkv, int64_t qkv_stride,
-                          const float *rope, int H, int KVH, int hd, float *Kl, float *Vl, int64_t kv_row,
+                          const float *rope, int H, int KVH, int hd, int ctx, float *Kl, float *Vl, int64_t kv_row,
                           const float *ws = nullptr, int splits = 1, const float *bias = nullptr) {
     const int pos = row_pos(st, pos_base, pos_step, blockIdx.y);
     const int r = blockIdx.y;
@@ -210,9 +209,8 @@ __global__ void k_rope_kv(const pk_dstate *st, int pos_base, int pos_step, float
         v[j] = r0;
         v[j + half] = r1;
         if (head >= H) {
-            float *kr = Kl + (int64_t)pos * kv_dim + (head - H) * hd;
-            kr[j] = r0;
-            kr[j + half] = r1;
+            Kl[pk_k_off(pos, head - H, j, ctx, KVH, hd)] = r0;
+            Kl[pk_k_off(pos, head - H, j + half, ctx, KVH, hd)] = r1;
         }
     } else if (i < n_pairs + kv_dim) {
         const int c = i - n_pairs;
@@ -320,10 +318,13 @@ __device__ __forceinline__ void attn_part_block(const pk_dstate *st, int pos_bas
 #pragma unroll
     for (int k = 0; k < 4; ++k) qv[k] = qkv[h0 * hd + min(tid + k * (int)blockDim.x, G * hd - 1)];
     const int D4 = hd >> 2;
-    const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + (int64_t)(t0 + min(tt, n - 1)) * kv_dim + kvh * hd);
+    // (the K cache's chunk layout: float4 u of neighbouring positions adjacent)
+    const int tk = t0 + min(tt, n - 1);
+    const int kcs = pk_k_cs(tk, ctx);
+    const float4 *kt4 = reinterpret_cast<const float4 *>(Kl + pk_k_off(tk, kvh, 0, ctx, KVH, hd));
     float4 kv[KD4];
 #pragma unroll
-    for (int u = 0; u < KD4; ++u) kv[u] = kt4[min(u, D4 - 1)];
+    for (int u = 0; u < KD4; ++u) kv[u] = kt4[(int64_t)min(u, D4 - 1) * kcs];
     // (clamped like the loads: threads past G * hd write the last value
     // again; a guarded store would let its load sink behind the K loads)
 #pragma unroll
@@ -985,7 +986,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                  PK_ERR_UNSUPPORTED, "qkv: needs 16-byte aligned rows");
         const int n_pairs = (H + 2 * KVH) * hd / 2;
         hipLaunchKernelGGL(k_qkv_rope_norm, dim3((n_pairs + 1) / 2), dim3(256), 0, e->stream, st, xn, norm_w,
-                           c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, e->rope, qkv, Kl, Vl,
+                           c->eps, d.wqkv, d.bqkv, D, H, KVH, hd, c->ctx_len, e->rope, qkv, Kl, Vl,
                            e->counters + PK_CTR_ATT_EPOCH);
         PK_HIP(hipGetLastError());
     } else {
@@ -1002,7 +1003,7 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
                                       e->skinny_ws ? PK_SKINNY_WS : 0));
         const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
         hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base,
-                           pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, Kl, Vl, kv_row,
+                           pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, c->ctx_len, Kl, Vl, kv_row,
                            splits > 1 ? e->skinny_ws : nullptr, splits, d.bqkv);
         PK_HIP(hipGetLastError());
     }

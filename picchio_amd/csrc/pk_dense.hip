@@ -724,6 +724,36 @@ int pk_launch_fill_normal(float *out, int64_t n, uint64_t stream_seed, float std
     return PK_OK;
 }
 
+// The same values for a K cache region of n_pos positions, value f (f =
+// pos * KVH * hd + kvh * hd + i, the position-major order) stored at its
+// place in the chunk layout (pk_k_off).
+__global__ void k_fill_normal_k(float *out, int n_pos, int ctx, int KVH, int hd, uint64_t s, float std) {
+    const int64_t n = (int64_t)n_pos * KVH * hd;
+    const int64_t pair = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (2 * pair >= n) return;
+    double nv[2];
+    pk_normal_pair(s, (uint64_t)pair, &nv[0], &nv[1]);
+    const int kv_dim = KVH * hd;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int64_t f = 2 * pair + k;
+        if (f >= n) break;
+        const int pos = (int)(f / kv_dim), i = (int)(f - (int64_t)pos * kv_dim);
+        out[pk_k_off(pos, i / hd, i % hd, ctx, KVH, hd)] = (float)(nv[k] * (double)std);
+    }
+}
+
+int pk_launch_fill_normal_k(float *out, int n_pos, int ctx, int KVH, int hd, uint64_t stream_seed, float std,
+                            hipStream_t st) {
+    PK_CHECK(n_pos >= 0 && n_pos <= ctx && hd % 4 == 0, PK_ERR_ARG, "k fill: %d positions of %d", n_pos, ctx);
+    const int64_t pairs = ((int64_t)n_pos * KVH * hd + 1) / 2;
+    if (pairs == 0) return PK_OK;
+    hipLaunchKernelGGL(k_fill_normal_k, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, st, out, n_pos, ctx,
+                       KVH, hd, stream_seed, std);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 __global__ void k_fill_const(float *out, int64_t n, float v) {
     const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) out[i] = v;

@@ -186,6 +186,9 @@ int pk_launch_combine(float *out, const float *eo, const float *w, int K, int D,
                       const float *residual, float *res_out, hipStream_t st);
 int pk_launch_axpy(float *dst, const float *eo, float w, int D, hipStream_t st);
 int pk_launch_fill_normal(float *out, int64_t n, uint64_t stream_seed, float std, hipStream_t st);
+// The same values for n_pos positions of a K cache region, in its chunk layout (pk_k_off).
+int pk_launch_fill_normal_k(float *out, int n_pos, int ctx, int KVH, int hd, uint64_t stream_seed, float std,
+                            hipStream_t st);
 int pk_launch_fill_const(float *out, int64_t n, float v, hipStream_t st);
 
 // profiling brackets around a launch (no-ops unless profiling is on)

@@ -192,11 +192,14 @@ __global__ __launch_bounds__(64) void k_attn_rows_exact(int pos_base, const floa
     const float *qh = qkv + (int64_t)r * qkv_stride + h * hd;
     const float scale = 1.0f / sqrtf((float)hd);
     for (int t = lane; t < n; t += 64) {
-        const float4 *kt = reinterpret_cast<const float4 *>(Kl + (int64_t)(start + t) * kv_dim + kvh * hd);
+        // (the K cache's chunk layout: a position's float4 columns cs apart)
+        const int tk = start + t;
+        const int cs = pk_k_cs(tk, ctx);
+        const float4 *kt = reinterpret_cast<const float4 *>(Kl + pk_k_off(tk, kvh, 0, ctx, KVH, hd));
         const float4 *q4 = reinterpret_cast<const float4 *>(qh);
         float dot = 0.0f;
         for (int i = 0; i < hd / 4; ++i) {
-            const float4 k4 = kt[i], qq = q4[i];
+            const float4 k4 = kt[(int64_t)i * cs], qq = q4[i];
             float p;
             p = qq.x * k4.x; dot = dot + p;
             p = qq.y * k4.y; dot = dot + p;

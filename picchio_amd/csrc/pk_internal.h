@@ -11,6 +11,24 @@
 typedef float pk_f32x4 __attribute__((ext_vector_type(4)));
 typedef int32_t pk_i32x4 __attribute__((ext_vector_type(4)));
 
+// K cache layout of one (sequence, layer) region: ctx positions x KVH * hd
+// floats, the size of position-major rows. Positions go in chunks of 128
+// (the last one ctx % 128 long); inside a chunk, KV head by KV head, then
+// the head's float4 column u, then the chunk's positions. A position's
+// float4 u sits next to its neighbours', so the attention's row reads (one
+// lane per position, float4 u at a time) are contiguous across a wave.
+constexpr int PK_K_CHUNK = 128;
+// Positions in pos's chunk: the float4 stride between a position's columns.
+__host__ __device__ inline int pk_k_cs(int pos, int ctx) {
+    const int b = pos & ~(PK_K_CHUNK - 1);
+    return ctx - b < PK_K_CHUNK ? ctx - b : PK_K_CHUNK;
+}
+// Offset in floats of element i (< hd) of KV head kvh at position pos (< ctx).
+__host__ __device__ inline int64_t pk_k_off(int pos, int kvh, int i, int ctx, int KVH, int hd) {
+    const int b = pos & ~(PK_K_CHUNK - 1), p = pos - b;
+    return (int64_t)b * KVH * hd + ((int64_t)(kvh * (hd >> 2) + (i >> 2)) * pk_k_cs(pos, ctx) + p) * 4 + (i & 3);
+}
+
 // ───────────────────────── error plumbing ─────────────────────────
 void pk_set_error(const char *fmt, ...);
 

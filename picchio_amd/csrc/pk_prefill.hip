@@ -654,7 +654,8 @@ extern "C" int pk_kv_fill_synthetic(pk_engine *e, int seq, int n_pos, uint64_t s
     for (int l = 0; l < c->n_layers; ++l) {
         const int64_t off = seq * e->seq_stride + (int64_t)l * c->ctx_len * kv_dim;
         const uint64_t s = seed * 0x9E3779B97F4A7C15ull + (uint64_t)(seq * 1024 + l) * 2;
-        PK_TRY(pk_launch_fill_normal(e->K + off, n_pos * kv_dim, s, 1.0f, e->stream));
+        PK_TRY(pk_launch_fill_normal_k(e->K + off, n_pos, c->ctx_len, c->n_kv_heads, c->head_dim, s, 1.0f,
+                                       e->stream));
         PK_TRY(pk_launch_fill_normal(e->V + off, n_pos * kv_dim, s + 1, 1.0f, e->stream));
     }
     return PK_OK;
