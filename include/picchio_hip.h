@@ -233,6 +233,14 @@ int pk_moe_ffn_plan(int gu_RB, int dn_RB, int K, int n_cu, int dot, int *down_ta
  * (item, row block, group), group fastest. Returns 1 if mode 2 runs this
  * shape on W workgroups, 0 if it falls back, or a negative PK_ERR_* code. */
 int pk_moe_bal_plan(int K, int gu_RB, int gu_NG, int dn_RB, int dn_NG, int W, int *ranges, int n_out);
+/* Diagnostic (no reference counterpart; no device work): where the device KV
+ * caches keep each value. For one (sequence, layer) region of ctx positions
+ * x KVH heads x hd values, k_off[f] receives the float offset of K value f
+ * (f = (pos * KVH + kvh) * hd + i, picchio's kv_store order, picchio.c:492-498):
+ * positions in chunks of 128, inside a chunk by KV head, then by the head's
+ * float4 column, then by position. V stays in picchio's order (offset f).
+ * n_out >= ctx * KVH * hd. Returns 0 or a negative PK_ERR_* code. */
+int pk_kv_layout(int ctx, int KVH, int hd, int64_t *k_off, int64_t n_out);
 /* Batch-1 decode attention (pk_forward_token, pk_generate; gqa_attention,
  * picchio.c:504-623) and its output projection with the residual
  * (picchio.c:615-616, :1690) as one launch per layer (k_attn_oproj: the

@@ -124,6 +124,7 @@ def lib():
         "pk_set_grouped_f16": (C.c_int, [vp, C.c_int]),
         "pk_set_moe_fused": (C.c_int, [vp, C.c_int]),
         "pk_moe_ffn_plan": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, vp, C.c_int]),
+        "pk_kv_layout": (C.c_int, [C.c_int, C.c_int, C.c_int, vp, C.c_int64]),
         "pk_moe_bal_plan": (C.c_int, [C.c_int] * 6 + [vp, C.c_int]),
         "pk_set_router_trace": (C.c_int, [vp, vp, C.c_int64]),
         "pk_router_trace_used": (C.c_int64, [vp]),

@@ -963,6 +963,17 @@ int pk_check_model(pk_engine *e) {
     return PK_OK;
 }
 
+extern "C" int pk_kv_layout(int ctx, int KVH, int hd, int64_t *k_off, int64_t n_out) {
+    PK_CHECK(ctx > 0 && KVH > 0 && hd > 0 && hd % 4 == 0 && k_off, PK_ERR_ARG, "kv layout: ctx %d KVH %d hd %d", ctx,
+             KVH, hd);
+    const int64_t n = (int64_t)ctx * KVH * hd;
+    PK_CHECK(n_out >= n, PK_ERR_ARG, "kv layout: %lld outputs for %lld values", (long long)n_out, (long long)n);
+    for (int pos = 0; pos < ctx; ++pos)
+        for (int h = 0; h < KVH; ++h)
+            for (int i = 0; i < hd; ++i) k_off[((int64_t)pos * KVH + h) * hd + i] = pk_k_off(pos, h, i, ctx, KVH, hd);
+    return PK_OK;
+}
+
 // Attention of layer l for n rows of normalised input xn: the decode token
 // (st = device state, n = 1), prompt positions pos_base .. pos_base+n-1 of
 // one sequence (pos_step 1, seq_step 0), or n sequences at one position

@@ -137,6 +137,33 @@ def test_moe_ffn_down_tasks_are_a_permutation(lib, n_cu, gu_rb, dn_rb, k):
         assert all(got[t] < n_cu - n2 for t in alone)
 
 
+@pytest.mark.parametrize("ctx,kvh,hd", [(16, 8, 64), (128, 2, 64), (200, 3, 32), (4105, 8, 64), (1200, 1, 128)])
+def test_kv_layout_k_chunks(lib, ctx, kvh, hd):
+    """The device K cache layout: a permutation of the region; inside each
+    128-position chunk a head's float4 column of consecutive positions is
+    contiguous (one lane per position reads one contiguous run), and a
+    position's four values of a column are adjacent."""
+    n = ctx * kvh * hd
+    off = np.zeros(n, np.int64)
+    assert lib.pk_kv_layout(ctx, kvh, hd, off.ctypes.data, n) == 0
+    assert np.array_equal(np.sort(off), np.arange(n))
+    o = off.reshape(ctx, kvh, hd // 4, 4)
+    assert np.all(np.diff(o, axis=3) == 1)
+    for c0 in range(0, ctx, 128):
+        cs = min(128, ctx - c0)
+        blk = o[c0:c0 + cs, :, :, 0]                       # [pos][head][column]
+        assert np.all(np.diff(blk, axis=0) == 4)           # neighbouring positions 16 bytes apart
+        assert blk.min() == c0 * kvh * hd and blk.max() == (c0 + cs) * kvh * hd - 4
+        assert np.all(np.diff(blk[0].reshape(-1)) == 4 * cs)   # columns, then heads, cs positions apart
+
+
+def test_kv_layout_checks_arguments(lib):
+    out = np.zeros(16, np.int64)
+    assert lib.pk_kv_layout(0, 8, 64, out.ctypes.data, 16) < 0
+    assert lib.pk_kv_layout(4, 1, 6, out.ctypes.data, 16) < 0         # head_dim not a multiple of 4
+    assert lib.pk_kv_layout(4, 1, 8, out.ctypes.data, 16) < 0         # too few outputs
+
+
 def test_moe_ffn_plan_checks_arguments(lib):
     out = (C.c_int * 4)()
     assert lib.pk_moe_ffn_plan(0, 45, 4, 256, 0, None, 0) == -1
