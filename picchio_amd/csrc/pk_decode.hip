@@ -1008,10 +1008,10 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
             PK_TRY(pk_launch_gemm_chain8(xn, D, d.wqkv, d.bqkv, qkv, qkv_dim, n, D, qkv_dim, false, e->stream));
         else if (split_rope)
             PK_TRY(pk_launch_gemm_skinny(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, 0, e->stream, e->skinny_ws,
-                                         PK_SKINNY_WS, &splits));
+                                         PK_SKINNY_WS, &splits, pk_tiles_current(e) ? d.wqkv_t : nullptr));
         else
             PK_TRY(pk_launch_gemv_f32(qkv, xn, d.wqkv, d.bqkv, n, D, qkv_dim, e->stream, e->skinny_ws,
-                                      e->skinny_ws ? PK_SKINNY_WS : 0));
+                                      e->skinny_ws ? PK_SKINNY_WS : 0, pk_tiles_current(e) ? d.wqkv_t : nullptr));
         const int n_rope = (H + KVH) * (hd / 2) + kv_dim;
         hipLaunchKernelGGL(k_rope_kv, dim3((n_rope + 255) / 256, n), dim3(256), 0, e->stream, st, pos_base,
                            pos_step, qkv, (int64_t)qkv_dim, e->rope, H, KVH, hd, c->ctx_len, Kl, Vl, kv_row,
@@ -1090,7 +1090,8 @@ int pk_attention_rows(pk_engine *e, int l, const pk_dstate *st, int pos_base, in
         for (int r0 = 0; r0 < n; r0 += 32)
             PK_TRY(pk_launch_gemm_skinny(h + (int64_t)r0 * D, att + (int64_t)r0 * H * hd, d.wo, d.bo,
                                          n - r0 < 32 ? n - r0 : 32, H * hd, D, 1, e->stream, e->skinny_ws,
-                                         e->skinny_ws ? PK_SKINNY_WS : 0));
+                                         e->skinny_ws ? PK_SKINNY_WS : 0, nullptr,
+                                         pk_tiles_current(e) ? d.wo_t : nullptr));
     } else {
         hipLaunchKernelGGL(k_gemv_res, dim3((D + 3) / 4, n), dim3(256), 0, e->stream, h, att, d.wo, d.bo,
                            H * hd, D);

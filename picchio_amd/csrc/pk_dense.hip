@@ -151,6 +151,9 @@ constexpr int SK_WAVES = 4, SK_ROWS = 16 * SK_WAVES;
 constexpr int SK_ST = 4;                  // 32-column steps per LDS stage
 constexpr int SK_PAD = 36;                // floats per LDS input row (32 + 4: conflict-free 16-byte reads)
 
+// TILED: W is the tile-order copy (pk_launch_tile_skinny): each weight load
+// reads one contiguous kilobyte instead of sixteen 64-byte pieces of rows.
+template <bool TILED>
 __global__ __launch_bounds__(64 * SK_WAVES) void k_gemm_mfma32(float *__restrict__ Y, const float *__restrict__ X,
                                                                const float *__restrict__ W,
                                                                const float *__restrict__ bias, int S, int I,
@@ -182,12 +185,15 @@ __global__ __launch_bounds__(64 * SK_WAVES) void k_gemm_mfma32(float *__restrict
         }
     };
     // this lane's 8 columns of W at K0 (zero past ke)
+    const int n_step = (I + 31) >> 5;
+    const float *wtile = W + (int64_t)min(o0 >> 4, (O - 1) >> 4) * n_step * 512 + lane * 4;
     auto load_w = [&](int k0, float4 (&wv)[2]) {
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
             const int k = k0 + 8 * kq + 4 * j;
             if (k < ke) {
-                const pk_f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4v *>(wrow + k));
+                const float *src = TILED ? wtile + (int64_t)(k0 >> 5) * 512 + j * 256 : wrow + k;
+                const pk_f32x4v t = __builtin_nontemporal_load(reinterpret_cast<const pk_f32x4v *>(src));
                 wv[j] = make_float4(t.x, t.y, t.z, t.w);
             } else {
                 wv[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -268,8 +274,34 @@ __global__ __launch_bounds__(256) void k_gemm_splits(float *__restrict__ Y, cons
     Y[i] = residual ? Y[i] + sum : sum;
 }
 
+__global__ void k_tile_skinny(const float *__restrict__ W, int O, int I, float *__restrict__ Wt, int64_t n4) {
+    const int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= n4) return;
+    const int n_step = (I + 31) >> 5;
+    const int64_t t = q >> 7;                                 // tile: 128 float4
+    const int w = (int)(q & 127), j = w >> 6, l = w & 63;
+    const int R = (int)(t / n_step), Sx = (int)(t - (int64_t)R * n_step);
+    const int row = min(16 * R + (l & 15), O - 1), col = 32 * Sx + 8 * (l >> 4) + 4 * j;
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (col < I) v = *reinterpret_cast<const float4 *>(W + (int64_t)row * I + col);
+    reinterpret_cast<float4 *>(Wt)[q] = v;
+}
+
+int64_t pk_skinny_tile_floats(int O, int I) {
+    return (int64_t)((O + 15) / 16) * ((I + 31) / 32) * 512;
+}
+
+int pk_launch_tile_skinny(const float *W, int O, int I, float *Wt, hipStream_t st) {
+    PK_CHECK(W && Wt && O > 0 && I > 0 && (I & 3) == 0, PK_ERR_ARG, "tile skinny: O=%d I=%d", O, I);
+    const int64_t n4 = pk_skinny_tile_floats(O, I) / 4;
+    hipLaunchKernelGGL(k_tile_skinny, dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, st, W, O, I, Wt, n4);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
-                          int residual, hipStream_t st, float *ws, int64_t ws_floats, int *splits_out) {
+                          int residual, hipStream_t st, float *ws, int64_t ws_floats, int *splits_out,
+                          const float *Wt) {
     PK_CHECK(S > 0 && S <= 32 && I > 0 && O > 0, PK_ERR_ARG, "skinny gemm: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0, PK_ERR_UNSUPPORTED,
              "skinny gemm: needs 16-byte aligned rows (I=%d)", I);
@@ -285,8 +317,12 @@ int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float 
             splits = (I + kchunk - 1) / kchunk;
         }
     }
-    hipLaunchKernelGGL(k_gemm_mfma32, dim3(rb, splits), dim3(64 * SK_WAVES), 0, st, y, x, W, bias, S, I, O,
-                       residual, kchunk, ws);
+    if (Wt)
+        hipLaunchKernelGGL(k_gemm_mfma32<true>, dim3(rb, splits), dim3(64 * SK_WAVES), 0, st, y, x, Wt, bias, S, I,
+                           O, residual, kchunk, ws);
+    else
+        hipLaunchKernelGGL(k_gemm_mfma32<false>, dim3(rb, splits), dim3(64 * SK_WAVES), 0, st, y, x, W, bias, S, I,
+                           O, residual, kchunk, ws);
     PK_HIP(hipGetLastError());
     if (splits_out) *splits_out = splits;
     if (splits > 1 && !splits_out) {
@@ -298,7 +334,7 @@ int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float 
 }
 
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
-                       int S, int I, int O, hipStream_t st, float *ws, int64_t ws_floats) {
+                       int S, int I, int O, hipStream_t st, float *ws, int64_t ws_floats, const float *Wt) {
     PK_CHECK(S > 0 && I > 0 && O > 0 && S <= 65535, PK_ERR_ARG, "gemv f32: bad shape");
     PK_CHECK(((uintptr_t)W & 15) == 0 && ((uintptr_t)x & 15) == 0 && (I & 3) == 0,
              PK_ERR_UNSUPPORTED, "gemv f32: needs 16-byte aligned rows (I=%d)", I);
@@ -306,7 +342,7 @@ int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bi
         // several inputs: one weight read per block of up to 32 inputs
         for (int s0 = 0; s0 < S; s0 += 32)
             PK_TRY(pk_launch_gemm_skinny(y + (int64_t)s0 * O, x + (int64_t)s0 * I, W, bias,
-                                         S - s0 < 32 ? S - s0 : 32, I, O, 0, st, ws, ws_floats));
+                                         S - s0 < 32 ? S - s0 : 32, I, O, 0, st, ws, ws_floats, nullptr, Wt));
         return PK_OK;
     }
     if (O <= 2048) {

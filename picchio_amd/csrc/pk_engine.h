@@ -9,6 +9,7 @@ struct pk_layer_dev {
     float *wo = nullptr, *bo = nullptr;       // [D][H hd], bias
     float *sinks = nullptr;                   // [H]
     float *router = nullptr, *router_b = nullptr;  // [E][D], [E]
+    float *wqkv_t = nullptr, *wo_t = nullptr;  // the batched GEMM's tile-order copies (pk_dense_tiles)
     bool have_attn = false, have_router = false;
 };
 
@@ -57,13 +58,17 @@ struct pk_engine {
     pk_layer_dev *L = nullptr;                // host array of device pointers
     float *embed = nullptr;                   // [vocab][D] fp32
     float *lm_f32 = nullptr;                  // [vocab][D]
+    float *lm_t = nullptr;                    // its tile-order copy (pk_dense_tiles)
+    // the tile-order copies are current when tiles_ver == dense_ver; every
+    // upload or build of the fp32 projections and lm_head advances dense_ver
+    int64_t dense_ver = 1, tiles_ver = 0;
     int8_t *lm_q8 = nullptr;                  // [vocab][D]
     float *lm_s = nullptr;                    // [vocab]
     float *final_norm = nullptr;
     bool have_globals = false;
 
     float *rope = nullptr;                    // [ctx][hd/2][2] (cos, sin) * attn_factor
-    float *K = nullptr, *V = nullptr;         // [n_seq][L][ctx][kv_dim]
+    float *K = nullptr, *V = nullptr;         // [n_seq][L] regions of ctx x kv_dim (K chunked: pk_k_off)
     int n_seq = 1;                            // sequences with a KV cache (pk_batch_reserve)
     int64_t seq_stride = 0;                   // floats per sequence in K / V
 
@@ -236,6 +241,12 @@ constexpr int PK_F16_TILE = 64;
 int pk_launch_act_f16(const float *x, int64_t x_stride, int rows, int cols, uint16_t *xf, int64_t fplane,
                       int32_t *exps, hipStream_t st);
 int pk_launch_moe_f16(const pk_mfma_args &a, int max_tiles, int epilogue, hipStream_t st);
+
+// Builds (outside a capture) the tile-order copies of the fp32 QKV and
+// O-projection weights and of the fp32 lm_head for the batched GEMM, when
+// they are not current; pk_tiles_current says whether they may be read.
+int pk_dense_tiles(pk_engine *e);
+inline bool pk_tiles_current(const pk_engine *e) { return e->tiles_ver == e->dense_ver; }
 
 // decode driver pieces (pk_decode.hip) reused by the prompt driver
 int pk_decode_reserve(pk_engine *e);

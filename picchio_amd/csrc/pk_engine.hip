@@ -149,12 +149,13 @@ static void engine_free(pk_engine *e) {
                     e->b_eo, e->b_sel, e->b_perm, e->p_H, e->p_XN, e->p_qkv, e->p_att,
                     e->p_part, e->p_ids, e->bd_logits, e->bd_toks, e->g_limbs, e->g_exps, e->g_pairs, e->g_tiles,
                     e->lm_bval, e->lm_bidx, e->dstate, e->step_out, e->samp, e->samp_av, e->samp_ai, e->hn_q, e->act_q, e->b_xq, e->b_actq, e->b_pairs, e->b_tiles,
-                    e->moe_act_t, e->moe_eo_t, e->moe_cont_t, e->att_t, e->skinny_ws};
+                    e->moe_act_t, e->moe_eo_t, e->moe_cont_t, e->att_t, e->skinny_ws, e->lm_t};
     for (void *p : ptrs) pk_dev_free(e, p);
     if (e->L) {
         for (int l = 0; l < e->c.n_layers; ++l) {
             pk_layer_dev &d = e->L[l];
-            void *lp[] = {d.in_ln, d.post_ln, d.wqkv, d.bqkv, d.wo, d.bo, d.sinks, d.router, d.router_b};
+            void *lp[] = {d.in_ln, d.post_ln, d.wqkv, d.bqkv, d.wo, d.bo, d.sinks, d.router, d.router_b,
+                          d.wqkv_t, d.wo_t};
             for (void *p : lp) pk_dev_free(e, p);
         }
         delete[] e->L;
@@ -601,6 +602,28 @@ extern "C" int pk_store_expert(pk_engine *e, int layer, int eid, const pk_qt_hos
     return PK_OK;
 }
 
+int pk_dense_tiles(pk_engine *e) {
+    if (pk_tiles_current(e)) return PK_OK;
+    PK_CHECK(!e->capturing, PK_ERR_ARG, "tile copies: not built while capturing");
+    const pk_cfg *c = &e->c;
+    const int D = c->hidden, A = c->n_heads * c->head_dim, Q = (c->n_heads + 2 * c->n_kv_heads) * c->head_dim;
+    const int64_t ver = e->dense_ver;
+    for (int l = 0; l < c->n_layers; ++l) {
+        pk_layer_dev &d = e->L[l];
+        if (!d.have_attn) continue;
+        if (!d.wqkv_t) ALLOC(d.wqkv_t, pk_skinny_tile_floats(Q, D) * 4);
+        if (!d.wo_t) ALLOC(d.wo_t, pk_skinny_tile_floats(D, A) * 4);
+        PK_TRY(pk_launch_tile_skinny(d.wqkv, Q, D, d.wqkv_t, e->stream));
+        PK_TRY(pk_launch_tile_skinny(d.wo, D, A, d.wo_t, e->stream));
+    }
+    if (e->lm_f32) {
+        if (!e->lm_t) ALLOC(e->lm_t, pk_skinny_tile_floats(c->vocab, D) * 4);
+        PK_TRY(pk_launch_tile_skinny(e->lm_f32, c->vocab, D, e->lm_t, e->stream));
+    }
+    e->tiles_ver = ver;
+    return PK_OK;
+}
+
 static int upload_f32(pk_engine *e, float **dst, const float *src, int64_t n) {
     if (!*dst) ALLOC(*dst, n * 4);
     PK_HIP(hipMemcpyAsync(*dst, src, (size_t)n * 4, hipMemcpyHostToDevice, e->stream));
@@ -647,6 +670,7 @@ extern "C" int pk_store_layer(pk_engine *e, int layer, const pk_layer_host *l) {
         PK_TRY(upload_f32(e, &d.bo, l->bo, D));
         PK_TRY(upload_f32(e, &d.sinks, l->sinks, H));
         d.have_attn = true;
+        ++e->dense_ver;
     }
     PK_HIP(hipStreamSynchronize(e->stream));
     return PK_OK;
@@ -665,6 +689,7 @@ extern "C" int pk_store_globals(pk_engine *e, const pk_qt_host *embed, const pk_
     PK_TRY(upload_f32(e, &e->embed, (const float *)embed->data, (int64_t)c->vocab * D));
     if (c->lm_head_fmt == PK_FMT_F32) {
         PK_TRY(upload_f32(e, &e->lm_f32, (const float *)lm_head->data, (int64_t)c->vocab * D));
+        ++e->dense_ver;
     } else {
         PK_CHECK(lm_head->s, PK_ERR_ARG, "lm_head scales are null");
         if (!e->lm_q8) ALLOC(e->lm_q8, (int64_t)c->vocab * D);
@@ -742,6 +767,7 @@ extern "C" int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, 
             PK_TRY(synth_fill(e, d.bo, D, seed, PK_T_BO, l, 0, 0.02f));
             PK_TRY(synth_fill(e, d.sinks, H, seed, PK_T_SINKS, l, 0, 0.02f));
             d.have_attn = true;
+            ++e->dense_ver;
         }
     }
     if (what & 4) {
@@ -751,6 +777,7 @@ extern "C" int pk_engine_build_synthetic(pk_engine *e, uint64_t seed, int what, 
         if (c->lm_head_fmt == PK_FMT_F32) {
             if (!e->lm_f32) ALLOC(e->lm_f32, n * 4);
             PK_TRY(synth_fill(e, e->lm_f32, n, seed, PK_T_LM_HEAD, 0, 0, 0.02f));
+            ++e->dense_ver;
         } else {
             pk_set_error("synthetic INT8 lm_head is built by the host loader");
             return PK_ERR_UNSUPPORTED;

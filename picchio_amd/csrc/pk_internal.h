@@ -249,15 +249,25 @@ int pk_launch_quantize_i4(const float *w, int O, int I, int gs, uint8_t *packed,
 
 // ws / ws_floats (optional): workspace that lets the skinny GEMM split K
 // (partial tiles [splits][32][O]); without it every row block takes all of K
+// Wt (optional): W's copy in the skinny GEMM's tile order (pk_launch_tile_skinny), read instead of W
 int pk_launch_gemv_f32(float *y, const float *x, const float *W, const float *bias,
-                       int S, int I, int O, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0);
+                       int S, int I, int O, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0,
+                       const float *Wt = nullptr);
 // Y[s][o] = (residual ? Y[s][o] : 0) + X[s].W[o] + bias[o] for up to 32 inputs, one read of W.
 // splits_out (optional): when K is split, the partial tiles stay in ws
 // ([splits][32][O]) for the caller to add (*splits_out = splits, the sums
 // and bias / residual not applied); 1 when y holds the result.
 int pk_launch_gemm_skinny(float *y, const float *x, const float *W, const float *bias, int S, int I, int O,
                           int residual, hipStream_t st, float *ws = nullptr, int64_t ws_floats = 0,
-                          int *splits_out = nullptr);
+                          int *splits_out = nullptr, const float *Wt = nullptr);
+// W [O][I] (I % 4 == 0) copied into the skinny GEMM's tile order: a tile per
+// 16 rows and 32 columns, 512 floats, holding what each lane of the wave
+// that multiplies those rows reads at that column step, as two 1 KB halves
+// (the lane's first, then its second four columns), so that every weight
+// load of the GEMM is one contiguous kilobyte. Rows past O repeat row O - 1,
+// columns past I are zero. Floats of the copy:
+int64_t pk_skinny_tile_floats(int O, int I);
+int pk_launch_tile_skinny(const float *W, int O, int I, float *Wt, hipStream_t st);
 int pk_launch_gemv_q8(float *y, const float *x, const int8_t *q, const float *s,
                       int S, int I, int O, hipStream_t st);
 int pk_launch_i4_rowscale_gemv(float *y, const float *x, const uint8_t *q4, const float *s,

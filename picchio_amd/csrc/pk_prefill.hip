@@ -696,6 +696,8 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
              "decode_batch: greedy only (one sampler state is one sequence's history and rng)");
     PK_TRY(pk_check_model(e));
     PK_TRY(pk_decode_reserve(e));
+    // the batched projections read the tile-order weight copies
+    PK_TRY(pk_dense_tiles(e));
     const pk_cfg *c = &e->c;
     const int D = c->hidden, V = c->vocab;
     PK_TRY(prefill_reserve(e, n_seq));
@@ -746,7 +748,8 @@ extern "C" int pk_decode_batch(pk_engine *e, int n_seq, const int32_t *toks_host
             PK_TRY(pk_launch_gemv_q8(e->bd_logits, e->p_XN, e->lm_q8, e->lm_s, n_seq, D, V, e->stream));
         else
             PK_TRY(pk_launch_gemv_f32(e->bd_logits, e->p_XN, e->lm_f32, nullptr, n_seq, D, V, e->stream,
-                                      e->skinny_ws, e->skinny_ws ? PK_SKINNY_WS : 0));
+                                      e->skinny_ws, e->skinny_ws ? PK_SKINNY_WS : 0,
+                                      pk_tiles_current(e) ? e->lm_t : nullptr));
         hipLaunchKernelGGL(k_argmax_rows, dim3(n_seq), dim3(1024), 0, e->stream, e->bd_logits, V,
                            e->bd_toks + (int64_t)(step + 1) * n_seq);
         PK_HIP(hipGetLastError());
