@@ -14,7 +14,15 @@ router launch, then the experts launch), replayed from a HIP graph. Token t
 uses layer copy t % L (L = 24, the 20B model's MoE layers, 10.8 GB of
 experts) so the expert bytes come from HBM, not from the 256 MB MALL.
 
-value = algorithmic HBM bytes per token (experts + router + x/out) x tokens/s.
+Expert arithmetic (configs 1, 2 and 4 at batch 1): by default the integer
+dot -- the input as exact base-16 digit records, exact int32 group sums, the
+fp32 scale fold; per layer within 2e-5 of picchio's fp32 chains and the same
+256-step greedy stream -- with picchio's fp32 chains (bit-identical to
+quant.h) timed beside it under "other_arithmetic"; --dot 0 swaps them.
+
+value = algorithmic HBM bytes per token (experts + router + x/out) x tokens/s
+(the integer dot reads the same weight bytes; its input and output records
+differ from the fp32 rows by under 0.01 % of them).
 roofline = the dominant kernel (the experts launch): its algorithmic bytes per
 launch / its mean duration (graph replays with HIP events on the engine
 stream: router + experts, minus the router launches alone).
@@ -69,12 +77,28 @@ TOKENS_PER_STEP = 1000                              # config 1: "time 1000 fresh
 #  * k_moe_f16<SWIGLU>, config 3's gate_up
 #    (profiles/k_moe_f16_prefill_config3.txt, commit 73774fc): FETCH_SIZE
 #    369465.17 KiB x 2 + WRITE_SIZE 92160.00 KiB.
+#  * k_moe_ffn<integer dot>, config 1's default (passes over --mode kernels,
+#    profiles/k_moe_ffn_moe_config1.txt): FETCH_SIZE 27700.78 KiB x 2 +
+#    WRITE_SIZE 146.34 KiB.
 MOE_FFN_TRAFFIC = 57088267
+MOE_FFN_DOT_TRAFFIC = 56879493
 GATE_UP_TRAFFIC = 37780589
 STREAM_DOT_TRAFFIC = 305834925
 LM_HEAD_TRAFFIC = 2319025051
 FFN_TRAFFIC = 9691127 + 4995704
 F16_GATE_UP_TRAFFIC = 851036516
+
+
+# the batch-1 expert arithmetic of a run: --dot 1 (and the default) the
+# integer dot -- inputs as exact base-16 digit records, exact int32 group sums,
+# within 2e-5 of picchio's fp32 per layer and the same 256-step greedy stream;
+# --dot 0 picchio's fp32 chains, bit-identical to quant.h. The default run
+# times the other one beside the headline.
+ARITH = {True: "integer-dot (exact int32 group sums)", False: "fp32 chains (bit-exact with quant.h)"}
+
+
+def run_dot(args):
+    return args.dot != 0
 
 
 def host_info():
@@ -311,6 +335,8 @@ def measure_decode20b(args, steps, warmup, cpu_on):
     n_prompt = 512
     cfg = pa.gptoss_cfg(ctx_len=n_prompt + steps + 1)
     eng = pa.Engine(cfg)
+    main_dot = run_dot(args)
+    eng.set_i4_dot(main_dot)
     t0 = time.perf_counter()
     eng.build_synthetic(args.seed, what=7)
     eng.sync()
@@ -344,19 +370,20 @@ def measure_decode20b(args, steps, warmup, cpu_on):
     lm_ms, _ = eng.profile_read(pa.PROF_LM_HEAD)
     att_ms, att_n = eng.profile_read(pa.PROF_ATTENTION)
     eng.profile(False)
-    # the same steps with the experts on the integer-dot arithmetic (an
-    # option, not picchio's fp32 chains): rate and whether the stream matches
-    dot = None
-    if not sampling:
-        eng.set_i4_dot(True)
+    # the same steps on the other expert arithmetic: rate and whether the
+    # greedy stream is the same
+    alt = None
+    if not sampling and args.dot < 0:
+        eng.set_i4_dot(not main_dot)
         eng.decode_replay(nxt, n_prompt, max(warmup, 1))
         ev0.record(eng.stream)
-        toks_dot = eng.decode_replay(nxt, n_prompt, steps)
+        toks_alt = eng.decode_replay(nxt, n_prompt, steps)
         ev1.record(eng.stream)
         ev1.synchronize()
-        dot = {"tok_s": round(steps / (ev0.elapsed_time(ev1) * 1e-3), 2),
-               "same_stream": bool(list(toks_dot) == list(toks))}
-        eng.set_i4_dot(False)
+        alt = {"expert_arithmetic": ARITH[not main_dot],
+               "tok_s": round(steps / (ev0.elapsed_time(ev1) * 1e-3), 2),
+               "same_stream": bool(list(toks_alt) == list(toks))}
+        eng.set_i4_dot(main_dot)
     eng.close()
     tok_s = steps / (ms * 1e-3)
     bpt = sum(decode_bytes_per_token(cfg, n_prompt + i) for i in range(steps)) / steps
@@ -366,7 +393,8 @@ def measure_decode20b(args, steps, warmup, cpu_on):
         cpu = cpu_decode_baseline(cfg, args.seed, args.cpu_seconds, prompt, n_prompt)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
     print(f"[bench] config 2: {tok_s:.1f} tok/s ({ms / steps * 1e3:.1f} us/token), prefill "
-          f"{prefill_s:.3f} s; integer-dot experts {dot}", file=sys.stderr, flush=True)
+          f"{prefill_s:.3f} s; experts on the {ARITH[main_dot]}; other arithmetic {alt}", file=sys.stderr,
+          flush=True)
     line = {
         "metric": METRIC, "value": round(tok_s, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms / steps, 5),
@@ -383,7 +411,7 @@ def measure_decode20b(args, steps, warmup, cpu_on):
                    "hbm_frac": round(bpt * tok_s / 1e9 / HBM_PEAK_GBPS, 4),
                    "prefill_s": round(prefill_s, 3), "prefill_tok_s": round(n_prompt / prefill_s, 1),
                    "attention_us_per_layer": round(att_ms / max(att_n, 1) * 1e3, 2),
-                   "integer_dot_experts": dot,
+                   "expert_arithmetic": ARITH[main_dot], "other_arithmetic": alt,
                    "first_tokens": [int(nxt)] + [int(t) for t in toks[:8]]},
         "roofline": {"bound": "hbm", "achieved": round(lm_bytes / (lm_ms * 1e-3) / 1e9, 1),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s",
@@ -406,6 +434,8 @@ def measure_decode120b(args, steps, warmup, cpu_on):
     ctx, B = 4096, 32
     cfg = pa.gptoss_cfg(n_layers=36, n_experts=128, ctx_len=ctx + steps + 1)
     eng = pa.Engine(cfg)
+    main_dot = run_dot(args)
+    eng.set_i4_dot(main_dot)
     t0 = time.perf_counter()
     eng.build_synthetic(args.seed, what=7)
     eng.sync()
@@ -428,6 +458,20 @@ def measure_decode120b(args, steps, warmup, cpu_on):
     eng.forward_token(int(toks1[-1]), ctx + steps, None)
     lm_ms, _ = eng.profile_read(pa.PROF_LM_HEAD)
     eng.profile(False)
+    # batch 1 on the other expert arithmetic (the same state: the KV rows the
+    # steps above wrote are rewritten by the same positions' steps)
+    alt1 = None
+    if args.dot < 0:
+        eng.set_i4_dot(not main_dot)
+        eng.decode_replay(tok, ctx, max(warmup, 1))
+        ev0.record(eng.stream)
+        toks_alt = eng.decode_replay(tok, ctx, steps)
+        ev1.record(eng.stream)
+        ev1.synchronize()
+        alt1 = {"expert_arithmetic": ARITH[not main_dot],
+                "tok_s": round(steps / (ev0.elapsed_time(ev1) * 1e-3), 2),
+                "same_stream": bool(list(toks_alt) == list(toks1))}
+        eng.set_i4_dot(main_dot)
     # batch 32
     eng.batch_reserve(B)
     for sq in range(B):
@@ -457,8 +501,8 @@ def measure_decode120b(args, steps, warmup, cpu_on):
     if cpu_on:
         cpu = cpu_decode120_baseline(args.seed, args.cpu_seconds, first, ctx)
         print(f"[bench] cpu baseline: {cpu}", file=sys.stderr, flush=True)
-    print(f"[bench] config 4: batch 1 {tok1:.1f} tok/s, batch 32 {tok32:.1f} tok/s", file=sys.stderr,
-          flush=True)
+    print(f"[bench] config 4: batch 1 {tok1:.1f} tok/s ({ARITH[main_dot]}; other arithmetic {alt1}), "
+          f"batch 32 {tok32:.1f} tok/s", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC, "value": round(tok1, 2), "unit": "tok/s", "n_gpus": 1,
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms1 / steps, 5),
@@ -469,6 +513,7 @@ def measure_decode120b(args, steps, warmup, cpu_on):
                                f"{steps} steps at batch 1 and at batch 32",
                    "layers": cfg.n_layers, "experts": E, "vocab": cfg.vocab,
                    "batch1_tok_s": round(tok1, 2), "batch1_bytes_per_token": int(bpt1),
+                   "batch1_expert_arithmetic": ARITH[main_dot], "batch1_other_arithmetic": alt1,
                    "batch1_hbm_gbps": round(bpt1 * tok1 / 1e9, 1),
                    "batch32_tok_s": round(tok32, 2), "batch32_ms_per_step": round(ms32 / steps, 4),
                    "batch32_bytes_per_step": int(bstep32),
@@ -646,8 +691,8 @@ def measure_moe_layer(args):
     L = args.layers
     cfg = pa.gptoss_cfg(n_layers=L, n_experts=E, ctx_len=16, vocab=64)
     eng = pa.Engine(cfg)
-    if args.dot >= 0:
-        eng.set_i4_dot(args.dot == 1)
+    dot_on = run_dot(args)
+    eng.set_i4_dot(dot_on)
     t0 = time.perf_counter()
     eng.build_synthetic(args.seed, what=1)
     build_s = time.perf_counter() - t0
@@ -696,14 +741,11 @@ def measure_moe_layer(args):
     for g in graphs:
         eng.graph_destroy(g)
 
-    # the same tokens on the integer-dot arithmetic (within 2e-5 of picchio's
-    # fp32 chains, the north star's 1e-4 per layer; the same 256-step greedy
-    # stream in config 2), timed the same way over fewer steps, when the run
-    # is on the default fp32 chains
-    dot_on = args.dot == 1 or (args.dot < 0 and os.environ.get("PK_I4_DOT", "0") not in ("", "0"))
+    # the same tokens on the other expert arithmetic, timed the same way over
+    # fewer steps (default run)
     alt = None
-    if args.dot < 0 and not dot_on:
-        eng.set_i4_dot(True)
+    if args.dot < 0:
+        eng.set_i4_dot(not dot_on)
         S2 = min(S, 5)
 
         def replay(steps, fn):
@@ -721,15 +763,16 @@ def measure_moe_layer(args):
         steps2 = range(W, W + S2)
         ms2 = replay(steps2, enqueue)
         ms2_router = replay(steps2, lambda t: eng.router_logits(t % L, xd[t], lg))
-        eng.set_i4_dot(False)
+        eng.set_i4_dot(dot_on)
         n2 = S2 * T
         moe2 = (ms2 - ms2_router) / n2
-        alt = {"expert_arithmetic": "integer-dot", "tokens_timed": n2,
+        alt = {"expert_arithmetic": ARITH[not dot_on], "tokens_timed": n2,
                "us_per_token": round(ms2 / n2 * 1e3, 3),
                "gbps": round(TOKEN_BYTES / (ms2 / n2 * 1e-3) / 1e9, 1),
                "kernel_us": {"router": round(ms2_router / n2 * 1e3, 3), "moe_ffn": round(moe2 * 1e3, 3)},
                "moe_ffn_gbps": round((gate_up_bytes(K) + down_bytes(K)) / (moe2 * 1e-3) / 1e9, 1)}
-        print(f"[bench] config 1 on the integer dot: {alt['us_per_token']:.2f} us/token, {alt['gbps']:.1f} GB/s; "
+        print(f"[bench] config 1 on the {ARITH[not dot_on]}: {alt['us_per_token']:.2f} us/token, "
+              f"{alt['gbps']:.1f} GB/s; "
               f"moe_ffn {alt['kernel_us']['moe_ffn']:.2f} us = {alt['moe_ffn_gbps']:.1f} GB/s", file=sys.stderr,
               flush=True)
 
@@ -782,7 +825,7 @@ def measure_moe_layer(args):
     ffn_ms = replay_ms(eng, ev0, ev1, n_ffn, ffn)
     ffn_gu_ms = replay_ms(eng, ev0, ev1, n_ffn, lambda i: eng.expert_gate_up(i % L, eid(i), x0d[i], act0))
 
-    arith = "integer-dot" if dot_on else "fp32 chains (bit-exact with quant.h)"
+    arith = ARITH[dot_on]
     eng.close()
 
     ms_tok = ms / n_timed
@@ -790,9 +833,10 @@ def measure_moe_layer(args):
     if fused:
         # the dominant kernel: all routed experts of the token in one launch
         dom, dom_bytes = "moe_ffn", gate_up_bytes(K) + down_bytes(K)
-        dom_name = ("k_moe_ffn (gate_up + bias + SwiGLU, then down + bias + routing-weighted combine, "
+        dom_name = (f"k_moe_ffn<{'integer dot' if dot_on else 'fp32 chains'}> (gate_up + bias + SwiGLU, "
+                    "then down + bias + routing-weighted combine, "
                     "the token's 4 routed experts selected in the launch)")
-        traffic = MOE_FFN_TRAFFIC
+        traffic = MOE_FFN_DOT_TRAFFIC if dot_on else MOE_FFN_TRAFFIC
     else:
         dom, dom_bytes = "gate_up", gate_up_bytes(K)
         dom_name = ("k_i4_gemv<SWIGLU> (gate_up + bias + SwiGLU, the layer's 4 routed experts "
@@ -838,7 +882,8 @@ def measure_moe_layer(args):
         "gate_up_us": round(ffn_gu_ms * 1e3, 3), "down_us": round((ffn_ms - ffn_gu_ms) * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(ffn_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(ffn_gbps / HBM_PEAK_GBPS, 4), "traffic": FFN_TRAFFIC,
-                     "kernel": "k_i4_gemv<SWIGLU> (gate_up) then k_i4_gemv<PLAIN> (down), one expert",
+                     "kernel": "k_i4_gemv<SWIGLU> (gate_up) then k_i4_gemv<PLAIN> (down), one expert, "
+                               "fp32 chains (expert_apply's arithmetic, bit-exact with quant.h)",
                      "bytes_per_launch": FFN_BYTES, "mean_us": round(ffn_ms * 1e3, 3)},
         "cpu_baseline": cpu0,
     }
@@ -853,7 +898,7 @@ def measure_moe_layer(args):
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "fp32",
+        "dtype": "int32" if dot_on else "fp32",
         "data": "synthetic",
         "config": {"workload": "config1: GPT-OSS-20B MoE layer, batch-1 decode, top-4 of 32 "
                                f"INT4 gs64 experts; a step = {T} fresh seeded tokens one after another",
@@ -867,7 +912,7 @@ def measure_moe_layer(args):
                    "kernel_us_method": ("graph replays: router launches alone, and router + expert "
                                         "launches; the expert launch = the difference" if fused else
                                         "HIP events around each launch of an eager pass"),
-                   "integer_dot_experts": alt,
+                   "other_arithmetic": alt,
                    "int4_gemv_streaming": streaming,
                    "config0_expert_ffn": config0},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBPS,
@@ -890,7 +935,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--profile-tokens", type=int, default=400)
     ap.add_argument("--dot", type=int, default=-1,
-                    help="config 1 expert arithmetic: 1 integer dot, 0 fp32 chains, -1 the engine's default")
+                    help="batch-1 expert arithmetic of configs 1, 2 and 4: 1 integer dot, 0 picchio's fp32 "
+                         "chains; -1 (default) the integer dot, with the fp32 chains timed beside it")
     ap.add_argument("--grouped", choices=["f16", "int8"], default="f16",
                     help="config 3 arithmetic: f16 hi/lo activation pairs (default) or exact int8 limbs")
     ap.add_argument("--decode-steps", type=int, default=256,
@@ -930,7 +976,8 @@ def main():
         line["config"]["decode_20b"] = {"tok_s": d20["value"], "ms_per_token": d20["ms_per_step"],
                                         "steps": ds, **{k: d20["config"][k] for k in
                                                         ("workload", "bytes_per_token", "hbm_gbps", "hbm_frac",
-                                                         "prefill_tok_s", "attention_us_per_layer")},
+                                                         "prefill_tok_s", "attention_us_per_layer",
+                                                         "expert_arithmetic", "other_arithmetic")},
                                         "lm_head_roofline": d20["roofline"], "cpu_baseline": d20["cpu_baseline"]}
         line["config"]["prefill_grouped"] = {"tflops": pf["value"], "ms_per_layer": pf["ms_per_step"],
                                              "steps": pf["steps"], "dtype": pf["dtype"],
@@ -940,6 +987,7 @@ def main():
         line["config"]["decode_120b"] = {"batch1_tok_s": d120["config"]["batch1_tok_s"],
                                          "steps": ds4, **{k: d120["config"][k] for k in
                                                           ("workload", "batch1_bytes_per_token", "batch1_hbm_gbps",
+                                                           "batch1_expert_arithmetic", "batch1_other_arithmetic",
                                                            "batch32_tok_s", "batch32_ms_per_step",
                                                            "batch32_hbm_gbps")},
                                          "lm_head_roofline": d120["roofline"],
