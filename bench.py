@@ -468,9 +468,13 @@ def measure_decode120b(args, steps, warmup, cpu_on):
         toks_alt = eng.decode_replay(tok, ctx, steps)
         ev1.record(eng.stream)
         ev1.synchronize()
+        diff = [i for i, (a, b) in enumerate(zip(toks_alt, toks1)) if int(a) != int(b)]
         alt1 = {"expert_arithmetic": ARITH[not main_dot],
                 "tok_s": round(steps / (ev0.elapsed_time(ev1) * 1e-3), 2),
-                "same_stream": bool(list(toks_alt) == list(toks1))}
+                "same_stream": not diff, "first_departure_step": diff[0] if diff else None,
+                "note": "the two arithmetics differ by at most 2e-5 relative per layer; over 36 layers of "
+                        "synthetic weights a routing or top-2 near-tie can separate their greedy streams "
+                        "(tests/test_gpu_configs.py traces each departure from the oracle's stream to one)"}
         eng.set_i4_dot(main_dot)
     # batch 32
     eng.batch_reserve(B)
