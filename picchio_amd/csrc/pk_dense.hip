@@ -474,10 +474,8 @@ int pk_launch_rmsnorm(float *out, const float *x, const float *w, int D, float e
 // index, already-chosen experts skipped), softmax over the K raw logits
 // (quant.h:406-412), weight_k * routed_scale for the combine (:1445).
 // One wave per token; logits [T][E] -> sel [T][K], w [T][K].
-__global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E, int K,
-                                                     float routed_scale, int32_t *sel,
-                                                     float *w_scaled, float *w_soft) {
-    const int t = blockIdx.x;
+__device__ __forceinline__ void topk_softmax_row(int t, const float *logits, int E, int K, float routed_scale,
+                                                 int32_t *sel, float *w_scaled, float *w_soft) {
     const int lane = threadIdx.x;
     const float *lg = logits + (int64_t)t * E;
     // each lane holds experts lane, lane+64 (E <= 128)
@@ -518,6 +516,29 @@ __global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E,
             w_scaled[(int64_t)t * K + k] = p * routed_scale;
         }
     }
+}
+
+__global__ __launch_bounds__(64) void k_topk_softmax(const float *logits, int E, int K,
+                                                     float routed_scale, int32_t *sel,
+                                                     float *w_scaled, float *w_soft) {
+    topk_softmax_row(blockIdx.x, logits, E, K, routed_scale, sel, w_scaled, w_soft);
+}
+
+// The same top-k for T rows and, in the launch's other blocks, the
+// half-group records of x[0..n) (k_act_records' body): the two depend on
+// nothing of each other, and one launch of both saves a dependent launch
+// in the batched MoE on the integer dot.
+__global__ __launch_bounds__(64) void k_topk_records(const float *logits, int T, int E, int K, float routed_scale,
+                                                     int32_t *sel, float *w_scaled, const float *x, int n,
+                                                     int32_t *rec) {
+    if ((int)blockIdx.x < T) {
+        topk_softmax_row(blockIdx.x, logits, E, K, routed_scale, sel, w_scaled, nullptr);
+        return;
+    }
+    const int b = (int)blockIdx.x - T, lane = threadIdx.x;
+    const int i = b * 32 + lane;
+    const bool has = lane < 32 && i < n;
+    pk_write_digits<1>(x[has ? i : 0], has, rec + (int64_t)b * PK_XQ_INTS);
 }
 
 // Router + top-k in one launch: block e computes logit e (one row per
@@ -697,6 +718,20 @@ int pk_launch_topk_batch(const float *logits, int T, int E, int K, float routed_
              "router: E=%d K=%d outside 1..128 / 1..16", E, K);
     hipLaunchKernelGGL(k_topk_softmax, dim3(T), dim3(64), 0, st, logits, E, K, routed_scale,
                        sel, w_scaled, w_soft);
+    PK_HIP(hipGetLastError());
+    return PK_OK;
+}
+
+// Batched router's top-k together with the records of the rows x [n floats]
+// (k_topk_records): sel / w_scaled as pk_launch_topk_batch, rec as
+// pk_launch_act_records.
+int pk_launch_topk_records(const float *logits, int T, int E, int K, float routed_scale, int32_t *sel,
+                           float *w_scaled, const float *x, int n, int32_t *rec, hipStream_t st) {
+    PK_CHECK(E > 0 && E <= 128 && K > 0 && K <= 16 && K <= E, PK_ERR_UNSUPPORTED,
+             "router: E=%d K=%d outside 1..128 / 1..16", E, K);
+    PK_CHECK(T > 0 && n > 0 && n % 32 == 0, PK_ERR_ARG, "topk records: T=%d n=%d", T, n);
+    hipLaunchKernelGGL(k_topk_records, dim3(T + n / 32), dim3(64), 0, st, logits, T, E, K, routed_scale, sel,
+                       w_scaled, x, n, rec);
     PK_HIP(hipGetLastError());
     return PK_OK;
 }

@@ -185,6 +185,8 @@ void pk_dev_free(pk_engine *e, void *p);
 int pk_stage_reserve(pk_engine *e, int64_t bytes);
 
 // kernels defined in pk_dense.hip / pk_attn.hip without a launcher above
+int pk_launch_topk_records(const float *logits, int T, int E, int K, float routed_scale, int32_t *sel,
+                           float *w_scaled, const float *x, int n, int32_t *rec, hipStream_t st);
 int pk_launch_topk_batch(const float *logits, int T, int E, int K, float routed_scale,
                          int32_t *sel, float *w_scaled, float *w_soft, hipStream_t st);
 int pk_launch_combine(float *out, const float *eo, const float *w, int K, int D,

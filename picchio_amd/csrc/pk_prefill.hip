@@ -197,7 +197,10 @@ static rows_scratch engine_rows_scratch(pk_engine *e) {
 // products in order; the lockstep decode of several sequences sums them in a
 // fixed tree and adds the bias last (within the fp32 bar of moe_forward's
 // order, picchio.c:1316-1324).
-static int route_rows(pk_engine *e, const rows_scratch &sc, int layer, const float *x, int T, bool prompt_order) {
+// With xq: the top-k launch also writes the records of the T rows of x into
+// xq (the integer-dot arithmetic's input).
+static int route_rows(pk_engine *e, const rows_scratch &sc, int layer, const float *x, int T, bool prompt_order,
+                      int32_t *xq = nullptr) {
     const pk_cfg *c = &e->c;
     const pk_layer_dev &d = e->L[layer];
     if (prompt_order)
@@ -205,6 +208,9 @@ static int route_rows(pk_engine *e, const rows_scratch &sc, int layer, const flo
     else
         PK_TRY(pk_launch_gemv_f32(sc.logits, x, d.router, d.router_b, T, c->hidden, c->n_experts, e->stream));
     PK_TRY(pk_trace_router(e, sc.logits, T));
+    if (xq)
+        return pk_launch_topk_records(sc.logits, T, c->n_experts, c->topk, c->routed_scale, sc.sel, sc.w, x,
+                                      T * c->hidden, xq, e->stream);
     return pk_launch_topk_batch(sc.logits, T, c->n_experts, c->topk, c->routed_scale, sc.sel, sc.w, nullptr,
                                 e->stream);
 }
@@ -218,16 +224,16 @@ static int moe_rows_on(pk_engine *e, const rows_scratch &sc, int layer, const fl
                        const float *residual, bool decode_order) {
     const pk_cfg *c = &e->c;
     const int D = c->hidden, E = c->n_experts, K = c->topk, half = c->moe_inter / 2;
-    PK_TRY(route_rows(e, sc, layer, x, T, !decode_order));
+    // the integer-dot option: records of the token rows (written by the top-k
+    // launch), then of each pair's SwiGLU outputs (the lockstep decode of
+    // several sequences, decode_order, uses it by default)
+    const bool dot = (e->i4_dot || (decode_order && e->i4_dot_batch)) && D % 64 == 0 && c->moe_inter % 128 == 0;
+    const int64_t xq_row = (int64_t)(D / 32) * PK_XQ_INTS, aq_row = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
+    PK_TRY(route_rows(e, sc, layer, x, T, !decode_order, dot ? sc.xq : nullptr));
     if (!decode_order) {
         hipLaunchKernelGGL(k_uniq_perm, dim3(1), dim3(1024), 0, e->stream, sc.sel, T, K, E, sc.perm);
         PK_HIP(hipGetLastError());
     }
-    // the integer-dot option: records of the token rows, then of each pair's SwiGLU outputs
-    // (the lockstep decode of several sequences, decode_order, uses it by default)
-    const bool dot = (e->i4_dot || (decode_order && e->i4_dot_batch)) && D % 64 == 0 && c->moe_inter % 128 == 0;
-    const int64_t xq_row = (int64_t)(D / 32) * PK_XQ_INTS, aq_row = (int64_t)e->ex.gu.RB * PK_XQ_INTS;
-    if (dot) PK_TRY(pk_launch_act_records(x, T * D, sc.xq, e->stream));
     pk_i4_items gu = pk_expert_items(e, layer, false);
     gu.slots = sc.sel;
     gu.x = x; gu.x_stride = D; gu.x_div = K;
