@@ -569,6 +569,17 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
     const int e = blockIdx.x;
     float v;
     float rn = 1.0f;
+    // the inputs of this wave's first record go out with the others (read at
+    // the end they would add a round trip to the launch)
+    const int nhg = (D + 31) >> 5, per = (nhg + E - 1) / E;
+    const int hg0 = e * per + (threadIdx.x >> 6);
+    float rx = 0.0f, rw = 0.0f;
+    if (hq && (int)(threadIdx.x >> 6) < per && hg0 < nhg) {
+        const int i = hg0 * 32 + (threadIdx.x & 63);
+        const int ic = ((threadIdx.x & 63) < 32 && i < D) ? i : 0;
+        rx = x[ic];
+        if (nw) rw = nw[ic];
+    }
     if (nw) {
         const float4 *w4 = reinterpret_cast<const float4 *>(R + (int64_t)e * D);
         const float4 *x4 = reinterpret_cast<const float4 *>(x);
@@ -633,12 +644,12 @@ __global__ __launch_bounds__(256) void k_router_topk(const float *__restrict__ x
         // of the integer-dot arithmetic: one wave per 32 values, whole
         // half-groups per workgroup (with the norm, hn is written here too)
         const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
-        const int nhg = (D + 31) >> 5, per = (nhg + E - 1) / E;
         for (int hg = e * per + wv; hg < min(nhg, (e + 1) * per); hg += 4) {
             const int i = hg * 32 + lane;
             const bool has = lane < 32 && i < D;
             const int ic = has ? i : 0;
-            const float xv = nw ? x[ic] * rn * nw[ic] : x[ic];
+            const float xi = hg == hg0 ? rx : x[ic], wi = hg == hg0 ? rw : (nw ? nw[ic] : 0.0f);
+            const float xv = nw ? xi * rn * wi : xi;
             if (has && nw) hn[i] = xv;
             pk_write_digits<1>(xv, has, hq + (int64_t)hg * PK_XQ_INTS);
         }
